@@ -1,0 +1,97 @@
+"""ctypes mirror of include/fwhip.h: status codes, hyper-parameters and the
+weight descriptor structs (the ggml tensor layout of the reference's
+EncoderWeights / DecoderWeights, src/native_engine/encoder.rs:129-161 and
+decoder.rs:514-545)."""
+from __future__ import annotations
+
+import ctypes as C
+
+OK = 0
+ERR_GENERIC = 1
+ERR_INVALID = 2
+ERR_UNSUPPORTED = 5
+ERR_CANCELLED = 6
+
+ENC_F32 = 0
+ENC_INT8 = 1
+DEC_INT8 = 0
+DEC_F16 = 1
+
+K_ENC_GEMM_I8 = 1
+K_ENC_GEMM_F32 = 2
+K_ENC_ATTN = 3
+K_DEC_GEMV = 4
+K_DEC_LOGITS = 5
+
+DS_CROSS_K_F16 = 1
+DS_CROSS_VT_F16 = 2
+DS_KV_K = 3
+DS_KV_V = 4
+
+f32p = C.POINTER(C.c_float)
+u16p = C.POINTER(C.c_uint16)
+
+
+class HParams(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "n_vocab", "n_audio_ctx", "n_audio_state", "n_audio_head", "n_audio_layer",
+        "n_text_ctx", "n_text_state", "n_text_head", "n_text_layer", "n_mels")]
+
+
+class EncLayer(C.Structure):
+    _fields_ = [
+        ("attn_ln_w", f32p), ("attn_ln_b", f32p),
+        ("q_w", u16p), ("q_b", f32p), ("k_w", u16p), ("v_w", u16p), ("v_b", f32p),
+        ("o_w", u16p), ("o_b", f32p),
+        ("mlp_ln_w", f32p), ("mlp_ln_b", f32p),
+        ("fc1_w", u16p), ("fc1_b", f32p), ("fc2_w", u16p), ("fc2_b", f32p),
+    ]
+
+
+class EncoderWeights(C.Structure):
+    _fields_ = [
+        ("hp", HParams),
+        ("conv1_w", u16p), ("conv1_b", f32p), ("conv2_w", u16p), ("conv2_b", f32p),
+        ("pos_emb", f32p), ("layers", C.POINTER(EncLayer)),
+        ("ln_post_w", f32p), ("ln_post_b", f32p),
+    ]
+
+
+class DecLayer(C.Structure):
+    _fields_ = [
+        ("attn_ln_w", f32p), ("attn_ln_b", f32p),
+        ("q_w", u16p), ("q_b", f32p), ("k_w", u16p), ("v_w", u16p), ("v_b", f32p),
+        ("o_w", u16p), ("o_b", f32p),
+        ("cross_ln_w", f32p), ("cross_ln_b", f32p),
+        ("cq_w", u16p), ("cq_b", f32p), ("ck_w", u16p), ("cv_w", u16p), ("cv_b", f32p),
+        ("co_w", u16p), ("co_b", f32p),
+        ("mlp_ln_w", f32p), ("mlp_ln_b", f32p),
+        ("fc1_w", u16p), ("fc1_b", f32p), ("fc2_w", u16p), ("fc2_b", f32p),
+    ]
+
+
+class DecoderWeights(C.Structure):
+    _fields_ = [
+        ("hp", HParams),
+        ("tok_emb", u16p), ("pos_emb", f32p), ("layers", C.POINTER(DecLayer)),
+        ("ln_w", f32p), ("ln_b", f32p),
+    ]
+
+
+class Filter(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "eot", "sot", "sot_prev", "solm", "no_speech", "no_timestamps",
+        "translate", "transcribe", "timestamp_begin", "space_token", "n_languages")]
+
+
+class ExecRecord(C.Structure):
+    _fields_ = [("route", C.c_char * 48), ("precision", C.c_int32), ("n_windows", C.c_int32),
+                ("device_ms", C.c_double)]
+
+
+def ptr(arr, ctype):
+    """Pointer to a contiguous numpy array's buffer (caller keeps `arr` alive)."""
+    if arr is None:
+        return C.cast(None, C.POINTER(ctype))
+    assert arr.flags["C_CONTIGUOUS"], "array must be C-contiguous"
+    return arr.ctypes.data_as(C.POINTER(ctype))

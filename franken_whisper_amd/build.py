@@ -1,0 +1,65 @@
+"""In-tree build of the native libraries.
+
+  lib/libfwhip.so   HIP kernels + C ABI (include/fwhip.h), gfx950 only
+  lib/libfwsynth.so seeded synthetic weights/audio (host C, OpenMP)
+
+Compiles every time it is called (the driver's "does it build" check); hipcc
+cross-compiles gfx950 code objects without a GPU.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIBDIR = os.path.join(HERE, "lib")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_SOURCES = ["fwhip.hip", "dec_kernels.hip", "load_kernels.hip", "encoder.hip"]
+# Packed-FP32 instructions are disabled for every HIP translation unit; exact
+# reference epilogues need -ffp-contract=off (Rust never contracts a*b+c).
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off", "-fno-fast-math",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument", "-Wno-unknown-warning-option", "-Wno-unused-value",
+    "-Wno-unused-result",
+    "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+]
+
+
+def _run(cmd):
+    print("+", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build_synth():
+    os.makedirs(LIBDIR, exist_ok=True)
+    out = os.path.join(LIBDIR, "libfwsynth.so")
+    _run(["gcc", "-O2", "-fPIC", "-shared", "-fopenmp", "-std=gnu11",
+          os.path.join(CSRC, "synth.c"), "-o", out, "-lm"])
+    return out
+
+
+def build_hip():
+    os.makedirs(LIBDIR, exist_ok=True)
+    out = os.path.join(LIBDIR, "libfwhip.so")
+    tmp = out + ".tmp"
+    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
+    _run([HIPCC] + HIP_FLAGS + srcs + ["-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
+def build_all():
+    build_synth()
+    build_hip()
+
+
+if __name__ == "__main__":
+    what = sys.argv[1:] or ["all"]
+    for w in what:
+        {"all": build_all, "synth": build_synth, "hip": build_hip}[w]()

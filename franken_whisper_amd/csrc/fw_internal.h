@@ -1,0 +1,82 @@
+// fw_internal.h — host-side internals shared by the API translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "fwhip.h"
+
+struct fw_event_pair {
+    hipEvent_t a, b;
+    int cls;
+    double units;
+    bool active;
+};
+
+struct fw_kstat {
+    int64_t launches = 0;
+    double ms = 0.0;
+    double units = 0.0;
+};
+
+struct fwhip_ctx {
+    int device = 0;
+    int n_cu = 0;
+    hipStream_t stream = nullptr;
+    std::atomic<int> cancel{0};
+    bool timing = false;
+    std::vector<fw_event_pair> pending;
+    std::map<int, fw_kstat> stats;
+    float *gelu_tab = nullptr; // device [65536]
+};
+
+fwhip_status fw_fail(fwhip_status code, const std::string &msg);
+void fw_timed_begin(fwhip_ctx *c, int cls, double units, fw_event_pair *ev);
+void fw_timed_end(fwhip_ctx *c, fw_event_pair *ev);
+void *fw_dalloc(std::vector<void *> &owned, size_t bytes);
+void *fw_dupload(std::vector<void *> &owned, const void *host, size_t bytes);
+void fw_free_all(std::vector<void *> &owned);
+
+// IEEE binary16 <-> binary32 on the host (round-to-nearest-even).
+static inline float fw_host_h2f(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, ex = (h >> 10) & 0x1fu, man = h & 0x3ffu, bits;
+    if (ex == 0) {
+        if (man == 0) bits = sign;
+        else {
+            int e = -1;
+            do {
+                e++;
+                man <<= 1;
+            } while (!(man & 0x400u));
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((man & 0x3ffu) << 13);
+        }
+    } else if (ex == 31) bits = sign | 0x7f800000u | (man << 13) | (man ? 0x400000u : 0u);
+    else bits = sign | ((ex + 112u) << 23) | (man << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+static inline uint16_t fw_host_f2h(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t a = x & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+    if (a == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+    if (a >= 0x38800000u) {
+        uint32_t r = a - (112u << 23);
+        r += 0xfffu + ((r >> 13) & 1u);
+        r >>= 13;
+        return (uint16_t)(sign | (r >= 0x7c00u ? 0x7c00u : r));
+    }
+    uint32_t e = a >> 23;
+    if (e < 102) return sign;
+    uint32_t m = (a & 0x7fffffu) | 0x800000u, s = 126u - e;
+    uint32_t q = m >> s, rem = m & ((1u << s) - 1u), half = 1u << (s - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}

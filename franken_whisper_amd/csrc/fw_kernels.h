@@ -1,0 +1,42 @@
+// fw_kernels.h — kernel launch wrappers shared between translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "fw_device.h"
+#include "fwhip.h"
+
+// decoder (dec_kernels.hip)
+void fw_launch_embed(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb,
+                     const float *pemb, float *x, int d, int ns);
+void fw_launch_layernorm(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d,
+                         int rows);
+void fw_launch_gemv_i8(hipStream_t st, const int8_t *W, const float *sw, const float *bias, const float *x,
+                       float *y, int N, int K, int ns, int ldy, int mode, const float *gelu_tab);
+void fw_launch_gemv_f16(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *y, int N,
+                        int K, int ns, int ldy, int mode, const float *gelu_tab);
+void fw_launch_gemv_blk(hipStream_t st, const int8_t *W, const float *sc, const float *bias, const float *x,
+                        float *y, int N, int K, int ns, int ldy, int mode);
+void fw_launch_self_attn(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att,
+                         const int *posp, int d, int H, int nctx, int L, int layer, int ns, float scale);
+void fw_launch_cross_attn_i8(hipStream_t st, const float *qc, const int8_t *ck, const float *cks,
+                             const int8_t *cvt, const float *cvs, float *att, int d, int T, int H, int L,
+                             int layer, int ns, float scale);
+void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,
+                              float *att, int d, int T, int H, int L, int layer, int ns, float scale);
+void fw_launch_argmax(hipStream_t st, const float *logits, int V, const fwhip_filter *f, const int *initialp,
+                      int32_t *out, int ns);
+void fw_launch_gemm_strict(hipStream_t st, const float *A, const uint16_t *B, int m, int n, int k, int epi,
+                           float *C, const float *bias, float scale, uint16_t *out16, int T, int H, int L,
+                           int layer);
+void fw_launch_quant_f16_rows(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n);
+void fw_launch_step_bookkeeping(hipStream_t st, int *posp, int *initialp, const int32_t *tok, int32_t *hist,
+                                int hist_stride, int step, int ns);
+
+// load-time quantizers (load_kernels.hip)
+void fw_launch_quant_blocked(hipStream_t st, const uint16_t *w, int8_t *q, float *s, int64_t out, int inp,
+                             int block);
+void fw_launch_quant_i7(hipStream_t st, const uint16_t *w, int8_t *q, float *s, int32_t *cs, int64_t out,
+                        int inp, int ef);
+void fw_launch_quant_enc_i8(hipStream_t st, const uint16_t *w, int8_t *q, float *s, int64_t out, int inp);

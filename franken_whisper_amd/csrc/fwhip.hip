@@ -1,0 +1,686 @@
+// fwhip.hip — C ABI of the gfx950 Whisper hot path (include/fwhip.h).
+//
+// Host-side orchestration only: weight upload and load-time quantization,
+// decoder state, per-token step, greedy loop, encoder forward.  All arithmetic
+// runs in the kernels of dec_kernels.hip / enc_kernels.hip / load_kernels.hip.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "fw_internal.h"
+#include "fw_kernels.h"
+
+static thread_local std::string g_err;
+
+fwhip_status fw_fail(fwhip_status code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                         \
+    do {                                                                                      \
+        hipError_t _e = (expr);                                                               \
+        if (_e != hipSuccess)                                                                 \
+            return fw_fail(FWHIP_ERR_GENERIC, std::string(#expr ": ") + hipGetErrorString(_e)); \
+    } while (0)
+
+extern "C" const char *fwhip_last_error(void) { return g_err.c_str(); }
+extern "C" int32_t fwhip_abi_version(void) { return FWHIP_ABI_VERSION; }
+
+// ---------------------------------------------------------------------------
+// context
+extern "C" fwhip_status fwhip_init(int32_t device, fwhip_ctx **out) {
+    if (!out) return fw_fail(FWHIP_ERR_INVALID, "fwhip_init: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fw_fail(FWHIP_ERR_UNSUPPORTED, "cpu:no-hip-device");
+    if (device < 0 || device >= n) return fw_fail(FWHIP_ERR_INVALID, "fwhip_init: device out of range");
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::string(prop.gcnArchName).find("gfx950") == std::string::npos)
+        return fw_fail(FWHIP_ERR_UNSUPPORTED, std::string("cpu:unsupported-arch:") + prop.gcnArchName);
+    HIP_TRY(hipSetDevice(device));
+    fwhip_ctx *c = new fwhip_ctx();
+    c->device = device;
+    c->n_cu = prop.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return fw_fail(FWHIP_ERR_GENERIC, "hipStreamCreate failed");
+    }
+    // GELU table (gelu_table, nn.rs:4561-4575) built on the host with the
+    // platform tanhf, exactly as the reference builds it.
+    std::vector<float> tab(1 << 16);
+    for (int i = 0; i < (1 << 16); i++) {
+        float f = fw_host_h2f((uint16_t)i);
+        float g = 0.5f * f * (1.0f + tanhf(0.7978846f * f * (1.0f + 0.044715f * f * f)));
+        tab[i] = fw_host_h2f(fw_host_f2h(g));
+    }
+    if (hipMalloc(&c->gelu_tab, sizeof(float) * tab.size()) != hipSuccess ||
+        hipMemcpy(c->gelu_tab, tab.data(), sizeof(float) * tab.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        fwhip_destroy(c);
+        return fw_fail(FWHIP_ERR_GENERIC, "gelu table upload failed");
+    }
+    *out = c;
+    return FWHIP_OK;
+}
+
+extern "C" void fwhip_destroy(fwhip_ctx *c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    for (auto &e : c->pending) {
+        hipEventDestroy(e.a);
+        hipEventDestroy(e.b);
+    }
+    if (c->gelu_tab) hipFree(c->gelu_tab);
+    hipStreamDestroy(c->stream);
+    delete c;
+}
+
+extern "C" fwhip_status fwhip_malloc(fwhip_ctx *c, size_t bytes, void **dev) {
+    if (!c || !dev) return fw_fail(FWHIP_ERR_INVALID, "fwhip_malloc: NULL argument");
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipMalloc(dev, bytes ? bytes : 1));
+    return FWHIP_OK;
+}
+extern "C" fwhip_status fwhip_free(fwhip_ctx *c, void *dev) {
+    if (!c) return fw_fail(FWHIP_ERR_INVALID, "fwhip_free: NULL ctx");
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (dev) HIP_TRY(hipFree(dev));
+    return FWHIP_OK;
+}
+extern "C" fwhip_status fwhip_upload(fwhip_ctx *c, void *dev, const void *host, size_t bytes) {
+    if (!c || (!dev && bytes) || (!host && bytes)) return fw_fail(FWHIP_ERR_INVALID, "fwhip_upload: NULL");
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return FWHIP_OK;
+}
+extern "C" fwhip_status fwhip_download(fwhip_ctx *c, void *host, const void *dev, size_t bytes) {
+    if (!c || (!dev && bytes) || (!host && bytes)) return fw_fail(FWHIP_ERR_INVALID, "fwhip_download: NULL");
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return FWHIP_OK;
+}
+extern "C" fwhip_status fwhip_synchronize(fwhip_ctx *c) {
+    if (!c) return fw_fail(FWHIP_ERR_INVALID, "NULL ctx");
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("kernel error: ") + hipGetErrorString(e));
+    return FWHIP_OK;
+}
+extern "C" fwhip_status fwhip_request_cancel(fwhip_ctx *c) {
+    if (!c) return fw_fail(FWHIP_ERR_INVALID, "NULL ctx");
+    c->cancel.store(1);
+    return FWHIP_OK;
+}
+
+// ---- kernel timing ---------------------------------------------------------
+void fw_timed_begin(fwhip_ctx *c, int cls, double units, fw_event_pair *ev) {
+    ev->active = c->timing;
+    if (!ev->active) return;
+    ev->cls = cls;
+    ev->units = units;
+    hipEventCreate(&ev->a);
+    hipEventCreate(&ev->b);
+    hipEventRecord(ev->a, c->stream);
+}
+void fw_timed_end(fwhip_ctx *c, fw_event_pair *ev) {
+    if (!ev->active) return;
+    hipEventRecord(ev->b, c->stream);
+    c->pending.push_back(*ev);
+}
+static void fw_drain_events(fwhip_ctx *c) {
+    if (c->pending.empty()) return;
+    hipStreamSynchronize(c->stream);
+    for (auto &e : c->pending) {
+        float ms = 0.0f;
+        hipEventElapsedTime(&ms, e.a, e.b);
+        auto &s = c->stats[e.cls];
+        s.launches += 1;
+        s.ms += ms;
+        s.units += e.units;
+        hipEventDestroy(e.a);
+        hipEventDestroy(e.b);
+    }
+    c->pending.clear();
+}
+extern "C" fwhip_status fwhip_kernel_timing(fwhip_ctx *c, int32_t enable) {
+    if (!c) return fw_fail(FWHIP_ERR_INVALID, "NULL ctx");
+    fw_drain_events(c);
+    c->stats.clear();
+    c->timing = enable != 0;
+    return FWHIP_OK;
+}
+extern "C" fwhip_status fwhip_kernel_stats(fwhip_ctx *c, int32_t cls, int64_t *launches, double *total_ms,
+                                           double *units) {
+    if (!c) return fw_fail(FWHIP_ERR_INVALID, "NULL ctx");
+    fw_drain_events(c);
+    auto it = c->stats.find(cls);
+    if (launches) *launches = it == c->stats.end() ? 0 : it->second.launches;
+    if (total_ms) *total_ms = it == c->stats.end() ? 0.0 : it->second.ms;
+    if (units) *units = it == c->stats.end() ? 0.0 : it->second.units;
+    return FWHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// device buffers owned by a model/state
+void *fw_dalloc(std::vector<void *> &owned, size_t bytes) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) return nullptr;
+    owned.push_back(p);
+    return p;
+}
+void *fw_dupload(std::vector<void *> &owned, const void *host, size_t bytes) {
+    void *p = fw_dalloc(owned, bytes);
+    if (p && host && bytes) {
+        if (hipMemcpy(p, host, bytes, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    }
+    return p;
+}
+void fw_free_all(std::vector<void *> &owned) {
+    for (void *p : owned) hipFree(p);
+    owned.clear();
+}
+
+// ---------------------------------------------------------------------------
+// decoder
+struct DecLayerDev {
+    const float *attn_ln_w, *attn_ln_b, *cross_ln_w, *cross_ln_b, *mlp_ln_w, *mlp_ln_b;
+    const float *qkv_b, *o_b, *cq_b, *co_b, *fc1_b, *fc2_b, *cv_b;
+    const int8_t *qkv8 = nullptr, *o8 = nullptr, *cq8 = nullptr, *co8 = nullptr, *fc1_8 = nullptr,
+                 *fc2_b8 = nullptr;
+    const float *qkv8s = nullptr, *o8s = nullptr, *cq8s = nullptr, *co8s = nullptr, *fc1_8s = nullptr,
+                *fc2_b8s = nullptr;
+    const uint16_t *qkv16 = nullptr, *o16 = nullptr, *cq16 = nullptr, *co16 = nullptr, *fc1_16 = nullptr,
+                   *fc2_16 = nullptr, *ck16w = nullptr, *cv16w = nullptr;
+};
+
+struct fwhip_decoder {
+    fwhip_ctx *ctx;
+    int arm;
+    fwhip_hparams hp;
+    int d, H, L, V, nctx, dff;
+    const uint16_t *emb16 = nullptr;
+    const int8_t *emb8 = nullptr;
+    const float *emb8s = nullptr;
+    const float *pos_emb = nullptr, *ln_w = nullptr, *ln_b = nullptr;
+    std::vector<DecLayerDev> layers;
+    std::vector<void *> owned;
+};
+
+struct fwhip_dstate {
+    fwhip_decoder *dec;
+    int S, T, len;
+    uint16_t *kv_k, *kv_v, *ck16, *cvt16;
+    int8_t *ck8 = nullptr, *cvt8 = nullptr;
+    float *ck8s = nullptr, *cvt8s = nullptr;
+    float *x, *h, *qkv, *att, *y, *ff, *logits;
+    int32_t *tok, *amax, *hist, *rows;
+    int *pos, *initial;
+    int hist_cap;
+    std::vector<void *> owned;
+};
+
+// Quantize a host f16 [out, inp] matrix to per-row int8 on the device.
+static bool dev_quant_rows(fwhip_ctx *c, std::vector<void *> &owned, const uint16_t *host, int64_t out, int inp,
+                           const int8_t **q, const float **s) {
+    uint16_t *tmp = nullptr;
+    size_t bytes = sizeof(uint16_t) * (size_t)out * inp;
+    if (hipMalloc(&tmp, bytes) != hipSuccess) return false;
+    if (hipMemcpy(tmp, host, bytes, hipMemcpyHostToDevice) != hipSuccess) return false;
+    int8_t *qq = (int8_t *)fw_dalloc(owned, (size_t)out * inp);
+    float *ss = (float *)fw_dalloc(owned, sizeof(float) * out);
+    if (!qq || !ss) return false;
+    fw_launch_quant_f16_rows(c->stream, tmp, qq, ss, (int)out, inp);
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return false;
+    hipFree(tmp);
+    *q = qq;
+    *s = ss;
+    return true;
+}
+
+static bool dev_quant_blocked(fwhip_ctx *c, std::vector<void *> &owned, const uint16_t *host, int64_t out,
+                              int inp, const int8_t **q, const float **s) {
+    uint16_t *tmp = nullptr;
+    size_t bytes = sizeof(uint16_t) * (size_t)out * inp;
+    if (hipMalloc(&tmp, bytes) != hipSuccess) return false;
+    if (hipMemcpy(tmp, host, bytes, hipMemcpyHostToDevice) != hipSuccess) return false;
+    int nb = (inp + 31) / 32;
+    int8_t *qq = (int8_t *)fw_dalloc(owned, (size_t)out * inp);
+    float *ss = (float *)fw_dalloc(owned, sizeof(float) * out * nb);
+    if (!qq || !ss) return false;
+    fw_launch_quant_blocked(c->stream, tmp, qq, ss, out, inp, 32);
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return false;
+    hipFree(tmp);
+    *q = qq;
+    *s = ss;
+    return true;
+}
+
+static bool hp_decoder_ok(const fwhip_hparams &hp, std::string &why) {
+    if (hp.n_text_state <= 0 || hp.n_text_head <= 0 || hp.n_text_layer <= 0 || hp.n_vocab <= 0 ||
+        hp.n_text_ctx <= 0) {
+        why = "non-positive decoder hparam";
+        return false;
+    }
+    if (hp.n_text_state % hp.n_text_head) {
+        why = "n_text_head must divide n_text_state";
+        return false;
+    }
+    if (hp.n_text_state / hp.n_text_head != 64) {
+        why = "d_head must be 64";
+        return false;
+    }
+
+    return true;
+}
+
+extern "C" fwhip_status fwhip_decoder_load(fwhip_ctx *c, const fwhip_decoder_weights *w, int32_t arm,
+                                           fwhip_decoder **out) {
+    if (!c || !w || !out) return fw_fail(FWHIP_ERR_INVALID, "fwhip_decoder_load: NULL argument");
+    *out = nullptr;
+    if (arm != FWHIP_DEC_INT8 && arm != FWHIP_DEC_F16) return fw_fail(FWHIP_ERR_INVALID, "unknown decoder arm");
+    std::string why;
+    if (!hp_decoder_ok(w->hp, why)) return fw_fail(FWHIP_ERR_INVALID, "fwhip_decoder_load: " + why);
+    HIP_TRY(hipSetDevice(c->device));
+    fwhip_decoder *dd = new fwhip_decoder();
+    dd->ctx = c;
+    dd->arm = arm;
+    dd->hp = w->hp;
+    dd->d = w->hp.n_text_state;
+    dd->H = w->hp.n_text_head;
+    dd->L = w->hp.n_text_layer;
+    dd->V = w->hp.n_vocab;
+    dd->nctx = w->hp.n_text_ctx;
+    dd->dff = 4 * dd->d;
+    int d = dd->d, dff = dd->dff;
+    auto &own = dd->owned;
+    bool ok = true;
+    auto up32 = [&](const float *p, size_t n) -> const float * {
+        if (!p) return nullptr;
+        const float *r = (const float *)fw_dupload(own, p, sizeof(float) * n);
+        ok = ok && r;
+        return r;
+    };
+    auto up16 = [&](const uint16_t *p, size_t n) -> const uint16_t * {
+        const uint16_t *r = (const uint16_t *)fw_dupload(own, p, sizeof(uint16_t) * n);
+        ok = ok && r;
+        return r;
+    };
+    dd->emb16 = up16(w->tok_emb, (size_t)dd->V * d);
+    dd->pos_emb = up32(w->pos_emb, (size_t)dd->nctx * d);
+    dd->ln_w = up32(w->ln_w, d);
+    dd->ln_b = up32(w->ln_b, d);
+    if (ok && arm == FWHIP_DEC_INT8) ok = dev_quant_rows(c, own, w->tok_emb, dd->V, d, &dd->emb8, &dd->emb8s);
+    for (int li = 0; ok && li < dd->L; li++) {
+        const fwhip_dec_layer &s = w->layers[li];
+        DecLayerDev l;
+        l.attn_ln_w = up32(s.attn_ln_w, d);
+        l.attn_ln_b = up32(s.attn_ln_b, d);
+        l.cross_ln_w = up32(s.cross_ln_w, d);
+        l.cross_ln_b = up32(s.cross_ln_b, d);
+        l.mlp_ln_w = up32(s.mlp_ln_w, d);
+        l.mlp_ln_b = up32(s.mlp_ln_b, d);
+        // fuse_qkv (decoder.rs:2245-2289): [q; k; v] rows, bias [q_b | 0 | v_b]
+        std::vector<uint16_t> qkv((size_t)3 * d * d);
+        memcpy(qkv.data(), s.q_w, sizeof(uint16_t) * d * d);
+        memcpy(qkv.data() + (size_t)d * d, s.k_w, sizeof(uint16_t) * d * d);
+        memcpy(qkv.data() + (size_t)2 * d * d, s.v_w, sizeof(uint16_t) * d * d);
+        std::vector<float> qkvb((size_t)3 * d, 0.0f);
+        memcpy(qkvb.data(), s.q_b, sizeof(float) * d);
+        memcpy(qkvb.data() + 2 * d, s.v_b, sizeof(float) * d);
+        l.qkv_b = up32(qkvb.data(), 3 * d);
+        l.o_b = up32(s.o_b, d);
+        l.cq_b = up32(s.cq_b, d);
+        l.co_b = up32(s.co_b, d);
+        l.fc1_b = up32(s.fc1_b, dff);
+        l.fc2_b = up32(s.fc2_b, d);
+        l.cv_b = up32(s.cv_b, d);
+        l.ck16w = up16(s.ck_w, (size_t)d * d);
+        l.cv16w = up16(s.cv_w, (size_t)d * d);
+        l.fc2_16 = up16(s.fc2_w, (size_t)d * dff); // prefill arm of mlp_2 in both arms
+        if (arm == FWHIP_DEC_INT8) {
+            ok = ok && dev_quant_rows(c, own, qkv.data(), 3 * d, d, &l.qkv8, &l.qkv8s);
+            ok = ok && dev_quant_rows(c, own, s.o_w, d, d, &l.o8, &l.o8s);
+            ok = ok && dev_quant_rows(c, own, s.cq_w, d, d, &l.cq8, &l.cq8s);
+            ok = ok && dev_quant_rows(c, own, s.co_w, d, d, &l.co8, &l.co8s);
+            ok = ok && dev_quant_rows(c, own, s.fc1_w, dff, d, &l.fc1_8, &l.fc1_8s);
+            ok = ok && dev_quant_blocked(c, own, s.fc2_w, d, dff, &l.fc2_b8, &l.fc2_b8s);
+        } else {
+            l.qkv16 = up16(qkv.data(), (size_t)3 * d * d);
+            l.o16 = up16(s.o_w, (size_t)d * d);
+            l.cq16 = up16(s.cq_w, (size_t)d * d);
+            l.co16 = up16(s.co_w, (size_t)d * d);
+            l.fc1_16 = up16(s.fc1_w, (size_t)dff * d);
+        }
+        dd->layers.push_back(l);
+    }
+    if (!ok || hipDeviceSynchronize() != hipSuccess) {
+        fw_free_all(own);
+        delete dd;
+        return fw_fail(FWHIP_ERR_GENERIC, "fwhip_decoder_load: device allocation or upload failed");
+    }
+    *out = dd;
+    return FWHIP_OK;
+}
+
+extern "C" void fwhip_decoder_free(fwhip_decoder *dd) {
+    if (!dd) return;
+    hipSetDevice(dd->ctx->device);
+    hipStreamSynchronize(dd->ctx->stream);
+    fw_free_all(dd->owned);
+    delete dd;
+}
+
+extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T, fwhip_dstate **out) {
+    if (!dd || !out) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_new: NULL argument");
+    *out = nullptr;
+    if (S <= 0 || T <= 0) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_new: n_streams and enc_frames must be > 0");
+    fwhip_ctx *c = dd->ctx;
+    HIP_TRY(hipSetDevice(c->device));
+    fwhip_dstate *st = new fwhip_dstate();
+    st->dec = dd;
+    st->S = S;
+    st->T = T;
+    st->len = 0;
+    int d = dd->d, L = dd->L, nctx = dd->nctx;
+    auto &own = st->owned;
+    size_t kvn = (size_t)S * L * nctx * d;
+    size_t crn = (size_t)S * L * T * d;
+    st->kv_k = (uint16_t *)fw_dalloc(own, kvn * 2);
+    st->kv_v = (uint16_t *)fw_dalloc(own, kvn * 2);
+    st->ck16 = (uint16_t *)fw_dalloc(own, crn * 2);
+    st->cvt16 = (uint16_t *)fw_dalloc(own, crn * 2);
+    bool ok = st->kv_k && st->kv_v && st->ck16 && st->cvt16;
+    if (dd->arm == FWHIP_DEC_INT8) {
+        st->ck8 = (int8_t *)fw_dalloc(own, crn);
+        st->cvt8 = (int8_t *)fw_dalloc(own, crn);
+        st->ck8s = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * L * dd->H * T);
+        st->cvt8s = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * L * d);
+        ok = ok && st->ck8 && st->cvt8 && st->ck8s && st->cvt8s;
+    }
+    st->x = (float *)fw_dalloc(own, sizeof(float) * S * d);
+    st->h = (float *)fw_dalloc(own, sizeof(float) * S * d);
+    st->qkv = (float *)fw_dalloc(own, sizeof(float) * S * 3 * d);
+    st->att = (float *)fw_dalloc(own, sizeof(float) * S * d);
+    st->y = (float *)fw_dalloc(own, sizeof(float) * S * d);
+    st->ff = (float *)fw_dalloc(own, sizeof(float) * S * dd->dff);
+    st->logits = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * dd->V);
+    st->tok = (int32_t *)fw_dalloc(own, sizeof(int32_t) * S);
+    st->amax = (int32_t *)fw_dalloc(own, sizeof(int32_t) * S);
+    st->rows = (int32_t *)fw_dalloc(own, sizeof(int32_t) * (size_t)S * nctx);
+    st->hist_cap = nctx;
+    st->hist = (int32_t *)fw_dalloc(own, sizeof(int32_t) * (size_t)S * nctx);
+    st->pos = (int *)fw_dalloc(own, sizeof(int) * 2);
+    st->initial = st->pos + 1;
+    ok = ok && st->x && st->h && st->qkv && st->att && st->y && st->ff && st->logits && st->tok && st->amax && st->rows &&
+         st->hist && st->pos;
+    if (!ok) {
+        fw_free_all(own);
+        delete st;
+        return fw_fail(FWHIP_ERR_GENERIC, "fwhip_dstate_new: device allocation failed");
+    }
+    *out = st;
+    return FWHIP_OK;
+}
+
+extern "C" void fwhip_dstate_free(fwhip_dstate *st) {
+    if (!st) return;
+    hipSetDevice(st->dec->ctx->device);
+    hipStreamSynchronize(st->dec->ctx->stream);
+    fw_free_all(st->owned);
+    delete st;
+}
+
+extern "C" fwhip_status fwhip_dstate_reset(fwhip_dstate *st) {
+    if (!st) return fw_fail(FWHIP_ERR_INVALID, "NULL state");
+    st->len = 0;
+    return FWHIP_OK;
+}
+extern "C" int32_t fwhip_dstate_len(const fwhip_dstate *st, int32_t) { return st ? st->len : -1; }
+
+extern "C" fwhip_status fwhip_dstate_read(const fwhip_dstate *st, int32_t what, int32_t stream, void *host,
+                                          size_t bytes) {
+    if (!st || !host) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_read: NULL argument");
+    if (stream < 0 || stream >= st->S) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_read: stream out of range");
+    const fwhip_decoder *dd = st->dec;
+    HIP_TRY(hipSetDevice(dd->ctx->device));
+    size_t cr = (size_t)dd->L * st->T * dd->d * 2, kv = (size_t)dd->L * dd->nctx * dd->d * 2;
+    const void *src = nullptr;
+    size_t n = 0;
+    switch (what) {
+    case FWHIP_DS_CROSS_K_F16: src = (const char *)st->ck16 + stream * cr; n = cr; break;
+    case FWHIP_DS_CROSS_VT_F16: src = (const char *)st->cvt16 + stream * cr; n = cr; break;
+    case FWHIP_DS_KV_K: src = (const char *)st->kv_k + stream * kv; n = kv; break;
+    case FWHIP_DS_KV_V: src = (const char *)st->kv_v + stream * kv; n = kv; break;
+    default: return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_read: unknown buffer");
+    }
+    if (bytes != n) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_read: size mismatch, need " + std::to_string(n));
+    HIP_TRY(hipStreamSynchronize(dd->ctx->stream));
+    HIP_TRY(hipMemcpy(host, src, n, hipMemcpyDeviceToHost));
+    return FWHIP_OK;
+}
+
+// DecoderState::new (decoder.rs:1040-1285) for every stream: strict f32
+// projection GEMMs writing per-head f16 K (scaled) and transposed f16 V, then
+// per-row int8 copies for the default arm.
+extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *enc_dev) {
+    if (!st || !enc_dev) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_set_cross: NULL argument");
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    HIP_TRY(hipSetDevice(c->device));
+    int d = dd->d, H = dd->H, L = dd->L, T = st->T, S = st->S;
+    float kscale = powf(64.0f, -0.25f);
+    fw_event_pair ev;
+    for (int li = 0; li < L; li++) {
+        const DecLayerDev &l = dd->layers[li];
+        fw_timed_begin(c, FWHIP_K_DEC_GEMV, 2.0 * S * T * (double)d * d, &ev);
+        fw_launch_gemm_strict(c->stream, enc_dev, l.ck16w, S * T, d, d, 1, nullptr, nullptr, kscale, st->ck16, T,
+                              H, L, li);
+        fw_timed_end(c, &ev);
+        fw_launch_gemm_strict(c->stream, enc_dev, l.cv16w, S * T, d, d, 2, nullptr, l.cv_b, 1.0f, st->cvt16, T,
+                              H, L, li);
+    }
+    if (dd->arm == FWHIP_DEC_INT8) {
+        fw_launch_quant_f16_rows(c->stream, st->ck16, st->ck8, st->ck8s, S * L * H * T, 64);
+        fw_launch_quant_f16_rows(c->stream, st->cvt16, st->cvt8, st->cvt8s, S * L * H * 64, T);
+    }
+    HIP_TRY(hipGetLastError());
+    st->len = 0;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return FWHIP_OK;
+}
+
+static fwhip_status check_cancel(fwhip_ctx *c) {
+    if (c->cancel.exchange(0)) return fw_fail(FWHIP_ERR_CANCELLED, "cancelled");
+    return FWHIP_OK;
+}
+
+// One token row for every stream at the device-side position *st->pos
+// (forward_step_hidden decoder.rs:1754-1906 + logits_last 2087-2147).
+static fwhip_status dec_forward_row_tok(fwhip_dstate *st, const int32_t *tok, bool prefill, bool want_logits) {
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    hipStream_t s = c->stream;
+    int d = dd->d, H = dd->H, L = dd->L, T = st->T, S = st->S, dff = dd->dff;
+    bool i8 = dd->arm == FWHIP_DEC_INT8;
+    float scale = powf(64.0f, -0.25f);
+    const float *gt = c->gelu_tab;
+    fw_launch_embed(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S);
+    for (int li = 0; li < L; li++) {
+        const DecLayerDev &l = dd->layers[li];
+        fw_launch_layernorm(s, st->x, st->h, l.attn_ln_w, l.attn_ln_b, d, S);
+        if (i8) fw_launch_gemv_i8(s, l.qkv8, l.qkv8s, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
+        else fw_launch_gemv_f16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
+        fw_launch_self_attn(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
+        if (i8) fw_launch_gemv_i8(s, l.o8, l.o8s, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
+        else fw_launch_gemv_f16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
+        fw_launch_layernorm(s, st->x, st->h, l.cross_ln_w, l.cross_ln_b, d, S);
+        if (i8) fw_launch_gemv_i8(s, l.cq8, l.cq8s, l.cq_b, st->h, st->y, d, d, S, d, 0, gt);
+        else fw_launch_gemv_f16(s, l.cq16, l.cq_b, st->h, st->y, d, d, S, d, 0, gt);
+        if (i8)
+            fw_launch_cross_attn_i8(s, st->y, st->ck8, st->ck8s, st->cvt8, st->cvt8s, st->att, d, T, H, L, li, S,
+                                    scale);
+        else fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
+        if (i8) fw_launch_gemv_i8(s, l.co8, l.co8s, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
+        else fw_launch_gemv_f16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
+        fw_launch_layernorm(s, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, d, S);
+        if (i8) fw_launch_gemv_i8(s, l.fc1_8, l.fc1_8s, l.fc1_b, st->h, st->ff, dff, d, S, dff, 2, gt);
+        else fw_launch_gemv_f16(s, l.fc1_16, l.fc1_b, st->h, st->ff, dff, d, S, dff, 2, gt);
+        if (i8 && !prefill) fw_launch_gemv_blk(s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, S, d, 1);
+        else fw_launch_gemv_f16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
+        fwhip_status cs = check_cancel(c);
+        if (cs != FWHIP_OK) return cs;
+    }
+    if (want_logits) {
+        fw_launch_layernorm(s, st->x, st->h, dd->ln_w, dd->ln_b, d, S);
+        fw_event_pair ev;
+        fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d * (i8 ? 1.0 : 2.0), &ev);
+        if (i8) fw_launch_gemv_i8(s, dd->emb8, dd->emb8s, nullptr, st->h, st->logits, dd->V, d, S, dd->V, 0, gt);
+        else fw_launch_gemv_f16(s, dd->emb16, nullptr, st->h, st->logits, dd->V, d, S, dd->V, 0, gt);
+        fw_timed_end(c, &ev);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("launch failed: ") + hipGetErrorString(e));
+    return FWHIP_OK;
+}
+
+// Host values are staged with a synchronous copy ordered after the queued work,
+// so no host buffer is read after the call returns.
+static fwhip_status set_dev_int(fwhip_ctx *c, int *dst, int v) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipMemcpy(dst, &v, sizeof(int), hipMemcpyHostToDevice));
+    return FWHIP_OK;
+}
+
+// Run `tq` token rows ([S, tq] host tokens) through the decoder for every
+// stream: the token matrix is uploaded once (position-major) and each row reads
+// its column; the device position advances between rows.
+static fwhip_status stage_rows(fwhip_dstate *st, const int32_t *tokens, int tq, bool keep_len) {
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    int S = st->S;
+    std::vector<int32_t> pm((size_t)S * tq);
+    for (int t = 0; t < tq; t++)
+        for (int s = 0; s < S; s++) pm[(size_t)t * S + s] = tokens[(size_t)s * tq + t];
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipMemcpy(st->rows, pm.data(), sizeof(int32_t) * pm.size(), hipMemcpyHostToDevice));
+    fwhip_status r = set_dev_int(c, st->pos, st->len);
+    if (r != FWHIP_OK) return r;
+    for (int t = 0; t < tq; t++) {
+        r = dec_forward_row_tok(st, st->rows + (size_t)t * S, tq > 1, t == tq - 1);
+        if (r != FWHIP_OK) return r;
+        if (t + 1 < tq) fw_launch_step_bookkeeping(c->stream, st->pos, nullptr, st->rows, nullptr, 0, 0, S);
+    }
+    (void)keep_len;
+    return FWHIP_OK;
+}
+
+extern "C" fwhip_status fwhip_decoder_step(fwhip_dstate *st, const int32_t *tokens, int32_t tq, float *logits_dev,
+                                           int32_t *argmax_host, const fwhip_filter *filter, int32_t initial) {
+    if (!st || !tokens) return fw_fail(FWHIP_ERR_INVALID, "fwhip_decoder_step: NULL argument");
+    if (tq <= 0) return fw_fail(FWHIP_ERR_INVALID, "forward_step: empty token batch");
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    HIP_TRY(hipSetDevice(c->device));
+    int S = st->S;
+    for (int i = 0; i < S * tq; i++)
+        if (tokens[i] < 0 || tokens[i] >= dd->V)
+            return fw_fail(FWHIP_ERR_INVALID, "token id " + std::to_string(tokens[i]) + " out of range");
+    if (st->len + tq > dd->nctx)
+        return fw_fail(FWHIP_ERR_INVALID, "decode position " + std::to_string(st->len + tq - 1) +
+                                              " >= n_text_ctx " + std::to_string(dd->nctx));
+    fwhip_status r = stage_rows(st, tokens, tq, false);
+    if (r != FWHIP_OK) return r;
+    st->len += tq;
+    if (logits_dev)
+        HIP_TRY(hipMemcpyAsync(logits_dev, st->logits, sizeof(float) * (size_t)S * dd->V, hipMemcpyDeviceToDevice,
+                               c->stream));
+    if (argmax_host) {
+        fwhip_status r = set_dev_int(c, st->initial, initial ? 1 : 0);
+        if (r != FWHIP_OK) return r;
+        fw_launch_argmax(c->stream, st->logits, dd->V, filter, st->initial, st->amax, S);
+        HIP_TRY(hipMemcpyAsync(argmax_host, st->amax, sizeof(int32_t) * S, hipMemcpyDeviceToHost, c->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipGetLastError());
+    return FWHIP_OK;
+}
+
+// Greedy no-timestamps loop (decode.rs:3429-3566): prefill the prompt, then
+// argmax -> step.  Sampled tokens accumulate on the device; the host polls for
+// end-of-text every few steps, so steps stream without a per-token sync.
+extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *prompt, int32_t n_prompt,
+                                            int32_t n_max, const fwhip_filter *filter, int32_t *out_tokens,
+                                            int32_t *out_len) {
+    if (!st || !prompt || !filter || !out_tokens || !out_len)
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_decode_greedy: NULL argument");
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    HIP_TRY(hipSetDevice(c->device));
+    int S = st->S;
+    if (n_prompt <= 0 || n_max <= 0) return fw_fail(FWHIP_ERR_INVALID, "empty prompt or n_max <= 0");
+    if (st->len + n_prompt + n_max - 1 > dd->nctx)
+        return fw_fail(FWHIP_ERR_INVALID, "prompt + n_max exceeds n_text_ctx");
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= dd->V) return fw_fail(FWHIP_ERR_INVALID, "prompt token out of range");
+    std::vector<int32_t> rows((size_t)S * n_prompt);
+    for (int s = 0; s < S; s++)
+        for (int t = 0; t < n_prompt; t++) rows[(size_t)s * n_prompt + t] = prompt[t];
+    fwhip_status r = stage_rows(st, rows.data(), n_prompt, true);
+    if (r != FWHIP_OK) return r;
+    r = set_dev_int(c, st->initial, 1);
+    if (r != FWHIP_OK) return r;
+    std::vector<int32_t> hist((size_t)S * n_max, -1);
+    int steps = 0;
+    const int poll = 8;
+    for (int i = 0; i < n_max; i++) {
+        if (i > 0) {
+            r = dec_forward_row_tok(st, st->tok, false, true);
+            if (r != FWHIP_OK) return r;
+        }
+        fw_launch_argmax(c->stream, st->logits, dd->V, filter, st->initial, st->tok, S);
+        fw_launch_step_bookkeeping(c->stream, st->pos, st->initial, st->tok, st->hist, st->hist_cap, i, S);
+        steps = i + 1;
+        if (steps == n_max) break;
+        if (steps % poll == 0) {
+            HIP_TRY(hipMemcpy2DAsync(hist.data(), sizeof(int32_t) * n_max, st->hist, sizeof(int32_t) * st->hist_cap,
+                                     sizeof(int32_t) * steps, S, hipMemcpyDeviceToHost, c->stream));
+            HIP_TRY(hipStreamSynchronize(c->stream));
+            bool all = true;
+            for (int s = 0; s < S && all; s++) {
+                bool found = false;
+                for (int k = 0; k < steps; k++)
+                    if (hist[(size_t)s * n_max + k] == filter->eot) found = true;
+                all = found;
+            }
+            if (all) break;
+        }
+    }
+    HIP_TRY(hipMemcpy2DAsync(hist.data(), sizeof(int32_t) * n_max, st->hist, sizeof(int32_t) * st->hist_cap,
+                             sizeof(int32_t) * steps, S, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipGetLastError());
+    for (int s = 0; s < S; s++) {
+        int n = steps;
+        for (int k = 0; k < steps; k++)
+            if (hist[(size_t)s * n_max + k] == filter->eot) {
+                n = k + 1;
+                break;
+            }
+        out_len[s] = n;
+        for (int k = 0; k < n_max; k++) out_tokens[(size_t)s * n_max + k] = k < n ? hist[(size_t)s * n_max + k] : 0;
+    }
+    st->len += n_prompt + steps - 1;
+    return FWHIP_OK;
+}

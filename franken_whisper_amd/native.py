@@ -1,0 +1,248 @@
+"""ctypes binding of lib/libfwhip.so (include/fwhip.h).
+
+The product path: every call here runs HIP kernels through the C ABI.  There
+is no CPU fallback — a missing or unloadable library raises, and a machine
+without a gfx950 GPU gets FWHIP_ERR_UNSUPPORTED from fwhip_init.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import abi
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libfwhip.so")
+
+_vp = C.c_void_p
+_i32p = C.POINTER(C.c_int32)
+_i64p = C.POINTER(C.c_int64)
+
+# name -> (restype, argtypes); every symbol include/fwhip.h declares
+SIGNATURES = {
+    "fwhip_init": (C.c_int32, [C.c_int32, C.POINTER(_vp)]),
+    "fwhip_destroy": (None, [_vp]),
+    "fwhip_last_error": (C.c_char_p, []),
+    "fwhip_abi_version": (C.c_int32, []),
+    "fwhip_malloc": (C.c_int32, [_vp, C.c_size_t, C.POINTER(_vp)]),
+    "fwhip_free": (C.c_int32, [_vp, _vp]),
+    "fwhip_upload": (C.c_int32, [_vp, _vp, _vp, C.c_size_t]),
+    "fwhip_download": (C.c_int32, [_vp, _vp, _vp, C.c_size_t]),
+    "fwhip_synchronize": (C.c_int32, [_vp]),
+    "fwhip_request_cancel": (C.c_int32, [_vp]),
+    "fwhip_kernel_timing": (C.c_int32, [_vp, C.c_int32]),
+    "fwhip_kernel_stats": (C.c_int32, [_vp, C.c_int32, _i64p, C.POINTER(C.c_double),
+                                       C.POINTER(C.c_double)]),
+    "fwhip_encoder_load": (C.c_int32, [_vp, C.POINTER(abi.EncoderWeights), C.c_int32, C.POINTER(_vp)]),
+    "fwhip_encoder_free": (None, [_vp]),
+    "fwhip_encoder_forward": (C.c_int32, [_vp, _vp, C.c_int64, _i64p, C.c_int32, C.c_int32, _vp,
+                                          C.POINTER(abi.ExecRecord)]),
+    "fwhip_encoder_forward_time_major": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, _vp,
+                                                     C.POINTER(abi.ExecRecord)]),
+    "fwhip_decoder_load": (C.c_int32, [_vp, C.POINTER(abi.DecoderWeights), C.c_int32, C.POINTER(_vp)]),
+    "fwhip_decoder_free": (None, [_vp]),
+    "fwhip_dstate_new": (C.c_int32, [_vp, C.c_int32, C.c_int32, C.POINTER(_vp)]),
+    "fwhip_dstate_free": (None, [_vp]),
+    "fwhip_dstate_set_cross": (C.c_int32, [_vp, _vp]),
+    "fwhip_dstate_reset": (C.c_int32, [_vp]),
+    "fwhip_dstate_len": (C.c_int32, [_vp, C.c_int32]),
+    "fwhip_decoder_step": (C.c_int32, [_vp, _i32p, C.c_int32, _vp, _i32p, C.POINTER(abi.Filter),
+                                       C.c_int32]),
+    "fwhip_dstate_read": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_size_t]),
+    "fwhip_decode_greedy": (C.c_int32, [_vp, _i32p, C.c_int32, C.c_int32, C.POINTER(abi.Filter), _i32p,
+                                        _i32p]),
+}
+
+_lib = None
+
+
+class FwhipError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"fwhip error {code}: {msg}")
+        self.code = code
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(code):
+    if code != abi.OK:
+        msg = lib().fwhip_last_error()
+        raise FwhipError(code, msg.decode() if msg else "")
+
+
+class DeviceArray:
+    """A device allocation with a numpy dtype/shape (freed with the context)."""
+
+    def __init__(self, ctx: "Context", shape, dtype):
+        self.ctx, self.shape, self.dtype = ctx, tuple(shape), np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        p = _vp()
+        check(lib().fwhip_malloc(ctx.h, self.nbytes, C.byref(p)))
+        self.ptr = p
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        check(lib().fwhip_upload(self.ctx.h, self.ptr, a.ctypes.data_as(_vp), self.nbytes))
+        return self
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(lib().fwhip_download(self.ctx.h, out.ctypes.data_as(_vp), self.ptr, self.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().fwhip_free(self.ctx.h, self.ptr)
+            self.ptr = None
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        h = _vp()
+        check(lib().fwhip_init(device, C.byref(h)))
+        self.h = h
+
+    def array(self, a: np.ndarray) -> DeviceArray:
+        return DeviceArray(self, a.shape, a.dtype).upload(a)
+
+    def empty(self, shape, dtype) -> DeviceArray:
+        return DeviceArray(self, shape, dtype)
+
+    def synchronize(self):
+        check(lib().fwhip_synchronize(self.h))
+
+    def timing(self, enable: bool):
+        check(lib().fwhip_kernel_timing(self.h, 1 if enable else 0))
+
+    def kernel_stats(self, kclass: int):
+        n = C.c_int64()
+        ms = C.c_double()
+        units = C.c_double()
+        check(lib().fwhip_kernel_stats(self.h, kclass, C.byref(n), C.byref(ms), C.byref(units)))
+        return n.value, ms.value, units.value
+
+    def cancel(self):
+        check(lib().fwhip_request_cancel(self.h))
+
+    def close(self):
+        if self.h:
+            lib().fwhip_destroy(self.h)
+            self.h = None
+
+
+class Encoder:
+    """EncoderWeights + forward (encoder.rs:764, 1224) on the GPU."""
+
+    def __init__(self, ctx: Context, model, precision: int):
+        self.ctx, self.cfg = ctx, model.cfg
+        self._desc = model.encoder_weights()
+        h = _vp()
+        check(lib().fwhip_encoder_load(ctx.h, C.byref(self._desc), precision, C.byref(h)))
+        self.h = h
+        self.precision = precision
+
+    def forward_time_major(self, x_dev: DeviceArray, n_windows: int, n_frames: int, out_dev: DeviceArray):
+        rec = abi.ExecRecord()
+        check(lib().fwhip_encoder_forward_time_major(self.h, x_dev.ptr, n_windows, n_frames, out_dev.ptr,
+                                                     C.byref(rec)))
+        return rec
+
+    def forward_mel(self, mel_dev: DeviceArray, mel_frames: int, offsets, n_frames: int, out_dev: DeviceArray):
+        offs = np.ascontiguousarray(offsets, dtype=np.int64)
+        rec = abi.ExecRecord()
+        check(lib().fwhip_encoder_forward(self.h, mel_dev.ptr, mel_frames, offs.ctypes.data_as(_i64p),
+                                          offs.size, n_frames, out_dev.ptr, C.byref(rec)))
+        return rec
+
+    def close(self):
+        if self.h:
+            lib().fwhip_encoder_free(self.h)
+            self.h = None
+
+
+class Decoder:
+    """DecoderWeights (decoder.rs:752-932) resident on the GPU."""
+
+    def __init__(self, ctx: Context, model, arm: int):
+        self.ctx, self.cfg = ctx, model.cfg
+        self._desc = model.decoder_weights()
+        h = _vp()
+        check(lib().fwhip_decoder_load(ctx.h, C.byref(self._desc), arm, C.byref(h)))
+        self.h = h
+        self.arm = arm
+
+    def state(self, n_streams: int, enc_frames: int) -> "DecoderState":
+        return DecoderState(self, n_streams, enc_frames)
+
+    def close(self):
+        if self.h:
+            lib().fwhip_decoder_free(self.h)
+            self.h = None
+
+
+class DecoderState:
+    """A cohort of DecoderStates (decoder.rs:980-1285) sharing one weight read."""
+
+    def __init__(self, dec: Decoder, n_streams: int, enc_frames: int):
+        self.dec, self.S, self.T = dec, n_streams, enc_frames
+        h = _vp()
+        check(lib().fwhip_dstate_new(dec.h, n_streams, enc_frames, C.byref(h)))
+        self.h = h
+
+    def set_cross(self, enc_dev: DeviceArray):
+        check(lib().fwhip_dstate_set_cross(self.h, enc_dev.ptr))
+
+    def reset(self):
+        check(lib().fwhip_dstate_reset(self.h))
+
+    @property
+    def len(self):
+        return lib().fwhip_dstate_len(self.h, 0)
+
+    def step(self, tokens, logits_dev: DeviceArray | None = None, filt=None, initial=False):
+        """forward_step for every stream; tokens [S, tq].  Returns argmax [S]."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(self.S, -1))
+        am = np.zeros(self.S, np.int32)
+        check(lib().fwhip_decoder_step(self.h, t.ctypes.data_as(_i32p), t.shape[1],
+                                       logits_dev.ptr if logits_dev is not None else None,
+                                       am.ctypes.data_as(_i32p), C.byref(filt) if filt is not None else None,
+                                       1 if initial else 0))
+        return am
+
+    def read(self, what: int, stream: int = 0) -> np.ndarray:
+        c = self.dec.cfg
+        if what in (abi.DS_CROSS_K_F16, abi.DS_CROSS_VT_F16):
+            n = c.n_text_layer * self.T * c.n_text_state
+        else:
+            n = c.n_text_layer * c.n_text_ctx * c.n_text_state
+        out = np.empty(n, np.uint16)
+        check(lib().fwhip_dstate_read(self.h, what, stream, out.ctypes.data_as(_vp), out.nbytes))
+        return out
+
+    def greedy(self, prompt, n_max: int, filt):
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        toks = np.zeros((self.S, n_max), np.int32)
+        lens = np.zeros(self.S, np.int32)
+        check(lib().fwhip_decode_greedy(self.h, p.ctypes.data_as(_i32p), p.size, n_max, C.byref(filt),
+                                        toks.ctypes.data_as(_i32p), lens.ctypes.data_as(_i32p)))
+        return [toks[s, : lens[s]].copy() for s in range(self.S)]
+
+    def close(self):
+        if self.h:
+            lib().fwhip_dstate_free(self.h)
+            self.h = None

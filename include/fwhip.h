@@ -1,0 +1,265 @@
+/*
+ * fwhip.h — C ABI of the MI355X (gfx950) Whisper engine hot path.
+ *
+ * This is the drop-in boundary for franken_whisper's native engine
+ * (src/native_engine/): the encoder forward and the greedy decoder step run on
+ * one GPU behind these entry points, and the Rust engine (or any other host)
+ * binds them through a thin FFI crate.  Every entry point names the reference
+ * interface it replaces (file:line under the reference tree).
+ *
+ * Conventions
+ *  - Plain C types only: pointers, sizes, int32/int64, float.  No GPU-runtime
+ *    types cross the boundary.
+ *  - "dev" pointers are device addresses obtained from fwhip_malloc (or any
+ *    allocation on the context's device); "host" pointers are ordinary memory.
+ *  - Weights are passed as host pointers in ggml layout ([out, in] row-major for
+ *    linears, f16 stored as raw IEEE binary16 bits in uint16_t, f32 otherwise).
+ *    The library copies, quantizes (with the reference quantizers) and uploads
+ *    them once; the caller keeps ownership of its buffers.
+ *  - Status codes mirror fw-ios/include/fw_ios.h:8-12 and FwError
+ *    (src/error.rs:75-115): FWHIP_ERR_INVALID ~ FwError::InvalidRequest,
+ *    FWHIP_ERR_CANCELLED ~ FwError::Cancelled, FWHIP_ERR_UNSUPPORTED tells the
+ *    caller to fall back to its CPU route with a named reason (the pattern of
+ *    encoder.rs:1700-1725 / 1993-2003).
+ *  - fwhip_last_error() returns a thread-local message for the last failing call
+ *    on the calling thread (fw_ios.h:14-20 pattern).
+ *  - Threading: a context owns one HIP stream.  Calls on one context must be
+ *    serialized by the caller; separate contexts may run concurrently.
+ */
+#ifndef FWHIP_H
+#define FWHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FWHIP_ABI_VERSION 1
+
+typedef int32_t fwhip_status;
+#define FWHIP_OK 0
+#define FWHIP_ERR_GENERIC 1
+#define FWHIP_ERR_INVALID 2
+#define FWHIP_ERR_UNSUPPORTED 5
+#define FWHIP_ERR_CANCELLED 6
+
+typedef struct fwhip_ctx fwhip_ctx;
+typedef struct fwhip_encoder fwhip_encoder;
+typedef struct fwhip_decoder fwhip_decoder;
+typedef struct fwhip_dstate fwhip_dstate;
+
+/* Model hyper-parameters: the eleven ggml header fields of WhisperHParams
+ * (src/native_engine/mod.rs:56-77), minus ftype. */
+typedef struct fwhip_hparams {
+    int32_t n_vocab;
+    int32_t n_audio_ctx;
+    int32_t n_audio_state;
+    int32_t n_audio_head;
+    int32_t n_audio_layer;
+    int32_t n_text_ctx;
+    int32_t n_text_state;
+    int32_t n_text_head;
+    int32_t n_text_layer;
+    int32_t n_mels;
+} fwhip_hparams;
+
+/* One encoder block, ggml tensor names encoder.blocks.{i}.* (encoder.rs:78-120). */
+typedef struct fwhip_enc_layer {
+    const float *attn_ln_w, *attn_ln_b;         /* [d] */
+    const uint16_t *q_w; const float *q_b;       /* [d,d] f16, [d] */
+    const uint16_t *k_w;                         /* [d,d] f16, no bias */
+    const uint16_t *v_w; const float *v_b;
+    const uint16_t *o_w; const float *o_b;
+    const float *mlp_ln_w, *mlp_ln_b;
+    const uint16_t *fc1_w; const float *fc1_b;   /* [4d,d] f16, [4d] */
+    const uint16_t *fc2_w; const float *fc2_b;   /* [d,4d] f16, [d]  */
+} fwhip_enc_layer;
+
+/* Encoder weights (EncoderWeights, encoder.rs:129-161; load encoder.rs:772-1029). */
+typedef struct fwhip_encoder_weights {
+    fwhip_hparams hp;
+    const uint16_t *conv1_w; const float *conv1_b;  /* [d, n_mels, 3] f16 */
+    const uint16_t *conv2_w; const float *conv2_b;  /* [d, d, 3] f16 */
+    const float *pos_emb;                           /* [n_audio_ctx, d] f32 */
+    const fwhip_enc_layer *layers;                  /* n_audio_layer entries */
+    const float *ln_post_w, *ln_post_b;
+} fwhip_encoder_weights;
+
+/* One decoder block, ggml names decoder.blocks.{i}.* (decoder.rs:487-512). */
+typedef struct fwhip_dec_layer {
+    const float *attn_ln_w, *attn_ln_b;
+    const uint16_t *q_w; const float *q_b;
+    const uint16_t *k_w;                         /* no bias */
+    const uint16_t *v_w; const float *v_b;
+    const uint16_t *o_w; const float *o_b;
+    const float *cross_ln_w, *cross_ln_b;
+    const uint16_t *cq_w; const float *cq_b;
+    const uint16_t *ck_w;                        /* no bias */
+    const uint16_t *cv_w; const float *cv_b;
+    const uint16_t *co_w; const float *co_b;
+    const float *mlp_ln_w, *mlp_ln_b;
+    const uint16_t *fc1_w; const float *fc1_b;
+    const uint16_t *fc2_w; const float *fc2_b;
+} fwhip_dec_layer;
+
+/* Decoder weights (DecoderWeights, decoder.rs:514-545; load decoder.rs:752-932). */
+typedef struct fwhip_decoder_weights {
+    fwhip_hparams hp;
+    const uint16_t *tok_emb;                     /* [n_vocab, d] f16 (tied logits head) */
+    const float *pos_emb;                        /* [n_text_ctx, d] f32 */
+    const fwhip_dec_layer *layers;               /* n_text_layer entries */
+    const float *ln_w, *ln_b;
+} fwhip_decoder_weights;
+
+/* Encoder precision plan (encoder.rs:474-512, mod.rs:777-841). */
+#define FWHIP_ENC_F32 0   /* default f32 path: every linear f32 */
+#define FWHIP_ENC_INT8 1  /* FW_ENC_ATTN_OUT_I8I32 quality-safe plan: q/k/v/fc1/fc2 i7
+                             (error-feedback weight quant), attn.out full i8 */
+
+/* Decoder arm (Appendix-A flag sets; mod.rs:335-1110, decoder.rs:776-892). */
+#define FWHIP_DEC_INT8 0  /* reference default: int8 fused QKV, attn_out, cross_q,
+                             cross_out, mlp_0, block-int8 mlp_2, int8 cross K/V,
+                             int8 tied logits; f16 KV cache */
+#define FWHIP_DEC_F16 1   /* pure-f16 arm: every GEMV f16 (dot_f16c order),
+                             f16 cross K/V, f16 tied logits; f16 KV cache */
+
+/* Greedy filter for the no-timestamps decode (process_logits, decode.rs:702-867,
+ * with FilterConfig decode.rs:3031-3040 and no_timestamps = true).  Special ids
+ * as derived by Tokenizer::from_vocab (tokenizer.rs:230-300). */
+typedef struct fwhip_filter {
+    int32_t eot, sot, sot_prev, solm, no_speech, no_timestamps;
+    int32_t translate, transcribe, timestamp_begin;
+    int32_t space_token;      /* id of " " (suppress_blank), -1 if absent */
+    int32_t n_languages;      /* language tokens sot+1 .. sot+n_languages are masked */
+} fwhip_filter;
+
+/* Per-forward execution record (EncoderExecution, encoder.rs:1883-2048). */
+typedef struct fwhip_exec_record {
+    char route[48];           /* e.g. "hip:gfx950:int8" */
+    int32_t precision;        /* FWHIP_ENC_* */
+    int32_t n_windows;
+    double device_ms;         /* stream time of the forward */
+} fwhip_exec_record;
+
+/* ---- context, memory ---------------------------------------------------- */
+
+/* Open device `device` and create a context with its own stream.
+ * FWHIP_ERR_UNSUPPORTED when no gfx950 device is visible. */
+fwhip_status fwhip_init(int32_t device, fwhip_ctx **out);
+void fwhip_destroy(fwhip_ctx *ctx);
+const char *fwhip_last_error(void);
+int32_t fwhip_abi_version(void);
+
+fwhip_status fwhip_malloc(fwhip_ctx *ctx, size_t bytes, void **dev);
+fwhip_status fwhip_free(fwhip_ctx *ctx, void *dev);
+fwhip_status fwhip_upload(fwhip_ctx *ctx, void *dev, const void *host, size_t bytes);
+fwhip_status fwhip_download(fwhip_ctx *ctx, void *host, const void *dev, size_t bytes);
+fwhip_status fwhip_synchronize(fwhip_ctx *ctx);
+
+/* Cancellation between layers and tokens, the checkpoint() contract of
+ * nn.rs:29-37 / encoder.rs:1628 / decoder.rs:1877: the next layer boundary
+ * returns FWHIP_ERR_CANCELLED and clears the flag. */
+fwhip_status fwhip_request_cancel(fwhip_ctx *ctx);
+
+/* Kernel timing: when enabled, the library brackets every launch of kernel
+ * class `kclass` with events on its stream; fwhip_kernel_stats returns the
+ * launch count and summed device milliseconds since the last reset. */
+#define FWHIP_K_ENC_GEMM_I8 1
+#define FWHIP_K_ENC_GEMM_F32 2
+#define FWHIP_K_ENC_ATTN 3
+#define FWHIP_K_DEC_GEMV 4
+#define FWHIP_K_DEC_LOGITS 5
+fwhip_status fwhip_kernel_timing(fwhip_ctx *ctx, int32_t enable);
+fwhip_status fwhip_kernel_stats(fwhip_ctx *ctx, int32_t kclass, int64_t *launches,
+                                double *total_ms, double *work_units);
+
+/* ---- encoder ------------------------------------------------------------ */
+
+/* Replaces EncoderWeights::from_ggml (encoder.rs:764) + the quant plan
+ * (encoder.rs:838-843).  precision = FWHIP_ENC_F32 | FWHIP_ENC_INT8. */
+fwhip_status fwhip_encoder_load(fwhip_ctx *ctx, const fwhip_encoder_weights *w,
+                                int32_t precision, fwhip_encoder **out);
+void fwhip_encoder_free(fwhip_encoder *enc);
+
+/* Replaces encoder::forward_from_full_mel_window (encoder.rs:1224-1238) for a
+ * batch of windows: window b is frames [frame_offsets[b], +n_frames) of the
+ * mel-major log-mel `mel_dev` ([n_mels, mel_frames] f32), padded with -1.5 past
+ * the end (encoder.rs:684-714).  Output `out_dev` is [n_windows, n_frames/2, d]
+ * f32 (after ln_post).  n_frames must be even and <= 2*n_audio_ctx
+ * (encoder.rs:716-737).  rec may be NULL. */
+fwhip_status fwhip_encoder_forward(fwhip_encoder *enc, const float *mel_dev, int64_t mel_frames,
+                                   const int64_t *frame_offsets, int32_t n_windows,
+                                   int32_t n_frames, float *out_dev, fwhip_exec_record *rec);
+
+/* Same contract, time-major input already windowed: `x_dev` is
+ * [n_windows, n_frames, n_mels] (the Mat that forward_time_major consumes,
+ * encoder.rs:1520). */
+fwhip_status fwhip_encoder_forward_time_major(fwhip_encoder *enc, const float *x_dev,
+                                              int32_t n_windows, int32_t n_frames,
+                                              float *out_dev, fwhip_exec_record *rec);
+
+/* ---- decoder ------------------------------------------------------------ */
+
+/* Replaces DecoderWeights::from_ggml (decoder.rs:752-932).  arm = FWHIP_DEC_*. */
+fwhip_status fwhip_decoder_load(fwhip_ctx *ctx, const fwhip_decoder_weights *w, int32_t arm,
+                                fwhip_decoder **out);
+void fwhip_decoder_free(fwhip_decoder *dec);
+
+/* A cohort of n_streams independent DecoderStates (decoder.rs:980-1027), each
+ * with its own f16 self-attention KV cache (KvCache, nn.rs:5138) of
+ * n_text_ctx tokens and its own cross K/V over enc_frames encoder rows. */
+fwhip_status fwhip_dstate_new(fwhip_decoder *dec, int32_t n_streams, int32_t enc_frames,
+                              fwhip_dstate **out);
+void fwhip_dstate_free(fwhip_dstate *st);
+
+/* Replaces DecoderState::new (decoder.rs:1040-1285): cross K/V precompute for
+ * every stream from `enc_dev` ([n_streams, enc_frames, d] f32), then reset the
+ * self-attention caches. */
+fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *enc_dev);
+
+/* DecoderState::reset (decoder.rs:1289): clear the self-attention caches. */
+fwhip_status fwhip_dstate_reset(fwhip_dstate *st);
+int32_t fwhip_dstate_len(const fwhip_dstate *st, int32_t stream);
+
+/* Replaces decoder::forward_step (decoder.rs:2048-2085) and, for n_streams > 1,
+ * forward_step_batch (decoder.rs:1907-2046): every stream consumes `tq` tokens
+ * (host `tokens`, [n_streams, tq]); tq > 1 is the prompt prefill.  Writes the
+ * last position's logits to `logits_dev` ([n_streams, n_vocab] f32, may be NULL)
+ * and, when `argmax_host` is non-NULL, the filtered first-index argmax
+ * (process_logits + argmax, decode.rs:702-867, 1727-1790) per stream; `filter`
+ * may be NULL for the raw argmax.  `initial` marks the first sampling step
+ * (suppress_blank). */
+fwhip_status fwhip_decoder_step(fwhip_dstate *st, const int32_t *tokens, int32_t tq,
+                                float *logits_dev, int32_t *argmax_host,
+                                const fwhip_filter *filter, int32_t initial);
+
+/* Read back decoder-state buffers for stream `stream` into host memory
+ * (the cross K/V built by DecoderState::new and the self-attention cache, for
+ * parity checks; decoder.rs:1129-1245 layouts):
+ *   FWHIP_DS_CROSS_K_F16   [n_layer, n_head, enc_frames, 64] f16 (scaled keys)
+ *   FWHIP_DS_CROSS_VT_F16  [n_layer, n_head, 64, enc_frames] f16
+ *   FWHIP_DS_KV_K, _KV_V   [n_layer, n_text_ctx, d] f16
+ * `bytes` must equal the buffer size. */
+#define FWHIP_DS_CROSS_K_F16 1
+#define FWHIP_DS_CROSS_VT_F16 2
+#define FWHIP_DS_KV_K 3
+#define FWHIP_DS_KV_V 4
+fwhip_status fwhip_dstate_read(const fwhip_dstate *st, int32_t what, int32_t stream, void *host,
+                               size_t bytes);
+
+/* Greedy no-timestamps decode of every stream (the loop of
+ * transcribe_samples_uncached, decode.rs:3429-3566, with max_context = 0):
+ * prefill `prompt` (n_prompt tokens, shared by all streams), then argmax ->
+ * step until eot or n_max_tokens sampled tokens.  out_tokens is host
+ * [n_streams, n_max_tokens]; out_len[s] receives the sampled count including a
+ * final eot. */
+fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *prompt, int32_t n_prompt,
+                                 int32_t n_max_tokens, const fwhip_filter *filter,
+                                 int32_t *out_tokens, int32_t *out_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FWHIP_H */

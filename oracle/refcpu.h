@@ -1,0 +1,110 @@
+/*
+ * refcpu.h — CPU restatement of franken_whisper's native Whisper engine hot
+ * path, written from the reference's Rust sources (src/native_engine/) as
+ * TEST INFRASTRUCTURE: the parity oracle for the HIP library and the CPU
+ * baseline timed beside it.  Nothing in the product links or calls this.
+ *
+ * Flag set restated (the "PINNED" mode, which makes every operation in-tree
+ * Rust or IEEE/glibc and therefore restatable bit for bit):
+ *   FT_SGEMM_STRICT_PARITY=1 (nn.rs:535-541, 587-604): every f32 matmul is an
+ *       ascending-k sequential mul+add per output, no FMA;
+ *   FW_ATTN_NO_SDPA=1 (nn.rs:5917-5921): encoder attention is the per-head
+ *       matmul -> softmax -> matmul of attention_raw (nn.rs:6035-6131);
+ *   FW_ENC_QKV_FUSED=0, FW_TOME_R=0, FW_SDPA_POLY_EXP=0, FW_KV_F16=1;
+ *   x86-64-v3 build (.cargo/config.toml:37): the AVX2/F16C/FMA kernels are the
+ *       ones restated (their lane orders and add-trunc rounding), with their
+ *       scalar tails where the Rust has them.
+ * Default-mode FrankenTorch arithmetic (ft sgemm tile order, ft SDPA, poly-exp)
+ * is NOT restated: it lives in the absent ft-kernel-cpu 0.1.2 crate.
+ *
+ * Build: -O2 -ffp-contract=off (Rust never contracts a*b+c), -mfma -mf16c only
+ * for the explicit FMA/F16C the reference itself uses.
+ */
+#ifndef REFCPU_H
+#define REFCPU_H
+#include <stdint.h>
+#include "../include/fwhip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar primitives ---- */
+float ref_f16_to_f32(uint16_t h);
+uint16_t ref_f32_to_f16(float f);
+void ref_f16_to_f32_n(const uint16_t *h, float *f, int64_t n);
+void ref_f32_to_f16_n(const float *f, uint16_t *h, int64_t n);
+float ref_gelu_scalar(float x);
+const float *ref_gelu_table(void);
+
+/* ---- quantizers ---- */
+void ref_quantize_act_i8(const float *x, int n, float xinv, int8_t *out);
+void ref_quantize_row_i7_u8(const float *x, int n, float inv, uint8_t *out);
+void ref_quant_row_i8_exact(const float *x, int n, float inv, int8_t *out);
+float ref_quantize_f16_row_to_i8(const uint16_t *w, int n, int8_t *out);
+void ref_quantize_f16_to_i8(const uint16_t *w, int64_t out, int inp, int8_t *q, float *s);
+void ref_quantize_f16_to_i8_blocked(const uint16_t *w, int64_t out, int inp, int block,
+                                    int8_t *q, float *s);
+void ref_quantize_rows_to_i7(const uint16_t *w, int64_t out, int inp, int ef, int8_t *q,
+                             float *s, int32_t *colsum);
+void ref_quantize_enc_i8_rows(const uint16_t *w, int64_t out, int inp, int8_t *q, float *s);
+float ref_act_scale(const float *x, int n); /* max(max|x|,1e-9)/127 */
+
+/* ---- GEMV / dots ---- */
+int32_t ref_dot_i8(const int8_t *w, const int8_t *x, int n);
+float ref_dot_f16c(const uint16_t *w, const float *x, int n);
+float ref_dot_i8w_f32(const int8_t *w, const float *x, int n);
+void ref_gemv_i8(const int8_t *W, const float *s_w, int64_t out, int inp, const float *x,
+                 const float *bias, float *y);
+void ref_gemv_f16(const uint16_t *W, int64_t out, int inp, const float *x, const float *bias,
+                  float *y);
+void ref_gemv_i8w_f32a_blocked(const int8_t *W, const float *s, int64_t out, int inp, int block,
+                               const float *x, const float *bias, float *y);
+
+/* ---- row ops ---- */
+void ref_layer_norm(const float *x, float *y, int64_t rows, int cols, const float *w,
+                    const float *b, float eps);
+void ref_gelu_inplace(float *x, int64_t n);
+void ref_softmax_rows(float *x, int64_t rows, int cols);
+void ref_matmul_strict(const float *a, const float *b, float *c, int64_t m, int k, int n);
+int ref_argmax_first(const float *l, int n);
+
+/* ---- encoder ---- */
+typedef struct ref_encoder ref_encoder;
+ref_encoder *ref_encoder_new(const fwhip_encoder_weights *w, int precision);
+void ref_encoder_free(ref_encoder *e);
+/* x: time-major [n_frames, n_mels]; out: [n_frames/2, d].  n_layers_run < 0
+ * runs every block (encoder_layer_limit semantics otherwise). */
+int ref_encoder_forward(const ref_encoder *e, const float *x, int n_frames, float *out,
+                        int n_layers_run);
+void ref_mel_window(const float *full_mel, int n_mel, int64_t mel_frames, int64_t frame_offset,
+                    int n_frames, float *out);
+/* one encoder int8 GEMM, for per-GEMM parity: i32 accumulators and epilogue */
+void ref_enc_i7_gemm(const ref_encoder *e, int layer, int which, const float *x, int64_t m,
+                     int32_t *acc_out, float *y_out);
+
+/* ---- decoder ---- */
+typedef struct ref_decoder ref_decoder;
+typedef struct ref_dstate ref_dstate;
+ref_decoder *ref_decoder_new(const fwhip_decoder_weights *w, int arm);
+void ref_decoder_free(ref_decoder *d);
+ref_dstate *ref_dstate_new(const ref_decoder *d, const float *enc, int enc_frames);
+void ref_dstate_free(ref_dstate *s);
+void ref_dstate_reset(ref_dstate *s);
+int ref_dstate_len(const ref_dstate *s);
+/* cross K/V accessors (layer-major then head) for parity of the precompute */
+const uint16_t *ref_dstate_cross_k_f16(const ref_dstate *s);
+const uint16_t *ref_dstate_cross_vt_f16(const ref_dstate *s);
+int ref_decoder_step(const ref_decoder *d, ref_dstate *s, const int32_t *tokens, int tq,
+                     float *logits);
+int ref_process_argmax(const fwhip_filter *f, const float *logits, int n_vocab, int initial);
+int ref_decode_greedy(const ref_decoder *d, ref_dstate *s, const int32_t *prompt, int n_prompt,
+                      int n_max, const fwhip_filter *f, int32_t *out_tokens, int32_t *out_len);
+
+int ref_num_threads(void);
+void ref_set_num_threads(int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
