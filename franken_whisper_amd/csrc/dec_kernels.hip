@@ -576,7 +576,8 @@ __global__ void __launch_bounds__(256) k_argmax(const float *logits, int V, fwhi
 __global__ void __launch_bounds__(256) k_gemm_strict(const float *__restrict__ A, const uint16_t *__restrict__ B,
                                                      int m, int n, int k, int epi, float *C,
                                                      const float *bias, float scale, uint16_t *out16,
-                                                     int T, int H, int L, int layer) {
+                                                     int T, int H, int L, int layer, int ldc,
+                                                     const float *gelu_tab, const float *pos) {
     __shared__ float As[16][65];
     __shared__ float Bs[16][65];
     int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
@@ -612,7 +613,14 @@ __global__ void __launch_bounds__(256) k_gemm_strict(const float *__restrict__ A
             float v = c[i][jj];
             if (epi == 0) {
                 if (bias) v = v + bias[gn];
-                C[(size_t)gr * n + gn] = v;
+                C[(size_t)gr * ldc + gn] = v;
+            } else if (epi == 3) { // matmul_bias then GELU (conv stem, gelu_add_bias)
+                C[(size_t)gr * ldc + gn] = fw_gelu(v + bias[gn], gelu_tab);
+            } else if (epi == 4) { // conv2: GELU then + pos_emb (encoder.rs:1557-1572)
+                C[(size_t)gr * ldc + gn] = fw_gelu(v + bias[gn], gelu_tab) + pos[(size_t)(gr % T) * ldc + gn];
+            } else if (epi == 5) { // residual x += (acc + b) (add_bias_residual, nn.rs:4741)
+                float *p = C + (size_t)gr * ldc + gn;
+                *p = *p + (v + bias[gn]);
             } else {
                 int s = gr / T, row = gr % T, h = gn >> 6, dd = gn & 63;
                 size_t lh = ((size_t)s * L + layer) * H + h;
@@ -742,10 +750,10 @@ void fw_launch_step_bookkeeping(hipStream_t st, int *posp, int *initialp, const 
 
 void fw_launch_gemm_strict(hipStream_t st, const float *A, const uint16_t *B, int m, int n, int k, int epi,
                            float *C, const float *bias, float scale, uint16_t *out16, int T, int H, int L,
-                           int layer) {
+                           int layer, int ldc, const float *gelu_tab, const float *pos) {
     dim3 grid((n + 63) / 64, (m + 63) / 64);
     hipLaunchKernelGGL(k_gemm_strict, grid, dim3(256), 0, st, A, B, m, n, k, epi, C, bias, scale, out16, T, H,
-                       L, layer);
+                       L, layer, ldc > 0 ? ldc : n, gelu_tab, pos);
 }
 
 void fw_launch_quant_f16_rows(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n) {

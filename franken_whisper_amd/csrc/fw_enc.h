@@ -1,0 +1,53 @@
+// fw_enc.h — encoder kernel interface.
+#pragma once
+#include <type_traits>
+
+#include "fw_kernels.h"
+
+#define FW_KIND_I8 0
+#define FW_KIND_F16S 1
+
+#define FW_EPI_F32 0
+#define FW_EPI_RESID 1
+#define FW_EPI_GELU_F32 2
+#define FW_EPI_GELU_SPLIT 3
+#define FW_EPI_CONV2 4
+#define FW_EPI_QKV 5
+#define FW_EPI_ACC32 6
+
+#define FW_LN_F32 0
+#define FW_LN_SPLIT 1
+#define FW_LN_I7 2
+
+struct FwGemm {
+    const void *A;  // [M, lda] i8, or f16 hi
+    const void *A2; // f16 lo (KIND_F16S)
+    const void *B;  // [N, ldb] i8 or f16
+    int M, N, K, lda, ldb;
+    const float *sx, *sw, *bias;
+    int epi;
+    float *C;
+    int ldc;
+    uint16_t *o16[6];
+    const float *pos;
+    const float *gelu_tab;
+    int T, H, Tp;
+};
+
+void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g);
+void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
+                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs);
+void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs);
+void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int n, const float *tab, int8_t *q,
+                                  float *qs);
+void fw_launch_im2col(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, int Kp,
+                      uint16_t *hi, uint16_t *lo);
+void fw_launch_mel_window(hipStream_t st, const float *mel, int n_mel, long long mel_frames, const long long *offs,
+                          int n_frames, float *out, int B);
+void fw_launch_fill_u16(hipStream_t st, uint16_t *p, size_t n, uint16_t v);
+void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
+                         const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
+                         int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol);
+void fw_launch_im2col_f32(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, float *out);
+void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qoff, int koff, int voff, int B, int T,
+                               int H, int d, float *S, float *out);

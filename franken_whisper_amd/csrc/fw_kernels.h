@@ -29,7 +29,7 @@ void fw_launch_argmax(hipStream_t st, const float *logits, int V, const fwhip_fi
                       int32_t *out, int ns);
 void fw_launch_gemm_strict(hipStream_t st, const float *A, const uint16_t *B, int m, int n, int k, int epi,
                            float *C, const float *bias, float scale, uint16_t *out16, int T, int H, int L,
-                           int layer);
+                           int layer, int ldc = 0, const float *gelu_tab = nullptr, const float *pos = nullptr);
 void fw_launch_quant_f16_rows(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n);
 void fw_launch_step_bookkeeping(hipStream_t st, int *posp, int *initialp, const int32_t *tok, int32_t *hist,
                                 int hist_stride, int step, int ns);

@@ -41,6 +41,8 @@ SIGNATURES = {
                                           C.POINTER(abi.ExecRecord)]),
     "fwhip_encoder_forward_time_major": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, _vp,
                                                      C.POINTER(abi.ExecRecord)]),
+    "fwhip_encoder_set_exact": (C.c_int32, [_vp, C.c_int32]),
+    "fwhip_encoder_gemm_i8": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, _vp, _vp]),
     "fwhip_decoder_load": (C.c_int32, [_vp, C.POINTER(abi.DecoderWeights), C.c_int32, C.POINTER(_vp)]),
     "fwhip_decoder_free": (None, [_vp]),
     "fwhip_dstate_new": (C.c_int32, [_vp, C.c_int32, C.c_int32, C.POINTER(_vp)]),
@@ -168,6 +170,13 @@ class Encoder:
         check(lib().fwhip_encoder_forward(self.h, mel_dev.ptr, mel_frames, offs.ctypes.data_as(_i64p),
                                           offs.size, n_frames, out_dev.ptr, C.byref(rec)))
         return rec
+
+    def set_exact(self, exact: bool):
+        check(lib().fwhip_encoder_set_exact(self.h, 1 if exact else 0))
+
+    def gemm_i8(self, layer: int, which: int, x_dev: DeviceArray, acc_dev: DeviceArray, y_dev: DeviceArray):
+        check(lib().fwhip_encoder_gemm_i8(self.h, layer, which, x_dev.ptr, x_dev.shape[0], acc_dev.ptr,
+                                          y_dev.ptr))
 
     def close(self):
         if self.h:

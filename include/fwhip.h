@@ -193,12 +193,32 @@ fwhip_status fwhip_encoder_forward(fwhip_encoder *enc, const float *mel_dev, int
                                    const int64_t *frame_offsets, int32_t n_windows,
                                    int32_t n_frames, float *out_dev, fwhip_exec_record *rec);
 
+/* Exact mode (exact = 1): reproduce the reference's strict-parity arithmetic
+ * (FT_SGEMM_STRICT_PARITY=1, FW_ATTN_NO_SDPA=1; nn.rs:587-604, 6035-6131)
+ * for every f32 operation of the forward — sequential-k f32 GEMMs for the
+ * conv stem (and every linear on the f32 plan), per-head attention with a
+ * glibc-exact softmax — so encoder states are bit-identical to the reference
+ * CPU path.  A parity mode, orders of magnitude slower than the default fast
+ * mode (exact = 0: MFMA f16-pair GEMMs and flash attention, within the 1e-3
+ * tolerance; int8 accumulators are exact in both). */
+fwhip_status fwhip_encoder_set_exact(fwhip_encoder *enc, int32_t exact);
+
 /* Same contract, time-major input already windowed: `x_dev` is
  * [n_windows, n_frames, n_mels] (the Mat that forward_time_major consumes,
  * encoder.rs:1520). */
 fwhip_status fwhip_encoder_forward_time_major(fwhip_encoder *enc, const float *x_dev,
                                               int32_t n_windows, int32_t n_frames,
                                               float *out_dev, fwhip_exec_record *rec);
+
+/* Per-GEMM parity of the int8 plan: quantize f32 rows x_dev [m, in] with the
+ * reference quantizer for linear `which` of block `layer` (0 q, 1 k, 2 v:
+ * quantize_act_i7 nn.rs:1443; 3 attn.out: quant_row_i8 encoder.rs:2468; 4 fc1:
+ * quantize_act_i7; 5 fc2: quantize_act_i7_gelu nn.rs:1791), run the i8 GEMM
+ * and write the exact i32 accumulators acc_dev [m, out] (= the reference's
+ * maddubs sum - 128*colsum, nn.rs:1660-1700, or its i8 dot, encoder.rs:2573)
+ * and the epilogue output y_dev [m, out] ((f32)acc*s_x*s_w + b). */
+fwhip_status fwhip_encoder_gemm_i8(fwhip_encoder *enc, int32_t layer, int32_t which, const float *x_dev,
+                                   int32_t m, int32_t *acc_dev, float *y_dev);
 
 /* ---- decoder ------------------------------------------------------------ */
 

@@ -1,0 +1,180 @@
+"""GPU parity of the encoder against the oracle (the CPU restatement of
+encoder.rs + nn.rs in strict-parity mode).
+
+- int8 plan: every GEMM's i32 accumulators are compared BIT-EXACTLY on the same
+  quantized inputs, and the epilogue output too (same f32 formula);
+- whole encoder: output within max-abs 1e-3 relative (BASELINE tolerance) on
+  both plans; the f32 plan uses f16-pair MFMA products (error <= 2^-22
+  relative per product) and a different summation order than the
+  reference's sequential f32 GEMM, so it is a tolerance comparison by design."""
+import numpy as np
+import pytest
+
+from franken_whisper_amd import abi, native, synth
+from oracle import oracle as O
+from tests.helpers import assert_bitexact, model, rel_maxabs
+
+pytestmark = pytest.mark.gpu
+
+# two-layer large-v3-turbo-shaped encoder (d 1280, 20 heads, 128 mels)
+TURBO2 = synth.Config("turbo-2L", 51866, 1500, 1280, 20, 2, 448, 1280, 20, 4, 128)
+TINY2 = synth.Config("tiny-2L", 51864, 1500, 384, 6, 2, 448, 384, 6, 4, 80)
+
+
+def _ln_like(rng, m, n):
+    return (rng.standard_normal((m, n)) * 1.3).astype(np.float32)
+
+
+@pytest.mark.parametrize("cfg", [synth.MICRO, TINY2, TURBO2], ids=lambda c: c.name)
+def test_int8_gemm_accumulators_bitexact(ctx, cfg):
+    m = synth.Model(cfg, seed=4, decoder=False)
+    enc = native.Encoder(ctx, m, abi.ENC_INT8)
+    oenc = O.Encoder(m, abi.ENC_INT8)
+    rng = np.random.default_rng(1)
+    d = cfg.n_audio_state
+    rows = 300
+    for layer in range(cfg.n_audio_layer):
+        for which in range(6):
+            inp = 4 * d if which == 5 else d
+            out = 4 * d if which == 4 else d
+            x = _ln_like(rng, rows, inp)
+            if which == 5:
+                x = x * 2.0
+            acc = ctx.empty((rows, out), np.int32)
+            y = ctx.empty((rows, out), np.float32)
+            xd = ctx.array(x)
+            enc.gemm_i8(layer, which, xd, acc, y)
+            want_acc, want_y = oenc.gemm(layer, which, x)
+            print(f"{cfg.name} layer {layer} gemm {which}", flush=True)
+            np.testing.assert_array_equal(acc.download(), want_acc, err_msg=f"acc layer {layer} which {which}")
+            assert_bitexact(y.download(), want_y, f"{cfg.name} layer {layer} which {which} epilogue")
+            for a in (acc, y, xd):
+                a.free()
+    enc.close()
+
+
+def _encoder_pair(ctx, cfg, precision, n_windows, seed=2, exact=False):
+    m = synth.Model(cfg, seed=seed, decoder=False)
+    nf = 2 * cfg.n_audio_ctx
+    x = synth.mel_input(seed + 1, n_windows, nf, cfg.n_mels)
+    enc = native.Encoder(ctx, m, precision)
+    if exact:
+        enc.set_exact(True)
+    out = ctx.empty((n_windows, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+    rec = enc.forward_time_major(ctx.array(x), n_windows, nf, out)
+    got = out.download()
+    oenc = O.Encoder(m, precision)
+    want = np.stack([oenc.forward(x[b]) for b in range(n_windows)])
+    enc.close()
+    return got, want, rec
+
+
+@pytest.mark.parametrize("cfg", [synth.MICRO, TINY2], ids=lambda c: c.name)
+def test_encoder_f32_within_tolerance(ctx, cfg):
+    """f32 plan: max-abs 1e-3 relative (BASELINE tolerance).  The residual
+    spread (~1e-4) is the reference's own f16-table GELU turning sub-ulp
+    summation-order differences into one-f16-ulp steps; the GEMM and attention
+    kernels alone are within ~1e-7 of float64."""
+    got, want, rec = _encoder_pair(ctx, cfg, abi.ENC_F32, n_windows=2)
+    err = rel_maxabs(got, want)
+    med = float(np.median(np.abs(got - want)))
+    print(f"{cfg.name} f32 rel max-abs {err:.3e} median abs {med:.2e} route={rec.route.decode()}", flush=True)
+    assert rec.route.decode() == "hip:gfx950:f32"
+    assert err < 1e-3, err
+    assert med < 1e-4, med
+
+
+@pytest.mark.parametrize("cfg", [synth.MICRO, TINY2], ids=lambda c: c.name)
+def test_encoder_int8_fast_mode_deviation(ctx, cfg):
+    """int8 plan, fast mode: the MFMA f16-pair attention/conv move f32 values by
+    ~1e-7, which quantizer boundaries occasionally turn into +-1 steps; the
+    deviation stays at the int8-noise level."""
+    got, want, rec = _encoder_pair(ctx, cfg, abi.ENC_INT8, n_windows=2)
+    err = rel_maxabs(got, want)
+    print(f"{cfg.name} int8 fast rel max-abs {err:.3e} route={rec.route.decode()}", flush=True)
+    assert rec.route.decode() == "hip:gfx950:int8"
+    assert err < 0.1, err
+
+
+@pytest.mark.parametrize("precision", [abi.ENC_F32, abi.ENC_INT8])
+@pytest.mark.parametrize("cfg", [synth.MICRO, TINY2], ids=lambda c: c.name)
+def test_encoder_exact_mode_bitexact(ctx, cfg, precision):
+    """Exact mode reproduces the strict-parity reference bit for bit (the one
+    documented exception, the f64 LayerNorm reduction order, would show as a
+    handful of differing elements)."""
+    got, want, rec = _encoder_pair(ctx, cfg, precision, n_windows=2, exact=True)
+    assert rec.route.decode().endswith(":exact")
+    assert_bitexact(got, want, f"{cfg.name} precision {precision} exact")
+
+
+@pytest.mark.parametrize("cfg", [synth.MICRO, TINY2], ids=lambda c: c.name)
+def test_encoder_int8_end_to_end_tokens(ctx, cfg):
+    """int8 plan end to end: encoder states from the exact mode, cross K/V,
+    greedy decode — identical tokens to the oracle."""
+    got, want, rec = _encoder_pair(ctx, cfg, abi.ENC_INT8, n_windows=2, exact=True)
+    m = synth.Model(cfg, seed=2, encoder=False)
+    tk = m.tokens
+    dec = native.Decoder(ctx, m, abi.DEC_INT8)
+    st = dec.state(2, cfg.n_audio_ctx)
+    st.set_cross(ctx.array(got))
+    toks = st.greedy(tk.sot_sequence(), 24, tk.filter())
+    odec = O.Decoder(m, abi.DEC_INT8)
+    for b in range(2):
+        want_toks = odec.state(want[b]).greedy(tk.sot_sequence(), 24, tk.filter())
+        np.testing.assert_array_equal(toks[b], want_toks)
+    st.close()
+    dec.close()
+
+
+def test_encoder_batch_equals_single_windows(ctx):
+    cfg = synth.MICRO
+    m = synth.Model(cfg, seed=6, decoder=False)
+    nf = 2 * cfg.n_audio_ctx
+    x = synth.mel_input(9, 3, nf, cfg.n_mels)
+    enc = native.Encoder(ctx, m, abi.ENC_INT8)
+    out3 = ctx.empty((3, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+    enc.forward_time_major(ctx.array(x), 3, nf, out3)
+    got3 = out3.download()
+    for b in range(3):
+        o1 = ctx.empty((1, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+        enc.forward_time_major(ctx.array(x[b: b + 1]), 1, nf, o1)
+        assert_bitexact(o1.download()[0], got3[b], f"window {b}")
+    enc.close()
+
+
+def test_encoder_full_mel_windows_and_padding(ctx):
+    """forward_from_full_mel_window semantics: windows sliced from a mel-major
+    log-mel, frames past the end padded with -1.5 (encoder.rs:684-714)."""
+    cfg = synth.MICRO
+    m = synth.Model(cfg, seed=7, decoder=False)
+    nf = 2 * cfg.n_audio_ctx
+    total = nf + nf // 3
+    mel = synth.normal_f32(3, "fullmel", (cfg.n_mels, total), std=1.0)
+    offs = [0, nf // 2, nf]  # the last window is mostly padding
+    enc = native.Encoder(ctx, m, abi.ENC_F32)
+    out = ctx.empty((3, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+    enc.forward_mel(ctx.array(mel), total, offs, nf, out)
+    got = out.download()
+    oenc = O.Encoder(m, abi.ENC_F32)
+    for b, off in enumerate(offs):
+        win = np.empty((nf, cfg.n_mels), np.float32)
+        O.lib().ref_mel_window(abi.ptr(mel, __import__("ctypes").c_float), cfg.n_mels, total, off, nf,
+                               abi.ptr(win, __import__("ctypes").c_float))
+        if off + nf > total:
+            assert np.all(win[total - off:] == -1.5)
+        want = oenc.forward(win)
+        assert rel_maxabs(got[b], want) < 1e-3
+    enc.close()
+
+
+def test_encoder_rejects_bad_frame_count(ctx):
+    cfg = synth.MICRO
+    m = model("micro", seed=0, decoder=False)
+    enc = native.Encoder(ctx, m, abi.ENC_F32)
+    x = ctx.empty((1, 2 * cfg.n_audio_ctx + 2, cfg.n_mels), np.float32)
+    out = ctx.empty((1, cfg.n_audio_ctx + 1, cfg.n_audio_state), np.float32)
+    for nf in (2 * cfg.n_audio_ctx + 2, 7, 0):
+        with pytest.raises(native.FwhipError) as e:
+            enc.forward_time_major(x, 1, nf, out)
+        assert e.value.code == abi.ERR_INVALID
+    enc.close()
