@@ -1,0 +1,249 @@
+"""Benchmark of the hot path on one MI355X.
+
+Default workload (the whole job the headline metric is quoted on): large-v3-turbo
+architecture with seeded random-init weights, 10 windows x 30 s (3000 log-mel
+frames x 128 bins each, seeded synthetic log-mel), int8 encoder plan
+(FW_ENC_ATTN_OUT_I8I32: i7 q/k/v/fc1/fc2, i8 attn.out), cross K/V precompute,
+then greedy no-timestamps decode of every window as one cohort with the int8
+decoder arm and the f16 KV cache: 4-token prompt + 220 sampled tokens.
+One step = that whole job.  Prints one JSON line.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload job|enc-f32|enc-int8|decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+PEAK_TFLOPS = {"int8": 5000.0, "f16": 2500.0, "f32": 157.3}
+# dense algorithmic work, large-v3-turbo, per 30 s window (no ToMe)
+ENC_GOP_PER_WINDOW = 2273.8  # all GEMMs + SDPA
+ENC_GEMM_GOP_PER_WINDOW = 1887.4
+
+
+def _args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--workload", default="job", choices=["job", "enc-f32", "enc-int8", "decode"])
+    p.add_argument("--windows", type=int, default=None)
+    p.add_argument("--tokens", type=int, default=220)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")))
+    return p.parse_args()
+
+
+def cpu_baseline(model, n_windows, n_tokens, threads):
+    """The oracle (C restatement of the reference CPU path, OpenMP) on a bounded
+    sample of the same job, extrapolated to the whole job: one window's conv
+    stem + 2 encoder layers (int8 plan), one window's cross K/V precompute, the
+    prompt prefill and 16 single-token steps of one stream."""
+    from franken_whisper_amd import abi, synth
+    from oracle import oracle as O
+
+    O.lib().ref_set_num_threads(threads)
+    cfg = model.cfg
+    e = O.Encoder(model, abi.ENC_INT8)
+    x = synth.mel_input(1, 1, 2 * cfg.n_audio_ctx, cfg.n_mels)[0]
+    t0 = time.perf_counter()
+    e.forward(x, n_layers=1)
+    t1 = time.perf_counter()
+    y = e.forward(x, n_layers=2)
+    t2 = time.perf_counter()
+    per_layer = (t2 - t1) - (t1 - t0)
+    stem = (t1 - t0) - per_layer
+    enc_window = stem + cfg.n_audio_layer * per_layer
+    d = O.Decoder(model, abi.DEC_INT8)
+    t3 = time.perf_counter()
+    st = d.state(y)
+    t4 = time.perf_counter()
+    tk = model.tokens
+    st.step(tk.sot_sequence())
+    t5 = time.perf_counter()
+    for i in range(16):
+        st.step([1000 + i])
+    t6 = time.perf_counter()
+    step = (t6 - t5) / 16
+    job = n_windows * (enc_window + (t4 - t3) + (t5 - t4) + (n_tokens - 1) * step)
+    sample_s = t6 - t0 + (t2 - t1)
+    audio_s = n_windows * 30.0
+    return {
+        "value": round(audio_s / job, 4),
+        "unit": "audio-s/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle (C restatement, -O3 -march=x86-64-v3, {threads} OpenMP threads): one window's conv stem "
+                   f"+ 2 int8 encoder layers ({per_layer:.2f} s/layer, stem {stem:.2f} s), cross K/V {t4 - t3:.2f} s, "
+                   f"prefill {t5 - t4:.3f} s, 16 decode steps ({step * 1e3:.1f} ms/step); extrapolated to "
+                   f"{n_windows} windows x ({cfg.n_audio_layer} layers + {n_tokens} tokens) = {job:.1f} s; "
+                   f"{sample_s:.1f} s of CPU work"),
+    }
+
+
+def main():
+    a = _args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs shard windows/streams "
+                                   "(data parallel, no exchange) and are not part of this benchmark",
+                          "n_gpus": a.gpus}))
+        sys.exit(2)
+    from franken_whisper_amd import abi, native, synth
+
+    cfg = synth.TURBO
+    W = a.windows or (8 if a.workload == "enc-f32" else 16 if a.workload == "enc-int8" else 10)
+    nf = 2 * cfg.n_audio_ctx
+    t_setup = time.perf_counter()
+    model = synth.Model(cfg, seed=0, encoder=a.workload != "decode", decoder=a.workload in ("job", "decode"))
+    ctx = native.Context(0)
+    enc = dec = st = None
+    mel = synth.mel_input(1234, W, nf, cfg.n_mels) * np.float32(0.5)
+    mel_dev = ctx.array(mel)
+    enc_out = ctx.empty((W, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+    if a.workload in ("job", "enc-int8"):
+        enc = native.Encoder(ctx, model, abi.ENC_INT8)
+    elif a.workload == "enc-f32":
+        enc = native.Encoder(ctx, model, abi.ENC_F32)
+    tk = model.tokens
+    filt = tk.filter()
+    prompt = tk.sot_sequence(language_id=0)
+    if a.workload in ("job", "decode"):
+        dec = native.Decoder(ctx, model, abi.DEC_INT8)
+        st = dec.state(W, cfg.n_audio_ctx)
+        if a.workload == "decode":
+            enc_out.upload(synth.encoder_states(77, W, cfg.n_audio_ctx, cfg.n_audio_state))
+            st.set_cross(enc_out)
+    ctx.synchronize()
+    t_setup = time.perf_counter() - t_setup
+
+    tokens_out = [0]
+
+    def step():
+        if enc is not None:
+            enc.forward_time_major(mel_dev, W, nf, enc_out)
+        if st is not None:
+            if a.workload == "job":
+                st.set_cross(enc_out)
+            else:
+                st.reset()
+            toks = st.greedy(prompt, a.tokens, filt)
+            tokens_out[0] = sum(len(t) for t in toks)
+
+    for _ in range(a.warmup):
+        step()
+    ctx.synchronize()
+    # per-component wall times (untimed diagnostic pass)
+    comp = {}
+    if enc is not None:
+        t = time.perf_counter()
+        enc.forward_time_major(mel_dev, W, nf, enc_out)
+        ctx.synchronize()
+        comp["encoder_ms"] = (time.perf_counter() - t) * 1e3
+    if st is not None:
+        if a.workload == "job":
+            t = time.perf_counter()
+            st.set_cross(enc_out)
+            ctx.synchronize()
+            comp["cross_kv_ms"] = (time.perf_counter() - t) * 1e3
+        else:
+            st.reset()
+        t = time.perf_counter()
+        toks = st.greedy(prompt, a.tokens, filt)
+        ctx.synchronize()
+        comp["decode_ms"] = (time.perf_counter() - t) * 1e3
+        comp["decode_tokens"] = int(sum(len(x) for x in toks))
+
+    ctx.timing(True)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    stats = {k: ctx.kernel_stats(k) for k in (abi.K_ENC_GEMM_I8, abi.K_ENC_GEMM_F32, abi.K_ENC_ATTN,
+                                              abi.K_DEC_LOGITS)}
+    ctx.timing(False)
+    ms_per_step = elapsed * 1e3 / a.steps
+
+    names = {abi.K_ENC_GEMM_I8: ("encoder int8 GEMM (k_gemm<I8>)", "mfma", "int8"),
+             abi.K_ENC_GEMM_F32: ("encoder f16-pair GEMM (k_gemm<F16S>)", "mfma", "f16"),
+             abi.K_ENC_ATTN: ("encoder attention (k_attention, f16-pair x3)", "mfma", "f16"),
+             abi.K_DEC_LOGITS: ("decoder logits GEMV (k_gemv_i8)", "hbm", None)}
+    kclass = max(stats, key=lambda k: stats[k][1])
+    n, ms, units = stats[kclass]
+    name, bound, op = names[kclass]
+    if bound == "mfma":
+        achieved = units / (ms * 1e-3) / 1e12
+        roof = {"kernel": name, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS[op],
+                "unit": "TFLOP/s", "op_dtype": op, "frac": round(achieved / PEAK_TFLOPS[op], 4), "traffic": None,
+                "launches": n, "avg_launch_ms": round(ms / max(n, 1), 4)}
+    else:
+        achieved = units / (ms * 1e-3) / 1e9
+        roof = {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "launches": n,
+                "avg_launch_ms": round(ms / max(n, 1), 4)}
+    kernel_classes = {names[k][0]: {"launches": v[0], "total_ms": round(v[1], 3)} for k, v in stats.items() if v[0]}
+
+    audio_s = 30.0 * W
+    out = {
+        "metric": "audio-s/sec large-v3-turbo encode+greedy decode; enc TFLOP/s; decode tok/s",
+        "value": None,
+        "unit": "audio-s/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8+f32",
+        "data": "synthetic (seeded random-init weights N(0,0.02), seeded synthetic log-mel input)",
+        "config": {},
+        "roofline": roof,
+    }
+    if a.workload == "job":
+        out["value"] = round(audio_s / (ms_per_step * 1e-3), 2)
+        out["config"] = {"workload": f"large-v3-turbo whole job: {W} x 30 s windows, int8 encoder "
+                                     f"(FW_ENC_ATTN_OUT_I8I32 plan, dense, no ToMe), cross K/V, greedy no-timestamps "
+                                     f"decode of {a.tokens} tokens/window (cohort of {W} streams), int8 decoder arm, "
+                                     f"f16 KV cache; log-mel input precomputed", "windows": W, "audio_s": audio_s,
+                         "n_frames": nf, "prompt_tokens": len(prompt), "max_tokens": a.tokens}
+    elif a.workload.startswith("enc"):
+        out["value"] = round(audio_s / (ms_per_step * 1e-3), 2)
+        out["dtype"] = "int8+f32" if a.workload == "enc-int8" else "f32 (f16-pair MFMA)"
+        out["config"] = {"workload": f"large-v3-turbo encoder only ({a.workload[4:]} plan), {W} x 30 s windows",
+                         "windows": W}
+    else:
+        out["unit"] = "tok/s"
+        out["value"] = round(tokens_out[0] / (ms_per_step * 1e-3), 1)
+        out["config"] = {"workload": f"large-v3-turbo decoder: {W} streams, prompt + {a.tokens} greedy steps, "
+                                     f"int8 arm, f16 KV cache", "streams": W}
+    enc_ms = comp.get("encoder_ms")
+    out["enc_tflops"] = round(ENC_GOP_PER_WINDOW * W / enc_ms, 1) if enc_ms else None
+    if "decode_ms" in comp:
+        out["decode_tok_s"] = round(comp["decode_tokens"] / (comp["decode_ms"] * 1e-3), 1)
+    out["components_ms"] = {k: round(v, 2) if isinstance(v, float) else v for k, v in comp.items()}
+    out["kernel_classes"] = kernel_classes
+    out["setup_s"] = round(t_setup, 1)
+    if a.workload == "job" and not a.no_cpu_baseline:
+        cb = cpu_baseline(model, W, a.tokens, a.cpu_threads)
+        out["cpu_baseline"] = cb
+        out["gpu_over_cpu"] = round(out["value"] / cb["value"], 1)
+    for x in (st, dec, enc):
+        if x is not None:
+            x.close()
+    ctx.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -485,39 +485,46 @@ static void attention_per_head(const float *q, int tq, const float *k, const flo
                                int n_state, int n_head, int causal, int cache_len, float *out) {
     int dh = n_state / n_head;
     float scale = powf((float)dh, -0.25f);
-#pragma omp parallel for schedule(dynamic)
+    /* Heads in order, rows in parallel inside (the same per-element order as
+     * the reference: kh is transposed to kh_t [dh, tk] exactly as
+     * attention_raw builds it, so each score accumulates d ascending while the
+     * inner loop runs across independent keys). */
+    float *qh = (float *)malloc(sizeof(float) * (size_t)tq * dh);
+    float *kht = (float *)malloc(sizeof(float) * (size_t)tk * dh);
     for (int h = 0; h < n_head; h++) {
         int base = h * dh;
-        float *qh = (float *)malloc(sizeof(float) * (size_t)tq * dh);
-        float *kh = (float *)malloc(sizeof(float) * (size_t)tk * dh);
-        float *sc = (float *)malloc(sizeof(float) * (size_t)tq * tk);
         for (int i = 0; i < tq; i++)
             for (int d = 0; d < dh; d++) qh[i * dh + d] = q[(int64_t)i * n_state + base + d] * scale;
         for (int j = 0; j < tk; j++)
-            for (int d = 0; d < dh; d++) kh[j * dh + d] = k[(int64_t)j * n_state + base + d] * scale;
-        for (int i = 0; i < tq; i++) {
-            float *srow = sc + (int64_t)i * tk;
-            for (int j = 0; j < tk; j++) {
-                float acc = 0.0f;
-                for (int d = 0; d < dh; d++) acc += qh[i * dh + d] * kh[j * dh + d];
-                srow[j] = acc;
-            }
-            if (causal)
-                for (int j = cache_len + i + 1; j < tk; j++) srow[j] = -INFINITY;
-            softmax_row(srow, tk);
+            for (int d = 0; d < dh; d++) kht[(int64_t)d * tk + j] = k[(int64_t)j * n_state + base + d] * scale;
+#pragma omp parallel
+        {
+            float *srow = (float *)malloc(sizeof(float) * (size_t)tk);
             float acc[256];
-            for (int d = 0; d < dh; d++) acc[d] = 0.0f;
-            for (int j = 0; j < tk; j++) {
-                float p = srow[j];
-                const float *vr = v + (int64_t)j * n_state + base;
-                for (int d = 0; d < dh; d++) acc[d] += p * vr[d];
+#pragma omp for schedule(static)
+            for (int i = 0; i < tq; i++) {
+                for (int j = 0; j < tk; j++) srow[j] = 0.0f;
+                for (int d = 0; d < dh; d++) {
+                    float qd = qh[i * dh + d];
+                    const float *kr = kht + (int64_t)d * tk;
+                    for (int j = 0; j < tk; j++) srow[j] += qd * kr[j];
+                }
+                if (causal)
+                    for (int j = cache_len + i + 1; j < tk; j++) srow[j] = -INFINITY;
+                softmax_row(srow, tk);
+                for (int d = 0; d < dh; d++) acc[d] = 0.0f;
+                for (int j = 0; j < tk; j++) {
+                    float p = srow[j];
+                    const float *vr = v + (int64_t)j * n_state + base;
+                    for (int d = 0; d < dh; d++) acc[d] += p * vr[d];
+                }
+                for (int d = 0; d < dh; d++) out[(int64_t)i * n_state + base + d] = acc[d];
             }
-            for (int d = 0; d < dh; d++) out[(int64_t)i * n_state + base + d] = acc[d];
+            free(srow);
         }
-        free(qh);
-        free(kh);
-        free(sc);
     }
+    free(qh);
+    free(kht);
 }
 
 /* ------------------------------------------------------------------------ */
