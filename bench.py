@@ -35,59 +35,69 @@ def _args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--workload", default="job", choices=["job", "enc-f32", "enc-int8", "decode"])
+    p.add_argument("--workload", default="job", choices=["job", "enc-f32", "enc-int8", "decode", "copy"])
     p.add_argument("--windows", type=int, default=None)
     p.add_argument("--tokens", type=int, default=220)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")))
+    p.add_argument("--cpu-windows", type=int, default=2, help="windows of the job the CPU baseline runs")
+    p.add_argument("--copy-mb", type=int, default=512)
     return p.parse_args()
 
 
-def cpu_baseline(model, n_windows, n_tokens, threads):
+def cpu_baseline(model, n_windows, n_tokens, threads, sample_windows):
     """The oracle (C restatement of the reference CPU path, OpenMP) on a bounded
-    sample of the same job, extrapolated to the whole job: one window's conv
-    stem + 2 encoder layers (int8 plan), one window's cross K/V precompute, the
-    prompt prefill and 16 single-token steps of one stream."""
+    sample of the same job: `sample_windows` of the job's windows run end to end
+    (int8-plan encoder over all layers, cross K/V precompute, prompt prefill and
+    greedy decode of n_tokens), timed, and scaled to audio-seconds per second."""
     from franken_whisper_amd import abi, synth
     from oracle import oracle as O
 
     O.lib().ref_set_num_threads(threads)
     cfg = model.cfg
     e = O.Encoder(model, abi.ENC_INT8)
-    x = synth.mel_input(1, 1, 2 * cfg.n_audio_ctx, cfg.n_mels)[0]
-    t0 = time.perf_counter()
-    e.forward(x, n_layers=1)
-    t1 = time.perf_counter()
-    y = e.forward(x, n_layers=2)
-    t2 = time.perf_counter()
-    per_layer = (t2 - t1) - (t1 - t0)
-    stem = (t1 - t0) - per_layer
-    enc_window = stem + cfg.n_audio_layer * per_layer
     d = O.Decoder(model, abi.DEC_INT8)
-    t3 = time.perf_counter()
-    st = d.state(y)
-    t4 = time.perf_counter()
     tk = model.tokens
-    st.step(tk.sot_sequence())
-    t5 = time.perf_counter()
-    for i in range(16):
-        st.step([1000 + i])
-    t6 = time.perf_counter()
-    step = (t6 - t5) / 16
-    job = n_windows * (enc_window + (t4 - t3) + (t5 - t4) + (n_tokens - 1) * step)
-    sample_s = t6 - t0 + (t2 - t1)
-    audio_s = n_windows * 30.0
+    filt = tk.filter()
+    prompt = tk.sot_sequence(language_id=0)
+    mel = synth.mel_input(1234, sample_windows, 2 * cfg.n_audio_ctx, cfg.n_mels) * np.float32(0.5)
+    t_enc = t_dec = 0.0
+    n_tok = 0
+    for w in range(sample_windows):
+        t0 = time.perf_counter()
+        y = e.forward(mel[w])
+        t1 = time.perf_counter()
+        toks = d.state(y).greedy(prompt, n_tokens, filt)
+        t2 = time.perf_counter()
+        t_enc += t1 - t0
+        t_dec += t2 - t1
+        n_tok += len(toks)
+    total = t_enc + t_dec
     return {
-        "value": round(audio_s / job, 4),
+        "value": round(sample_windows * 30.0 / total, 4),
         "unit": "audio-s/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle (C restatement, -O3 -march=x86-64-v3, {threads} OpenMP threads): one window's conv stem "
-                   f"+ 2 int8 encoder layers ({per_layer:.2f} s/layer, stem {stem:.2f} s), cross K/V {t4 - t3:.2f} s, "
-                   f"prefill {t5 - t4:.3f} s, 16 decode steps ({step * 1e3:.1f} ms/step); extrapolated to "
-                   f"{n_windows} windows x ({cfg.n_audio_layer} layers + {n_tokens} tokens) = {job:.1f} s; "
-                   f"{sample_s:.1f} s of CPU work"),
+        "sample": (f"oracle (C restatement of the reference CPU path, -O3 -march=x86-64-v3, {threads} OpenMP "
+                   f"threads) on {sample_windows} of the job's {n_windows} windows end to end: int8-plan encoder "
+                   f"{t_enc / sample_windows:.2f} s/window, cross K/V + prefill + greedy decode "
+                   f"{t_dec / sample_windows:.2f} s/window ({n_tok} tokens); {total:.1f} s of CPU work"),
     }
+
+
+def copy_calibration(mb, reps):
+    """A plain device-to-device copy of known size (torch's elementwise copy
+    kernel): the reference reading for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    n = mb * (1 << 20) // 4
+    a = torch.randn(n, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"workload": "copy", "bytes_per_copy": 4 * n, "reps": reps}))
 
 
 def main():
@@ -97,6 +107,9 @@ def main():
                                    "(data parallel, no exchange) and are not part of this benchmark",
                           "n_gpus": a.gpus}))
         sys.exit(2)
+    if a.workload == "copy":
+        copy_calibration(a.copy_mb, a.steps)
+        return
     from franken_whisper_amd import abi, native, synth
 
     cfg = synth.TURBO
@@ -235,7 +248,7 @@ def main():
     out["kernel_classes"] = kernel_classes
     out["setup_s"] = round(t_setup, 1)
     if a.workload == "job" and not a.no_cpu_baseline:
-        cb = cpu_baseline(model, W, a.tokens, a.cpu_threads)
+        cb = cpu_baseline(model, W, a.tokens, a.cpu_threads, a.cpu_windows)
         out["cpu_baseline"] = cb
         out["gpu_over_cpu"] = round(out["value"] / cb["value"], 1)
     for x in (st, dec, enc):

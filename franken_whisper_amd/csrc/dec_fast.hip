@@ -1,0 +1,770 @@
+// dec_fast.hip — the int8 decoder arm's per-token kernels (gfx950).
+//
+// Decode is HBM-bound: per step the cohort reads every weight once (161 MB
+// int8 at large-v3-turbo) plus each stream's cross K/V (15.9 MB int8) and
+// self-attention cache.  The kernels here keep the reference's arithmetic
+// exactly (integer dots are exact in any order; every floating-point rounding
+// is reproduced in the reference's order) while spreading the bytes over the
+// whole chip:
+//  - activations are quantized once per use (quantize_act_i8_into,
+//    nn.rs:3020-3064) — in the LayerNorm kernel or a row kernel — instead of in
+//    every GEMV block;
+//  - int8 GEMVs run on v_mfma_i32_16x16x64_i8 with the cohort's (up to 16)
+//    quantized activation rows as the A operand and 16 weight rows as B: one
+//    16-byte weight load per lane per MFMA, K split over the block's 4 waves,
+//    exact i32 partial sums added in LDS, then gemv_i8's epilogue
+//    ((f32)acc * s_w) * s_x + b (nn.rs:3187-3188);
+//  - the logits GEMV also emits per-block (value, index) argmax keys over the
+//    filtered logits (process_logits no-timestamps masks, decode.rs:702-867;
+//    first-index strict '>' argmax, decode.rs:1708-1780); a one-block kernel
+//    finishes the argmax and the greedy bookkeeping on the device.
+#include "fw_kernels.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// LayerNorm (nn.rs:4455-4545: f64 mean/var, ((x-mean)*inv)*w + b rounded to
+// f32) of one stream row per wave, then the decoder activation quantizer of
+// the normalized row (per-row amax/127, add-trunc body, exact n%8 tail) into
+// the int8 activation buffer.  y may be NULL (int8-only consumers), xq may be
+// NULL (f32-only consumers).  Rows up to 2048 values; 4 rows per block.
+#define DEC_LN_V 32
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, const float *w, const float *b, int d,
+                                                  int rows, int8_t *xq, float *xs) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float *xr = x + (size_t)r * d;
+    float xv[DEC_LN_V];
+    double s = 0.0;
+    // unconditional loads from clamped addresses: a guarded load becomes a
+    // branch with its own wait, serializing the row's memory latency
+#pragma unroll
+    for (int k = 0; k < DEC_LN_V; k++) {
+        int i = lane + k * 64;
+        float t = xr[i < d ? i : 0];
+        xv[k] = i < d ? t : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < DEC_LN_V; k++)
+        if (lane + k * 64 < d) s += (double)xv[k];
+    const double mean = wave_sum_f64(s) / (double)d;
+    double v = 0.0;
+#pragma unroll
+    for (int k = 0; k < DEC_LN_V; k++) {
+        int i = lane + k * 64;
+        if (i < d) {
+            double t = (double)xv[k] - mean;
+            v += t * t;
+        }
+    }
+    const double var = wave_sum_f64(v) / (double)d;
+    const double inv = 1.0 / sqrt(var + (double)1e-5f);
+    float m = 0.0f;
+    float wv[DEC_LN_V], bv[DEC_LN_V];
+#pragma unroll
+    for (int k = 0; k < DEC_LN_V; k++) {
+        int i = lane + k * 64;
+        wv[k] = w[i < d ? i : 0];
+        bv[k] = b[i < d ? i : 0];
+    }
+#pragma unroll
+    for (int k = 0; k < DEC_LN_V; k++) {
+        int i = lane + k * 64;
+        if (i < d) {
+            double nrm = ((double)xv[k] - mean) * inv;
+            xv[k] = (float)(nrm * (double)wv[k] + (double)bv[k]);
+            m = fmaxf(m, fabsf(xv[k]));
+            if (y) y[(size_t)r * d + i] = xv[k];
+        }
+    }
+    if (!xq) return;
+    m = fw_wave_max(m);
+    const float sc = fmaxf(m, 1e-9f) / 127.0f;
+    const float iv = 1.0f / sc;
+#pragma unroll
+    for (int k = 0; k < DEC_LN_V; k++) {
+        int i = lane + k * 64;
+        if (i < d) xq[(size_t)r * d + i] = fw_q8_avx(xv[k], iv, i, d);
+    }
+    if (lane == 0) xs[r] = sc;
+}
+
+// quantize_act_i8_into of f32 rows [rows, n] (one wave per row, n <= 2048).
+__global__ void __launch_bounds__(256) k_quant_act_rows(const float *x, int rows, int n, int8_t *xq, float *xs) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float *xr = x + (size_t)r * n;
+    float xv[DEC_LN_V];
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < DEC_LN_V; k++) {
+        int i = lane + k * 64;
+        float t = xr[i < n ? i : 0];
+        xv[k] = i < n ? t : 0.0f;
+        m = fmaxf(m, fabsf(xv[k]));
+    }
+    m = fw_wave_max(m);
+    const float sc = fmaxf(m, 1e-9f) / 127.0f;
+    const float iv = 1.0f / sc;
+#pragma unroll
+    for (int k = 0; k < DEC_LN_V; k++) {
+        int i = lane + k * 64;
+        if (i < n) xq[(size_t)r * n + i] = fw_q8_avx(xv[k], iv, i, n);
+    }
+    if (lane == 0) xs[r] = sc;
+}
+
+// ---------------------------------------------------------------------------
+// Order-preserving argmax key: larger value first, then smaller index; 0 means
+// "no candidate" (masked, -inf or NaN never compare greater, as in the
+// reference's strict '>' scan).
+__device__ __forceinline__ unsigned long long am_key(float v, int idx) {
+    if (!(v > -INFINITY)) return 0ull;
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ unsigned long long shfl_max_u64(unsigned long long k, int off) {
+    uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    uint32_t lo2 = __shfl_xor(lo, off, 64), hi2 = __shfl_xor(hi, off, 64);
+    unsigned long long o = ((unsigned long long)hi2 << 32) | lo2;
+    return o > k ? o : k;
+}
+
+// The suppress set of process_logits in no-timestamps mode (decode.rs:702-867).
+__device__ __forceinline__ bool dec_masked(int i, const fwhip_filter &f, int initial) {
+    if (initial && (i == f.eot || i == f.space_token)) return true;
+    if (i >= f.timestamp_begin) return true;
+    if (i == f.no_timestamps || i == f.sot || i == f.no_speech || i == f.solm || i == f.translate ||
+        i == f.transcribe || i == f.sot_prev)
+        return true;
+    if (i >= f.sot + 1 && i <= f.sot + f.n_languages) return true;
+    return false;
+}
+
+// ---------------------------------------------------------------------------
+// int8 GEMV on MFMA.  W [N, K] i8 row-major, sw [N]; xq [16, K] i8 (rows >=
+// ns are zero), xs [ns]; y [ns, ldy].  Block = 4 waves over 16*RG rows; wave
+// w takes the 64-wide k blocks kb = w, w+4, ...
+// mode 0 store, 1 residual add (add_into, decoder.rs:2369), 2 GELU
+// (nn.rs:4603), 3 logits: store + per-block argmax keys keys[s*nblk + block].
+#define GV_KPW 5 // k blocks per wave held in registers (K <= 1280 in one pass)
+template <int RG>
+__global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, const float *__restrict__ sw,
+                                                  const float *__restrict__ bias, const int8_t *__restrict__ xq,
+                                                  const float *__restrict__ xs, float *y, int N, int K, int ns,
+                                                  int ldy, int mode, const float *__restrict__ gelu_tab,
+                                                  fwhip_filter filt, int use_filter, const int *initialp,
+                                                  unsigned long long *keys) {
+    __shared__ int red[4][RG * 4][64];
+    __shared__ unsigned long long ksh[RG][16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row_base = blockIdx.x * 16 * RG;
+    const int nkb = K >> 6;
+    const int ko = (lane >> 4) * 16;
+    v4i acc[RG];
+#pragma unroll
+    for (int g = 0; g < RG; g++) acc[g] = (v4i){0, 0, 0, 0};
+    const int8_t *xrow = xq + (size_t)(lane & 15) * K + ko;
+    // this wave's k blocks kb = wave + 4*i, i < GV_KPW: every operand load is
+    // issued before the first MFMA (addresses clamped, unused blocks zeroed)
+    v4i xa[GV_KPW], wb[GV_KPW][RG];
+#pragma unroll
+    for (int i = 0; i < GV_KPW; i++) {
+        const int kb = wave + 4 * i;
+        const int kbc = kb < nkb ? kb : nkb - 1;
+        xa[i] = *(const v4i *)(xrow + kbc * 64);
+#pragma unroll
+        for (int g = 0; g < RG; g++) {
+            const int row = row_base + g * 16 + (lane & 15);
+            wb[i][g] = *(const v4i *)(W + (size_t)(row < N ? row : N - 1) * K + ko + kbc * 64);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < GV_KPW; i++) {
+        if (wave + 4 * i < nkb) {
+#pragma unroll
+            for (int g = 0; g < RG; g++) acc[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i], wb[i][g], acc[g], 0, 0, 0);
+        }
+    }
+    // K beyond 4 * GV_KPW * 64
+    for (int kb = wave + 4 * GV_KPW; kb < nkb; kb += 4) {
+        v4i x1 = *(const v4i *)(xrow + kb * 64);
+#pragma unroll
+        for (int g = 0; g < RG; g++) {
+            const int row = row_base + g * 16 + (lane & 15);
+            v4i w1 = *(const v4i *)(W + (size_t)(row < N ? row : N - 1) * K + ko + kb * 64);
+            acc[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, w1, acc[g], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < RG; g++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[wave][g * 4 + r][lane] = acc[g][r];
+    __syncthreads();
+    const int initial = (mode == 3 && use_filter) ? *initialp : 0;
+    for (int g = wave; g < RG; g += 4) {
+        const int row = row_base + g * 16 + (lane & 15);
+        const bool okr = row < N;
+        const float swr = okr ? sw[row] : 0.0f;
+        const float b = (okr && bias) ? bias[row] : 0.0f;
+        const bool masked = mode == 3 && use_filter && okr && dec_masked(row, filt, initial);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int s = (lane >> 4) * 4 + r;
+            const int tot = red[0][g * 4 + r][lane] + red[1][g * 4 + r][lane] + red[2][g * 4 + r][lane] +
+                            red[3][g * 4 + r][lane];
+            unsigned long long key = 0ull;
+            if (okr && s < ns) {
+                const float v = (float)tot * swr * xs[s] + b;
+                float *yp = y + (size_t)s * ldy + row;
+                if (mode == 1) *yp = *yp + v;
+                else if (mode == 2) *yp = fw_gelu(v, gelu_tab);
+                else *yp = v;
+                if (mode == 3 && !masked) key = am_key(v, row);
+            }
+            if (mode == 3) {
+                // max over the 16 lanes holding stream s (same lane>>4)
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) key = shfl_max_u64(key, off);
+                if ((lane & 15) == 0) ksh[g][s] = key;
+            }
+        }
+    }
+    if (mode != 3) return;
+    __syncthreads();
+    if (threadIdx.x < ns) {
+        unsigned long long k = 0ull;
+#pragma unroll
+        for (int g = 0; g < RG; g++) k = ksh[g][threadIdx.x] > k ? ksh[g][threadIdx.x] : k;
+        keys[(size_t)threadIdx.x * gridDim.x + blockIdx.x] = k;
+    }
+}
+
+// Finish the argmax from the per-block keys and do the greedy bookkeeping:
+// tok[s] = argmax, hist[s*cap + *stepp] = tok[s], advance the position, clear
+// the first-step flag, advance the step counter.  One block of 16 waves, wave
+// w reduces streams w, w+16, ...
+__global__ void __launch_bounds__(1024) k_argmax_finish(const unsigned long long *keys, int nblk, int ns,
+                                                        int32_t *tok, int32_t *hist, int hist_cap, int *posp,
+                                                        int *initialp, int *stepp, int advance) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int step = stepp ? *stepp : 0;
+    for (int s = wave; s < ns; s += 16) {
+        const unsigned long long *ks = keys + (size_t)s * nblk;
+        unsigned long long k = 0ull;
+        int i = lane;
+        for (; i + 192 < nblk; i += 256) {
+            unsigned long long a0 = ks[i], a1 = ks[i + 64], a2 = ks[i + 128], a3 = ks[i + 192];
+            a0 = a0 > a1 ? a0 : a1;
+            a2 = a2 > a3 ? a2 : a3;
+            a0 = a0 > a2 ? a0 : a2;
+            k = a0 > k ? a0 : k;
+        }
+        for (; i < nblk; i += 64) k = ks[i] > k ? ks[i] : k;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) k = shfl_max_u64(k, off);
+        if (lane == 0) {
+            int t = k ? (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull)) : 0;
+            tok[s] = t;
+            if (hist) hist[(size_t)s * hist_cap + step] = t;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (advance) *posp = *posp + 1;
+        if (initialp) *initialp = 0;
+        if (stepp) *stepp = step + 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Block-int8-weight x f32-activation GEMV with 32-wide blocks
+// (gemv_i8w_f32a_blocked, nn.rs:3756-3824): for each (row, stream) the block
+// dots dot_i8w_f32 (nn.rs:3501-3564; one 32-chunk: products, lane-wise
+// (a0+a1)+(a2+a3), then ((t0+t1)+(t2+t3))+((t4+t5)+(t6+t7))) are folded in
+// ascending block order, acc = acc + dot_b * s_b, then + bias.
+// Block = 256 threads over BLK_R rows.  Work items are (stream, 32-block)
+// pairs: an item loads its activation chunk once and computes the block dot
+// for each of the BLK_R rows into LDS; then one thread per (row, stream)
+// folds the row's block dots in order.
+#define BLK_R 4
+__device__ __forceinline__ float blk_dot32(const int4 w0, const int4 w1, const float (&xv)[32]) {
+    const int wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float p[32];
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            p[q * 4 + e] = __builtin_fmaf((float)(int8_t)((wv[q] >> (8 * e)) & 0xff), xv[q * 4 + e], 0.0f);
+    float tl[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) tl[l] = (p[l] + p[8 + l]) + (p[16 + l] + p[24 + l]);
+    return ((tl[0] + tl[1]) + (tl[2] + tl[3])) + ((tl[4] + tl[5]) + (tl[6] + tl[7]));
+}
+
+__global__ void __launch_bounds__(256) k_gemv_blk3(const int8_t *__restrict__ W, const float *__restrict__ sc,
+                                                   const float *__restrict__ bias, const float *__restrict__ x,
+                                                   float *y, int N, int K, int ns, int ldy, int mode) {
+    extern __shared__ float blk_sm[];
+    const int nb = K >> 5, ldd = nb + 1;
+    float *dots = blk_sm;                          // [BLK_R][ns][ldd]
+    float *scl = blk_sm + (size_t)BLK_R * ns * ldd; // [BLK_R][nb]
+    const int t = threadIdx.x;
+    const int row0 = blockIdx.x * BLK_R;
+    for (int i = t; i < BLK_R * nb; i += 256) {
+        int r = i / nb, b = i - r * nb;
+        scl[i] = row0 + r < N ? sc[(size_t)(row0 + r) * nb + b] : 0.0f;
+    }
+    const int items = ns * nb;
+    // software pipeline: the next item's activation and weight chunks load
+    // while this item's dots are computed
+    float4 xn[8];
+    int4 wn[BLK_R][2];
+    auto load_item = [&](int it) {
+        const int itc = it < items ? it : items - 1;
+        const int s = itc / nb, b = itc - s * nb;
+        const float4 *xp = (const float4 *)(x + (size_t)s * K + (size_t)b * 32);
+#pragma unroll
+        for (int q = 0; q < 8; q++) xn[q] = xp[q];
+#pragma unroll
+        for (int r = 0; r < BLK_R; r++) {
+            const int row = row0 + r;
+            const int4 *wp = (const int4 *)(W + (size_t)(row < N ? row : N - 1) * K + (size_t)b * 32);
+            wn[r][0] = wp[0];
+            wn[r][1] = wp[1];
+        }
+    };
+    load_item(t);
+    for (int it = t; it < items; it += 256) {
+        float xv[32];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            xv[q * 4 + 0] = xn[q].x;
+            xv[q * 4 + 1] = xn[q].y;
+            xv[q * 4 + 2] = xn[q].z;
+            xv[q * 4 + 3] = xn[q].w;
+        }
+        int4 wc[BLK_R][2];
+#pragma unroll
+        for (int r = 0; r < BLK_R; r++) {
+            wc[r][0] = wn[r][0];
+            wc[r][1] = wn[r][1];
+        }
+        load_item(it + 256);
+        const int s = it / nb, b = it - s * nb;
+#pragma unroll
+        for (int r = 0; r < BLK_R; r++)
+            dots[((size_t)r * ns + s) * ldd + b] = blk_dot32(wc[r][0], wc[r][1], xv); // rows past N never fold
+    }
+    __syncthreads();
+    if (t < BLK_R * ns) {
+        const int r = t / ns, s = t - r * ns, row = row0 + r;
+        if (row < N) {
+            const float *dr = dots + ((size_t)r * ns + s) * ldd;
+            const float *sr = scl + (size_t)r * nb;
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) acc = acc + dr[b] * sr[b];
+            const float v = acc + (bias ? bias[row] : 0.0f);
+            float *yp = y + (size_t)s * ldy + row;
+            if (mode == 1) *yp = *yp + v;
+            else *yp = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Self-attention over the f16 KV cache for one (head, stream), tq == 1
+// (attention_with_cache nn.rs:6267-6337 -> KvCache::append nn.rs:5352 ->
+// attention_decode_step_f16 nn.rs:6466-6540).  Appends this token's k/v (RNE
+// to f16) at pos and attends over [0, pos]: per-key ascending-d scores of
+// (q*s)*(k*s), softmax with glibc-exact expf and a sequential sum, then per
+// output the ascending-j sum of p_j * v_j.  256 threads: one key per thread
+// for the scores; the cache rows of this head are staged in LDS for the
+// value pass.
+#define SA_STG 4
+__global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *kc, uint16_t *vc, float *att,
+                                                    const int *posp, int d, int nctx, int L, int layer,
+                                                    float scale) {
+    extern __shared__ __align__(16) unsigned char sm2[];
+    float *sc = (float *)sm2;                               // [nctx]
+    uint16_t *vs = (uint16_t *)(sm2 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
+    __shared__ float qh[64];
+    __shared__ float red[4];
+    __shared__ float inv_s;
+    const int pos = *posp;
+    const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const int base = h * 64;
+    const float *q = qkv + (size_t)s * 3 * d;
+    const size_t cbase = ((size_t)s * L + layer) * nctx * d;
+    if (t < 64) {
+        uint16_t kh = fw_f2h(q[d + base + t]), vh = fw_f2h(q[2 * d + base + t]);
+        kc[cbase + (size_t)pos * d + base + t] = kh;
+        vc[cbase + (size_t)pos * d + base + t] = vh;
+        qh[t] = q[base + t] * scale;
+    }
+    __syncthreads(); // this block's own cache row is visible to its threads
+    const int tk = pos + 1;
+    // stage V rows [0, tk) of this head (8 x 16 bytes per row), SA_STG chunks
+    // per thread per round, loads issued before the LDS stores
+    for (int c0 = 0; c0 < tk * 8; c0 += 256 * SA_STG) {
+        uint4 v[SA_STG];
+#pragma unroll
+        for (int u = 0; u < SA_STG; u++) {
+            int c = c0 + t + u * 256;
+            int cc = c < tk * 8 ? c : tk * 8 - 1;
+            v[u] = *(const uint4 *)(vc + cbase + (size_t)(cc >> 3) * d + base + (cc & 7) * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < SA_STG; u++) {
+            int c = c0 + t + u * 256;
+            if (c < tk * 8) *(uint4 *)(vs + (c >> 3) * 64 + (c & 7) * 8) = v[u];
+        }
+    }
+    float mx = -INFINITY;
+    for (int j = t; j < tk; j += 256) {
+        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)j * d + base);
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            uint4 u = kr[c];
+            uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                acc += qh[c * 8 + 2 * e] * (fw_h2f(ww[e] & 0xffff) * scale);
+                acc += qh[c * 8 + 2 * e + 1] * (fw_h2f(ww[e] >> 16) * scale);
+            }
+        }
+        sc[j] = acc;
+        mx = fmaxf(mx, acc);
+    }
+    mx = fw_block_max(mx, red);
+    const bool fin = isfinite(mx);
+    if (fin)
+        for (int j = t; j < tk; j += 256) {
+            float e = fw_expf(sc[j] - mx);
+            sc[j] = isfinite(e) ? e : 0.0f;
+        }
+    __syncthreads();
+    if (t == 0) {
+        float sum = 0.0f;
+        if (fin) {
+            int j = 0;
+            for (; j + 4 <= tk; j += 4) {
+                float4 v = *(const float4 *)(sc + j);
+                sum += v.x;
+                sum += v.y;
+                sum += v.z;
+                sum += v.w;
+            }
+            for (; j < tk; j++) sum += sc[j];
+        }
+        inv_s = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    if (inv > 0.0f)
+        for (int j = t; j < tk; j += 256) sc[j] = sc[j] * inv;
+    __syncthreads();
+    if (t < 64) {
+        // ascending-j accumulation; operands for 8 keys are read before the adds
+        float acc = 0.0f;
+        int j = 0;
+        for (; j + 8 <= tk; j += 8) {
+            float pv[8], vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                pv[u] = sc[j + u];
+                vv[u] = fw_h2f(vs[(j + u) * 64 + t]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc += pv[u] * vv[u];
+        }
+        for (; j < tk; j++) acc += sc[j] * fw_h2f(vs[j * 64 + t]);
+        att[(size_t)s * d + base + t] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Cross-attention for one (head, stream) with int8 K/V (cross_attention,
+// decoder.rs:1524-1716, int8 cross K/V — the default): qh = q*s quantized per
+// vector; scores = gemv_i8(K_h, qh); softmax; p quantized per vector;
+// out = gemv_i8(Vt_h, p).  512 threads.  Vt rows have stride Tq (T rounded up
+// to 16, zero padded).  Both K (CA_KPT keys per thread) and this wave's 8 Vt
+// rows (CA_VPL 16-byte chunks per lane per row) are loaded into registers at
+// entry, so their latency overlaps the score/softmax chain.
+#define CA_KPT 3
+#define CA_VPL 2
+__global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const int8_t *ck, const float *cks,
+                                                         const int8_t *cvt, const float *cvs, float *att, int d,
+                                                         int T, int Tq, int H, int L, int layer, float scale) {
+    extern __shared__ __align__(16) unsigned char smc2[];
+    float *sc = (float *)smc2;                                       // [T]
+    int8_t *p8 = (int8_t *)(smc2 + sizeof(float) * ((T + 3) & ~3)); // [Tq]
+    __shared__ __align__(16) int8_t q8[64];
+    __shared__ float red[8];
+    __shared__ float bc[2];
+    const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const size_t lh = ((size_t)s * L + layer) * H + h;
+    const int8_t *Kp = ck + lh * (size_t)T * 64;
+    const float *Ks = cks + lh * T;
+    const int8_t *Vp = cvt + lh * (size_t)Tq * 64;
+    const float *Vs = cvs + lh * 64;
+    const int nch = Tq >> 4;
+    // register prefetch: this thread's keys and this wave's value rows
+    int4 kr[CA_KPT][4];
+    float ksc[CA_KPT];
+#pragma unroll
+    for (int u = 0; u < CA_KPT; u++) {
+        const int j = t + u * 512;
+        const int jc = j < T ? j : T - 1; // clamped: unconditional loads
+        const int4 *kp = (const int4 *)(Kp + (size_t)jc * 64);
+#pragma unroll
+        for (int c = 0; c < 4; c++) kr[u][c] = kp[c];
+        ksc[u] = Ks[jc];
+    }
+    int4 vr[8][CA_VPL];
+#pragma unroll
+    for (int rr = 0; rr < 8; rr++) {
+        const int8_t *vrow = Vp + (size_t)(wave * 8 + rr) * Tq;
+#pragma unroll
+        for (int u = 0; u < CA_VPL; u++) {
+            const int c = lane + u * 64;
+            int4 v = *(const int4 *)(vrow + (c < nch ? c : nch - 1) * 16);
+            vr[rr][u] = c < nch ? v : make_int4(0, 0, 0, 0);
+        }
+    }
+    if (wave == 0) {
+        float v = qc[(size_t)s * d + h * 64 + lane] * scale;
+        float m = fw_wave_max(fabsf(v));
+        float xs = fmaxf(m, 1e-9f) / 127.0f;
+        q8[lane] = fw_q8_avx(v, 1.0f / xs, lane, 64);
+        if (lane == 0) bc[0] = xs;
+    }
+    __syncthreads();
+    const float xs = bc[0];
+    const int *qw = (const int *)q8;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < CA_KPT; u++) {
+        const int j = t + u * 512;
+        if (j < T) {
+            int acc = 0;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                acc = fw_sdot4(kr[u][c].x, qw[4 * c + 0], acc);
+                acc = fw_sdot4(kr[u][c].y, qw[4 * c + 1], acc);
+                acc = fw_sdot4(kr[u][c].z, qw[4 * c + 2], acc);
+                acc = fw_sdot4(kr[u][c].w, qw[4 * c + 3], acc);
+            }
+            float v = (float)acc * ksc[u] * xs + 0.0f;
+            sc[j] = v;
+            mx = fmaxf(mx, v);
+        }
+    }
+    // keys beyond the prefetched range (T > CA_KPT * 512)
+    for (int j = t + CA_KPT * 512; j < T; j += 512) {
+        const int4 *kp = (const int4 *)(Kp + (size_t)j * 64);
+        int acc = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            int4 kv = kp[c];
+            acc = fw_sdot4(kv.x, qw[4 * c + 0], acc);
+            acc = fw_sdot4(kv.y, qw[4 * c + 1], acc);
+            acc = fw_sdot4(kv.z, qw[4 * c + 2], acc);
+            acc = fw_sdot4(kv.w, qw[4 * c + 3], acc);
+        }
+        float v = (float)acc * Ks[j] * xs + 0.0f;
+        sc[j] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = fw_block_max(mx, red);
+    const bool fin = isfinite(mx);
+    if (fin)
+        for (int j = t; j < T; j += 512) {
+            float e = fw_expf(sc[j] - mx);
+            sc[j] = isfinite(e) ? e : 0.0f;
+        }
+    __syncthreads();
+    if (t == 0) {
+        // softmax_rows' sequential sum (nn.rs:4880-4963)
+        float sum = 0.0f;
+        if (fin) {
+            int j = 0;
+            for (; j + 4 <= T; j += 4) {
+                float4 v = *(const float4 *)(sc + j);
+                sum += v.x;
+                sum += v.y;
+                sum += v.z;
+                sum += v.w;
+            }
+            for (; j < T; j++) sum += sc[j];
+        }
+        bc[1] = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    const float inv = bc[1];
+    float pm = 0.0f;
+    for (int j = t; j < T; j += 512) {
+        float p = inv > 0.0f ? sc[j] * inv : sc[j];
+        sc[j] = p;
+        pm = fmaxf(pm, fabsf(p));
+    }
+    pm = fw_block_max(pm, red);
+    const float ps = fmaxf(pm, 1e-9f) / 127.0f;
+    const float pinv = 1.0f / ps;
+    for (int j = t; j < Tq; j += 512) p8[j] = j < T ? fw_q8_avx(sc[j], pinv, j, T) : (int8_t)0;
+    __syncthreads();
+    // out[dd] = sum_j Vt[dd, j] * p8[j]: wave w owns rows dd = w*8 .. w*8+7
+    int4 pp[CA_VPL];
+#pragma unroll
+    for (int u = 0; u < CA_VPL; u++) {
+        const int c = lane + u * 64;
+        pp[u] = c < nch ? *(const int4 *)(p8 + c * 16) : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 8; rr++) {
+        const int dd = wave * 8 + rr;
+        int acc = 0;
+#pragma unroll
+        for (int u = 0; u < CA_VPL; u++) {
+            acc = fw_sdot4(vr[rr][u].x, pp[u].x, acc);
+            acc = fw_sdot4(vr[rr][u].y, pp[u].y, acc);
+            acc = fw_sdot4(vr[rr][u].z, pp[u].z, acc);
+            acc = fw_sdot4(vr[rr][u].w, pp[u].w, acc);
+        }
+        // rows longer than the prefetched chunks
+        for (int c = lane + CA_VPL * 64; c < nch; c += 64) {
+            int4 vv = *(const int4 *)(Vp + (size_t)dd * Tq + c * 16);
+            int4 q4 = *(const int4 *)(p8 + c * 16);
+            acc = fw_sdot4(vv.x, q4.x, acc);
+            acc = fw_sdot4(vv.y, q4.y, acc);
+            acc = fw_sdot4(vv.z, q4.z, acc);
+            acc = fw_sdot4(vv.w, q4.w, acc);
+        }
+        acc = fw_wave_sum(acc);
+        if (lane == 0) att[(size_t)s * d + h * 64 + dd] = (float)acc * Vs[dd] * ps + 0.0f;
+    }
+}
+
+// Per-row int8 quantization of f16 rows into a row stride ldq >= n (zero
+// padded; quantize_f16_row_to_i8_into, nn.rs:2490-2555).  One 64-thread block
+// per row.
+__global__ void __launch_bounds__(64) k_quant_f16_rows_ld(const uint16_t *src, int8_t *q, float *s, int n, int ldq) {
+    size_t r = blockIdx.x;
+    const uint16_t *row = src + r * n;
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 64) m = fmaxf(m, fabsf(fw_h2f(row[i])));
+    m = fw_wave_max(m);
+    float sc = fmaxf(m, 1e-9f) / 127.0f;
+    float inv = 1.0f / sc;
+    for (int i = threadIdx.x; i < ldq; i += 64) q[r * ldq + i] = i < n ? fw_q8_avx(fw_h2f(row[i]), inv, i, n) : 0;
+    if (threadIdx.x == 0) s[r] = sc;
+}
+
+// ---------------------------------------------------------------------------
+// launch wrappers
+void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d, int rows,
+                        int8_t *xq, float *xs) {
+    hipLaunchKernelGGL(k_ln_quant, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, d, rows, xq, xs);
+}
+
+void fw_launch_quant_act_rows(hipStream_t st, const float *x, int rows, int n, int8_t *xq, float *xs) {
+    hipLaunchKernelGGL(k_quant_act_rows, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, xq, xs);
+}
+
+int fw_gemv_i8m_blocks(int N) { return N >= 16384 ? (N + 63) / 64 : (N + 15) / 16; }
+
+void fw_launch_gemv_i8m(hipStream_t st, const int8_t *W, const float *sw, const float *bias, const int8_t *xq,
+                        const float *xs, float *y, int N, int K, int ns, int ldy, int mode, const float *gelu_tab,
+                        const fwhip_filter *filt, const int *initialp, unsigned long long *keys) {
+    fwhip_filter ff;
+    int use = filt != nullptr;
+    if (filt) ff = *filt;
+    else memset(&ff, 0, sizeof ff);
+    int nblk = fw_gemv_i8m_blocks(N);
+    if (N >= 16384)
+        hipLaunchKernelGGL(k_gemv_i8m<4>, dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy, mode,
+                           gelu_tab, ff, use, initialp, keys);
+    else
+        hipLaunchKernelGGL(k_gemv_i8m<1>, dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy, mode,
+                           gelu_tab, ff, use, initialp, keys);
+}
+
+void fw_launch_argmax_finish(hipStream_t st, const unsigned long long *keys, int nblk, int ns, int32_t *tok,
+                             int32_t *hist, int hist_cap, int *posp, int *initialp, int *stepp, int advance) {
+    hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(1024), 0, st, keys, nblk, ns, tok, hist, hist_cap, posp,
+                       initialp, stepp, advance);
+}
+
+void fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const float *bias, const float *x, float *y,
+                         int N, int K, int ns, int ldy, int mode) {
+    const int nb = K >> 5;
+    size_t shm = sizeof(float) * ((size_t)BLK_R * ns * (nb + 1) + (size_t)BLK_R * nb);
+    hipLaunchKernelGGL(k_gemv_blk3, dim3((N + BLK_R - 1) / BLK_R), dim3(256), shm, st, W, sc, bias, x, y, N, K, ns, ldy,
+                       mode);
+}
+
+void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
+                          int d, int H, int nctx, int L, int layer, int ns, float scale) {
+    size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
+    hipLaunchKernelGGL(k_self_attn2, dim3(H, ns), dim3(256), shm, st, qkv, kc, vc, att, posp, d, nctx, L, layer,
+                       scale);
+}
+
+void fw_launch_cross_attn_i8v2(hipStream_t st, const float *qc, const int8_t *ck, const float *cks, const int8_t *cvt,
+                               const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
+                               float scale) {
+    size_t shm = sizeof(float) * ((T + 3) & ~3) + Tq;
+    hipLaunchKernelGGL(k_cross_attn_i8v2, dim3(H, ns), dim3(512), shm, st, qc, ck, cks, cvt, cvs, att, d, T, Tq, H, L,
+                       layer, scale);
+}
+
+void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq) {
+    hipLaunchKernelGGL(k_quant_f16_rows_ld, dim3(rows), dim3(64), 0, st, src, q, s, n, ldq);
+}
+
+// Per-block argmax keys over already computed logits [ns, V] (the f16 arm's
+// logits GEMV has no fused key epilogue): block (b, s) covers 2048 logits.
+__global__ void __launch_bounds__(256) k_logits_keys(const float *logits, int V, fwhip_filter filt, int use_filter,
+                                                     const int *initialp, unsigned long long *keys) {
+    __shared__ unsigned long long wk[4];
+    const int b = blockIdx.x, s = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int initial = use_filter ? *initialp : 0;
+    const float *l = logits + (size_t)s * V;
+    unsigned long long k = 0ull;
+    for (int i = b * 2048 + threadIdx.x; i < V && i < (b + 1) * 2048; i += 256) {
+        if (use_filter && dec_masked(i, filt, initial)) continue;
+        unsigned long long c = am_key(l[i], i);
+        k = c > k ? c : k;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) k = shfl_max_u64(k, off);
+    if (lane == 0) wk[wave] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long m = wk[0];
+        for (int w = 1; w < 4; w++) m = wk[w] > m ? wk[w] : m;
+        keys[(size_t)s * gridDim.x + b] = m;
+    }
+}
+
+int fw_logits_keys_blocks(int V) { return (V + 2047) / 2048; }
+
+void fw_launch_logits_keys(hipStream_t st, const float *logits, int V, int ns, const fwhip_filter *filt,
+                           const int *initialp, unsigned long long *keys) {
+    fwhip_filter ff;
+    int use = filt != nullptr;
+    if (filt) ff = *filt;
+    else memset(&ff, 0, sizeof ff);
+    hipLaunchKernelGGL(k_logits_keys, dim3(fw_logits_keys_blocks(V), ns), dim3(256), 0, st, logits, V, ff, use,
+                       initialp, keys);
+}

@@ -1,0 +1,362 @@
+// enc_gemm.hip — the encoder's dense contractions on MFMA (gfx950).
+//
+// One tiled GEMM template C[M,N] = A[M,K] x B[N,K]^T serves every encoder
+// linear and the conv stem (as an im2col GEMM).  Operand kinds:
+//   KIND_I8   : i8 x i8 -> i32 (v_mfma_i32_32x32x32_i8).  The int8 plan's
+//               accumulators are exact integers, equal to the reference's
+//               maddubs sum minus 128*colsum (nn.rs:1537-1771) or its i8 dot
+//               (encoder.rs:2524-2606); epilogue ((f32)acc * s_x) * s_w (+ b)
+//               in the reference's association (nn.rs:1660-1700,
+//               encoder.rs:2573-2580).
+//   KIND_F16S : f32 activations carried as an f16 pair (hi, lo = f16(a - hi))
+//               against the f16 weights (exact: the reference dequantizes f16
+//               weights to f32), two v_mfma_f32_32x32x16_f16 per product;
+//               per-product error <= 2^-22 |a| + 2^-25, f32 accumulation.
+//
+// Block = 256 threads as 2x2 waves; block tile BM x BN (128x128 by default;
+// 256x256 and 256x128 for sweeps);
+// each wave owns (BM/2) x (BN/2) as a grid of 32x32 MFMA tiles.  K advances
+// 64 bytes per stage (64 int8 or 32 f16 values); a stage is staged global ->
+// registers -> LDS (rows padded to 80 bytes: conflict-free 16-byte reads),
+// double buffered with one barrier per stage.  The epilogue is a template
+// parameter so its loops fully unroll and the accumulators stay in registers.
+//
+// Tile order: the hardware deals blocks round-robin to the 8 XCDs; block ids
+// are remapped so each XCD gets a contiguous run of tiles, walked in groups of
+// 8 M-tiles (N outer), so an XCD's L2 holds the A rows of its group and one B
+// tile at a time.
+//
+// MFMA operand layouts (gfx950): A lane l -> row l%32, k block (l/32)*16
+// bytes; B lane l -> col l%32, same k block; accumulator r of lane l -> row
+// (r/4)*8 + (l/32)*4 + r%4, col l%32.
+#include <cstdlib>
+#include <cstring>
+
+#include "fw_enc.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+#define GEMM_LDSR 80 // LDS row stride in bytes (64 data + 16 pad)
+
+__device__ __forceinline__ void fw_split2(float v, uint16_t &hi, uint16_t &lo) {
+    asm volatile("" : "+v"(v));
+    _Float16 h = (_Float16)v;
+    float r = v - (float)h;
+    asm volatile("" : "+v"(r));
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, (_Float16)r);
+}
+
+// Epilogue for the 4 consecutive rows row0..row0+3 of one column.
+template <int KIND, int EPI>
+__device__ __forceinline__ void gemm_store4(const FwGemm &g, int row0, int col, const float (&a)[4]) {
+    if (col >= g.N) return;
+    if constexpr (EPI == FW_EPI_QKV) {
+        // head-major split outputs: Q, K as [B, H, T, 64]; V as [B, H, 64, Tp]
+        const int d = g.ldc, which = col / d, cc = col - which * d, h = cc >> 6, dd = cc & 63;
+        float bias = g.bias ? g.bias[col] : 0.0f;
+        float sw = KIND == FW_KIND_I8 ? g.sw[col] : 1.0f;
+        float v[4];
+        uint16_t hi[4], lo[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            int row = row0 + e;
+            float x = a[e];
+            if constexpr (KIND == FW_KIND_I8) x = row < g.M ? x * g.sx[row] * sw : 0.0f;
+            if (g.bias) x = x + bias;
+            v[e] = x;
+            fw_split2(v[e], hi[e], lo[e]);
+        }
+        if (which < 2) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                int row = row0 + e;
+                if (row >= g.M) continue;
+                int b = row / g.T, t = row - b * g.T;
+                size_t o = (((size_t)b * g.H + h) * g.T + t) * 64 + dd;
+                g.o16[2 * which][o] = hi[e];
+                g.o16[2 * which + 1][o] = lo[e];
+            }
+        } else {
+            int b = row0 / g.T, t = row0 - b * g.T;
+            size_t o = (((size_t)b * g.H + h) * 64 + dd) * g.Tp + t;
+            if ((t & 3) == 0 && t + 3 < g.T && row0 + 3 < g.M) {
+                uint2 ph = make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+                uint2 pl = make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+                *(uint2 *)(g.o16[4] + o) = ph;
+                *(uint2 *)(g.o16[5] + o) = pl;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    int row = row0 + e;
+                    if (row >= g.M) continue;
+                    int bb = row / g.T, tt = row - bb * g.T;
+                    size_t oo = (((size_t)bb * g.H + h) * 64 + dd) * g.Tp + tt;
+                    g.o16[4][oo] = hi[e];
+                    g.o16[5][oo] = lo[e];
+                }
+            }
+        }
+        return;
+    } else {
+        float bias = g.bias ? g.bias[col] : 0.0f;
+        float sw = (KIND == FW_KIND_I8 && EPI != FW_EPI_ACC32) ? g.sw[col] : 1.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            int row = row0 + e;
+            if (row >= g.M) continue;
+            size_t o = (size_t)row * g.ldc + col;
+            if constexpr (EPI == FW_EPI_ACC32) {
+                if constexpr (KIND == FW_KIND_I8) ((int *)g.C)[o] = (int)a[e];
+                else g.C[o] = a[e];
+                continue;
+            } else {
+                float v = a[e];
+                if constexpr (KIND == FW_KIND_I8) v = v * g.sx[row] * sw;
+                if (g.bias) v = v + bias;
+                if constexpr (EPI == FW_EPI_F32) {
+                    g.C[o] = v;
+                } else if constexpr (EPI == FW_EPI_RESID) {
+                    g.C[o] = g.C[o] + v;
+                } else if constexpr (EPI == FW_EPI_GELU_F32) {
+                    g.C[o] = fw_gelu(v, g.gelu_tab);
+                } else if constexpr (EPI == FW_EPI_GELU_SPLIT) {
+                    uint16_t hi, lo;
+                    fw_split2(fw_gelu(v, g.gelu_tab), hi, lo);
+                    g.o16[0][o] = hi;
+                    g.o16[1][o] = lo;
+                } else if constexpr (EPI == FW_EPI_CONV2) {
+                    int t = row % g.T;
+                    g.C[o] = fw_gelu(v, g.gelu_tab) + g.pos[(size_t)t * g.ldc + col];
+                }
+            }
+        }
+    }
+}
+
+template <int KIND, int EPI, int BM, int BN>
+__global__ void __launch_bounds__(256) k_gemm(FwGemm g, int ntm, int ntn) {
+    constexpr int NA = KIND == FW_KIND_F16S ? 2 : 1;
+    constexpr int ES = KIND == FW_KIND_I8 ? 1 : 2;
+    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+    constexpr int ROWS = NA * BM + BN; // LDS rows per stage
+    constexpr int STAGE = ROWS * GEMM_LDSR;
+    constexpr int CH = ROWS * 4 / 256; // 16-byte chunks per thread per stage
+    constexpr int CHA = NA * BM / 64;  // chunks (per thread) that belong to A
+    __shared__ __align__(16) unsigned char lds[2 * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // XCD-contiguous, M-grouped tile order
+    const int nb = gridDim.x, bid = blockIdx.x;
+    const int xcd = bid & 7, loc = bid >> 3, per = nb >> 3, rem = nb & 7;
+    const int t = xcd < rem ? xcd * (per + 1) + loc : rem * (per + 1) + (xcd - rem) * per + loc;
+    constexpr int GM = 8;
+    const int gsize = GM * ntn, grp = t / gsize, first_m = grp * GM;
+    const int gm = min(ntm - first_m, GM), rr = t - grp * gsize;
+    const int m0 = (first_m + rr % gm) * BM, n0 = (rr / gm) * BN;
+    const int nsteps = g.K * ES / 64;
+
+    int4 stg[CH];
+    auto gload = [&](int s) {
+#pragma unroll
+        for (int q = 0; q < CH; q++) {
+            const int row = (tid >> 2) + q * 64, cc = tid & 3;
+            const size_t koff = (size_t)s * 64 + cc * 16;
+            if (q < CHA) {
+                const int a = (q * 64) / BM, r = row - a * BM, gr = m0 + r;
+                const unsigned char *base = (const unsigned char *)(a == 0 ? g.A : g.A2);
+                stg[q] = gr < g.M ? *(const int4 *)(base + (size_t)gr * g.lda * ES + koff) : make_int4(0, 0, 0, 0);
+            } else {
+                const int gn = n0 + row - NA * BM;
+                stg[q] = gn < g.N ? *(const int4 *)((const unsigned char *)g.B + (size_t)gn * g.ldb * ES + koff)
+                                  : make_int4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+        unsigned char *base = lds + buf * STAGE;
+#pragma unroll
+        for (int q = 0; q < CH; q++) {
+            const int row = (tid >> 2) + q * 64, cc = tid & 3;
+            *(int4 *)(base + row * GEMM_LDSR + cc * 16) = stg[q];
+        }
+    };
+
+    typedef typename std::conditional<KIND == FW_KIND_I8, v16i, v16f>::type accT;
+    accT acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    int buf = 0;
+    for (int s = 0; s < nsteps; s++) {
+        if (s + 1 < nsteps) gload(s + 1);
+        const unsigned char *tb = lds + buf * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const int koff = ks * 32 + (lane >> 5) * 16;
+            v4i af[NA][TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int row = wm * WM + i * 32 + (lane & 31);
+#pragma unroll
+                for (int a = 0; a < NA; a++) af[a][i] = *(const v4i *)(tb + (a * BM + row) * GEMM_LDSR + koff);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int row = wn * WN + j * 32 + (lane & 31);
+                bf[j] = *(const v4i *)(tb + (NA * BM + row) * GEMM_LDSR + koff);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    if constexpr (KIND == FW_KIND_I8) {
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0][i], bf[j], acc[i][j], 0, 0, 0);
+                    } else {
+                        const v8h bh = __builtin_bit_cast(v8h, bf[j]);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, af[0][i]), bh,
+                                                                           acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, af[1][i]), bh,
+                                                                           acc[i][j], 0, 0, 0);
+                    }
+                }
+        }
+        if (s + 1 < nsteps) lstore(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+
+    if constexpr (EPI == FW_EPI_QKV || EPI == FW_EPI_CONV2) {
+        // Heavy epilogues: written once, in a runtime loop over this wave's
+        // tiles, reading each tile back from a wave-private LDS slab (a fully
+        // unrolled copy of such an epilogue per tile is too large to unroll,
+        // which would push the accumulators to scratch memory).
+        float *slab = (float *)lds + wave * (32 * 33);
+        for (int tile = 0; tile < TM * TN; tile++) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    if (i * TN + j == tile)
+#pragma unroll
+                        for (int r = 0; r < 16; r++)
+                            slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * 33 + (lane & 31)] = (float)acc[i][j][r];
+            __syncthreads();
+            const int i = tile / TN, j = tile - i * TN;
+            const int col = n0 + wn * WN + j * 32 + (lane & 31);
+            for (int q = 0; q < 4; q++) {
+                const int rl = q * 8 + (lane >> 5) * 4;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = slab[(rl + e) * 33 + (lane & 31)];
+                gemm_store4<KIND, EPI>(g, m0 + wm * WM + i * 32 + rl, col, v);
+            }
+            __syncthreads();
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int col = n0 + wn * WN + j * 32 + (lane & 31);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int row0 = m0 + wm * WM + i * 32 + q * 8 + (lane >> 5) * 4;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = (float)acc[i][j][q * 4 + e];
+                if constexpr (KIND == FW_KIND_I8 && EPI == FW_EPI_ACC32) {
+                    // exact i32 accumulators: store the integers themselves
+                    if (col < g.N)
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (row0 + e < g.M) ((int *)g.C)[(size_t)(row0 + e) * g.ldc + col] = acc[i][j][q * 4 + e];
+                } else {
+                    gemm_store4<KIND, EPI>(g, row0, col, v);
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// Tile choice.  Measured on MI355X (large-v3-turbo int8 plan, 10 windows):
+// 128x128 tiles at two blocks per CU sustain 737 TOP/s against 427-434 TOP/s
+// for the one-block-per-CU 256-wide tiles, whose single wave per SIMD cannot
+// hide the global->LDS staging; 128x128 is the default and FWHIP_GEMM_TILE=
+// BMxBN selects another (tuning sweeps).
+struct TileCfg {
+    int bm, bn;
+};
+static const TileCfg kTiles[3] = {{256, 256}, {256, 128}, {128, 128}};
+
+static int pick_tile(int, int, int) {
+    static int forced = -2;
+    if (forced == -2) {
+        forced = -1;
+        const char *e = getenv("FWHIP_GEMM_TILE");
+        if (e)
+            for (int i = 0; i < 3; i++) {
+                char buf[16];
+                snprintf(buf, sizeof buf, "%dx%d", kTiles[i].bm, kTiles[i].bn);
+                if (!strcmp(e, buf)) forced = i;
+            }
+    }
+    return forced >= 0 ? forced : 2;
+}
+
+template <int KIND, int EPI, int BM, int BN>
+static void launch_one(hipStream_t st, const FwGemm &g) {
+    int ntm = (g.M + BM - 1) / BM, ntn = (g.N + BN - 1) / BN;
+    hipLaunchKernelGGL((k_gemm<KIND, EPI, BM, BN>), dim3(ntm * ntn), dim3(256), 0, st, g, ntm, ntn);
+}
+
+template <int KIND, int EPI>
+static void launch_tiles(hipStream_t st, const FwGemm &g, int tile) {
+    switch (tile) {
+    case 0: launch_one<KIND, EPI, 256, 256>(st, g); break;
+    case 1: launch_one<KIND, EPI, 256, 128>(st, g); break;
+    default: launch_one<KIND, EPI, 128, 128>(st, g); break;
+    }
+}
+
+void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g) {
+    static int ncu = 0;
+    if (!ncu) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+        if (ncu <= 0) ncu = 256;
+    }
+    int tile = pick_tile(g.M, g.N, ncu);
+    if (kind == FW_KIND_I8) {
+        switch (g.epi) {
+        case FW_EPI_F32: launch_tiles<FW_KIND_I8, FW_EPI_F32>(st, g, tile); break;
+        case FW_EPI_RESID: launch_tiles<FW_KIND_I8, FW_EPI_RESID>(st, g, tile); break;
+        case FW_EPI_QKV: launch_tiles<FW_KIND_I8, FW_EPI_QKV>(st, g, tile); break;
+        case FW_EPI_ACC32: launch_tiles<FW_KIND_I8, FW_EPI_ACC32>(st, g, tile); break;
+        default: break;
+        }
+    } else {
+        switch (g.epi) {
+        case FW_EPI_F32: launch_tiles<FW_KIND_F16S, FW_EPI_F32>(st, g, tile); break;
+        case FW_EPI_RESID: launch_tiles<FW_KIND_F16S, FW_EPI_RESID>(st, g, tile); break;
+        case FW_EPI_GELU_F32: launch_tiles<FW_KIND_F16S, FW_EPI_GELU_F32>(st, g, tile); break;
+        case FW_EPI_GELU_SPLIT: launch_tiles<FW_KIND_F16S, FW_EPI_GELU_SPLIT>(st, g, tile); break;
+        case FW_EPI_CONV2: launch_tiles<FW_KIND_F16S, FW_EPI_CONV2>(st, g, tile); break;
+        case FW_EPI_QKV: launch_tiles<FW_KIND_F16S, FW_EPI_QKV>(st, g, tile); break;
+        default: break;
+        }
+    }
+}

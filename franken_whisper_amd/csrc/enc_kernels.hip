@@ -1,29 +1,16 @@
-// enc_kernels.hip — encoder kernels for gfx950 (MFMA).
+// enc_kernels.hip — encoder kernels for gfx950 other than the GEMM
+// (enc_gemm.hip): LayerNorm/quantizer row kernels, im2col, attention.
 //
-// The encoder is a dense contraction: every linear and the conv stem are one
-// tiled MFMA GEMM template with two operand kinds:
-//   KIND_I8   : i8 x i8 -> i32 (v_mfma_i32_32x32x32_i8).  The int8 path's
-//               accumulators are exact integers, equal to the reference's
-//               maddubs sum minus 128*colsum (nn.rs:1537-1771) or its i8 dot
-//               (encoder.rs:2524-2606); epilogue ((f32)acc * s_x) * s_w (+ b).
-//   KIND_F16S : f32 activations carried as an f16 pair (hi, lo = f16(a - hi))
-//               against the f16 weights (exact: the reference dequantizes f16
-//               weights to f32), two v_mfma_f32_32x32x16_f16 per product;
-//               per-product error <= 2^-22 |a| + 2^-25, fp32 accumulation.
-// Tile 128x128 per 256-thread block (2x2 waves of 64x64 = 2x2 MFMA 32x32
-// tiles), K staged through LDS in 64-byte rows, double buffered.
+// The f32 path carries activations as an f16 pair (hi, lo = f16(a - hi)) so
+// that MFMA f16 products reproduce f32 products to within 2^-22 relative.
 //
-// MFMA operand layouts (verified on gfx950): A lane l -> row l%32, k block
-// (l/32)*16 bytes; B lane l -> col l%32, same k block; accumulator r of lane l
-// -> row (r/4)*8 + (l/32)*4 + r%4, col l%32.
+// MFMA operand layouts (gfx950): A lane l -> row l%32, k block (l/32)*8
+// halves; B lane l -> col l%32, same k block; accumulator r of lane l -> row
+// (r/4)*8 + (l/32)*4 + r%4, col l%32.
 #include "fw_enc.h"
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-
-#define LDSR 80 // padded LDS row stride in bytes (64 data + 16 pad)
 
 __device__ __forceinline__ void fw_split(float v, uint16_t &hi, uint16_t &lo) {
     asm volatile("" : "+v"(v));
@@ -32,175 +19,6 @@ __device__ __forceinline__ void fw_split(float v, uint16_t &hi, uint16_t &lo) {
     asm volatile("" : "+v"(r));
     hi = __builtin_bit_cast(uint16_t, h);
     lo = __builtin_bit_cast(uint16_t, (_Float16)r);
-}
-
-template <int KIND>
-__global__ void __launch_bounds__(256) k_gemm(FwGemm g) {
-    constexpr int NA = KIND == FW_KIND_F16S ? 2 : 1;
-    constexpr int ES = KIND == FW_KIND_I8 ? 1 : 2;
-    constexpr int BM = 128, BN = 128;
-    constexpr int TILE_BYTES = (NA * BM + BN) * LDSR;
-    __shared__ __align__(16) unsigned char lds[2 * TILE_BYTES];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    // XCD-friendly tile order: consecutive blocks walk N first within a band
-    // of row tiles so a band's A rows stay hot in one L2.
-    const int gx = gridDim.x;
-    const int bid = blockIdx.y * gx + blockIdx.x;
-    const int n_tile = bid % gx, m_tile = bid / gx;
-    const int m0 = m_tile * BM, n0 = n_tile * BN;
-    const int kstep = 64 / ES; // k elements per stage
-    const int nsteps = g.K / kstep;
-
-    // global -> register staging: 512 16-byte chunks per operand tile, 2 per thread
-    int4 ra[NA][2], rb[2];
-    auto gload = [&](int s) {
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            int c = tid + q * 256;
-            int row = c >> 2, cc = c & 3;
-            size_t koff = (size_t)s * 64 + cc * 16; // bytes
-            int gr = m0 + row;
-#pragma unroll
-            for (int a = 0; a < NA; a++) {
-                const unsigned char *base = (const unsigned char *)(a == 0 ? g.A : g.A2);
-                ra[a][q] = gr < g.M ? *(const int4 *)(base + (size_t)gr * g.lda * ES + koff) : make_int4(0, 0, 0, 0);
-            }
-            int gn = n0 + row;
-            rb[q] = gn < g.N ? *(const int4 *)((const unsigned char *)g.B + (size_t)gn * g.ldb * ES + koff)
-                             : make_int4(0, 0, 0, 0);
-        }
-    };
-    auto lstore = [&](int buf) {
-        unsigned char *t = lds + buf * TILE_BYTES;
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            int c = tid + q * 256;
-            int row = c >> 2, cc = c & 3;
-#pragma unroll
-            for (int a = 0; a < NA; a++) *(int4 *)(t + (a * BM + row) * LDSR + cc * 16) = ra[a][q];
-            *(int4 *)(t + (NA * BM + row) * LDSR + cc * 16) = rb[q];
-        }
-    };
-
-    typedef typename std::conditional<KIND == FW_KIND_I8, v16i, v16f>::type accT;
-    accT acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    int buf = 0;
-    for (int s = 0; s < nsteps; s++) {
-        if (s + 1 < nsteps) gload(s + 1);
-        const unsigned char *t = lds + buf * TILE_BYTES;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            int koff = ks * 32 + (lane >> 5) * 16;
-            v4i af[NA][2], bf[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                int row = wm * 64 + i * 32 + (lane & 31);
-#pragma unroll
-                for (int a = 0; a < NA; a++) af[a][i] = *(const v4i *)(t + (a * BM + row) * LDSR + koff);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                int row = wn * 64 + j * 32 + (lane & 31);
-                bf[j] = *(const v4i *)(t + (NA * BM + row) * LDSR + koff);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    if constexpr (KIND == FW_KIND_I8) {
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0][i], bf[j], acc[i][j], 0, 0, 0);
-                    } else {
-                        v8h bh = __builtin_bit_cast(v8h, bf[j]);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, af[0][i]), bh,
-                                                                           acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, af[1][i]), bh,
-                                                                           acc[i][j], 0, 0, 0);
-                    }
-                }
-        }
-        if (s + 1 < nsteps) lstore(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
-    }
-
-    // epilogue
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            int col = n0 + wn * 64 + j * 32 + (lane & 31);
-            if (col >= g.N) continue;
-            float sw = g.sw ? g.sw[col] : 1.0f;
-            float bias = g.bias ? g.bias[col] : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (row >= g.M) continue;
-                if (g.epi == FW_EPI_ACC32) { // raw accumulator (per-GEMM parity)
-                    if constexpr (KIND == FW_KIND_I8) ((int *)g.C)[(size_t)row * g.ldc + col] = acc[i][j][r];
-                    else g.C[(size_t)row * g.ldc + col] = acc[i][j][r];
-                    continue;
-                }
-                float v;
-                if constexpr (KIND == FW_KIND_I8) {
-                    v = (float)acc[i][j][r] * g.sx[row] * sw;
-                } else {
-                    v = acc[i][j][r];
-                }
-                if (g.bias) v = v + bias;
-                switch (g.epi) {
-                case FW_EPI_F32: g.C[(size_t)row * g.ldc + col] = v; break;
-                case FW_EPI_RESID: {
-                    float *p = g.C + (size_t)row * g.ldc + col;
-                    *p = *p + v;
-                    break;
-                }
-                case FW_EPI_GELU_F32: g.C[(size_t)row * g.ldc + col] = fw_gelu(v, g.gelu_tab); break;
-                case FW_EPI_GELU_SPLIT: {
-                    uint16_t hi, lo;
-                    fw_split(fw_gelu(v, g.gelu_tab), hi, lo);
-                    g.o16[0][(size_t)row * g.ldc + col] = hi;
-                    g.o16[1][(size_t)row * g.ldc + col] = lo;
-                    break;
-                }
-                case FW_EPI_CONV2: {
-                    int t = row % g.T;
-                    g.C[(size_t)row * g.ldc + col] = fw_gelu(v, g.gelu_tab) + g.pos[(size_t)t * g.ldc + col];
-                    break;
-                }
-                case FW_EPI_QKV: {
-                    // head-major split outputs: Q, K as [B, H, T, 64]; V as [B, H, 64, Tp]
-                    int d = g.ldc, which = col / d, cc = col % d, h = cc >> 6, dd = cc & 63;
-                    int b = row / g.T, t = row % g.T;
-                    size_t bh = (size_t)b * g.H + h;
-                    uint16_t hi, lo;
-                    fw_split(v, hi, lo);
-                    if (which < 2) {
-                        size_t o = (bh * g.T + t) * 64 + dd;
-                        g.o16[2 * which][o] = hi;
-                        g.o16[2 * which + 1][o] = lo;
-                    } else {
-                        size_t o = (bh * 64 + dd) * g.Tp + t;
-                        g.o16[4][o] = hi;
-                        g.o16[5][o] = lo;
-                    }
-                    break;
-                }
-                default: break;
-                }
-            }
-        }
 }
 
 // ---------------------------------------------------------------------------
@@ -289,12 +107,48 @@ __global__ void __launch_bounds__(256) k_quant_exact_rows(const float *x, int n,
 
 // quantize_act_i7_gelu (nn.rs:1791-1823): GELU (skipped when gelu_tab is
 // NULL: quantize_act_i7, nn.rs:1443-1466), per-row amax/127, add-trunc body /
-// exact tail, signed storage.
+// exact tail, signed storage.  Rows of up to 6144 values are read once and
+// held in registers (float4 per thread per slot); longer rows take two passes.
+#define FW_QROW_V4 6
 __global__ void __launch_bounds__(256) k_gelu_quant_i7_rows(const float *x, int n, const float *gelu_tab, int8_t *q,
                                                             float *qs) {
     __shared__ float shf[4];
     size_t r = blockIdx.x;
     const float *xr = x + r * n;
+    if ((n & 3) == 0 && n <= 4 * 256 * FW_QROW_V4) {
+        float4 v[FW_QROW_V4];
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < FW_QROW_V4; k++) {
+            int i4 = threadIdx.x + k * 256;
+            if (i4 * 4 < n) {
+                float4 t = ((const float4 *)xr)[i4];
+                if (gelu_tab) {
+                    t.x = fw_gelu(t.x, gelu_tab);
+                    t.y = fw_gelu(t.y, gelu_tab);
+                    t.z = fw_gelu(t.z, gelu_tab);
+                    t.w = fw_gelu(t.w, gelu_tab);
+                }
+                v[k] = t;
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+            }
+        }
+        m = fw_block_max(m, shf);
+        float sc = fmaxf(m, 1e-9f) / 127.0f;
+        float inv = 1.0f / sc;
+#pragma unroll
+        for (int k = 0; k < FW_QROW_V4; k++) {
+            int i4 = threadIdx.x + k * 256;
+            if (i4 * 4 < n) {
+                int i = i4 * 4;
+                uint32_t b0 = (uint8_t)fw_q8_avx(v[k].x, inv, i, n), b1 = (uint8_t)fw_q8_avx(v[k].y, inv, i + 1, n);
+                uint32_t b2 = (uint8_t)fw_q8_avx(v[k].z, inv, i + 2, n), b3 = (uint8_t)fw_q8_avx(v[k].w, inv, i + 3, n);
+                *(uint32_t *)(q + r * n + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
+        }
+        if (threadIdx.x == 0) qs[r] = sc;
+        return;
+    }
     float m = 0.0f;
     for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(gelu_tab ? fw_gelu(xr[i], gelu_tab) : xr[i]));
     m = fw_block_max(m, shf);
@@ -583,11 +437,6 @@ void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qof
 }
 
 // ---------------------------------------------------------------------------
-void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g) {
-    dim3 grid((g.N + 127) / 128, (g.M + 127) / 128);
-    if (kind == FW_KIND_I8) hipLaunchKernelGGL(k_gemm<FW_KIND_I8>, grid, dim3(256), 0, st, g);
-    else hipLaunchKernelGGL(k_gemm<FW_KIND_F16S>, grid, dim3(256), 0, st, g);
-}
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
                       float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs) {
     hipLaunchKernelGGL(k_enc_ln, dim3(rows), dim3(256), 0, st, x, w, b, d, mode, yf, hi, lo, q, qs);

@@ -8,6 +8,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -220,14 +221,21 @@ struct fwhip_decoder {
 
 struct fwhip_dstate {
     fwhip_decoder *dec;
-    int S, T, len;
+    int S, T, Tq, Sp, len;
     uint16_t *kv_k, *kv_v, *ck16, *cvt16;
-    int8_t *ck8 = nullptr, *cvt8 = nullptr;
+    int8_t *ck8 = nullptr, *cvt8 = nullptr; // cvt8 rows have stride Tq (T rounded up to 16)
     float *ck8s = nullptr, *cvt8s = nullptr;
     float *x, *h, *qkv, *att, *y, *ff, *logits;
-    int32_t *tok, *amax, *hist, *rows;
-    int *pos, *initial;
+    int8_t *xq;             // [Sp, d] quantized activation rows (rows >= S stay zero)
+    float *xs;              // [Sp]
+    unsigned long long *keys; // [S, nkeys] per-block argmax keys
+    int nkeys;
+    int32_t *tok, *hist, *rows;
+    int *pos, *initial, *stepc;
     int hist_cap;
+    // captured sampling step (forward of st->tok + argmax + bookkeeping)
+    hipGraphExec_t graph = nullptr;
+    fwhip_filter graph_filter;
     std::vector<void *> owned;
 };
 
@@ -392,6 +400,8 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     st->dec = dd;
     st->S = S;
     st->T = T;
+    st->Tq = (T + 15) & ~15;
+    st->Sp = (S + 15) & ~15;
     st->len = 0;
     int d = dd->d, L = dd->L, nctx = dd->nctx;
     auto &own = st->owned;
@@ -404,7 +414,7 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     bool ok = st->kv_k && st->kv_v && st->ck16 && st->cvt16;
     if (dd->arm == FWHIP_DEC_INT8) {
         st->ck8 = (int8_t *)fw_dalloc(own, crn);
-        st->cvt8 = (int8_t *)fw_dalloc(own, crn);
+        st->cvt8 = (int8_t *)fw_dalloc(own, (size_t)S * L * dd->H * 64 * st->Tq);
         st->ck8s = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * L * dd->H * T);
         st->cvt8s = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * L * d);
         ok = ok && st->ck8 && st->cvt8 && st->ck8s && st->cvt8s;
@@ -416,15 +426,21 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     st->y = (float *)fw_dalloc(own, sizeof(float) * S * d);
     st->ff = (float *)fw_dalloc(own, sizeof(float) * S * dd->dff);
     st->logits = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * dd->V);
+    st->xq = (int8_t *)fw_dalloc(own, (size_t)st->Sp * d);
+    st->xs = (float *)fw_dalloc(own, sizeof(float) * st->Sp);
+    st->nkeys = dd->arm == FWHIP_DEC_INT8 ? fw_gemv_i8m_blocks(dd->V) : fw_logits_keys_blocks(dd->V);
+    st->keys = (unsigned long long *)fw_dalloc(own, sizeof(unsigned long long) * (size_t)S * st->nkeys);
     st->tok = (int32_t *)fw_dalloc(own, sizeof(int32_t) * S);
-    st->amax = (int32_t *)fw_dalloc(own, sizeof(int32_t) * S);
     st->rows = (int32_t *)fw_dalloc(own, sizeof(int32_t) * (size_t)S * nctx);
     st->hist_cap = nctx;
     st->hist = (int32_t *)fw_dalloc(own, sizeof(int32_t) * (size_t)S * nctx);
-    st->pos = (int *)fw_dalloc(own, sizeof(int) * 2);
+    st->pos = (int *)fw_dalloc(own, sizeof(int) * 4);
     st->initial = st->pos + 1;
-    ok = ok && st->x && st->h && st->qkv && st->att && st->y && st->ff && st->logits && st->tok && st->amax && st->rows &&
-         st->hist && st->pos;
+    st->stepc = st->pos + 2;
+    ok = ok && st->x && st->h && st->qkv && st->att && st->y && st->ff && st->logits && st->xq && st->xs &&
+         st->keys && st->tok && st->rows && st->hist && st->pos;
+    // padding rows of the quantized activations must read as zeros
+    ok = ok && hipMemset(st->xq, 0, (size_t)st->Sp * d) == hipSuccess && hipMemset(st->pos, 0, sizeof(int) * 4) == hipSuccess;
     if (!ok) {
         fw_free_all(own);
         delete st;
@@ -438,6 +454,7 @@ extern "C" void fwhip_dstate_free(fwhip_dstate *st) {
     if (!st) return;
     hipSetDevice(st->dec->ctx->device);
     hipStreamSynchronize(st->dec->ctx->stream);
+    if (st->graph) hipGraphExecDestroy(st->graph);
     fw_free_all(st->owned);
     delete st;
 }
@@ -493,7 +510,7 @@ extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *en
     }
     if (dd->arm == FWHIP_DEC_INT8) {
         fw_launch_quant_f16_rows(c->stream, st->ck16, st->ck8, st->ck8s, S * L * H * T, 64);
-        fw_launch_quant_f16_rows(c->stream, st->cvt16, st->cvt8, st->cvt8s, S * L * H * 64, T);
+        fw_launch_quant_f16_rows_ld(c->stream, st->cvt16, st->cvt8, st->cvt8s, S * L * H * 64, T, st->Tq);
     }
     HIP_TRY(hipGetLastError());
     st->len = 0;
@@ -506,9 +523,32 @@ static fwhip_status check_cancel(fwhip_ctx *c) {
     return FWHIP_OK;
 }
 
+// int8 GEMV over every stream, 16 streams per launch (the MFMA tile height).
+static void gemv_i8_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const float *sw, const float *bias, float *y,
+                        int N, int K, int ldy, int mode, const fwhip_filter *filt) {
+    const float *gt = st->dec->ctx->gelu_tab;
+    int nblk = fw_gemv_i8m_blocks(N);
+    for (int s0 = 0; s0 < st->S; s0 += 16) {
+        int n = st->S - s0 < 16 ? st->S - s0 : 16;
+        fw_launch_gemv_i8m(s, W, sw, bias, st->xq + (size_t)s0 * K, st->xs + s0, y + (size_t)s0 * ldy, N, K, n, ldy,
+                           mode, gt, filt, st->initial, mode == 3 ? st->keys + (size_t)s0 * nblk : nullptr);
+    }
+}
+static void gemv_blk_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const float *sc, const float *bias,
+                         const float *x, float *y, int N, int K, int ldy) {
+    for (int s0 = 0; s0 < st->S; s0 += 16) {
+        int n = st->S - s0 < 16 ? st->S - s0 : 16;
+        fw_launch_gemv_blk2(s, W, sc, bias, x + (size_t)s0 * K, y + (size_t)s0 * ldy, N, K, n, ldy, 1);
+    }
+}
+
 // One token row for every stream at the device-side position *st->pos
-// (forward_step_hidden decoder.rs:1754-1906 + logits_last 2087-2147).
-static fwhip_status dec_forward_row_tok(fwhip_dstate *st, const int32_t *tok, bool prefill, bool want_logits) {
+// (forward_step_hidden decoder.rs:1754-1906 + logits_last 2087-2147).  With
+// want_logits the final LayerNorm, the logits and the per-block argmax keys
+// over the filtered logits (filt may be NULL: raw argmax) are produced too.
+// `timed` brackets the logits GEMV with events (never inside a graph capture).
+static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool prefill, bool want_logits,
+                                    const fwhip_filter *filt, bool timed) {
     fwhip_decoder *dd = st->dec;
     fwhip_ctx *c = dd->ctx;
     hipStream_t s = c->stream;
@@ -519,54 +559,69 @@ static fwhip_status dec_forward_row_tok(fwhip_dstate *st, const int32_t *tok, bo
     fw_launch_embed(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S);
     for (int li = 0; li < L; li++) {
         const DecLayerDev &l = dd->layers[li];
-        fw_launch_layernorm(s, st->x, st->h, l.attn_ln_w, l.attn_ln_b, d, S);
-        if (i8) fw_launch_gemv_i8(s, l.qkv8, l.qkv8s, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
-        else fw_launch_gemv_f16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
-        fw_launch_self_attn(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
-        if (i8) fw_launch_gemv_i8(s, l.o8, l.o8s, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
-        else fw_launch_gemv_f16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
-        fw_launch_layernorm(s, st->x, st->h, l.cross_ln_w, l.cross_ln_b, d, S);
-        if (i8) fw_launch_gemv_i8(s, l.cq8, l.cq8s, l.cq_b, st->h, st->y, d, d, S, d, 0, gt);
-        else fw_launch_gemv_f16(s, l.cq16, l.cq_b, st->h, st->y, d, d, S, d, 0, gt);
-        if (i8)
-            fw_launch_cross_attn_i8(s, st->y, st->ck8, st->ck8s, st->cvt8, st->cvt8s, st->att, d, T, H, L, li, S,
-                                    scale);
-        else fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
-        if (i8) fw_launch_gemv_i8(s, l.co8, l.co8s, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
-        else fw_launch_gemv_f16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
-        fw_launch_layernorm(s, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, d, S);
-        if (i8) fw_launch_gemv_i8(s, l.fc1_8, l.fc1_8s, l.fc1_b, st->h, st->ff, dff, d, S, dff, 2, gt);
-        else fw_launch_gemv_f16(s, l.fc1_16, l.fc1_b, st->h, st->ff, dff, d, S, dff, 2, gt);
-        if (i8 && !prefill) fw_launch_gemv_blk(s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, S, d, 1);
-        else fw_launch_gemv_f16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
-        fwhip_status cs = check_cancel(c);
-        if (cs != FWHIP_OK) return cs;
+        if (i8) {
+            fw_launch_ln_quant(s, st->x, nullptr, l.attn_ln_w, l.attn_ln_b, d, S, st->xq, st->xs);
+            gemv_i8_all(st, s, l.qkv8, l.qkv8s, l.qkv_b, st->qkv, 3 * d, d, 3 * d, 0, nullptr);
+            fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
+            fw_launch_quant_act_rows(s, st->att, S, d, st->xq, st->xs);
+            gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr);
+            fw_launch_ln_quant(s, st->x, nullptr, l.cross_ln_w, l.cross_ln_b, d, S, st->xq, st->xs);
+            gemv_i8_all(st, s, l.cq8, l.cq8s, l.cq_b, st->y, d, d, d, 0, nullptr);
+            fw_launch_cross_attn_i8v2(s, st->y, st->ck8, st->ck8s, st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li,
+                                      S, scale);
+            fw_launch_quant_act_rows(s, st->att, S, d, st->xq, st->xs);
+            gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr);
+            fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs);
+            gemv_i8_all(st, s, l.fc1_8, l.fc1_8s, l.fc1_b, st->ff, dff, d, dff, 2, nullptr);
+            // prefill rows take the f16 mlp_2 (the block-int8 arm has no batch form)
+            if (prefill) fw_launch_gemv_f16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
+            else gemv_blk_all(st, s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, d);
+        } else {
+            fw_launch_ln_quant(s, st->x, st->h, l.attn_ln_w, l.attn_ln_b, d, S, nullptr, nullptr);
+            fw_launch_gemv_f16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
+            fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
+            fw_launch_gemv_f16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
+            fw_launch_ln_quant(s, st->x, st->h, l.cross_ln_w, l.cross_ln_b, d, S, nullptr, nullptr);
+            fw_launch_gemv_f16(s, l.cq16, l.cq_b, st->h, st->y, d, d, S, d, 0, gt);
+            fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
+            fw_launch_gemv_f16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
+            fw_launch_ln_quant(s, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, d, S, nullptr, nullptr);
+            fw_launch_gemv_f16(s, l.fc1_16, l.fc1_b, st->h, st->ff, dff, d, S, dff, 2, gt);
+            fw_launch_gemv_f16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
+        }
     }
     if (want_logits) {
-        fw_launch_layernorm(s, st->x, st->h, dd->ln_w, dd->ln_b, d, S);
         fw_event_pair ev;
-        fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d * (i8 ? 1.0 : 2.0), &ev);
-        if (i8) fw_launch_gemv_i8(s, dd->emb8, dd->emb8s, nullptr, st->h, st->logits, dd->V, d, S, dd->V, 0, gt);
-        else fw_launch_gemv_f16(s, dd->emb16, nullptr, st->h, st->logits, dd->V, d, S, dd->V, 0, gt);
-        fw_timed_end(c, &ev);
+        ev.active = false;
+        if (i8) {
+            fw_launch_ln_quant(s, st->x, nullptr, dd->ln_w, dd->ln_b, d, S, st->xq, st->xs);
+            if (timed) fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d, &ev);
+            gemv_i8_all(st, s, dd->emb8, dd->emb8s, nullptr, st->logits, dd->V, d, dd->V, 3, filt);
+            if (timed) fw_timed_end(c, &ev);
+        } else {
+            fw_launch_ln_quant(s, st->x, st->h, dd->ln_w, dd->ln_b, d, S, nullptr, nullptr);
+            if (timed) fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d * 2.0, &ev);
+            fw_launch_gemv_f16(s, dd->emb16, nullptr, st->h, st->logits, dd->V, d, S, dd->V, 0, gt);
+            if (timed) fw_timed_end(c, &ev);
+            fw_launch_logits_keys(s, st->logits, dd->V, S, filt, st->initial, st->keys);
+        }
     }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("launch failed: ") + hipGetErrorString(e));
     return FWHIP_OK;
 }
 
 // Host values are staged with a synchronous copy ordered after the queued work,
 // so no host buffer is read after the call returns.
-static fwhip_status set_dev_int(fwhip_ctx *c, int *dst, int v) {
+static fwhip_status set_dev_ints(fwhip_ctx *c, int *dst, const int *v, int n) {
     HIP_TRY(hipStreamSynchronize(c->stream));
-    HIP_TRY(hipMemcpy(dst, &v, sizeof(int), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(dst, v, sizeof(int) * n, hipMemcpyHostToDevice));
     return FWHIP_OK;
 }
 
 // Run `tq` token rows ([S, tq] host tokens) through the decoder for every
 // stream: the token matrix is uploaded once (position-major) and each row reads
-// its column; the device position advances between rows.
-static fwhip_status stage_rows(fwhip_dstate *st, const int32_t *tokens, int tq, bool keep_len) {
+// its column; the device position starts at st->len and advances between rows.
+// The last row produces the logits and argmax keys.
+static fwhip_status stage_rows(fwhip_dstate *st, const int32_t *tokens, int tq, const fwhip_filter *filt) {
     fwhip_decoder *dd = st->dec;
     fwhip_ctx *c = dd->ctx;
     int S = st->S;
@@ -575,14 +630,21 @@ static fwhip_status stage_rows(fwhip_dstate *st, const int32_t *tokens, int tq, 
         for (int s = 0; s < S; s++) pm[(size_t)t * S + s] = tokens[(size_t)s * tq + t];
     HIP_TRY(hipStreamSynchronize(c->stream));
     HIP_TRY(hipMemcpy(st->rows, pm.data(), sizeof(int32_t) * pm.size(), hipMemcpyHostToDevice));
-    fwhip_status r = set_dev_int(c, st->pos, st->len);
+    int p0 = st->len;
+    fwhip_status r = set_dev_ints(c, st->pos, &p0, 1);
     if (r != FWHIP_OK) return r;
     for (int t = 0; t < tq; t++) {
-        r = dec_forward_row_tok(st, st->rows + (size_t)t * S, tq > 1, t == tq - 1);
+        r = dec_forward_row(st, st->rows + (size_t)t * S, tq > 1, t == tq - 1, filt, true);
         if (r != FWHIP_OK) return r;
         if (t + 1 < tq) fw_launch_step_bookkeeping(c->stream, st->pos, nullptr, st->rows, nullptr, 0, 0, S);
+        r = check_cancel(c);
+        if (r != FWHIP_OK) {
+            hipStreamSynchronize(c->stream);
+            return r;
+        }
     }
-    (void)keep_len;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("launch failed: ") + hipGetErrorString(e));
     return FWHIP_OK;
 }
 
@@ -600,26 +662,78 @@ extern "C" fwhip_status fwhip_decoder_step(fwhip_dstate *st, const int32_t *toke
     if (st->len + tq > dd->nctx)
         return fw_fail(FWHIP_ERR_INVALID, "decode position " + std::to_string(st->len + tq - 1) +
                                               " >= n_text_ctx " + std::to_string(dd->nctx));
-    fwhip_status r = stage_rows(st, tokens, tq, false);
+    int init = initial ? 1 : 0;
+    fwhip_status r = set_dev_ints(c, st->initial, &init, 1);
+    if (r != FWHIP_OK) return r;
+    r = stage_rows(st, tokens, tq, filter);
     if (r != FWHIP_OK) return r;
     st->len += tq;
     if (logits_dev)
         HIP_TRY(hipMemcpyAsync(logits_dev, st->logits, sizeof(float) * (size_t)S * dd->V, hipMemcpyDeviceToDevice,
                                c->stream));
     if (argmax_host) {
-        fwhip_status r = set_dev_int(c, st->initial, initial ? 1 : 0);
-        if (r != FWHIP_OK) return r;
-        fw_launch_argmax(c->stream, st->logits, dd->V, filter, st->initial, st->amax, S);
-        HIP_TRY(hipMemcpyAsync(argmax_host, st->amax, sizeof(int32_t) * S, hipMemcpyDeviceToHost, c->stream));
+        fw_launch_argmax_finish(c->stream, st->keys, st->nkeys, S, st->tok, nullptr, 0, st->pos, nullptr, nullptr, 0);
+        HIP_TRY(hipMemcpyAsync(argmax_host, st->tok, sizeof(int32_t) * S, hipMemcpyDeviceToHost, c->stream));
     }
     HIP_TRY(hipStreamSynchronize(c->stream));
     HIP_TRY(hipGetLastError());
     return FWHIP_OK;
 }
 
+// The sampling step after the first: forward of the sampled tokens st->tok,
+// logits + argmax keys, then argmax + bookkeeping on the device.
+static fwhip_status greedy_step(fwhip_dstate *st, const fwhip_filter *filt, bool timed) {
+    fwhip_status r = dec_forward_row(st, st->tok, false, true, filt, timed);
+    if (r != FWHIP_OK) return r;
+    fw_launch_argmax_finish(st->dec->ctx->stream, st->keys, st->nkeys, st->S, st->tok, st->hist, st->hist_cap, st->pos,
+                            st->initial, st->stepc, 1);
+    return FWHIP_OK;
+}
+
+// Capture greedy_step into a HIP graph (its kernels read the position, the
+// sampled tokens and the step counter from device memory, so one capture
+// replays for every step of this state).  Returns false when capture is
+// unavailable; the loop then launches the same kernels directly.
+static bool capture_step_impl(fwhip_dstate *st, const fwhip_filter *filt);
+static bool capture_step(fwhip_dstate *st, const fwhip_filter *filt) {
+    static int disabled = -1, debug = -1;
+    if (disabled < 0) disabled = getenv("FWHIP_NO_GRAPH") != nullptr;
+    if (debug < 0) debug = getenv("FWHIP_DEBUG") != nullptr;
+    if (disabled) return false;
+    bool ok = capture_step_impl(st, filt);
+    if (debug) fprintf(stderr, "fwhip: greedy step graph %s\n", ok ? "captured" : "unavailable (direct launches)");
+    return ok;
+}
+static bool capture_step_impl(fwhip_dstate *st, const fwhip_filter *filt) {
+    if (st->graph && !memcmp(&st->graph_filter, filt, sizeof *filt)) return true;
+    if (st->graph) {
+        hipGraphExecDestroy(st->graph);
+        st->graph = nullptr;
+    }
+    hipStream_t s = st->dec->ctx->stream;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return false;
+    greedy_step(st, filt, false);
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture(s, &g) != hipSuccess || !g) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    st->graph = ge;
+    st->graph_filter = *filt;
+    return true;
+}
+
 // Greedy no-timestamps loop (decode.rs:3429-3566): prefill the prompt, then
-// argmax -> step.  Sampled tokens accumulate on the device; the host polls for
-// end-of-text every few steps, so steps stream without a per-token sync.
+// argmax -> step.  Sampled tokens, the position and the step count live on the
+// device; each step after the first replays one captured graph; the host polls
+// for end-of-text every few steps, so steps stream without a per-token sync.
 extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *prompt, int32_t n_prompt,
                                             int32_t n_max, const fwhip_filter *filter, int32_t *out_tokens,
                                             int32_t *out_len) {
@@ -632,28 +746,38 @@ extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *pro
     if (n_prompt <= 0 || n_max <= 0) return fw_fail(FWHIP_ERR_INVALID, "empty prompt or n_max <= 0");
     if (st->len + n_prompt + n_max - 1 > dd->nctx)
         return fw_fail(FWHIP_ERR_INVALID, "prompt + n_max exceeds n_text_ctx");
+    if (n_max > st->hist_cap) return fw_fail(FWHIP_ERR_INVALID, "n_max exceeds n_text_ctx");
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= dd->V) return fw_fail(FWHIP_ERR_INVALID, "prompt token out of range");
     std::vector<int32_t> rows((size_t)S * n_prompt);
     for (int s = 0; s < S; s++)
         for (int t = 0; t < n_prompt; t++) rows[(size_t)s * n_prompt + t] = prompt[t];
-    fwhip_status r = stage_rows(st, rows.data(), n_prompt, true);
+    const int init[2] = {1, 0}; // initial = 1, step counter = 0
+    fwhip_status r = set_dev_ints(c, st->initial, init, 2);
     if (r != FWHIP_OK) return r;
-    r = set_dev_int(c, st->initial, 1);
+    r = stage_rows(st, rows.data(), n_prompt, filter);
     if (r != FWHIP_OK) return r;
+    // first sampled token: from the prefill's logits
+    fw_launch_argmax_finish(c->stream, st->keys, st->nkeys, S, st->tok, st->hist, st->hist_cap, st->pos, st->initial,
+                            st->stepc, 1);
     std::vector<int32_t> hist((size_t)S * n_max, -1);
-    int steps = 0;
+    int steps = 1;
     const int poll = 8;
-    for (int i = 0; i < n_max; i++) {
-        if (i > 0) {
-            r = dec_forward_row_tok(st, st->tok, false, true);
+    bool use_graph = n_max > 1 && capture_step(st, filter);
+    for (int i = 1; i < n_max; i++) {
+        r = check_cancel(c);
+        if (r != FWHIP_OK) {
+            hipStreamSynchronize(c->stream);
+            st->len += n_prompt + steps - 1;
+            return r;
+        }
+        if (use_graph) HIP_TRY(hipGraphLaunch(st->graph, c->stream));
+        else {
+            r = greedy_step(st, filter, false);
             if (r != FWHIP_OK) return r;
         }
-        fw_launch_argmax(c->stream, st->logits, dd->V, filter, st->initial, st->tok, S);
-        fw_launch_step_bookkeeping(c->stream, st->pos, st->initial, st->tok, st->hist, st->hist_cap, i, S);
         steps = i + 1;
-        if (steps == n_max) break;
-        if (steps % poll == 0) {
+        if (steps % poll == 0 && steps < n_max) {
             HIP_TRY(hipMemcpy2DAsync(hist.data(), sizeof(int32_t) * n_max, st->hist, sizeof(int32_t) * st->hist_cap,
                                      sizeof(int32_t) * steps, S, hipMemcpyDeviceToHost, c->stream));
             HIP_TRY(hipStreamSynchronize(c->stream));
