@@ -7,6 +7,8 @@
 // MFMA operand layouts (gfx950): A lane l -> row l%32, k block (l/32)*8
 // halves; B lane l -> col l%32, same k block; accumulator r of lane l -> row
 // (r/4)*8 + (l/32)*4 + r%4, col l%32.
+#include <cstdlib>
+
 #include "fw_enc.h"
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
@@ -25,67 +27,91 @@ __device__ __forceinline__ void fw_split(float v, uint16_t &hi, uint16_t &lo) {
 // LayerNorm per row (nn.rs:4455-4545, f64 statistics) with the output the next
 // GEMM consumes: mode F32 (ln_post), SPLIT (f16 hi/lo pair for the f32 path),
 // I7 (quantize_act_i7, nn.rs:1443-1466: per-row amax/127, add-trunc body /
-// exact tail, stored as the signed value q = u8 - 128).
-#define FW_LN_MAXV 8
-__global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, const float *b, int d, int mode,
-                                                float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs) {
-    __shared__ double shd[4];
-    __shared__ float shf[4];
-    size_t r = blockIdx.x;
-    const float *xr = x + r * d;
-    float xv[FW_LN_MAXV];
+// exact tail, stored as the signed value q = u8 - 128).  One wave per row (4
+// rows per block), the row held in registers as float4s (d <= 2048, d % 4 ==
+// 0); every load is unconditional (clamped index).
+#define ELN_V4 8
+__device__ __forceinline__ double eln_wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, const float *b, int rows, int d,
+                                                int mode, float *yf, uint16_t *hi, uint16_t *lo, int8_t *q,
+                                                float *qs) {
+    const int lane = threadIdx.x & 63;
+    const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= (size_t)rows) return;
+    const int n4 = d >> 2; // float4 per row; lane owns float4 slots lane + 64k
+    const float4 *xr = (const float4 *)(x + r * d);
+    float4 xv[ELN_V4];
+    bool ok[ELN_V4];
+#pragma unroll
+    for (int k = 0; k < ELN_V4; k++) {
+        const int c4 = lane + 64 * k;
+        ok[k] = c4 < n4;
+        xv[k] = xr[ok[k] ? c4 : 0];
+    }
     double s = 0.0;
 #pragma unroll
-    for (int k = 0; k < FW_LN_MAXV; k++) {
-        int i = threadIdx.x + k * 256;
-        xv[k] = i < d ? xr[i] : 0.0f;
-        if (i < d) s += (double)xv[k];
-    }
-    double mean = fw_block_sum(s, shd) / (double)d;
+    for (int k = 0; k < ELN_V4; k++)
+        if (ok[k]) s += ((double)xv[k].x + (double)xv[k].y) + ((double)xv[k].z + (double)xv[k].w);
+    const double mean = eln_wave_sum(s) / (double)d;
     double v = 0.0;
 #pragma unroll
-    for (int k = 0; k < FW_LN_MAXV; k++) {
-        int i = threadIdx.x + k * 256;
-        if (i < d) {
-            double t = (double)xv[k] - mean;
-            v += t * t;
+    for (int k = 0; k < ELN_V4; k++)
+        if (ok[k]) {
+            double t0 = (double)xv[k].x - mean, t1 = (double)xv[k].y - mean;
+            double t2 = (double)xv[k].z - mean, t3 = (double)xv[k].w - mean;
+            v += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
         }
-    }
-    double var = fw_block_sum(v, shd) / (double)d;
-    double inv = 1.0 / sqrt(var + (double)1e-5f);
-    float yv[FW_LN_MAXV];
+    const double var = eln_wave_sum(v) / (double)d;
+    const double inv = 1.0 / sqrt(var + (double)1e-5f);
+    const float4 *wr = (const float4 *)w, *br = (const float4 *)b;
+    float yv[ELN_V4][4];
     float amax = 0.0f;
 #pragma unroll
-    for (int k = 0; k < FW_LN_MAXV; k++) {
-        int i = threadIdx.x + k * 256;
-        if (i < d) {
-            double nrm = ((double)xv[k] - mean) * inv;
-            yv[k] = (float)(nrm * (double)w[i] + (double)b[i]);
-            amax = fmaxf(amax, fabsf(yv[k]));
+    for (int k = 0; k < ELN_V4; k++) {
+        const int c4 = ok[k] ? lane + 64 * k : 0;
+        const float4 ww = wr[c4], bb = br[c4];
+        const float xs[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+        const float wv[4] = {ww.x, ww.y, ww.z, ww.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            double nrm = ((double)xs[e] - mean) * inv;
+            yv[k][e] = (float)(nrm * (double)wv[e] + (double)bv[e]);
+            if (ok[k]) amax = fmaxf(amax, fabsf(yv[k][e]));
         }
     }
     if (mode == FW_LN_F32) {
 #pragma unroll
-        for (int k = 0; k < FW_LN_MAXV; k++) {
-            int i = threadIdx.x + k * 256;
-            if (i < d) yf[r * d + i] = yv[k];
-        }
+        for (int k = 0; k < ELN_V4; k++)
+            if (ok[k]) ((float4 *)(yf + r * d))[lane + 64 * k] = make_float4(yv[k][0], yv[k][1], yv[k][2], yv[k][3]);
     } else if (mode == FW_LN_SPLIT) {
 #pragma unroll
-        for (int k = 0; k < FW_LN_MAXV; k++) {
-            int i = threadIdx.x + k * 256;
-            if (i < d) fw_split(yv[k], hi[r * d + i], lo[r * d + i]);
-        }
-    } else {
-        amax = fw_block_max(amax, shf);
-        float sc = fmaxf(amax, 1e-9f) / 127.0f;
-        float iv = 1.0f / sc;
+        for (int k = 0; k < ELN_V4; k++)
+            if (ok[k]) {
+                uint16_t h[4], l[4];
 #pragma unroll
-        for (int k = 0; k < FW_LN_MAXV; k++) {
-            int i = threadIdx.x + k * 256;
-            if (i < d) q[r * d + i] = fw_q8_avx(yv[k], iv, i, d);
-        }
-        if (threadIdx.x == 0) qs[r] = sc;
+                for (int e = 0; e < 4; e++) fw_split(yv[k][e], h[e], l[e]);
+                ((uint2 *)(hi + r * d))[lane + 64 * k] =
+                    make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+                ((uint2 *)(lo + r * d))[lane + 64 * k] =
+                    make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+            }
+    } else {
+        amax = fw_wave_max(amax);
+        const float sc = fmaxf(amax, 1e-9f) / 127.0f;
+        const float iv = 1.0f / sc;
+#pragma unroll
+        for (int k = 0; k < ELN_V4; k++)
+            if (ok[k]) {
+                const int i = (lane + 64 * k) * 4;
+                uint32_t b0 = (uint8_t)fw_q8_avx(yv[k][0], iv, i, d), b1 = (uint8_t)fw_q8_avx(yv[k][1], iv, i + 1, d);
+                uint32_t b2 = (uint8_t)fw_q8_avx(yv[k][2], iv, i + 2, d), b3 = (uint8_t)fw_q8_avx(yv[k][3], iv, i + 3, d);
+                ((uint32_t *)(q + r * d))[lane + 64 * k] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
+        if (lane == 0) qs[r] = sc;
     }
 }
 
@@ -107,56 +133,60 @@ __global__ void __launch_bounds__(256) k_quant_exact_rows(const float *x, int n,
 
 // quantize_act_i7_gelu (nn.rs:1791-1823): GELU (skipped when gelu_tab is
 // NULL: quantize_act_i7, nn.rs:1443-1466), per-row amax/127, add-trunc body /
-// exact tail, signed storage.  Rows of up to 6144 values are read once and
-// held in registers (float4 per thread per slot); longer rows take two passes.
-#define FW_QROW_V4 6
-__global__ void __launch_bounds__(256) k_gelu_quant_i7_rows(const float *x, int n, const float *gelu_tab, int8_t *q,
-                                                            float *qs) {
-    __shared__ float shf[4];
-    size_t r = blockIdx.x;
+// exact tail, signed storage.  One wave per row (4 rows per block); rows of up
+// to 64 * 4 * GQ_V4 values (n % 4 == 0) are read once into registers with
+// unconditional loads, longer rows take two passes.
+#define GQ_V4 24
+__global__ void __launch_bounds__(256) k_gelu_quant_i7_rows(const float *x, int rows, int n, const float *gelu_tab,
+                                                            int8_t *q, float *qs) {
+    const int lane = threadIdx.x & 63;
+    const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= (size_t)rows) return;
     const float *xr = x + r * n;
-    if ((n & 3) == 0 && n <= 4 * 256 * FW_QROW_V4) {
-        float4 v[FW_QROW_V4];
+    const int n4 = n >> 2;
+    if ((n & 3) == 0 && n4 <= 64 * GQ_V4) {
+        float4 v[GQ_V4];
+#pragma unroll
+        for (int k = 0; k < GQ_V4; k++) {
+            const int c4 = lane + 64 * k;
+            v[k] = ((const float4 *)xr)[c4 < n4 ? c4 : 0];
+        }
         float m = 0.0f;
 #pragma unroll
-        for (int k = 0; k < FW_QROW_V4; k++) {
-            int i4 = threadIdx.x + k * 256;
-            if (i4 * 4 < n) {
-                float4 t = ((const float4 *)xr)[i4];
+        for (int k = 0; k < GQ_V4; k++) {
+            if (lane + 64 * k < n4) {
                 if (gelu_tab) {
-                    t.x = fw_gelu(t.x, gelu_tab);
-                    t.y = fw_gelu(t.y, gelu_tab);
-                    t.z = fw_gelu(t.z, gelu_tab);
-                    t.w = fw_gelu(t.w, gelu_tab);
+                    v[k].x = fw_gelu(v[k].x, gelu_tab);
+                    v[k].y = fw_gelu(v[k].y, gelu_tab);
+                    v[k].z = fw_gelu(v[k].z, gelu_tab);
+                    v[k].w = fw_gelu(v[k].w, gelu_tab);
                 }
-                v[k] = t;
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
             }
         }
-        m = fw_block_max(m, shf);
-        float sc = fmaxf(m, 1e-9f) / 127.0f;
-        float inv = 1.0f / sc;
+        m = fw_wave_max(m);
+        const float sc = fmaxf(m, 1e-9f) / 127.0f;
+        const float inv = 1.0f / sc;
 #pragma unroll
-        for (int k = 0; k < FW_QROW_V4; k++) {
-            int i4 = threadIdx.x + k * 256;
-            if (i4 * 4 < n) {
-                int i = i4 * 4;
+        for (int k = 0; k < GQ_V4; k++) {
+            const int c4 = lane + 64 * k;
+            if (c4 < n4) {
+                const int i = c4 * 4;
                 uint32_t b0 = (uint8_t)fw_q8_avx(v[k].x, inv, i, n), b1 = (uint8_t)fw_q8_avx(v[k].y, inv, i + 1, n);
                 uint32_t b2 = (uint8_t)fw_q8_avx(v[k].z, inv, i + 2, n), b3 = (uint8_t)fw_q8_avx(v[k].w, inv, i + 3, n);
-                *(uint32_t *)(q + r * n + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                ((uint32_t *)(q + r * n))[c4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
             }
         }
-        if (threadIdx.x == 0) qs[r] = sc;
+        if (lane == 0) qs[r] = sc;
         return;
     }
     float m = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(gelu_tab ? fw_gelu(xr[i], gelu_tab) : xr[i]));
-    m = fw_block_max(m, shf);
-    float sc = fmaxf(m, 1e-9f) / 127.0f;
-    float inv = 1.0f / sc;
-    for (int i = threadIdx.x; i < n; i += 256)
-        q[r * n + i] = fw_q8_avx(gelu_tab ? fw_gelu(xr[i], gelu_tab) : xr[i], inv, i, n);
-    if (threadIdx.x == 0) qs[r] = sc;
+    for (int i = lane; i < n; i += 64) m = fmaxf(m, fabsf(gelu_tab ? fw_gelu(xr[i], gelu_tab) : xr[i]));
+    m = fw_wave_max(m);
+    const float sc = fmaxf(m, 1e-9f) / 127.0f;
+    const float inv = 1.0f / sc;
+    for (int i = lane; i < n; i += 64) q[r * n + i] = fw_q8_avx(gelu_tab ? fw_gelu(xr[i], gelu_tab) : xr[i], inv, i, n);
+    if (lane == 0) qs[r] = sc;
 }
 
 // im2col for conv1d (kernel 3, pad 1; conv1d_wt nn.rs:5006-5103) into the f16
@@ -350,6 +380,207 @@ __global__ void __launch_bounds__(256) k_attention(const uint16_t *qh, const uin
 }
 
 // ---------------------------------------------------------------------------
+// Pipelined attention: the same arithmetic as k_attention (S^T = K Q^T on f16
+// pairs, online softmax over 64-key tiles, O^T += V^T P^T), with 8 waves (256
+// queries) per block sharing each K/V tile, and the tiles (K hi/lo, V^T hi/lo:
+// 4 x 8 KB) fed global -> LDS directly through an AT_NS-stage ring, one
+// barrier per tile.  Rows are 128 bytes; 16-byte chunk c of row r sits at
+// chunk c ^ (r & 7), which keeps the fragment reads free of bank conflicts.
+#define AT_NS 3
+#define AT_QW 8
+#define AT_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+#define AT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+__global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
+                                                           const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl,
+                                                           int T, int Tp, int H, int d, int out_mode, float *of,
+                                                           uint16_t *oh, uint16_t *ol) {
+    __shared__ __align__(1024) uint16_t sm[AT_NS][4][64 * 64]; // [stage][K hi, K lo, V^T hi, V^T lo][row][64]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const size_t bh = (size_t)b * H + h;
+    const int q0 = blockIdx.x * 32 * AT_QW + wave * 32;
+    const int myq = q0 + (lane & 31);
+    const int nt = (T + 63) >> 6;
+    // this lane's Q^T fragments: q = myq, dims ks*16 + (l/32)*8 .. +8
+    v8h qfh[4], qfl[4];
+    {
+        const int qc = myq < T ? myq : T - 1;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int dd = ks * 16 + (lane >> 5) * 8;
+            v8h a = *(const v8h *)(qh + (bh * T + qc) * 64 + dd), c = *(const v8h *)(ql + (bh * T + qc) * 64 + dd);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                qfh[ks][e] = myq < T ? a[e] : (_Float16)0.0f;
+                qfl[ks][e] = myq < T ? c[e] : (_Float16)0.0f;
+            }
+        }
+    }
+    // loader: 32 instructions of 1 KB per tile, AT_QW waves share them
+    constexpr int LPW = 32 / AT_QW;
+    const uint16_t *src[LPW];
+    int dsto[LPW];
+#pragma unroll
+    for (int qq = 0; qq < LPW; qq++) {
+        const int ii = wave * LPW + qq, arr = ii >> 3, r = ((ii & 7) << 3) + (lane >> 3);
+        const int c = (lane & 7) ^ (r & 7);
+        dsto[qq] = arr * 64 * 64 + ((ii & 7) << 3) * 64; // halves, wave-uniform
+        if (arr < 2) src[qq] = (arr ? kl : kh) + (bh * T) * 64 + (size_t)r * 64 + c * 8;  // + key0*64 per tile
+        else src[qq] = (arr == 3 ? vtl : vth) + (bh * 64 + r) * (size_t)Tp + c * 8;       // + key0 per tile
+    }
+    auto issue = [&](int it) {
+        const int itc = it < nt ? it : nt - 1;
+        const int k0 = itc * 64;
+        uint16_t *base = &sm[it % AT_NS][0][0];
+#pragma unroll
+        for (int qq = 0; qq < LPW; qq++) {
+            const int ii = wave * LPW + qq, arr = ii >> 3;
+            const uint16_t *g;
+            if (arr < 2) {
+                // key rows past T reload row T-1 (masked in the softmax)
+                const int r = ((ii & 7) << 3) + (lane >> 3);
+                const int kr = k0 + r < T ? k0 : T - 1 - r;
+                g = src[qq] + (size_t)kr * 64;
+            } else {
+                g = src[qq] + k0; // V^T rows are zero padded to Tp >= 64 * nt
+            }
+            __builtin_amdgcn_global_load_lds((const void *)g,
+                                             (void __attribute__((address_space(3))) *)(base + dsto[qq]), 16, 0, 0);
+        }
+    };
+    v16f o[2], oy[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            o[j][r] = 0.0f;
+            oy[j][r] = 0.0f;
+        }
+    float m = -INFINITY, l = 0.0f;
+    const float sl2 = 0.125f * 1.4426950408889634f;
+#pragma unroll
+    for (int p = 0; p < AT_NS - 1; p++) issue(p);
+    for (int it = 0; it < nt; it++) {
+        AT_WAIT_VM_LGKM0(LPW * (AT_NS - 2)); // this wave's loads of tile `it` have landed
+        asm volatile("s_barrier" ::: "memory");
+        issue(it + AT_NS - 1);
+        const uint16_t *sK = &sm[it % AT_NS][0][0];
+        const int k0 = it * 64;
+        // four independent accumulator chains (hh+hl and lh for each 32-key
+        // half) interleaved so consecutive MFMAs never depend on each other
+        v16f st[2], sy[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                st[t][r] = 0.0f;
+                sy[t][r] = 0.0f;
+            }
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            v8h ah[2], al[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int kr = t * 32 + (lane & 31), c = ks * 2 + (lane >> 5);
+                const int off = kr * 64 + ((c ^ (kr & 7)) << 3);
+                ah[t] = *(const v8h *)(sK + off);
+                al[t] = *(const v8h *)(sK + 64 * 64 + off);
+            }
+            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], qfh[ks], st[0], 0, 0, 0);
+            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], qfh[ks], st[1], 0, 0, 0);
+            sy[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0], qfh[ks], sy[0], 0, 0, 0);
+            sy[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1], qfh[ks], sy[1], 0, 0, 0);
+            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], qfl[ks], st[0], 0, 0, 0);
+            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], qfl[ks], st[1], 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) st[t][r] += sy[t][r];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = k0 + t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                const float sv = key < T ? st[t][r] : -INFINITY;
+                st[t][r] = sv;
+                tmax = fmaxf(tmax, sv);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(m, tmax);
+        const float alpha = __builtin_amdgcn_exp2f((m - mnew) * sl2);
+        float psum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float pv = __builtin_amdgcn_exp2f((st[t][r] - mnew) * sl2);
+                st[t][r] = pv;
+                psum += pv;
+            }
+        psum += __shfl_xor(psum, 32, 64);
+        l = l * alpha + psum;
+        m = mnew;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                o[j][r] *= alpha;
+                oy[j][r] *= alpha;
+            }
+        const uint16_t *sV = &sm[it % AT_NS][2][0];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                v8h ph, pl;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float pv = st[t][8 * u + e];
+                    const _Float16 hh = (_Float16)pv;
+                    ph[e] = hh;
+                    pl[e] = (_Float16)(pv - (float)hh);
+                }
+                const int c1 = t * 4 + u * 2, ko = (lane >> 5) * 4;
+                v8h vh[2], vl[2];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int dim = j * 32 + (lane & 31), sw = dim & 7;
+                    const int a0 = dim * 64 + ((c1 ^ sw) << 3) + ko, a1 = dim * 64 + (((c1 + 1) ^ sw) << 3) + ko;
+                    const uint2 x0 = *(const uint2 *)(sV + a0), x1 = *(const uint2 *)(sV + a1);
+                    const uint2 y0 = *(const uint2 *)(sV + 64 * 64 + a0), y1 = *(const uint2 *)(sV + 64 * 64 + a1);
+                    vh[j] = __builtin_bit_cast(v8h, make_uint4(x0.x, x0.y, x1.x, x1.y));
+                    vl[j] = __builtin_bit_cast(v8h, make_uint4(y0.x, y0.y, y1.x, y1.y));
+                }
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[0], ph, o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[1], ph, o[1], 0, 0, 0);
+                oy[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[0], ph, oy[0], 0, 0, 0);
+                oy[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[1], ph, oy[1], 0, 0, 0);
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[0], pl, o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[1], pl, o[1], 0, 0, 0);
+            }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[j][r] += oy[j][r];
+    AT_WAIT_VM(0); // dummy tiles landed before the block exits
+    if (myq >= T) return;
+    const float inv = 1.0f / l;
+    const size_t orow = ((size_t)b * T + myq) * d + (size_t)h * 64;
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int dim = j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            const float v = o[j][r] * inv;
+            if (out_mode == 0) of[orow + dim] = v;
+            else fw_split(v, oh[orow + dim], ol[orow + dim]);
+        }
+}
+
+// ---------------------------------------------------------------------------
 // Exact mode: the reference's strict-parity arithmetic for the f32 parts of the
 // encoder, for bit-exact parity checks (not the performance path).
 
@@ -439,14 +670,14 @@ void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qof
 // ---------------------------------------------------------------------------
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
                       float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs) {
-    hipLaunchKernelGGL(k_enc_ln, dim3(rows), dim3(256), 0, st, x, w, b, d, mode, yf, hi, lo, q, qs);
+    hipLaunchKernelGGL(k_enc_ln, dim3((rows + 3) / 4), dim3(256), 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs);
 }
 void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs) {
     hipLaunchKernelGGL(k_quant_exact_rows, dim3(rows), dim3(256), 0, st, x, n, q, qs);
 }
 void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int n, const float *tab, int8_t *q,
                                   float *qs) {
-    hipLaunchKernelGGL(k_gelu_quant_i7_rows, dim3(rows), dim3(256), 0, st, x, n, tab, q, qs);
+    hipLaunchKernelGGL(k_gelu_quant_i7_rows, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, tab, q, qs);
 }
 void fw_launch_im2col(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, int Kp,
                       uint16_t *hi, uint16_t *lo) {
@@ -466,7 +697,15 @@ void fw_launch_fill_u16(hipStream_t st, uint16_t *p, size_t n, uint16_t v) {
 void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                          const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
                          int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol) {
-    dim3 grid((T + 127) / 128, H, B);
-    hipLaunchKernelGGL(k_attention, grid, dim3(256), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d, out_mode, of, oh,
-                       ol);
+    static int old = -1;
+    if (old < 0) old = getenv("FWHIP_ATTN_V1") != nullptr;
+    if (old) {
+        dim3 grid((T + 127) / 128, H, B);
+        hipLaunchKernelGGL(k_attention, grid, dim3(256), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d, out_mode, of, oh,
+                           ol);
+        return;
+    }
+    dim3 grid((T + 32 * AT_QW - 1) / (32 * AT_QW), H, B);
+    hipLaunchKernelGGL(k_attention2, grid, dim3(64 * AT_QW), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d, out_mode, of,
+                       oh, ol);
 }

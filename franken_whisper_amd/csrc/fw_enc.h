@@ -32,6 +32,7 @@ struct FwGemm {
     const float *pos;
     const float *gelu_tab;
     int T, H, Tp;
+    int map; // tile order (set by fw_launch_gemm)
 };
 
 void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g);
