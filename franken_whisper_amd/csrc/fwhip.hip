@@ -289,7 +289,11 @@ static bool hp_decoder_ok(const fwhip_hparams &hp, std::string &why) {
         why = "d_head must be 64";
         return false;
     }
-
+    // The row LayerNorm/quantize kernels keep one row per wave in registers.
+    if (hp.n_text_state > 2048) {
+        why = "n_text_state must be at most 2048";
+        return false;
+    }
     return true;
 }
 
