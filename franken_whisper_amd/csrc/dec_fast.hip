@@ -18,6 +18,8 @@
 //    filtered logits (process_logits no-timestamps masks, decode.rs:702-867;
 //    first-index strict '>' argmax, decode.rs:1708-1780); a one-block kernel
 //    finishes the argmax and the greedy bookkeeping on the device.
+#include <cstdlib>
+
 #include "fw_kernels.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -27,96 +29,112 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // f32) of one stream row per wave, then the decoder activation quantizer of
 // the normalized row (per-row amax/127, add-trunc body, exact n%8 tail) into
 // the int8 activation buffer.  y may be NULL (int8-only consumers), xq may be
-// NULL (f32-only consumers).  Rows up to 2048 values; 4 rows per block.
-#define DEC_LN_V 32
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+// NULL (f32-only consumers).  4 rows per block; lane l holds the float4
+// groups l, l+64, ... (NV of them, d <= 256*NV, d % 4 == 0).  Every load of
+// x, w and b is issued before the first use, so the row costs one memory
+// round trip; the reductions run on DPP lane moves.
+template <int NV>
 __global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, const float *w, const float *b, int d,
                                                   int rows, int8_t *xq, float *xs) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
-    const float *xr = x + (size_t)r * d;
-    float xv[DEC_LN_V];
-    double s = 0.0;
-    // unconditional loads from clamped addresses: a guarded load becomes a
-    // branch with its own wait, serializing the row's memory latency
+    const int n4 = d >> 2;
+    const float4 *xr = (const float4 *)(x + (size_t)r * d);
+    const float4 *w4 = (const float4 *)w, *b4 = (const float4 *)b;
+    float4 xv[NV], wv[NV], bv[NV];
+    bool ok[NV];
 #pragma unroll
-    for (int k = 0; k < DEC_LN_V; k++) {
-        int i = lane + k * 64;
-        float t = xr[i < d ? i : 0];
-        xv[k] = i < d ? t : 0.0f;
+    for (int k = 0; k < NV; k++) {
+        const int i = lane + k * 64;
+        ok[k] = i < n4;
+        const int c = ok[k] ? i : 0;
+        xv[k] = xr[c];
+        wv[k] = w4[c];
+        bv[k] = b4[c];
     }
+    double s = 0.0;
 #pragma unroll
-    for (int k = 0; k < DEC_LN_V; k++)
-        if (lane + k * 64 < d) s += (double)xv[k];
-    const double mean = wave_sum_f64(s) / (double)d;
+    for (int k = 0; k < NV; k++)
+        if (ok[k]) s += ((double)xv[k].x + (double)xv[k].y) + ((double)xv[k].z + (double)xv[k].w);
+    const double mean = fw_dpp_wave_sum_f64(s) / (double)d;
     double v = 0.0;
 #pragma unroll
-    for (int k = 0; k < DEC_LN_V; k++) {
-        int i = lane + k * 64;
-        if (i < d) {
-            double t = (double)xv[k] - mean;
-            v += t * t;
+    for (int k = 0; k < NV; k++) {
+        if (ok[k]) {
+            const double a = (double)xv[k].x - mean, bb = (double)xv[k].y - mean;
+            const double c = (double)xv[k].z - mean, e = (double)xv[k].w - mean;
+            v += (a * a + bb * bb) + (c * c + e * e);
         }
     }
-    const double var = wave_sum_f64(v) / (double)d;
+    const double var = fw_dpp_wave_sum_f64(v) / (double)d;
     const double inv = 1.0 / sqrt(var + (double)1e-5f);
     float m = 0.0f;
-    float wv[DEC_LN_V], bv[DEC_LN_V];
 #pragma unroll
-    for (int k = 0; k < DEC_LN_V; k++) {
-        int i = lane + k * 64;
-        wv[k] = w[i < d ? i : 0];
-        bv[k] = b[i < d ? i : 0];
-    }
-#pragma unroll
-    for (int k = 0; k < DEC_LN_V; k++) {
-        int i = lane + k * 64;
-        if (i < d) {
-            double nrm = ((double)xv[k] - mean) * inv;
-            xv[k] = (float)(nrm * (double)wv[k] + (double)bv[k]);
-            m = fmaxf(m, fabsf(xv[k]));
-            if (y) y[(size_t)r * d + i] = xv[k];
+    for (int k = 0; k < NV; k++) {
+        float4 o;
+        o.x = (float)((((double)xv[k].x - mean) * inv) * (double)wv[k].x + (double)bv[k].x);
+        o.y = (float)((((double)xv[k].y - mean) * inv) * (double)wv[k].y + (double)bv[k].y);
+        o.z = (float)((((double)xv[k].z - mean) * inv) * (double)wv[k].z + (double)bv[k].z);
+        o.w = (float)((((double)xv[k].w - mean) * inv) * (double)wv[k].w + (double)bv[k].w);
+        xv[k] = o;
+        if (ok[k]) {
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+            if (y) ((float4 *)(y + (size_t)r * d))[lane + k * 64] = o;
         }
     }
     if (!xq) return;
-    m = fw_wave_max(m);
+    m = fw_dpp_wave_max(m);
     const float sc = fmaxf(m, 1e-9f) / 127.0f;
     const float iv = 1.0f / sc;
 #pragma unroll
-    for (int k = 0; k < DEC_LN_V; k++) {
-        int i = lane + k * 64;
-        if (i < d) xq[(size_t)r * d + i] = fw_q8_avx(xv[k], iv, i, d);
+    for (int k = 0; k < NV; k++) {
+        if (ok[k]) {
+            const int i = (lane + k * 64) * 4;
+            const uint32_t q = (uint32_t)(uint8_t)fw_q8_avx(xv[k].x, iv, i, d) |
+                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].y, iv, i + 1, d) << 8) |
+                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].z, iv, i + 2, d) << 16) |
+                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].w, iv, i + 3, d) << 24);
+            *(uint32_t *)(xq + (size_t)r * d + i) = q;
+        }
     }
     if (lane == 0) xs[r] = sc;
 }
 
-// quantize_act_i8_into of f32 rows [rows, n] (one wave per row, n <= 2048).
+// quantize_act_i8_into of f32 rows [rows, n] (one wave per row, n % 4 == 0,
+// n <= 256*NV), loads issued up front as in k_ln_quant.
+template <int NV>
 __global__ void __launch_bounds__(256) k_quant_act_rows(const float *x, int rows, int n, int8_t *xq, float *xs) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
-    const float *xr = x + (size_t)r * n;
-    float xv[DEC_LN_V];
+    const int n4 = n >> 2;
+    const float4 *xr = (const float4 *)(x + (size_t)r * n);
+    float4 xv[NV];
+    bool ok[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int i = lane + k * 64;
+        ok[k] = i < n4;
+        xv[k] = xr[ok[k] ? i : 0];
+    }
     float m = 0.0f;
 #pragma unroll
-    for (int k = 0; k < DEC_LN_V; k++) {
-        int i = lane + k * 64;
-        float t = xr[i < n ? i : 0];
-        xv[k] = i < n ? t : 0.0f;
-        m = fmaxf(m, fabsf(xv[k]));
-    }
-    m = fw_wave_max(m);
+    for (int k = 0; k < NV; k++)
+        if (ok[k]) m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[k].x), fabsf(xv[k].y)), fmaxf(fabsf(xv[k].z), fabsf(xv[k].w))));
+    m = fw_dpp_wave_max(m);
     const float sc = fmaxf(m, 1e-9f) / 127.0f;
     const float iv = 1.0f / sc;
 #pragma unroll
-    for (int k = 0; k < DEC_LN_V; k++) {
-        int i = lane + k * 64;
-        if (i < n) xq[(size_t)r * n + i] = fw_q8_avx(xv[k], iv, i, n);
+    for (int k = 0; k < NV; k++) {
+        if (ok[k]) {
+            const int i = (lane + k * 64) * 4;
+            const uint32_t q = (uint32_t)(uint8_t)fw_q8_avx(xv[k].x, iv, i, n) |
+                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].y, iv, i + 1, n) << 8) |
+                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].z, iv, i + 2, n) << 16) |
+                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].w, iv, i + 3, n) << 24);
+            *(uint32_t *)(xq + (size_t)r * n + i) = q;
+        }
     }
     if (lane == 0) xs[r] = sc;
 }
@@ -154,7 +172,8 @@ __device__ __forceinline__ bool dec_masked(int i, const fwhip_filter &f, int ini
 // ns are zero), xs [ns]; y [ns, ldy].  Block = 4 waves over 16*RG rows; wave
 // w takes the 64-wide k blocks kb = w, w+4, ...
 // mode 0 store, 1 residual add (add_into, decoder.rs:2369), 2 GELU
-// (nn.rs:4603), 3 logits: store + per-block argmax keys keys[s*nblk + block].
+// (nn.rs:4603), 3 logits: store + per-block argmax keys keys[s*nblk + block],
+// 4 GELU stored in the block-interleaved order of the block GEMV's input.
 #define GV_KPW 5 // k blocks per wave held in registers (K <= 1280 in one pass)
 template <int RG>
 __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, const float *__restrict__ sw,
@@ -163,6 +182,7 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
                                                   int ldy, int mode, const float *__restrict__ gelu_tab,
                                                   fwhip_filter filt, int use_filter, const int *initialp,
                                                   unsigned long long *keys) {
+    static_assert(RG <= 4, "one row group per wave in the epilogue");
     __shared__ int red[4][RG * 4][64];
     __shared__ unsigned long long ksh[RG][16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -173,6 +193,23 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
 #pragma unroll
     for (int g = 0; g < RG; g++) acc[g] = (v4i){0, 0, 0, 0};
     const int8_t *xrow = xq + (size_t)(lane & 15) * K + ko;
+    // epilogue operands of the row group this wave finishes (g = wave < RG),
+    // loaded now so their latency overlaps the operand loads and MFMAs
+    const int ge = wave;
+    const int erow = row_base + ge * 16 + (lane & 15);
+    const bool eok = ge < RG && erow < N;
+    const int erc = eok ? erow : 0;
+    const float e_sw = sw[erc];
+    const float e_b = bias ? bias[erc] : 0.0f;
+    const int initial = (mode == 3 && use_filter) ? *initialp : 0;
+    float e_xs[4], e_y[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int s = (lane >> 4) * 4 + r;
+        const int sc_ = s < ns ? s : 0;
+        e_xs[r] = xs[sc_];
+        e_y[r] = mode == 1 ? y[(size_t)sc_ * ldy + erc] : 0.0f;
+    }
     // this wave's k blocks kb = wave + 4*i, i < GV_KPW: every operand load is
     // issued before the first MFMA (addresses clamped, unused blocks zeroed)
     v4i xa[GV_KPW], wb[GV_KPW][RG];
@@ -209,12 +246,9 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
 #pragma unroll
         for (int r = 0; r < 4; r++) red[wave][g * 4 + r][lane] = acc[g][r];
     __syncthreads();
-    const int initial = (mode == 3 && use_filter) ? *initialp : 0;
-    for (int g = wave; g < RG; g += 4) {
-        const int row = row_base + g * 16 + (lane & 15);
-        const bool okr = row < N;
-        const float swr = okr ? sw[row] : 0.0f;
-        const float b = (okr && bias) ? bias[row] : 0.0f;
+    if (ge < RG) {
+        const int g = ge, row = erow;
+        const bool okr = eok;
         const bool masked = mode == 3 && use_filter && okr && dec_masked(row, filt, initial);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -223,10 +257,10 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
                             red[3][g * 4 + r][lane];
             unsigned long long key = 0ull;
             if (okr && s < ns) {
-                const float v = (float)tot * swr * xs[s] + b;
-                float *yp = y + (size_t)s * ldy + row;
-                if (mode == 1) *yp = *yp + v;
-                else if (mode == 2) *yp = fw_gelu(v, gelu_tab);
+                const float v = (float)tot * e_sw * e_xs[r] + e_b;
+                float *yp = y + (size_t)s * ldy + (mode == 4 ? fw_blk_perm(row, ldy >> 5) : row);
+                if (mode == 1) *yp = e_y[r] + v;
+                else if (mode == 2 || mode == 4) *yp = fw_gelu(v, gelu_tab);
                 else *yp = v;
                 if (mode == 3 && !masked) key = am_key(v, row);
             }
@@ -291,92 +325,119 @@ __global__ void __launch_bounds__(1024) k_argmax_finish(const unsigned long long
 // dots dot_i8w_f32 (nn.rs:3501-3564; one 32-chunk: products, lane-wise
 // (a0+a1)+(a2+a3), then ((t0+t1)+(t2+t3))+((t4+t5)+(t6+t7))) are folded in
 // ascending block order, acc = acc + dot_b * s_b, then + bias.
-// Block = 256 threads over BLK_R rows.  Work items are (stream, 32-block)
-// pairs: an item loads its activation chunk once and computes the block dot
-// for each of the BLK_R rows into LDS; then one thread per (row, stream)
-// folds the row's block dots in order.
-#define BLK_R 4
-__device__ __forceinline__ float blk_dot32(const int4 w0, const int4 w1, const float (&xv)[32]) {
-    const int wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-    float p[32];
-#pragma unroll
-    for (int q = 0; q < 8; q++)
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            p[q * 4 + e] = __builtin_fmaf((float)(int8_t)((wv[q] >> (8 * e)) & 0xff), xv[q * 4 + e], 0.0f);
-    float tl[8];
-#pragma unroll
-    for (int l = 0; l < 8; l++) tl[l] = (p[l] + p[8 + l]) + (p[16 + l] + p[24 + l]);
-    return ((tl[0] + tl[1]) + (tl[2] + tl[3])) + ((tl[4] + tl[5]) + (tl[6] + tl[7]));
-}
-
-__global__ void __launch_bounds__(256) k_gemv_blk3(const int8_t *__restrict__ W, const float *__restrict__ sc,
+//
+// A block owns R consecutive rows (R = ceil(N / CUs): one block per CU).
+// Thread c owns the (32-block b, stream group g) pair c = g * nb + b and holds
+// the activation chunks x[g*SG .. g*SG+SG)[b*32 .. b*32+32) in registers for
+// all R rows; per row it converts the weight chunk once and forms SG block
+// dots, writing dot_b * s_b to LDS; one thread per (row, stream) then folds
+// the products in ascending b.
+//
+// The activations arrive block-interleaved (fw_blk_perm: 16-byte chunk q of
+// block b at chunk index q*nb + b, written so by the producing GEMV), so the
+// q-th load of the lanes owning consecutive blocks reads consecutive 16-byte
+// chunks; in natural order every wave load would touch 64 cache lines.
+#define B7_RP 5
+template <int SG>
+__global__ void __launch_bounds__(512) k_gemv_blk7(const int8_t *__restrict__ W, const float *__restrict__ sc,
                                                    const float *__restrict__ bias, const float *__restrict__ x,
-                                                   float *y, int N, int K, int ns, int ldy, int mode) {
-    extern __shared__ float blk_sm[];
-    const int nb = K >> 5, ldd = nb + 1;
-    float *dots = blk_sm;                          // [BLK_R][ns][ldd]
-    float *scl = blk_sm + (size_t)BLK_R * ns * ldd; // [BLK_R][nb]
-    const int t = threadIdx.x;
-    const int row0 = blockIdx.x * BLK_R;
-    for (int i = t; i < BLK_R * nb; i += 256) {
-        int r = i / nb, b = i - r * nb;
-        scl[i] = row0 + r < N ? sc[(size_t)(row0 + r) * nb + b] : 0.0f;
-    }
-    const int items = ns * nb;
-    // software pipeline: the next item's activation and weight chunks load
-    // while this item's dots are computed
-    float4 xn[8];
-    int4 wn[BLK_R][2];
-    auto load_item = [&](int it) {
-        const int itc = it < items ? it : items - 1;
-        const int s = itc / nb, b = itc - s * nb;
-        const float4 *xp = (const float4 *)(x + (size_t)s * K + (size_t)b * 32);
+                                                   float *y, int N, int K, int ns, int ldy, int mode, int R) {
+    extern __shared__ __align__(16) float b7_sm[]; // P[R][ns][ldp]
+    const int nb = K >> 5, ldp = nb + 4;
+    const int row0 = blockIdx.x * R;
+    const int nr = N - row0 < R ? N - row0 : R;
+    const int nsg = (ns + SG - 1) / SG, combos = nb * nsg;
+    const int tid = threadIdx.x;
+    if (tid < combos) {
+        const int g = tid / nb, b = tid - g * nb;
+        int4 wr[B7_RP][2];
+        float sr[B7_RP];
+        auto load_rows = [&](int rc) {
+            const int nc = nr - rc < B7_RP ? nr - rc : B7_RP;
 #pragma unroll
-        for (int q = 0; q < 8; q++) xn[q] = xp[q];
+            for (int u = 0; u < B7_RP; u++) {
+                const int row = row0 + rc + (u < nc ? u : nc - 1);
+                const int4 *wq = (const int4 *)(W + (size_t)row * K + (size_t)b * 32);
+                wr[u][0] = wq[0];
+                wr[u][1] = wq[1];
+                sr[u] = sc[(size_t)row * nb + b];
+            }
+        };
+        load_rows(0);
+        float xv[SG][32];
 #pragma unroll
-        for (int r = 0; r < BLK_R; r++) {
-            const int row = row0 + r;
-            const int4 *wp = (const int4 *)(W + (size_t)(row < N ? row : N - 1) * K + (size_t)b * 32);
-            wn[r][0] = wp[0];
-            wn[r][1] = wp[1];
+        for (int j = 0; j < SG; j++) {
+            const int sj = g * SG + j < ns ? g * SG + j : ns - 1;
+            const float4 *xp = (const float4 *)(x + (size_t)sj * K) + b;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float4 v = xp[(size_t)q * nb];
+                xv[j][q * 4 + 0] = v.x;
+                xv[j][q * 4 + 1] = v.y;
+                xv[j][q * 4 + 2] = v.z;
+                xv[j][q * 4 + 3] = v.w;
+            }
         }
-    };
-    load_item(t);
-    for (int it = t; it < items; it += 256) {
-        float xv[32];
+        for (int rc = 0; rc < nr; rc += B7_RP) {
+            const int nc = nr - rc < B7_RP ? nr - rc : B7_RP;
+            if (rc > 0) load_rows(rc);
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            xv[q * 4 + 0] = xn[q].x;
-            xv[q * 4 + 1] = xn[q].y;
-            xv[q * 4 + 2] = xn[q].z;
-            xv[q * 4 + 3] = xn[q].w;
+            for (int u = 0; u < B7_RP; u++) {
+                if (u < nc) {
+                    const int r = rc + u;
+                    const int wv[8] = {wr[u][0].x, wr[u][0].y, wr[u][0].z, wr[u][0].w,
+                                       wr[u][1].x, wr[u][1].y, wr[u][1].z, wr[u][1].w};
+                    // element q*4+e sits in accumulation lane (q%2)*4+e of
+                    // group q/2
+                    float tl[SG][8];
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        float wf[16]; // words h, h+2, h+4, h+6 -> lanes h*4 .. h*4+3
+#pragma unroll
+                        for (int gq = 0; gq < 4; gq++)
+#pragma unroll
+                            for (int e = 0; e < 4; e++)
+                                wf[gq * 4 + e] = (float)(int8_t)((wv[gq * 2 + h] >> (8 * e)) & 0xff);
+#pragma unroll
+                        for (int j = 0; j < SG; j++)
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                const int l = h * 4 + e;
+                                const float p0 = __builtin_fmaf(wf[0 * 4 + e], xv[j][l], 0.0f);
+                                const float p1 = __builtin_fmaf(wf[1 * 4 + e], xv[j][8 + l], 0.0f);
+                                const float p2 = __builtin_fmaf(wf[2 * 4 + e], xv[j][16 + l], 0.0f);
+                                const float p3 = __builtin_fmaf(wf[3 * 4 + e], xv[j][24 + l], 0.0f);
+                                tl[j][l] = (p0 + p1) + (p2 + p3);
+                            }
+                    }
+                    float *pr = b7_sm + (size_t)r * ns * ldp + b;
+#pragma unroll
+                    for (int j = 0; j < SG; j++) {
+                        const float dot = ((tl[j][0] + tl[j][1]) + (tl[j][2] + tl[j][3])) +
+                                          ((tl[j][4] + tl[j][5]) + (tl[j][6] + tl[j][7]));
+                        if (g * SG + j < ns) pr[(size_t)(g * SG + j) * ldp] = dot * sr[u];
+                    }
+                }
+            }
         }
-        int4 wc[BLK_R][2];
-#pragma unroll
-        for (int r = 0; r < BLK_R; r++) {
-            wc[r][0] = wn[r][0];
-            wc[r][1] = wn[r][1];
-        }
-        load_item(it + 256);
-        const int s = it / nb, b = it - s * nb;
-#pragma unroll
-        for (int r = 0; r < BLK_R; r++)
-            dots[((size_t)r * ns + s) * ldd + b] = blk_dot32(wc[r][0], wc[r][1], xv); // rows past N never fold
     }
     __syncthreads();
-    if (t < BLK_R * ns) {
-        const int r = t / ns, s = t - r * ns, row = row0 + r;
-        if (row < N) {
-            const float *dr = dots + ((size_t)r * ns + s) * ldd;
-            const float *sr = scl + (size_t)r * nb;
-            float acc = 0.0f;
-            for (int b = 0; b < nb; b++) acc = acc + dr[b] * sr[b];
-            const float v = acc + (bias ? bias[row] : 0.0f);
-            float *yp = y + (size_t)s * ldy + row;
-            if (mode == 1) *yp = *yp + v;
-            else *yp = v;
+    for (int i = tid; i < nr * ns; i += blockDim.x) {
+        const int r = i / ns, s = i - r * ns, row = row0 + r;
+        const float4 *pp = (const float4 *)(b7_sm + (size_t)i * ldp);
+        float acc = 0.0f;
+#pragma unroll 20
+        for (int q = 0; q < (nb >> 2); q++) {
+            const float4 v = pp[q];
+            acc = acc + v.x;
+            acc = acc + v.y;
+            acc = acc + v.z;
+            acc = acc + v.w;
         }
+        const float v = acc + (bias ? bias[row] : 0.0f);
+        float *yp = y + (size_t)s * ldy + row;
+        if (mode == 1) *yp = *yp + v;
+        else *yp = v;
     }
 }
 
@@ -509,7 +570,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
     float *sc = (float *)smc2;                                       // [T]
     int8_t *p8 = (int8_t *)(smc2 + sizeof(float) * ((T + 3) & ~3)); // [Tq]
     __shared__ __align__(16) int8_t q8[64];
-    __shared__ float red[8];
+    __shared__ float red[16];
     __shared__ float bc[2];
     const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -544,7 +605,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
     }
     if (wave == 0) {
         float v = qc[(size_t)s * d + h * 64 + lane] * scale;
-        float m = fw_wave_max(fabsf(v));
+        float m = fw_dpp_wave_max(fabsf(v));
         float xs = fmaxf(m, 1e-9f) / 127.0f;
         q8[lane] = fw_q8_avx(v, 1.0f / xs, lane, 64);
         if (lane == 0) bc[0] = xs;
@@ -586,13 +647,25 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
         sc[j] = v;
         mx = fmaxf(mx, v);
     }
-    mx = fw_block_max(mx, red);
+    mx = fw_dpp_wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
     const bool fin = isfinite(mx);
-    if (fin)
-        for (int j = t; j < T; j += 512) {
-            float e = fw_expf(sc[j] - mx);
-            sc[j] = isfinite(e) ? e : 0.0f;
+    // exp pass; am = max |stored value| (the exps, or the raw scores when the
+    // max is not finite and softmax leaves them as they are)
+    float am = 0.0f;
+    for (int j = t; j < T; j += 512) {
+        float v = sc[j];
+        if (fin) {
+            const float e = fw_expf(v - mx);
+            v = isfinite(e) ? e : 0.0f;
+            sc[j] = v;
         }
+        am = fmaxf(am, fabsf(v));
+    }
+    am = fw_dpp_wave_max(am);
+    if (lane == 0) red[8 + wave] = am;
     __syncthreads();
     if (t == 0) {
         // softmax_rows' sequential sum (nn.rs:4880-4963)
@@ -612,16 +685,21 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
     }
     __syncthreads();
     const float inv = bc[1];
-    float pm = 0.0f;
-    for (int j = t; j < T; j += 512) {
-        float p = inv > 0.0f ? sc[j] * inv : sc[j];
-        sc[j] = p;
-        pm = fmaxf(pm, fabsf(p));
-    }
-    pm = fw_block_max(pm, red);
+    am = fmaxf(fmaxf(fmaxf(red[8], red[9]), fmaxf(red[10], red[11])),
+               fmaxf(fmaxf(red[12], red[13]), fmaxf(red[14], red[15])));
+    // max_j |p_j| of p_j = e_j * inv: rounding is monotonic and sign-symmetric,
+    // so it is (max_j |e_j|) * inv rounded once
+    const float pm = inv > 0.0f ? am * inv : am;
     const float ps = fmaxf(pm, 1e-9f) / 127.0f;
     const float pinv = 1.0f / ps;
-    for (int j = t; j < Tq; j += 512) p8[j] = j < T ? fw_q8_avx(sc[j], pinv, j, T) : (int8_t)0;
+    for (int j = t; j < Tq; j += 512) {
+        int8_t q = 0;
+        if (j < T) {
+            const float p = inv > 0.0f ? sc[j] * inv : sc[j];
+            q = fw_q8_avx(p, pinv, j, T);
+        }
+        p8[j] = q;
+    }
     __syncthreads();
     // out[dd] = sum_j Vt[dd, j] * p8[j]: wave w owns rows dd = w*8 .. w*8+7
     int4 pp[CA_VPL];
@@ -650,7 +728,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
             acc = fw_sdot4(vv.z, q4.z, acc);
             acc = fw_sdot4(vv.w, q4.w, acc);
         }
-        acc = fw_wave_sum(acc);
+        acc = fw_dpp_wave_sum_i32(acc);
         if (lane == 0) att[(size_t)s * d + h * 64 + dd] = (float)acc * Vs[dd] * ps + 0.0f;
     }
 }
@@ -672,13 +750,27 @@ __global__ void __launch_bounds__(64) k_quant_f16_rows_ld(const uint16_t *src, i
 
 // ---------------------------------------------------------------------------
 // launch wrappers
+// Row kernels hold ceil(d/256) float4 groups per lane; d % 4 == 0 and
+// d <= 2048 are checked when the decoder is loaded.
+#define FW_ROWS_DISPATCH(KERNEL, d, ...)                                                           \
+    switch ((d + 255) / 256) {                                                                      \
+    case 1: hipLaunchKernelGGL(KERNEL<1>, __VA_ARGS__); break;                                      \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, __VA_ARGS__); break;                                      \
+    case 3: hipLaunchKernelGGL(KERNEL<3>, __VA_ARGS__); break;                                      \
+    case 4: hipLaunchKernelGGL(KERNEL<4>, __VA_ARGS__); break;                                      \
+    case 5: hipLaunchKernelGGL(KERNEL<5>, __VA_ARGS__); break;                                      \
+    case 6: hipLaunchKernelGGL(KERNEL<6>, __VA_ARGS__); break;                                      \
+    case 7: hipLaunchKernelGGL(KERNEL<7>, __VA_ARGS__); break;                                      \
+    default: hipLaunchKernelGGL(KERNEL<8>, __VA_ARGS__); break;                                     \
+    }
+
 void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d, int rows,
                         int8_t *xq, float *xs) {
-    hipLaunchKernelGGL(k_ln_quant, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, d, rows, xq, xs);
+    FW_ROWS_DISPATCH(k_ln_quant, d, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, d, rows, xq, xs);
 }
 
 void fw_launch_quant_act_rows(hipStream_t st, const float *x, int rows, int n, int8_t *xq, float *xs) {
-    hipLaunchKernelGGL(k_quant_act_rows, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, xq, xs);
+    FW_ROWS_DISPATCH(k_quant_act_rows, n, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, xq, xs);
 }
 
 int fw_gemv_i8m_blocks(int N) { return N >= 16384 ? (N + 63) / 64 : (N + 15) / 16; }
@@ -705,12 +797,27 @@ void fw_launch_argmax_finish(hipStream_t st, const unsigned long long *keys, int
                        initialp, stepp, advance);
 }
 
-void fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const float *bias, const float *x, float *y,
-                         int N, int K, int ns, int ldy, int mode) {
-    const int nb = K >> 5;
-    size_t shm = sizeof(float) * ((size_t)BLK_R * ns * (nb + 1) + (size_t)BLK_R * nb);
-    hipLaunchKernelGGL(k_gemv_blk3, dim3((N + BLK_R - 1) / BLK_R), dim3(256), shm, st, W, sc, bias, x, y, N, K, ns, ldy,
-                       mode);
+// Streams go in chunks of SG * floor(512 / nb) (one (block, group) pair per
+// thread).  x is block-interleaved (fw_blk_perm).
+int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const float *bias, const float *x, float *y,
+                        int N, int K, int ns, int ldy, int mode, int n_cu) {
+    constexpr int SG = 4;
+    const int nb = K >> 5, ldp = nb + 4;
+    if ((K & 31) || nb > 512) return -1;
+    const int chunk = SG * (512 / nb);
+    for (int s0 = 0; s0 < ns; s0 += chunk) {
+        const int n = ns - s0 < chunk ? ns - s0 : chunk;
+        int R = (N + n_cu - 1) / n_cu;
+        const int rmax = (64 * 1024) / (int)(sizeof(float) * n * ldp);
+        if (R > rmax) R = rmax;
+        if (R < 1) return -1;
+        const int nsg = (n + SG - 1) / SG;
+        const int threads = ((nb * nsg + 63) / 64) * 64;
+        const size_t shm = sizeof(float) * (size_t)R * n * ldp;
+        hipLaunchKernelGGL(k_gemv_blk7<SG>, dim3((N + R - 1) / R), dim3(threads), shm, st, W, sc, bias,
+                           x + (size_t)s0 * K, y + (size_t)s0 * ldy, N, K, n, ldy, mode, R);
+    }
+    return 0;
 }
 
 void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,

@@ -29,10 +29,16 @@ __global__ void k_embed(const int32_t *tok, const int *posp, const uint16_t *emb
 // Lane j (0..3) of a 4-lane group owns accumulator vector a_j (8 lanes of the
 // AVX register); chunk c covers elements [32c, 32c+32).
 // Block = 256 threads; 64 rows per block.
+#define GF16_U 4
 template <int MAXS>
 __global__ void __launch_bounds__(256) k_gemv_f16(const uint16_t *__restrict__ W, const float *__restrict__ bias,
                                                   const float *__restrict__ x, float *y, int N, int K, int ns,
                                                   int ldy, int mode, const float *__restrict__ gelu_tab) {
+    // blockIdx.y selects the stream group [s0, s0 + MAXS)
+    const int s0 = blockIdx.y * MAXS;
+    x += (size_t)s0 * K;
+    y += (size_t)s0 * ldy;
+    ns = ns - s0 < MAXS ? ns - s0 : MAXS;
     int j = threadIdx.x & 3;
     int row = blockIdx.x * 64 + (threadIdx.x >> 2);
     bool ok = row < N;
@@ -42,10 +48,9 @@ __global__ void __launch_bounds__(256) k_gemv_f16(const uint16_t *__restrict__ W
     for (int s = 0; s < MAXS; s++)
 #pragma unroll
         for (int l = 0; l < 8; l++) a[s][l] = 0.0f;
-    int nc = K >> 5;
-    for (int c = 0; c < nc; c++) {
-        int off = c * 32 + j * 8;
-        uint4 wv = ok ? *(const uint4 *)(wr + off) : make_uint4(0, 0, 0, 0);
+    const int nc = K >> 5;
+    // fma of one 32-chunk (8 weights per lane) into the MAXS accumulators
+    auto chunk = [&](const uint4 wv, const float4 (&xc)[MAXS][2]) {
         float wf[8];
         wf[0] = fw_h2f(wv.x & 0xffff); wf[1] = fw_h2f(wv.x >> 16);
         wf[2] = fw_h2f(wv.y & 0xffff); wf[3] = fw_h2f(wv.y >> 16);
@@ -54,8 +59,7 @@ __global__ void __launch_bounds__(256) k_gemv_f16(const uint16_t *__restrict__ W
 #pragma unroll
         for (int s = 0; s < MAXS; s++) {
             if (s < ns) {
-                const float4 *xp = (const float4 *)(x + (size_t)s * K + off);
-                float4 x0 = xp[0], x1 = xp[1];
+                const float4 x0 = xc[s][0], x1 = xc[s][1];
                 a[s][0] = __builtin_fmaf(wf[0], x0.x, a[s][0]);
                 a[s][1] = __builtin_fmaf(wf[1], x0.y, a[s][1]);
                 a[s][2] = __builtin_fmaf(wf[2], x0.z, a[s][2]);
@@ -66,6 +70,40 @@ __global__ void __launch_bounds__(256) k_gemv_f16(const uint16_t *__restrict__ W
                 a[s][7] = __builtin_fmaf(wf[7], x1.w, a[s][7]);
             }
         }
+    };
+    auto load_x = [&](int c, float4 (&xc)[MAXS][2]) {
+#pragma unroll
+        for (int s = 0; s < MAXS; s++) {
+            const float4 *xp = (const float4 *)(x + (size_t)(s < ns ? s : ns - 1) * K + c * 32 + j * 8);
+            xc[s][0] = xp[0];
+            xc[s][1] = xp[1];
+        }
+    };
+    // the weight chunks of the next GF16_U iterations are in flight while the
+    // current ones are used (rows past N read row 0 and are never stored)
+    constexpr int U = GF16_U;
+    uint4 wq[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) wq[u] = *(const uint4 *)(wr + (u < nc ? u : nc - 1) * 32 + j * 8);
+    int c = 0;
+    for (; c + U <= nc; c += U) {
+        uint4 wc[U];
+        float4 xc[U][MAXS][2];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            wc[u] = wq[u];
+            const int cn = c + U + u < nc ? c + U + u : nc - 1;
+            wq[u] = *(const uint4 *)(wr + cn * 32 + j * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) load_x(c + u, xc[u]);
+#pragma unroll
+        for (int u = 0; u < U; u++) chunk(wc[u], xc[u]);
+    }
+    for (; c < nc; c++) {
+        float4 xc[MAXS][2];
+        load_x(c, xc);
+        chunk(*(const uint4 *)(wr + c * 32 + j * 8), xc);
     }
     int tail8 = nc * 32;
 #pragma unroll
@@ -264,29 +302,23 @@ __global__ void __launch_bounds__(64) k_quant_f16_rows(const uint16_t *src, int8
 
 // ---------------------------------------------------------------------------
 // launch wrappers
-#define FW_GEMV_DISPATCH(KER, MAXS_, ...)                                            \
-    do {                                                                               \
-        if (MAXS_ <= 1) hipLaunchKernelGGL(KER<1>, __VA_ARGS__);                     \
-        else if (MAXS_ <= 4) hipLaunchKernelGGL(KER<4>, __VA_ARGS__);                \
-        else if (MAXS_ <= 8) hipLaunchKernelGGL(KER<8>, __VA_ARGS__);                \
-        else hipLaunchKernelGGL(KER<16>, __VA_ARGS__);                               \
-    } while (0)
-
-static int fw_round_maxs(int ns) { return ns <= 1 ? 1 : ns <= 4 ? 4 : ns <= 8 ? 8 : 16; }
 
 void fw_launch_embed(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb,
                      const float *pemb, float *x, int d, int ns) {
     hipLaunchKernelGGL(k_embed, dim3(ns), dim3(256), 0, st, tok, posp, emb, pemb, x, d);
 }
 
+// Streams go in groups of 4 over grid.y (one group per block keeps the grid
+// wide enough to fill the CUs; a weight chunk is still converted once per 4
+// streams).
 void fw_launch_gemv_f16(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *y, int N,
                         int K, int ns, int ldy, int mode, const float *gelu_tab) {
-    for (int s0 = 0; s0 < ns; s0 += 16) {
-        int n = ns - s0 < 16 ? ns - s0 : 16;
-        int mx = fw_round_maxs(n);
-        FW_GEMV_DISPATCH(k_gemv_f16, mx, dim3((N + 63) / 64), dim3(256), 0, st, W, bias, x + (size_t)s0 * K,
-                         y + (size_t)s0 * ldy, N, K, n, ldy, mode, gelu_tab);
-    }
+    if (ns == 1)
+        hipLaunchKernelGGL(k_gemv_f16<1>, dim3((N + 63) / 64, 1), dim3(256), 0, st, W, bias, x, y, N, K, ns, ldy, mode,
+                           gelu_tab);
+    else
+        hipLaunchKernelGGL(k_gemv_f16<4>, dim3((N + 63) / 64, (ns + 3) / 4), dim3(256), 0, st, W, bias, x, y, N, K,
+                           ns, ldy, mode, gelu_tab);
 }
 
 void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,

@@ -353,12 +353,6 @@ __global__ void __launch_bounds__(256) k_gemm(FwGemm g, int ntm, int ntn) {
 // instruction writes 16 rows x 64 bytes = 1 KB contiguous in LDS).
 __device__ __forceinline__ int gsw(int r) { return (r ^ (r >> 2)) & 3; }
 
-// s_waitcnt vmcnt(n) (gfx9 encoding), lgkm/exp counters not waited on
-#define FW_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
-// s_waitcnt lgkmcnt(0) (vm/exp counters not waited on)
-#define FW_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (3 << 14))
-// s_waitcnt vmcnt(n) lgkmcnt(0)
-#define FW_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
 
 template <int KIND, int EPI, int BM, int BN, int NS>
 __global__ void __launch_bounds__(256) k_gemm2(FwGemm g, int ntm, int ntn) {

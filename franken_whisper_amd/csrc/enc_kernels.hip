@@ -388,8 +388,6 @@ __global__ void __launch_bounds__(256) k_attention(const uint16_t *qh, const uin
 // chunk c ^ (r & 7), which keeps the fragment reads free of bank conflicts.
 #define AT_NS 3
 #define AT_QW 8
-#define AT_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
-#define AT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 __global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                                                            const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl,
                                                            int T, int Tp, int H, int d, int out_mode, float *of,
@@ -461,7 +459,7 @@ __global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, c
 #pragma unroll
     for (int p = 0; p < AT_NS - 1; p++) issue(p);
     for (int it = 0; it < nt; it++) {
-        AT_WAIT_VM_LGKM0(LPW * (AT_NS - 2)); // this wave's loads of tile `it` have landed
+        FW_WAIT_VM_LGKM0(LPW * (AT_NS - 2)); // this wave's loads of tile `it` have landed
         asm volatile("s_barrier" ::: "memory");
         issue(it + AT_NS - 1);
         const uint16_t *sK = &sm[it % AT_NS][0][0];
@@ -565,7 +563,7 @@ __global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, c
     for (int j = 0; j < 2; j++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[j][r] += oy[j][r];
-    AT_WAIT_VM(0); // dummy tiles landed before the block exits
+    FW_WAIT_VM(0); // dummy tiles landed before the block exits
     if (myq >= T) return;
     const float inv = 1.0f / l;
     const size_t orow = ((size_t)b * T + myq) * d + (size_t)h * 64;

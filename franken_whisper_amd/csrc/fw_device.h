@@ -62,6 +62,68 @@ __device__ __forceinline__ float fw_wave_max(float v) {
     return v;
 }
 
+// Block-interleaved position of feature k in a row of nb 32-wide blocks:
+// 16-byte chunk q of block b goes to chunk index q * nb + b.
+__device__ __forceinline__ int fw_blk_perm(int k, int nb) {
+    return ((((k & 31) >> 2) * nb + (k >> 5)) << 2) | (k & 3);
+}
+
+// Explicit s_waitcnt (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8); the counters not named are not waited on.
+#define FW_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+#define FW_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (3 << 14))
+#define FW_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+
+// Whole-wave reductions over DPP lane moves (no LDS round trips): pair, quad,
+// half-row and row butterflies, then the four 16-lane row results are read
+// into scalars and combined as (r0 + r1) + (r2 + r3).  Every lane returns the
+// same value.
+template <int CTRL>
+__device__ __forceinline__ float fw_dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double fw_dpp_f64(double v) {
+    const int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xf, 0xf, false);
+    return __hiloint2double(hi, lo);
+}
+#define FW_DPP_XOR1 0xB1      // quad_perm [1,0,3,2]
+#define FW_DPP_XOR2 0x4E      // quad_perm [2,3,0,1]
+#define FW_DPP_HALF_MIRROR 0x141
+#define FW_DPP_MIRROR 0x140
+__device__ __forceinline__ double fw_rl_f64(double v, int lane) {
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
+                            __builtin_amdgcn_readlane(__double2loint(v), lane));
+}
+__device__ __forceinline__ double fw_dpp_wave_sum_f64(double v) {
+    v = v + fw_dpp_f64<FW_DPP_XOR1>(v);
+    v = v + fw_dpp_f64<FW_DPP_XOR2>(v);
+    v = v + fw_dpp_f64<FW_DPP_HALF_MIRROR>(v);
+    v = v + fw_dpp_f64<FW_DPP_MIRROR>(v);
+    return (fw_rl_f64(v, 0) + fw_rl_f64(v, 16)) + (fw_rl_f64(v, 32) + fw_rl_f64(v, 48));
+}
+__device__ __forceinline__ float fw_dpp_wave_max(float v) {
+    v = fmaxf(v, fw_dpp_f32<FW_DPP_XOR1>(v));
+    v = fmaxf(v, fw_dpp_f32<FW_DPP_XOR2>(v));
+    v = fmaxf(v, fw_dpp_f32<FW_DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, fw_dpp_f32<FW_DPP_MIRROR>(v));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+__device__ __forceinline__ int fw_dpp_wave_sum_i32(int v) {
+    v = v + __builtin_amdgcn_mov_dpp(v, FW_DPP_XOR1, 0xf, 0xf, false);
+    v = v + __builtin_amdgcn_mov_dpp(v, FW_DPP_XOR2, 0xf, 0xf, false);
+    v = v + __builtin_amdgcn_mov_dpp(v, FW_DPP_HALF_MIRROR, 0xf, 0xf, false);
+    v = v + __builtin_amdgcn_mov_dpp(v, FW_DPP_MIRROR, 0xf, 0xf, false);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+
 // Block-wide sum/max (all threads get the result).  `sh` needs blockDim/64 slots.
 template <typename T>
 __device__ __forceinline__ T fw_block_sum(T v, T *sh) {

@@ -31,8 +31,8 @@ void fw_launch_gemv_i8m(hipStream_t st, const int8_t *W, const float *sw, const 
                         const fwhip_filter *filt, const int *initialp, unsigned long long *keys);
 void fw_launch_argmax_finish(hipStream_t st, const unsigned long long *keys, int nblk, int ns, int32_t *tok,
                              int32_t *hist, int hist_cap, int *posp, int *initialp, int *stepp, int advance);
-void fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const float *bias, const float *x, float *y,
-                         int N, int K, int ns, int ldy, int mode);
+int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const float *bias, const float *x, float *y,
+                        int N, int K, int ns, int ldy, int mode, int n_cu);
 void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
                           int d, int H, int nctx, int L, int layer, int ns, float scale);
 void fw_launch_cross_attn_i8v2(hipStream_t st, const float *qc, const int8_t *ck, const float *cks, const int8_t *cvt,

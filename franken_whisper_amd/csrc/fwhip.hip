@@ -538,12 +538,9 @@ static void gemv_i8_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const 
                            mode, gt, filt, st->initial, mode == 3 ? st->keys + (size_t)s0 * nblk : nullptr);
     }
 }
-static void gemv_blk_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const float *sc, const float *bias,
+static bool gemv_blk_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const float *sc, const float *bias,
                          const float *x, float *y, int N, int K, int ldy) {
-    for (int s0 = 0; s0 < st->S; s0 += 16) {
-        int n = st->S - s0 < 16 ? st->S - s0 : 16;
-        fw_launch_gemv_blk2(s, W, sc, bias, x + (size_t)s0 * K, y + (size_t)s0 * ldy, N, K, n, ldy, 1);
-    }
+    return fw_launch_gemv_blk2(s, W, sc, bias, x, y, N, K, st->S, ldy, 1, st->dec->ctx->n_cu) == 0;
 }
 
 // One token row for every stream at the device-side position *st->pos
@@ -576,10 +573,13 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             fw_launch_quant_act_rows(s, st->att, S, d, st->xq, st->xs);
             gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr);
             fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs);
-            gemv_i8_all(st, s, l.fc1_8, l.fc1_8s, l.fc1_b, st->ff, dff, d, dff, 2, nullptr);
-            // prefill rows take the f16 mlp_2 (the block-int8 arm has no batch form)
+            // mode 4: GELU written block-interleaved for the block GEMV; prefill
+            // rows take the f16 mlp_2 (the block-int8 arm has no batch form),
+            // which reads natural order
+            gemv_i8_all(st, s, l.fc1_8, l.fc1_8s, l.fc1_b, st->ff, dff, d, dff, prefill ? 2 : 4, nullptr);
             if (prefill) fw_launch_gemv_f16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
-            else gemv_blk_all(st, s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, d);
+            else if (!gemv_blk_all(st, s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, d))
+                return fw_fail(FWHIP_ERR_INVALID, "block GEMV: unsupported mlp width");
         } else {
             fw_launch_ln_quant(s, st->x, st->h, l.attn_ln_w, l.attn_ln_b, d, S, nullptr, nullptr);
             fw_launch_gemv_f16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);

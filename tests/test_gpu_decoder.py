@@ -66,8 +66,16 @@ def test_tiny_en_step_bitexact(ctx, arm):
     _run_steps(ctx, "tiny.en", arm, n_streams=2, n_steps=3, seed=1)
 
 
-def test_turbo_step_bitexact_int8(ctx):
-    _run_steps(ctx, "large-v3-turbo", abi.DEC_INT8, n_streams=1, n_steps=2, seed=2)
+@pytest.mark.parametrize("arm", [abi.DEC_INT8, abi.DEC_F16])
+def test_micro_wide_cohort_bitexact(ctx, arm):
+    # 18 streams: the per-call stream chunking (16) and several stream groups
+    # of the block GEMV
+    _run_steps(ctx, "micro", arm, n_streams=18, n_steps=2, seed=4)
+
+
+@pytest.mark.parametrize("n_streams", [1, 10])
+def test_turbo_step_bitexact_int8(ctx, n_streams):
+    _run_steps(ctx, "large-v3-turbo", abi.DEC_INT8, n_streams=n_streams, n_steps=2, seed=2)
 
 
 @pytest.mark.parametrize("arm", [abi.DEC_INT8, abi.DEC_F16])
