@@ -33,23 +33,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // groups l, l+64, ... (NV of them, d <= 256*NV, d % 4 == 0).  Every load of
 // x, w and b is issued before the first use, so the row costs one memory
 // round trip; the reductions run on DPP lane moves.
+// Row r whose values xv (lane l: float4 groups l, l+64, ...; ok = in range)
+// are already loaded or in flight.
 template <int NV>
-__global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, const float *w, const float *b, int d,
-                                                  int rows, int8_t *xq, float *xs) {
-    const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= rows) return;
-    const int n4 = d >> 2;
-    const float4 *xr = (const float4 *)(x + (size_t)r * d);
+__device__ __forceinline__ void fw_ln_quant_vals(float4 (&xv)[NV], const bool (&ok)[NV], float *y, const float *w,
+                                                 const float *b, int d, int r, int8_t *xq, float *xs, int lane) {
     const float4 *w4 = (const float4 *)w, *b4 = (const float4 *)b;
-    float4 xv[NV], wv[NV], bv[NV];
-    bool ok[NV];
+    float4 wv[NV], bv[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int i = lane + k * 64;
-        ok[k] = i < n4;
-        const int c = ok[k] ? i : 0;
-        xv[k] = xr[c];
+        const int c = ok[k] ? lane + k * 64 : 0;
         wv[k] = w4[c];
         bv[k] = b4[c];
     }
@@ -101,15 +94,14 @@ __global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, cons
     if (lane == 0) xs[r] = sc;
 }
 
-// quantize_act_i8_into of f32 rows [rows, n] (one wave per row, n % 4 == 0,
-// n <= 256*NV), loads issued up front as in k_ln_quant.
 template <int NV>
-__global__ void __launch_bounds__(256) k_quant_act_rows(const float *x, int rows, int n, int8_t *xq, float *xs) {
+__global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, const float *w, const float *b, int d,
+                                                  int rows, int8_t *xq, float *xs) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
-    const int n4 = n >> 2;
-    const float4 *xr = (const float4 *)(x + (size_t)r * n);
+    const int n4 = d >> 2;
+    const float4 *xr = (const float4 *)(x + (size_t)r * d);
     float4 xv[NV];
     bool ok[NV];
 #pragma unroll
@@ -118,25 +110,34 @@ __global__ void __launch_bounds__(256) k_quant_act_rows(const float *x, int rows
         ok[k] = i < n4;
         xv[k] = xr[ok[k] ? i : 0];
     }
-    float m = 0.0f;
-#pragma unroll
-    for (int k = 0; k < NV; k++)
-        if (ok[k]) m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[k].x), fabsf(xv[k].y)), fmaxf(fabsf(xv[k].z), fabsf(xv[k].w))));
-    m = fw_dpp_wave_max(m);
-    const float sc = fmaxf(m, 1e-9f) / 127.0f;
-    const float iv = 1.0f / sc;
+    fw_ln_quant_vals<NV>(xv, ok, y, w, b, d, r, xq, xs, lane);
+}
+
+// embed_tokens (decoder.rs:1323-1385: x = f16(E[tok]) + P[pos]) of one stream
+// per block (one wave), followed by the first layer's attention LayerNorm of
+// the row (into ln_y and/or the int8 activation rows, as k_ln_quant).
+template <int NV>
+__global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *posp, const uint16_t *emb,
+                                                 const float *pemb, float *x, int d, const float *w, const float *b,
+                                                 float *ln_y, int8_t *xq, float *xs) {
+    const int s = blockIdx.x, lane = threadIdx.x;
+    const int n4 = d >> 2;
+    const uint2 *er = (const uint2 *)(emb + (size_t)tok[s] * d);
+    const float4 *pr = (const float4 *)(pemb + (size_t)(*posp) * d);
+    float4 xv[NV];
+    bool ok[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        if (ok[k]) {
-            const int i = (lane + k * 64) * 4;
-            const uint32_t q = (uint32_t)(uint8_t)fw_q8_avx(xv[k].x, iv, i, n) |
-                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].y, iv, i + 1, n) << 8) |
-                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].z, iv, i + 2, n) << 16) |
-                               ((uint32_t)(uint8_t)fw_q8_avx(xv[k].w, iv, i + 3, n) << 24);
-            *(uint32_t *)(xq + (size_t)r * n + i) = q;
-        }
+        const int i = lane + k * 64;
+        ok[k] = i < n4;
+        const int c = ok[k] ? i : 0;
+        const uint2 e = er[c];
+        const float4 p = pr[c];
+        xv[k] = make_float4(fw_h2f(e.x & 0xffff) + p.x, fw_h2f(e.x >> 16) + p.y, fw_h2f(e.y & 0xffff) + p.z,
+                            fw_h2f(e.y >> 16) + p.w);
+        if (ok[k]) ((float4 *)(x + (size_t)s * d))[i] = xv[k];
     }
-    if (lane == 0) xs[r] = sc;
+    fw_ln_quant_vals<NV>(xv, ok, ln_y, w, b, d, s, xq, xs, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -175,16 +176,37 @@ __device__ __forceinline__ bool dec_masked(int i, const fwhip_filter &f, int ini
 // (nn.rs:4603), 3 logits: store + per-block argmax keys keys[s*nblk + block],
 // 4 GELU stored in the block-interleaved order of the block GEMV's input.
 #define GV_KPW 5 // k blocks per wave held in registers (K <= 1280 in one pass)
-template <int RG>
+//
+// XF = 1: the activations arrive as f32 rows xf [ns, K] together with per-head
+// partial maxima pmax [ns, H] of |xf| (written by the attention kernel that
+// produced them); the block forms each row's quantize_act_i8_into scale from
+// the partial maxima and quantizes its own operand chunks, so no separate
+// quantization pass over the rows is needed.
+// 16 elements of a row whose length is a multiple of 8: all in the add-trunc
+// body of the quantizer.
+__device__ __forceinline__ uint32_t fw_q8_body(float v, float iv) {
+    return (uint32_t)(uint8_t)(int8_t)(int)fw_clamp(fw_round_add_trunc(v * iv), -127.0f, 127.0f);
+}
+__device__ __forceinline__ v4i fw_q8_chunk16(const float4 (&v)[4], float iv) {
+    v4i q;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        q[c] = (int)(fw_q8_body(v[c].x, iv) | (fw_q8_body(v[c].y, iv) << 8) | (fw_q8_body(v[c].z, iv) << 16) |
+                     (fw_q8_body(v[c].w, iv) << 24));
+    return q;
+}
+template <int RG, int XF>
 __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, const float *__restrict__ sw,
                                                   const float *__restrict__ bias, const int8_t *__restrict__ xq,
                                                   const float *__restrict__ xs, float *y, int N, int K, int ns,
                                                   int ldy, int mode, const float *__restrict__ gelu_tab,
                                                   fwhip_filter filt, int use_filter, const int *initialp,
-                                                  unsigned long long *keys) {
+                                                  unsigned long long *keys, const float *__restrict__ xf,
+                                                  const float *__restrict__ pmax, int H) {
     static_assert(RG <= 4, "one row group per wave in the epilogue");
     __shared__ int red[4][RG * 4][64];
     __shared__ unsigned long long ksh[RG][16];
+    __shared__ int smax[16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row_base = blockIdx.x * 16 * RG;
     const int nkb = K >> 6;
@@ -193,6 +215,8 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
 #pragma unroll
     for (int g = 0; g < RG; g++) acc[g] = (v4i){0, 0, 0, 0};
     const int8_t *xrow = xq + (size_t)(lane & 15) * K + ko;
+    const int sa = lane & 15;
+    const float *frow = xf + (size_t)(sa < ns ? sa : 0) * K + ko;
     // epilogue operands of the row group this wave finishes (g = wave < RG),
     // loaded now so their latency overlaps the operand loads and MFMAs
     const int ge = wave;
@@ -207,21 +231,70 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
     for (int r = 0; r < 4; r++) {
         const int s = (lane >> 4) * 4 + r;
         const int sc_ = s < ns ? s : 0;
-        e_xs[r] = xs[sc_];
+        e_xs[r] = XF ? 0.0f : xs[sc_]; // XF: from the row scales below
         e_y[r] = mode == 1 ? y[(size_t)sc_ * ldy + erc] : 0.0f;
     }
-    // this wave's k blocks kb = wave + 4*i, i < GV_KPW: every operand load is
-    // issued before the first MFMA (addresses clamped, unused blocks zeroed)
+    // XF: the head maxima are loaded first, so waiting for them does not wait
+    // for the operand loads behind them (ns * H <= 512)
+    float pm[2] = {0.0f, 0.0f};
+    if (XF) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int e = threadIdx.x + u * 256;
+            pm[u] = pmax[e < ns * H ? e : 0];
+        }
+    }
+    // weight chunks of this wave's k blocks kb = wave + 4*i, i < GV_KPW
     v4i xa[GV_KPW], wb[GV_KPW][RG];
 #pragma unroll
     for (int i = 0; i < GV_KPW; i++) {
         const int kb = wave + 4 * i;
         const int kbc = kb < nkb ? kb : nkb - 1;
-        xa[i] = *(const v4i *)(xrow + kbc * 64);
 #pragma unroll
         for (int g = 0; g < RG; g++) {
             const int row = row_base + g * 16 + (lane & 15);
             wb[i][g] = *(const v4i *)(W + (size_t)(row < N ? row : N - 1) * K + ko + kbc * 64);
+        }
+    }
+    float4 xfv[XF ? GV_KPW : 1][4];
+    if (XF) {
+        // operand chunks first (they are the long loads), then the row scales
+#pragma unroll
+        for (int i = 0; i < GV_KPW; i++) {
+            const int kb = wave + 4 * i;
+            const float4 *fp = (const float4 *)(frow + (kb < nkb ? kb : nkb - 1) * 64);
+#pragma unroll
+            for (int c = 0; c < 4; c++) xfv[i][c] = fp[c];
+        }
+        if (threadIdx.x < 16) smax[threadIdx.x] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int e = threadIdx.x + u * 256;
+            // m >= 0, so int order is float order; NaN never wins (as fmaxf)
+            if (e < ns * H && pm[u] == pm[u]) atomicMax(&smax[e / H], __float_as_int(pm[u]));
+        }
+        __syncthreads();
+    }
+    if (XF) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int st_ = (lane >> 4) * 4 + r;
+            e_xs[r] = fmaxf(__int_as_float(smax[st_ < ns ? st_ : 0]), 1e-9f) / 127.0f;
+        }
+    }
+    const float a_iv = XF ? 1.0f / (fmaxf(__int_as_float(smax[sa]), 1e-9f) / 127.0f) : 0.0f;
+    // activation operands (every operand load is issued before the first
+    // MFMA; addresses clamped, unused blocks never multiplied)
+#pragma unroll
+    for (int i = 0; i < GV_KPW; i++) {
+        const int kb = wave + 4 * i;
+        const int kbc = kb < nkb ? kb : nkb - 1;
+        if (XF) {
+            xa[i] = fw_q8_chunk16(xfv[i], a_iv);
+            if (sa >= ns) xa[i] = (v4i){0, 0, 0, 0};
+        } else {
+            xa[i] = *(const v4i *)(xrow + kbc * 64);
         }
     }
 #pragma unroll
@@ -233,7 +306,15 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
     }
     // K beyond 4 * GV_KPW * 64
     for (int kb = wave + 4 * GV_KPW; kb < nkb; kb += 4) {
-        v4i x1 = *(const v4i *)(xrow + kb * 64);
+        v4i x1;
+        if (XF) {
+            float4 v[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) v[c] = ((const float4 *)(frow + kb * 64))[c];
+            x1 = sa < ns ? fw_q8_chunk16(v, a_iv) : (v4i){0, 0, 0, 0};
+        } else {
+            x1 = *(const v4i *)(xrow + kb * 64);
+        }
 #pragma unroll
         for (int g = 0; g < RG; g++) {
             const int row = row_base + g * 16 + (lane & 15);
@@ -453,7 +534,7 @@ __global__ void __launch_bounds__(512) k_gemv_blk7(const int8_t *__restrict__ W,
 #define SA_STG 4
 __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *kc, uint16_t *vc, float *att,
                                                     const int *posp, int d, int nctx, int L, int layer,
-                                                    float scale) {
+                                                    float scale, float *pmax) {
     extern __shared__ __align__(16) unsigned char sm2[];
     float *sc = (float *)sm2;                               // [nctx]
     uint16_t *vs = (uint16_t *)(sm2 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
@@ -550,6 +631,9 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
         }
         for (; j < tk; j++) acc += sc[j] * fw_h2f(vs[j * 64 + t]);
         att[(size_t)s * d + base + t] = acc;
+        // this head's share of the row amax the int8 consumer needs
+        const float m = fw_dpp_wave_max(fabsf(acc));
+        if (pmax && t == 0) pmax[(size_t)s * gridDim.x + h] = m;
     }
 }
 
@@ -565,7 +649,8 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
 #define CA_VPL 2
 __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const int8_t *ck, const float *cks,
                                                          const int8_t *cvt, const float *cvs, float *att, int d,
-                                                         int T, int Tq, int H, int L, int layer, float scale) {
+                                                         int T, int Tq, int H, int L, int layer, float scale,
+                                                         float *pmax) {
     extern __shared__ __align__(16) unsigned char smc2[];
     float *sc = (float *)smc2;                                       // [T]
     int8_t *p8 = (int8_t *)(smc2 + sizeof(float) * ((T + 3) & ~3)); // [Tq]
@@ -702,6 +787,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
     }
     __syncthreads();
     // out[dd] = sum_j Vt[dd, j] * p8[j]: wave w owns rows dd = w*8 .. w*8+7
+    float om = 0.0f; // max |out| of this wave's rows (wave-uniform)
     int4 pp[CA_VPL];
 #pragma unroll
     for (int u = 0; u < CA_VPL; u++) {
@@ -729,7 +815,18 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
             acc = fw_sdot4(vv.w, q4.w, acc);
         }
         acc = fw_dpp_wave_sum_i32(acc);
-        if (lane == 0) att[(size_t)s * d + h * 64 + dd] = (float)acc * Vs[dd] * ps + 0.0f;
+        const float o = (float)acc * Vs[dd] * ps + 0.0f;
+        om = fmaxf(om, fabsf(o));
+        if (lane == 0) att[(size_t)s * d + h * 64 + dd] = o;
+    }
+    if (pmax) {
+        if (lane == 0) red[wave] = om;
+        __syncthreads();
+        if (t == 0) {
+            float m = red[0];
+            for (int w = 1; w < 8; w++) m = fmaxf(m, red[w]);
+            pmax[(size_t)s * H + h] = m;
+        }
     }
 }
 
@@ -769,26 +866,31 @@ void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w
     FW_ROWS_DISPATCH(k_ln_quant, d, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, d, rows, xq, xs);
 }
 
-void fw_launch_quant_act_rows(hipStream_t st, const float *x, int rows, int n, int8_t *xq, float *xs) {
-    FW_ROWS_DISPATCH(k_quant_act_rows, n, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, xq, xs);
+void fw_launch_embed_ln(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,
+                        float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs) {
+    FW_ROWS_DISPATCH(k_embed_ln, d, dim3(ns), dim3(64), 0, st, tok, posp, emb, pemb, x, d, w, b, ln_y, xq, xs);
 }
 
 int fw_gemv_i8m_blocks(int N) { return N >= 16384 ? (N + 63) / 64 : (N + 15) / 16; }
 
 void fw_launch_gemv_i8m(hipStream_t st, const int8_t *W, const float *sw, const float *bias, const int8_t *xq,
                         const float *xs, float *y, int N, int K, int ns, int ldy, int mode, const float *gelu_tab,
-                        const fwhip_filter *filt, const int *initialp, unsigned long long *keys) {
+                        const fwhip_filter *filt, const int *initialp, unsigned long long *keys, const float *xf,
+                        const float *pmax, int H) {
     fwhip_filter ff;
     int use = filt != nullptr;
     if (filt) ff = *filt;
     else memset(&ff, 0, sizeof ff);
     int nblk = fw_gemv_i8m_blocks(N);
-    if (N >= 16384)
-        hipLaunchKernelGGL(k_gemv_i8m<4>, dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy, mode,
-                           gelu_tab, ff, use, initialp, keys);
+    if (xf)
+        hipLaunchKernelGGL((k_gemv_i8m<1, 1>), dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy,
+                           mode, gelu_tab, ff, use, initialp, keys, xf, pmax, H);
+    else if (N >= 16384)
+        hipLaunchKernelGGL((k_gemv_i8m<4, 0>), dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy,
+                           mode, gelu_tab, ff, use, initialp, keys, xf, pmax, H);
     else
-        hipLaunchKernelGGL(k_gemv_i8m<1>, dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy, mode,
-                           gelu_tab, ff, use, initialp, keys);
+        hipLaunchKernelGGL((k_gemv_i8m<1, 0>), dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy,
+                           mode, gelu_tab, ff, use, initialp, keys, xf, pmax, H);
 }
 
 void fw_launch_argmax_finish(hipStream_t st, const unsigned long long *keys, int nblk, int ns, int32_t *tok,
@@ -821,18 +923,18 @@ int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const 
 }
 
 void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
-                          int d, int H, int nctx, int L, int layer, int ns, float scale) {
+                          int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax) {
     size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
     hipLaunchKernelGGL(k_self_attn2, dim3(H, ns), dim3(256), shm, st, qkv, kc, vc, att, posp, d, nctx, L, layer,
-                       scale);
+                       scale, pmax);
 }
 
 void fw_launch_cross_attn_i8v2(hipStream_t st, const float *qc, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
-                               float scale) {
+                               float scale, float *pmax) {
     size_t shm = sizeof(float) * ((T + 3) & ~3) + Tq;
     hipLaunchKernelGGL(k_cross_attn_i8v2, dim3(H, ns), dim3(512), shm, st, qc, ck, cks, cvt, cvs, att, d, T, Tq, H, L,
-                       layer, scale);
+                       layer, scale, pmax);
 }
 
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq) {

@@ -14,17 +14,6 @@
 #define LN_EPS_F 1e-5f
 
 // ---------------------------------------------------------------------------
-// embed_tokens (decoder.rs:1323-1385): x = f16(E[tok]) + P[pos]
-__global__ void k_embed(const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,
-                        float *x, int d) {
-    int s = blockIdx.x;
-    int pos = *posp;
-    const uint16_t *er = emb + (size_t)tok[s] * d;
-    const float *pr = pemb + (size_t)pos * d;
-    for (int i = threadIdx.x; i < d; i += blockDim.x) x[(size_t)s * d + i] = fw_h2f(er[i]) + pr[i];
-}
-
-// ---------------------------------------------------------------------------
 // f16 GEMV in dot_f16c order (nn.rs:1983-2051), S streams per weight read.
 // Lane j (0..3) of a 4-lane group owns accumulator vector a_j (8 lanes of the
 // AVX register); chunk c covers elements [32c, 32c+32).
@@ -302,11 +291,6 @@ __global__ void __launch_bounds__(64) k_quant_f16_rows(const uint16_t *src, int8
 
 // ---------------------------------------------------------------------------
 // launch wrappers
-
-void fw_launch_embed(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb,
-                     const float *pemb, float *x, int d, int ns) {
-    hipLaunchKernelGGL(k_embed, dim3(ns), dim3(256), 0, st, tok, posp, emb, pemb, x, d);
-}
 
 // Streams go in groups of 4 over grid.y (one group per block keeps the grid
 // wide enough to fill the CUs; a weight chunk is still converted once per 4

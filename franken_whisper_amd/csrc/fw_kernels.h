@@ -8,8 +8,6 @@
 #include "fwhip.h"
 
 // decoder (dec_kernels.hip)
-void fw_launch_embed(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb,
-                     const float *pemb, float *x, int d, int ns);
 void fw_launch_gemv_f16(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *y, int N,
                         int K, int ns, int ldy, int mode, const float *gelu_tab);
 void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,
@@ -24,20 +22,24 @@ void fw_launch_step_bookkeeping(hipStream_t st, int *posp, int *initialp, const 
 // int8 decoder arm (dec_fast.hip)
 void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d, int rows,
                         int8_t *xq, float *xs);
-void fw_launch_quant_act_rows(hipStream_t st, const float *x, int rows, int n, int8_t *xq, float *xs);
+void fw_launch_embed_ln(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,
+                        float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs);
 int fw_gemv_i8m_blocks(int N);
 void fw_launch_gemv_i8m(hipStream_t st, const int8_t *W, const float *sw, const float *bias, const int8_t *xq,
                         const float *xs, float *y, int N, int K, int ns, int ldy, int mode, const float *gelu_tab,
-                        const fwhip_filter *filt, const int *initialp, unsigned long long *keys);
+                        const fwhip_filter *filt, const int *initialp, unsigned long long *keys,
+                        const float *xf = nullptr, const float *pmax = nullptr, int H = 0);
 void fw_launch_argmax_finish(hipStream_t st, const unsigned long long *keys, int nblk, int ns, int32_t *tok,
                              int32_t *hist, int hist_cap, int *posp, int *initialp, int *stepp, int advance);
 int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const float *bias, const float *x, float *y,
                         int N, int K, int ns, int ldy, int mode, int n_cu);
+// pmax (nullable): [ns, H] max |output| of each head block, for a consumer
+// that quantizes the rows itself (fw_launch_gemv_i8m with xf)
 void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
-                          int d, int H, int nctx, int L, int layer, int ns, float scale);
+                          int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax = nullptr);
 void fw_launch_cross_attn_i8v2(hipStream_t st, const float *qc, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
-                               float scale);
+                               float scale, float *pmax = nullptr);
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq);
 int fw_logits_keys_blocks(int V);
 void fw_launch_logits_keys(hipStream_t st, const float *logits, int V, int ns, const fwhip_filter *filt,

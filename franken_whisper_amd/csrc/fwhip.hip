@@ -232,6 +232,7 @@ struct fwhip_dstate {
     int nkeys;
     int32_t *tok, *hist, *rows;
     int *pos, *initial, *stepc;
+    float *pmax;            // [S, H] per-head max |attention output|
     int hist_cap;
     // captured sampling step (forward of st->tok + argmax + bookkeeping)
     hipGraphExec_t graph = nullptr;
@@ -441,8 +442,9 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     st->pos = (int *)fw_dalloc(own, sizeof(int) * 4);
     st->initial = st->pos + 1;
     st->stepc = st->pos + 2;
+    st->pmax = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * dd->H);
     ok = ok && st->x && st->h && st->qkv && st->att && st->y && st->ff && st->logits && st->xq && st->xs &&
-         st->keys && st->tok && st->rows && st->hist && st->pos;
+         st->keys && st->tok && st->rows && st->hist && st->pos && st->pmax;
     // padding rows of the quantized activations must read as zeros
     ok = ok && hipMemset(st->xq, 0, (size_t)st->Sp * d) == hipSuccess && hipMemset(st->pos, 0, sizeof(int) * 4) == hipSuccess;
     if (!ok) {
@@ -528,14 +530,18 @@ static fwhip_status check_cancel(fwhip_ctx *c) {
 }
 
 // int8 GEMV over every stream, 16 streams per launch (the MFMA tile height).
+// xf (nullable): quantize the f32 rows xf inside the GEMV, with st->pmax
+// holding the per-head maxima of those rows
 static void gemv_i8_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const float *sw, const float *bias, float *y,
-                        int N, int K, int ldy, int mode, const fwhip_filter *filt) {
+                        int N, int K, int ldy, int mode, const fwhip_filter *filt, const float *xf = nullptr) {
     const float *gt = st->dec->ctx->gelu_tab;
+    const int H = st->dec->H;
     int nblk = fw_gemv_i8m_blocks(N);
     for (int s0 = 0; s0 < st->S; s0 += 16) {
         int n = st->S - s0 < 16 ? st->S - s0 : 16;
         fw_launch_gemv_i8m(s, W, sw, bias, st->xq + (size_t)s0 * K, st->xs + s0, y + (size_t)s0 * ldy, N, K, n, ldy,
-                           mode, gt, filt, st->initial, mode == 3 ? st->keys + (size_t)s0 * nblk : nullptr);
+                           mode, gt, filt, st->initial, mode == 3 ? st->keys + (size_t)s0 * nblk : nullptr,
+                           xf ? xf + (size_t)s0 * K : nullptr, xf ? st->pmax + (size_t)s0 * H : nullptr, H);
     }
 }
 static bool gemv_blk_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const float *sc, const float *bias,
@@ -557,21 +563,27 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
     bool i8 = dd->arm == FWHIP_DEC_INT8;
     float scale = powf(64.0f, -0.25f);
     const float *gt = c->gelu_tab;
-    fw_launch_embed(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S);
+    // embedding + layer 0's attention LayerNorm
+    if (i8)
+        fw_launch_embed_ln(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S, dd->layers[0].attn_ln_w,
+                           dd->layers[0].attn_ln_b, nullptr, st->xq, st->xs);
+    else
+        fw_launch_embed_ln(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S, dd->layers[0].attn_ln_w,
+                           dd->layers[0].attn_ln_b, st->h, nullptr, nullptr);
     for (int li = 0; li < L; li++) {
         const DecLayerDev &l = dd->layers[li];
         if (i8) {
-            fw_launch_ln_quant(s, st->x, nullptr, l.attn_ln_w, l.attn_ln_b, d, S, st->xq, st->xs);
+            if (li > 0) fw_launch_ln_quant(s, st->x, nullptr, l.attn_ln_w, l.attn_ln_b, d, S, st->xq, st->xs);
             gemv_i8_all(st, s, l.qkv8, l.qkv8s, l.qkv_b, st->qkv, 3 * d, d, 3 * d, 0, nullptr);
-            fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
-            fw_launch_quant_act_rows(s, st->att, S, d, st->xq, st->xs);
-            gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr);
+            // attention writes per-head maxima; the o / co GEMVs quantize att themselves
+            fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale,
+                                 st->pmax);
+            gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr, st->att);
             fw_launch_ln_quant(s, st->x, nullptr, l.cross_ln_w, l.cross_ln_b, d, S, st->xq, st->xs);
             gemv_i8_all(st, s, l.cq8, l.cq8s, l.cq_b, st->y, d, d, d, 0, nullptr);
             fw_launch_cross_attn_i8v2(s, st->y, st->ck8, st->ck8s, st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li,
-                                      S, scale);
-            fw_launch_quant_act_rows(s, st->att, S, d, st->xq, st->xs);
-            gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr);
+                                      S, scale, st->pmax);
+            gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr, st->att);
             fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs);
             // mode 4: GELU written block-interleaved for the block GEMV; prefill
             // rows take the f16 mlp_2 (the block-int8 arm has no batch form),
@@ -581,7 +593,7 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             else if (!gemv_blk_all(st, s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, d))
                 return fw_fail(FWHIP_ERR_INVALID, "block GEMV: unsupported mlp width");
         } else {
-            fw_launch_ln_quant(s, st->x, st->h, l.attn_ln_w, l.attn_ln_b, d, S, nullptr, nullptr);
+            if (li > 0) fw_launch_ln_quant(s, st->x, st->h, l.attn_ln_w, l.attn_ln_b, d, S, nullptr, nullptr);
             fw_launch_gemv_f16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
             fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
             fw_launch_gemv_f16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
