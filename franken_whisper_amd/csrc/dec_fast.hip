@@ -523,6 +523,51 @@ __global__ void __launch_bounds__(512) k_gemv_blk7(const int8_t *__restrict__ W,
 }
 
 // ---------------------------------------------------------------------------
+// 1 / (sequential f32 sum of v[0..n)) (softmax_rows' sum, nn.rs:4880-4963), 0
+// when the sum is not positive; one thread.  The dependent adds bound the
+// loop; reading 64 values per LDS round trip keeps the waits between batches
+// few.
+__device__ __forceinline__ float fw_seq_sum_inv(const float *v, int n) {
+    const float4 *v4 = (const float4 *)v;
+    const int n4 = n >> 2, n16 = n4 & ~15;
+    float sum = 0.0f;
+    for (int q = 0; q < n16; q += 16) {
+        float4 c[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) c[u] = v4[q + u];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            sum += c[u].x;
+            sum += c[u].y;
+            sum += c[u].z;
+            sum += c[u].w;
+        }
+    }
+    {
+        // the last n4 % 16 groups and n % 4 values, read in one round trip
+        float4 c[16];
+        float t[3];
+#pragma unroll
+        for (int u = 0; u < 16; u++) c[u] = v4[n16 + u < n4 ? n16 + u : 0];
+#pragma unroll
+        for (int u = 0; u < 3; u++) t[u] = v[n4 * 4 + u < n ? n4 * 4 + u : 0];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            if (n16 + u < n4) {
+                sum += c[u].x;
+                sum += c[u].y;
+                sum += c[u].z;
+                sum += c[u].w;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 3; u++)
+            if (n4 * 4 + u < n) sum += t[u];
+    }
+    return sum > 0.0f ? 1.0f / sum : 0.0f;
+}
+
+// ---------------------------------------------------------------------------
 // Self-attention over the f16 KV cache for one (head, stream), tq == 1
 // (attention_with_cache nn.rs:6267-6337 -> KvCache::append nn.rs:5352 ->
 // attention_decode_step_f16 nn.rs:6466-6540).  Appends this token's k/v (RNE
@@ -595,21 +640,7 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
             sc[j] = isfinite(e) ? e : 0.0f;
         }
     __syncthreads();
-    if (t == 0) {
-        float sum = 0.0f;
-        if (fin) {
-            int j = 0;
-            for (; j + 4 <= tk; j += 4) {
-                float4 v = *(const float4 *)(sc + j);
-                sum += v.x;
-                sum += v.y;
-                sum += v.z;
-                sum += v.w;
-            }
-            for (; j < tk; j++) sum += sc[j];
-        }
-        inv_s = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
-    }
+    if (t == 0) inv_s = fin ? fw_seq_sum_inv(sc, tk) : 0.0f;
     __syncthreads();
     const float inv = inv_s;
     if (inv > 0.0f)
@@ -754,19 +785,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
     __syncthreads();
     if (t == 0) {
         // softmax_rows' sequential sum (nn.rs:4880-4963)
-        float sum = 0.0f;
-        if (fin) {
-            int j = 0;
-            for (; j + 4 <= T; j += 4) {
-                float4 v = *(const float4 *)(sc + j);
-                sum += v.x;
-                sum += v.y;
-                sum += v.z;
-                sum += v.w;
-            }
-            for (; j < T; j++) sum += sc[j];
-        }
-        bc[1] = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
+        bc[1] = fin ? fw_seq_sum_inv(sc, T) : 0.0f;
     }
     __syncthreads();
     const float inv = bc[1];
