@@ -81,8 +81,11 @@ __device__ __forceinline__ void gemm_store4(const FwGemm &g, int row0, int col, 
                 g.o16[2 * which + 1][o] = lo[e];
             }
         } else {
+            // V^T key positions: bits 2 and 3 of the key index swapped within
+            // each 16-key group (the attention kernel reads the 8 keys one MFMA
+            // lane needs as one chunk); 4-key runs stay contiguous
             int b = row0 / g.T, t = row0 - b * g.T;
-            size_t o = (((size_t)b * g.H + h) * 64 + dd) * g.Tp + t;
+            size_t o = (((size_t)b * g.H + h) * 64 + dd) * g.Tp + fw_vt_pos(t);
             if ((t & 3) == 0 && t + 3 < g.T && row0 + 3 < g.M) {
                 uint2 ph = make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
                 uint2 pl = make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
@@ -94,7 +97,7 @@ __device__ __forceinline__ void gemm_store4(const FwGemm &g, int row0, int col, 
                     int row = row0 + e;
                     if (row >= g.M) continue;
                     int bb = row / g.T, tt = row - bb * g.T;
-                    size_t oo = (((size_t)bb * g.H + h) * 64 + dd) * g.Tp + tt;
+                    size_t oo = (((size_t)bb * g.H + h) * 64 + dd) * g.Tp + fw_vt_pos(tt);
                     g.o16[4][oo] = hi[e];
                     g.o16[5][oo] = lo[e];
                 }

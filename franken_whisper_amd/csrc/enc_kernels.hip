@@ -13,6 +13,8 @@
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void fw_split(float v, uint16_t &hi, uint16_t &lo) {
     asm volatile("" : "+v"(v));
@@ -232,157 +234,8 @@ __global__ void k_fill_u16(uint16_t *p, size_t n, uint16_t v) {
 }
 
 // ---------------------------------------------------------------------------
-// Bidirectional attention, one block per (window b, head h, 128 queries):
-// 4 waves x 32 queries.  Computes S^T = K Q^T per 64-key tile (A = K rows from
-// LDS, B = this wave's Q^T held in registers) so each lane owns one query and
-// the softmax max/sum over keys is in-register plus one cross-half shuffle; then
-// O^T += V^T P^T with P^T taken straight from the S^T accumulators (their key
-// order is matched by reading V^T in the same permuted order).  f16 pairs with
-// three MFMAs per product (hh + hl + lh); scores scaled by 1/8 = 64^-0.5 (the
-// SDPA scale, nn.rs:5867); online softmax in f32.
-__global__ void __launch_bounds__(256) k_attention(const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
-                                                   const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl,
-                                                   int T, int Tp, int H, int d, int out_mode, float *of,
-                                                   uint16_t *oh, uint16_t *ol) {
-    __shared__ __align__(16) uint16_t sK[2][64][72];  // [hi/lo][key][dim] (+pad)
-    __shared__ __align__(16) uint16_t sV[2][64][72];  // [hi/lo][dim][key]
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int h = blockIdx.y, b = blockIdx.z;
-    const int q0 = blockIdx.x * 128 + wave * 32;
-    const int myq = q0 + (lane & 31);
-    const size_t bh = (size_t)b * H + h;
-    // this lane's Q^T fragments: q = myq, dims (l/32)*8 + ks*16 .. +8, ks = 0..3
-    v8h qfh[4], qfl[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-        int dd = ks * 16 + (lane >> 5) * 8;
-        if (myq < T) {
-            qfh[ks] = *(const v8h *)(qh + (bh * T + myq) * 64 + dd);
-            qfl[ks] = *(const v8h *)(ql + (bh * T + myq) * 64 + dd);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                qfh[ks][e] = (_Float16)0.0f;
-                qfl[ks][e] = (_Float16)0.0f;
-            }
-        }
-    }
-    v16f o[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) o[j][r] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
-    const float sl2 = 0.125f * 1.4426950408889634f;
-    for (int k0 = 0; k0 < T; k0 += 64) {
-        __syncthreads();
-        // load K tile [64 keys][64 dims] and V^T tile [64 dims][64 keys] (hi, lo)
-        for (int c = threadIdx.x; c < 2 * 64 * 8; c += 256) {
-            int a = c >> 9, rr = (c >> 3) & 63, cc = c & 7;
-            int key = k0 + rr;
-            const uint16_t *ks_ = a ? kl : kh;
-            int4 kv = key < T ? *(const int4 *)(ks_ + (bh * T + key) * 64 + cc * 8) : make_int4(0, 0, 0, 0);
-            *(int4 *)&sK[a][rr][cc * 8] = kv;
-            const uint16_t *vs_ = a ? vtl : vth;
-            *(int4 *)&sV[a][rr][cc * 8] = *(const int4 *)(vs_ + (bh * 64 + rr) * Tp + k0 + cc * 8);
-        }
-        __syncthreads();
-        // S^T tiles: keys 32t .. 32t+31 x this wave's 32 queries
-        v16f st[2];
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) st[t][r] = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                int key = t * 32 + (lane & 31), dd = ks * 16 + (lane >> 5) * 8;
-                v8h ah = *(const v8h *)&sK[0][key][dd];
-                v8h al = *(const v8h *)&sK[1][key][dd];
-                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qfh[ks], st[t], 0, 0, 0);
-                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qfl[ks], st[t], 0, 0, 0);
-                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qfh[ks], st[t], 0, 0, 0);
-            }
-        }
-        // online softmax over this tile's keys for query myq
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                int key = k0 + t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                float s = key < T ? st[t][r] : -INFINITY;
-                st[t][r] = s;
-                tmax = fmaxf(tmax, s);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        float mnew = fmaxf(m, tmax);
-        float alpha = __builtin_amdgcn_exp2f((m - mnew) * sl2);
-        float psum = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float p = __builtin_amdgcn_exp2f((st[t][r] - mnew) * sl2);
-                st[t][r] = p;
-                psum += p;
-            }
-        psum += __shfl_xor(psum, 32, 64);
-        l = l * alpha + psum;
-        m = mnew;
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) o[j][r] *= alpha;
-        // O^T[dim][q] += V^T[dim][key] P^T[key][q]; key substep (t, u) uses
-        // accumulator regs 8u..8u+7 of S^T tile t: keys 32t+16u + (l/32)*4 + {0..3, 8..11}
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                v8h ph, pl;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    float p = st[t][8 * u + e];
-                    _Float16 hh = (_Float16)p;
-                    ph[e] = hh;
-                    pl[e] = (_Float16)(p - (float)hh);
-                }
-                int kb = t * 32 + u * 16 + (lane >> 5) * 4;
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    int dim = j * 32 + (lane & 31);
-                    v8h vh, vl;
-                    uint2 a0 = *(const uint2 *)&sV[0][dim][kb];
-                    uint2 a1 = *(const uint2 *)&sV[0][dim][kb + 8];
-                    uint2 b0 = *(const uint2 *)&sV[1][dim][kb];
-                    uint2 b1 = *(const uint2 *)&sV[1][dim][kb + 8];
-                    uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y), vb = make_uint4(b0.x, b0.y, b1.x, b1.y);
-                    vh = __builtin_bit_cast(v8h, va);
-                    vl = __builtin_bit_cast(v8h, vb);
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, ph, o[j], 0, 0, 0);
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pl, o[j], 0, 0, 0);
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph, o[j], 0, 0, 0);
-                }
-            }
-    }
-    if (myq >= T) return;
-    float inv = 1.0f / l;
-    size_t orow = ((size_t)b * T + myq) * d + (size_t)h * 64;
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            int dim = j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-            float v = o[j][r] * inv;
-            if (out_mode == 0) of[orow + dim] = v;
-            else fw_split(v, oh[orow + dim], ol[orow + dim]);
-        }
-}
-
-// ---------------------------------------------------------------------------
-// Pipelined attention: the same arithmetic as k_attention (S^T = K Q^T on f16
-// pairs, online softmax over 64-key tiles, O^T += V^T P^T), with 8 waves (256
-// queries) per block sharing each K/V tile, and the tiles (K hi/lo, V^T hi/lo:
+// Attention on f16 pairs (S^T = K Q^T, online softmax over 64-key tiles,
+// O^T += V^T P^T), with 8 waves (256 queries) per block sharing each K/V tile, and the tiles (K hi/lo, V^T hi/lo:
 // 4 x 8 KB) fed global -> LDS directly through an AT_NS-stage ring, one
 // barrier per tile.  Rows are 128 bytes; 16-byte chunk c of row r sits at
 // chunk c ^ (r & 7), which keeps the fragment reads free of bank conflicts.
@@ -446,14 +299,14 @@ __global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, c
                                              (void __attribute__((address_space(3))) *)(base + dsto[qq]), 16, 0, 0);
         }
     };
-    v16f o[2], oy[2];
+    // Each accumulator takes all three f16-pair products in turn (hi*hi,
+    // lo*hi, hi*lo); the two 32-key (or 32-dim) halves are independent
+    // chains, interleaved so consecutive MFMAs never depend on each other.
+    v16f o[2];
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            o[j][r] = 0.0f;
-            oy[j][r] = 0.0f;
-        }
+        for (int r = 0; r < 16; r++) o[j][r] = 0.0f;
     float m = -INFINITY, l = 0.0f;
     const float sl2 = 0.125f * 1.4426950408889634f;
 #pragma unroll
@@ -464,16 +317,9 @@ __global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, c
         issue(it + AT_NS - 1);
         const uint16_t *sK = &sm[it % AT_NS][0][0];
         const int k0 = it * 64;
-        // four independent accumulator chains (hh+hl and lh for each 32-key
-        // half) interleaved so consecutive MFMAs never depend on each other
-        v16f st[2], sy[2];
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                st[t][r] = 0.0f;
-                sy[t][r] = 0.0f;
-            }
+        // the first MFMA of each chain takes a zero accumulator operand
+        const v16f zero = {};
+        v16f st[2] = {zero, zero};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             v8h ah[2], al[2];
@@ -486,83 +332,88 @@ __global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, c
             }
             st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], qfh[ks], st[0], 0, 0, 0);
             st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], qfh[ks], st[1], 0, 0, 0);
-            sy[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0], qfh[ks], sy[0], 0, 0, 0);
-            sy[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1], qfh[ks], sy[1], 0, 0, 0);
+            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0], qfh[ks], st[0], 0, 0, 0);
+            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1], qfh[ks], st[1], 0, 0, 0);
             st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], qfl[ks], st[0], 0, 0, 0);
             st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], qfl[ks], st[1], 0, 0, 0);
         }
+        // keys past T exist only in the last tile
+        if (k0 + 64 > T) {
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+            for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) st[t][r] += sy[t][r];
+                for (int r = 0; r < 16; r++) {
+                    const int key = k0 + t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                    if (key >= T) st[t][r] = -INFINITY;
+                }
+        }
         float tmax = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = k0 + t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                const float sv = key < T ? st[t][r] : -INFINITY;
-                st[t][r] = sv;
-                tmax = fmaxf(tmax, sv);
-            }
+            for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, st[t][r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         const float mnew = fmaxf(m, tmax);
-        const float alpha = __builtin_amdgcn_exp2f((m - mnew) * sl2);
+        // exp2((s - mnew) * sl2) as one fma per score
+        const float nms = -mnew * sl2;
         float psum = 0.0f;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float pv = __builtin_amdgcn_exp2f((st[t][r] - mnew) * sl2);
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][r], sl2, nms));
                 st[t][r] = pv;
                 psum += pv;
             }
         psum += __shfl_xor(psum, 32, 64);
-        l = l * alpha + psum;
+        // rescale only when some row's running max moved (wave-uniform test)
+        if (__builtin_amdgcn_ballot_w64(mnew != m)) {
+            const float alpha = __builtin_amdgcn_exp2f((m - mnew) * sl2);
+            l *= alpha;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+        }
+        l += psum;
         m = mnew;
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                o[j][r] *= alpha;
-                oy[j][r] *= alpha;
-            }
         const uint16_t *sV = &sm[it % AT_NS][2][0];
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int u = 0; u < 2; u++) {
+                // f16 pair of P, two values per conversion
                 v8h ph, pl;
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float pv = st[t][8 * u + e];
-                    const _Float16 hh = (_Float16)pv;
-                    ph[e] = hh;
-                    pl[e] = (_Float16)(pv - (float)hh);
+                for (int e = 0; e < 8; e += 2) {
+                    const v2f pv = {st[t][8 * u + e], st[t][8 * u + e + 1]};
+                    const v2h hh = __builtin_convertvector(pv, v2h);
+                    const v2h lo = __builtin_convertvector(pv - __builtin_convertvector(hh, v2f), v2h);
+                    ph[e] = hh[0];
+                    ph[e + 1] = hh[1];
+                    pl[e] = lo[0];
+                    pl[e + 1] = lo[1];
                 }
-                const int c1 = t * 4 + u * 2, ko = (lane >> 5) * 4;
+                // P holds keys {G + 4h + 0..3, G + 8 + 4h + 0..3} (G = 32t + 16u,
+                // h = lane / 32); V^T stores each 16-key group with bits 2 and 3
+                // of the key swapped, so these 8 keys are one 16-byte chunk
+                const int c = t * 4 + u * 2 + (lane >> 5);
                 v8h vh[2], vl[2];
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
-                    const int dim = j * 32 + (lane & 31), sw = dim & 7;
-                    const int a0 = dim * 64 + ((c1 ^ sw) << 3) + ko, a1 = dim * 64 + (((c1 + 1) ^ sw) << 3) + ko;
-                    const uint2 x0 = *(const uint2 *)(sV + a0), x1 = *(const uint2 *)(sV + a1);
-                    const uint2 y0 = *(const uint2 *)(sV + 64 * 64 + a0), y1 = *(const uint2 *)(sV + 64 * 64 + a1);
-                    vh[j] = __builtin_bit_cast(v8h, make_uint4(x0.x, x0.y, x1.x, x1.y));
-                    vl[j] = __builtin_bit_cast(v8h, make_uint4(y0.x, y0.y, y1.x, y1.y));
+                    const int dim = j * 32 + (lane & 31);
+                    const int a = dim * 64 + ((c ^ (dim & 7)) << 3);
+                    vh[j] = *(const v8h *)(sV + a);
+                    vl[j] = *(const v8h *)(sV + 64 * 64 + a);
                 }
                 o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[0], ph, o[0], 0, 0, 0);
                 o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[1], ph, o[1], 0, 0, 0);
-                oy[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[0], ph, oy[0], 0, 0, 0);
-                oy[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[1], ph, oy[1], 0, 0, 0);
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[0], ph, o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[1], ph, o[1], 0, 0, 0);
                 o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[0], pl, o[0], 0, 0, 0);
                 o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[1], pl, o[1], 0, 0, 0);
             }
     }
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) o[j][r] += oy[j][r];
     FW_WAIT_VM(0); // dummy tiles landed before the block exits
     if (myq >= T) return;
     const float inv = 1.0f / l;
@@ -695,14 +546,6 @@ void fw_launch_fill_u16(hipStream_t st, uint16_t *p, size_t n, uint16_t v) {
 void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                          const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
                          int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol) {
-    static int old = -1;
-    if (old < 0) old = getenv("FWHIP_ATTN_V1") != nullptr;
-    if (old) {
-        dim3 grid((T + 127) / 128, H, B);
-        hipLaunchKernelGGL(k_attention, grid, dim3(256), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d, out_mode, of, oh,
-                           ol);
-        return;
-    }
     dim3 grid((T + 32 * AT_QW - 1) / (32 * AT_QW), H, B);
     hipLaunchKernelGGL(k_attention2, grid, dim3(64 * AT_QW), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d, out_mode, of,
                        oh, ol);

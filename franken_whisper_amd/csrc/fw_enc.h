@@ -15,6 +15,11 @@
 #define FW_EPI_QKV 5
 #define FW_EPI_ACC32 6
 
+// Position of key t in a V^T row: bits 2 and 3 swapped, so the keys
+// {16g + 4h + 0..3, 16g + 8 + 4h + 0..3} one attention MFMA lane multiplies
+// sit together at 16g + 8h + 0..7.
+__host__ __device__ __forceinline__ int fw_vt_pos(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
 #define FW_LN_F32 0
 #define FW_LN_SPLIT 1
 #define FW_LN_I7 2

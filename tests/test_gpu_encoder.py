@@ -84,6 +84,17 @@ def test_encoder_f32_within_tolerance(ctx, cfg):
     assert med < 1e-4, med
 
 
+def test_turbo_encoder_f32_full_depth_within_tolerance(ctx):
+    """All 32 large-v3-turbo layers, one window: the f32 plan stays within
+    max-abs 1e-3 relative of the oracle at full depth."""
+    got, want, rec = _encoder_pair(ctx, synth.TURBO, abi.ENC_F32, n_windows=1)
+    err = rel_maxabs(got, want)
+    med = float(np.median(np.abs(got - want))) / float(np.max(np.abs(want)))
+    print(f"large-v3-turbo f32 rel max-abs {err:.3e} rel median abs {med:.2e}", flush=True)
+    assert err < 1e-3, err
+    assert med < 1e-4, med
+
+
 @pytest.mark.parametrize("cfg", [synth.MICRO, TINY2], ids=lambda c: c.name)
 def test_encoder_int8_fast_mode_deviation(ctx, cfg):
     """int8 plan, fast mode: the MFMA f16-pair attention/conv move f32 values by
