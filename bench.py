@@ -85,6 +85,23 @@ def cpu_baseline(model, n_windows, n_tokens, threads, sample_windows):
     }
 
 
+TRAFFIC_FILE = "profiles/k_gemm2_int8_encoder_job.md"
+
+
+def measured_traffic():
+    """HBM bytes per int8 encoder GEMM dispatch on this job's shapes, as measured
+    with rocprofv3 counters and recorded in TRAFFIC_FILE (the counters cannot be
+    read from inside a timed run)."""
+    import re
+
+    try:
+        with open(os.path.join(ROOT, TRAFFIC_FILE)) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 def copy_calibration(mb, reps):
     """A plain device-to-device copy of known size (torch's elementwise copy
     kernel): the reference reading for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -187,10 +204,10 @@ def main():
     ctx.timing(False)
     ms_per_step = elapsed * 1e3 / a.steps
 
-    names = {abi.K_ENC_GEMM_I8: ("encoder int8 GEMM (k_gemm<I8>)", "mfma", "int8"),
-             abi.K_ENC_GEMM_F32: ("encoder f16-pair GEMM (k_gemm<F16S>)", "mfma", "f16"),
-             abi.K_ENC_ATTN: ("encoder attention (k_attention, f16-pair x3)", "mfma", "f16"),
-             abi.K_DEC_LOGITS: ("decoder logits GEMV (k_gemv_i8)", "hbm", None)}
+    names = {abi.K_ENC_GEMM_I8: ("encoder int8 GEMM (k_gemm2, int8 tiles)", "mfma", "int8"),
+             abi.K_ENC_GEMM_F32: ("encoder f16-pair GEMM (k_gemm2, f16-pair tiles)", "mfma", "f16"),
+             abi.K_ENC_ATTN: ("encoder attention (k_attention2, f16 pairs)", "mfma", "f16"),
+             abi.K_DEC_LOGITS: ("decoder logits GEMV (k_gemv_i8m)", "hbm", None)}
     kclass = max(stats, key=lambda k: stats[k][1])
     n, ms, units = stats[kclass]
     name, bound, op = names[kclass]
@@ -205,6 +222,11 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "launches": n,
                 "avg_launch_ms": round(ms / max(n, 1), 4)}
     kernel_classes = {names[k][0]: {"launches": v[0], "total_ms": round(v[1], 3)} for k, v in stats.items() if v[0]}
+    if kclass == abi.K_ENC_GEMM_I8 and a.workload == "job" and W == 10:
+        tb = measured_traffic()
+        if tb:
+            roof["traffic"] = tb
+            roof["traffic_source"] = TRAFFIC_FILE + " (rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0, per dispatch)"
 
     audio_s = 30.0 * W
     out = {
