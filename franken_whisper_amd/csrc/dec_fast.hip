@@ -670,18 +670,21 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
 
 // ---------------------------------------------------------------------------
 // Cross-attention for one (head, stream) with int8 K/V (cross_attention,
-// decoder.rs:1524-1716, int8 cross K/V — the default): qh = q*s quantized per
-// vector; scores = gemv_i8(K_h, qh); softmax; p quantized per vector;
-// out = gemv_i8(Vt_h, p).  512 threads.  Vt rows have stride Tq (T rounded up
+// decoder.rs:1524-1716, int8 cross K/V — the default), including the head's
+// rows of the cross q projection: q = gemv_i8(Wq_h, xq) (+ bias); qh = q*s
+// quantized per vector; scores = gemv_i8(K_h, qh); softmax; p quantized per
+// vector; out = gemv_i8(Vt_h, p).  512 threads.  Vt rows have stride Tq (T rounded up
 // to 16, zero padded).  Both K (CA_KPT keys per thread) and this wave's 8 Vt
 // rows (CA_VPL 16-byte chunks per lane per row) are loaded into registers at
 // entry, so their latency overlaps the score/softmax chain.
 #define CA_KPT 3
 #define CA_VPL 2
-__global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const int8_t *ck, const float *cks,
-                                                         const int8_t *cvt, const float *cvs, float *att, int d,
-                                                         int T, int Tq, int H, int L, int layer, float scale,
-                                                         float *pmax) {
+__global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restrict__ wq, const float *__restrict__ swq,
+                                                         const float *__restrict__ bq, const int8_t *__restrict__ xq,
+                                                         const float *__restrict__ xqs, const int8_t *ck,
+                                                         const float *cks, const int8_t *cvt, const float *cvs,
+                                                         float *att, int d, int T, int Tq, int H, int L, int layer,
+                                                         float scale, float *pmax) {
     extern __shared__ __align__(16) unsigned char smc2[];
     float *sc = (float *)smc2;                                       // [T]
     int8_t *p8 = (int8_t *)(smc2 + sizeof(float) * ((T + 3) & ~3)); // [Tq]
@@ -696,6 +699,30 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
     const int8_t *Vp = cvt + lh * (size_t)Tq * 64;
     const float *Vs = cvs + lh * 64;
     const int nch = Tq >> 4;
+    // This head's 64 rows of the cross q projection for stream s (gemv_i8,
+    // nn.rs:3168-3231: exact i32 dots, ((f32)acc * s_w) * s_x + b), 8 rows per
+    // wave, lane c taking 16-byte chunks c and c + 64 of the row (d <= 2048).
+    // Its operands are loaded first: the K/V prefetch behind them is not
+    // waited for until the scores.
+    __shared__ float qf[64];
+    const int nq = d >> 4;
+    const int qc0 = lane < nq ? lane : 0, qc1 = lane + 64 < nq ? lane + 64 : 0;
+    int4 xa = *(const int4 *)(xq + (size_t)s * d + qc0 * 16), xb = *(const int4 *)(xq + (size_t)s * d + qc1 * 16);
+    int4 wa[8], wb[8];
+#pragma unroll
+    for (int rr = 0; rr < 8; rr++) {
+        const int8_t *wr = wq + (size_t)(h * 64 + wave * 8 + rr) * d;
+        wa[rr] = *(const int4 *)(wr + qc0 * 16);
+        wb[rr] = *(const int4 *)(wr + qc1 * 16);
+    }
+    const float sx = xqs[s];
+    float qsw[8], qb[8];
+#pragma unroll
+    for (int rr = 0; rr < 8; rr++) {
+        const int row = h * 64 + wave * 8 + rr;
+        qsw[rr] = swq[row];
+        qb[rr] = bq ? bq[row] : 0.0f;
+    }
     // register prefetch: this thread's keys and this wave's value rows
     int4 kr[CA_KPT][4];
     float ksc[CA_KPT];
@@ -708,6 +735,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
         for (int c = 0; c < 4; c++) kr[u][c] = kp[c];
         ksc[u] = Ks[jc];
     }
+    // (chunks past nch reload the last one; their p8 operand is zero)
     int4 vr[8][CA_VPL];
 #pragma unroll
     for (int rr = 0; rr < 8; rr++) {
@@ -715,12 +743,34 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const float *qc, const 
 #pragma unroll
         for (int u = 0; u < CA_VPL; u++) {
             const int c = lane + u * 64;
-            int4 v = *(const int4 *)(vrow + (c < nch ? c : nch - 1) * 16);
-            vr[rr][u] = c < nch ? v : make_int4(0, 0, 0, 0);
+            vr[rr][u] = *(const int4 *)(vrow + (c < nch ? c : nch - 1) * 16);
         }
     }
+    {
+        // zero the chunks past the row; the mask is opaque to the compiler so
+        // the (clamped, in-bounds) loads stay unconditional
+        int ma = lane < nq ? -1 : 0, mb = lane + 64 < nq ? -1 : 0;
+        asm volatile("" : "+v"(ma), "+v"(mb));
+        xa = make_int4(xa.x & ma, xa.y & ma, xa.z & ma, xa.w & ma);
+        xb = make_int4(xb.x & mb, xb.y & mb, xb.z & mb, xb.w & mb);
+#pragma unroll
+        for (int rr = 0; rr < 8; rr++) {
+            int acc = 0;
+            acc = fw_sdot4(wa[rr].x, xa.x, acc);
+            acc = fw_sdot4(wa[rr].y, xa.y, acc);
+            acc = fw_sdot4(wa[rr].z, xa.z, acc);
+            acc = fw_sdot4(wa[rr].w, xa.w, acc);
+            acc = fw_sdot4(wb[rr].x, xb.x, acc);
+            acc = fw_sdot4(wb[rr].y, xb.y, acc);
+            acc = fw_sdot4(wb[rr].z, xb.z, acc);
+            acc = fw_sdot4(wb[rr].w, xb.w, acc);
+            acc = fw_dpp_wave_sum_i32(acc);
+            if (lane == 0) qf[wave * 8 + rr] = (float)acc * qsw[rr] * sx + qb[rr];
+        }
+    }
+    __syncthreads();
     if (wave == 0) {
-        float v = qc[(size_t)s * d + h * 64 + lane] * scale;
+        float v = qf[lane] * scale;
         float m = fw_dpp_wave_max(fabsf(v));
         float xs = fmaxf(m, 1e-9f) / 127.0f;
         q8[lane] = fw_q8_avx(v, 1.0f / xs, lane, 64);
@@ -948,12 +998,13 @@ void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16
                        scale, pmax);
 }
 
-void fw_launch_cross_attn_i8v2(hipStream_t st, const float *qc, const int8_t *ck, const float *cks, const int8_t *cvt,
+void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const int8_t *xq,
+                               const float *xqs, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
                                float scale, float *pmax) {
     size_t shm = sizeof(float) * ((T + 3) & ~3) + Tq;
-    hipLaunchKernelGGL(k_cross_attn_i8v2, dim3(H, ns), dim3(512), shm, st, qc, ck, cks, cvt, cvs, att, d, T, Tq, H, L,
-                       layer, scale, pmax);
+    hipLaunchKernelGGL(k_cross_attn_i8v2, dim3(H, ns), dim3(512), shm, st, wq, swq, bq, xq, xqs, ck, cks, cvt, cvs, att,
+                       d, T, Tq, H, L, layer, scale, pmax);
 }
 
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq) {

@@ -580,9 +580,9 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                                  st->pmax);
             gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr, st->att);
             fw_launch_ln_quant(s, st->x, nullptr, l.cross_ln_w, l.cross_ln_b, d, S, st->xq, st->xs);
-            gemv_i8_all(st, s, l.cq8, l.cq8s, l.cq_b, st->y, d, d, d, 0, nullptr);
-            fw_launch_cross_attn_i8v2(s, st->y, st->ck8, st->ck8s, st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li,
-                                      S, scale, st->pmax);
+            // the cross q projection runs inside the cross-attention kernel
+            fw_launch_cross_attn_i8v2(s, l.cq8, l.cq8s, l.cq_b, st->xq, st->xs, st->ck8, st->ck8s, st->cvt8, st->cvt8s,
+                                      st->att, d, T, st->Tq, H, L, li, S, scale, st->pmax);
             gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr, st->att);
             fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs);
             // mode 4: GELU written block-interleaved for the block GEMV; prefill
