@@ -114,8 +114,9 @@ __global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, cons
 }
 
 // embed_tokens (decoder.rs:1323-1385: x = f16(E[tok]) + P[pos]) of one stream
-// per block (one wave), followed by the first layer's attention LayerNorm of
-// the row (into ln_y and/or the int8 activation rows, as k_ln_quant).
+// per block (one wave), followed, when w is given, by the first layer's
+// attention LayerNorm of the row (into ln_y and/or the int8 activation rows,
+// as k_ln_quant).
 template <int NV>
 __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *posp, const uint16_t *emb,
                                                  const float *pemb, float *x, int d, const float *w, const float *b,
@@ -137,7 +138,7 @@ __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *
                             fw_h2f(e.y >> 16) + p.w);
         if (ok[k]) ((float4 *)(x + (size_t)s * d))[i] = xv[k];
     }
-    fw_ln_quant_vals<NV>(xv, ok, ln_y, w, b, d, s, xq, xs, lane);
+    if (w) fw_ln_quant_vals<NV>(xv, ok, ln_y, w, b, d, s, xq, xs, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -237,7 +238,7 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
     // XF: the head maxima are loaded first, so waiting for them does not wait
     // for the operand loads behind them (ns * H <= 512)
     float pm[2] = {0.0f, 0.0f};
-    if (XF) {
+    if (XF == 1) {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int e = threadIdx.x + u * 256;
@@ -256,8 +257,8 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
             wb[i][g] = *(const v4i *)(W + (size_t)(row < N ? row : N - 1) * K + ko + kbc * 64);
         }
     }
-    float4 xfv[XF ? GV_KPW : 1][4];
-    if (XF) {
+    float4 xfv[XF == 1 ? GV_KPW : 1][4];
+    if (XF == 1) {
         // operand chunks first (they are the long loads), then the row scales
 #pragma unroll
         for (int i = 0; i < GV_KPW; i++) {
@@ -276,21 +277,21 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
         }
         __syncthreads();
     }
-    if (XF) {
+    if (XF == 1) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int st_ = (lane >> 4) * 4 + r;
             e_xs[r] = fmaxf(__int_as_float(smax[st_ < ns ? st_ : 0]), 1e-9f) / 127.0f;
         }
     }
-    const float a_iv = XF ? 1.0f / (fmaxf(__int_as_float(smax[sa]), 1e-9f) / 127.0f) : 0.0f;
+    const float a_iv = XF == 1 ? 1.0f / (fmaxf(__int_as_float(smax[sa]), 1e-9f) / 127.0f) : 0.0f;
     // activation operands (every operand load is issued before the first
     // MFMA; addresses clamped, unused blocks never multiplied)
 #pragma unroll
     for (int i = 0; i < GV_KPW; i++) {
         const int kb = wave + 4 * i;
         const int kbc = kb < nkb ? kb : nkb - 1;
-        if (XF) {
+        if (XF == 1) {
             xa[i] = fw_q8_chunk16(xfv[i], a_iv);
             if (sa >= ns) xa[i] = (v4i){0, 0, 0, 0};
         } else {
@@ -307,7 +308,7 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
     // K beyond 4 * GV_KPW * 64
     for (int kb = wave + 4 * GV_KPW; kb < nkb; kb += 4) {
         v4i x1;
-        if (XF) {
+        if (XF == 1) {
             float4 v[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) v[c] = ((const float4 *)(frow + kb * 64))[c];
@@ -674,17 +675,19 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
 // rows of the cross q projection: q = gemv_i8(Wq_h, xq) (+ bias); qh = q*s
 // quantized per vector; scores = gemv_i8(K_h, qh); softmax; p quantized per
 // vector; out = gemv_i8(Vt_h, p).  512 threads.  Vt rows have stride Tq (T rounded up
-// to 16, zero padded).  Both K (CA_KPT keys per thread) and this wave's 8 Vt
-// rows (CA_VPL 16-byte chunks per lane per row) are loaded into registers at
-// entry, so their latency overlaps the score/softmax chain.
+// to 16, zero padded).  K (CA_KPT keys per thread) is loaded into registers at
+// entry and this wave's 8 Vt rows (CA_VPL 16-byte chunks per lane per row)
+// right after the q projection, so their latency overlaps the score/softmax
+// chain.
 #define CA_KPT 3
 #define CA_VPL 2
+template <int NV>
 __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restrict__ wq, const float *__restrict__ swq,
-                                                         const float *__restrict__ bq, const int8_t *__restrict__ xq,
-                                                         const float *__restrict__ xqs, const int8_t *ck,
-                                                         const float *cks, const int8_t *cvt, const float *cvs,
-                                                         float *att, int d, int T, int Tq, int H, int L, int layer,
-                                                         float scale, float *pmax) {
+                                                         const float *__restrict__ bq, const float *__restrict__ x,
+                                                         const float *__restrict__ lnw, const float *__restrict__ lnb,
+                                                         const int8_t *ck, const float *cks, const int8_t *cvt,
+                                                         const float *cvs, float *att, int d, int T, int Tq, int H,
+                                                         int L, int layer, float scale, float *pmax) {
     extern __shared__ __align__(16) unsigned char smc2[];
     float *sc = (float *)smc2;                                       // [T]
     int8_t *p8 = (int8_t *)(smc2 + sizeof(float) * ((T + 3) & ~3)); // [Tq]
@@ -699,15 +702,24 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
     const int8_t *Vp = cvt + lh * (size_t)Tq * 64;
     const float *Vs = cvs + lh * 64;
     const int nch = Tq >> 4;
-    // This head's 64 rows of the cross q projection for stream s (gemv_i8,
-    // nn.rs:3168-3231: exact i32 dots, ((f32)acc * s_w) * s_x + b), 8 rows per
-    // wave, lane c taking 16-byte chunks c and c + 64 of the row (d <= 2048).
-    // Its operands are loaded first: the K/V prefetch behind them is not
-    // waited for until the scores.
+    // The cross LayerNorm of stream s's residual row (wave 0, k_ln_quant's
+    // arithmetic, into LDS), then this head's 64 rows of the cross q
+    // projection (gemv_i8, nn.rs:3168-3231: exact i32 dots,
+    // ((f32)acc * s_w) * s_x + b), 8 rows per wave, lane c taking 16-byte
+    // chunks c and c + 64 of the row (d <= 2048).  These operands are loaded
+    // first: the K/V prefetch behind them is not waited for until the scores.
     __shared__ float qf[64];
+    __shared__ __align__(16) int8_t xql[256 * NV];
+    __shared__ float xsl;
+    float4 lv[NV];
+    bool lok[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        lok[k] = lane + k * 64 < (d >> 2);
+        lv[k] = ((const float4 *)(x + (size_t)s * d))[lok[k] ? lane + k * 64 : 0];
+    }
     const int nq = d >> 4;
     const int qc0 = lane < nq ? lane : 0, qc1 = lane + 64 < nq ? lane + 64 : 0;
-    int4 xa = *(const int4 *)(xq + (size_t)s * d + qc0 * 16), xb = *(const int4 *)(xq + (size_t)s * d + qc1 * 16);
     int4 wa[8], wb[8];
 #pragma unroll
     for (int rr = 0; rr < 8; rr++) {
@@ -715,7 +727,6 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
         wa[rr] = *(const int4 *)(wr + qc0 * 16);
         wb[rr] = *(const int4 *)(wr + qc1 * 16);
     }
-    const float sx = xqs[s];
     float qsw[8], qb[8];
 #pragma unroll
     for (int rr = 0; rr < 8; rr++) {
@@ -735,24 +746,13 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
         for (int c = 0; c < 4; c++) kr[u][c] = kp[c];
         ksc[u] = Ks[jc];
     }
-    // (chunks past nch reload the last one; their p8 operand is zero)
-    int4 vr[8][CA_VPL];
-#pragma unroll
-    for (int rr = 0; rr < 8; rr++) {
-        const int8_t *vrow = Vp + (size_t)(wave * 8 + rr) * Tq;
-#pragma unroll
-        for (int u = 0; u < CA_VPL; u++) {
-            const int c = lane + u * 64;
-            vr[rr][u] = *(const int4 *)(vrow + (c < nch ? c : nch - 1) * 16);
-        }
-    }
+    if (wave == 0) fw_ln_quant_vals<NV>(lv, lok, nullptr, lnw, lnb, d, 0, xql, &xsl, lane);
+    __syncthreads();
     {
-        // zero the chunks past the row; the mask is opaque to the compiler so
-        // the (clamped, in-bounds) loads stay unconditional
-        int ma = lane < nq ? -1 : 0, mb = lane + 64 < nq ? -1 : 0;
-        asm volatile("" : "+v"(ma), "+v"(mb));
-        xa = make_int4(xa.x & ma, xa.y & ma, xa.z & ma, xa.w & ma);
-        xb = make_int4(xb.x & mb, xb.y & mb, xb.z & mb, xb.w & mb);
+        // chunks past the row read as zero
+        const int4 xa = lane < nq ? *(const int4 *)(xql + qc0 * 16) : make_int4(0, 0, 0, 0);
+        const int4 xb = lane + 64 < nq ? *(const int4 *)(xql + qc1 * 16) : make_int4(0, 0, 0, 0);
+        const float sx = xsl;
 #pragma unroll
         for (int rr = 0; rr < 8; rr++) {
             int acc = 0;
@@ -766,6 +766,18 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
             acc = fw_sdot4(wb[rr].w, xb.w, acc);
             acc = fw_dpp_wave_sum_i32(acc);
             if (lane == 0) qf[wave * 8 + rr] = (float)acc * qsw[rr] * sx + qb[rr];
+        }
+    }
+    // this wave's value rows, needed only after the softmax (chunks past nch
+    // reload the last one; their p8 operand is zero)
+    int4 vr[8][CA_VPL];
+#pragma unroll
+    for (int rr = 0; rr < 8; rr++) {
+        const int8_t *vrow = Vp + (size_t)(wave * 8 + rr) * Tq;
+#pragma unroll
+        for (int u = 0; u < CA_VPL; u++) {
+            const int c = lane + u * 64;
+            vr[rr][u] = *(const int4 *)(vrow + (c < nch ? c : nch - 1) * 16);
         }
     }
     __syncthreads();
@@ -951,15 +963,12 @@ void fw_launch_gemv_i8m(hipStream_t st, const int8_t *W, const float *sw, const 
     if (filt) ff = *filt;
     else memset(&ff, 0, sizeof ff);
     int nblk = fw_gemv_i8m_blocks(N);
-    if (xf)
-        hipLaunchKernelGGL((k_gemv_i8m<1, 1>), dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy,
-                           mode, gelu_tab, ff, use, initialp, keys, xf, pmax, H);
-    else if (N >= 16384)
-        hipLaunchKernelGGL((k_gemv_i8m<4, 0>), dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy,
-                           mode, gelu_tab, ff, use, initialp, keys, xf, pmax, H);
-    else
-        hipLaunchKernelGGL((k_gemv_i8m<1, 0>), dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy,
-                           mode, gelu_tab, ff, use, initialp, keys, xf, pmax, H);
+#define GV_ARGS dim3(nblk), dim3(256), 0, st, W, sw, bias, xq, xs, y, N, K, ns, ldy, mode, gelu_tab, ff, use, initialp, \
+                keys, xf, pmax, H
+    if (xf) hipLaunchKernelGGL((k_gemv_i8m<1, 1>), GV_ARGS);
+    else if (N >= 16384) hipLaunchKernelGGL((k_gemv_i8m<4, 0>), GV_ARGS);
+    else hipLaunchKernelGGL((k_gemv_i8m<1, 0>), GV_ARGS);
+#undef GV_ARGS
 }
 
 void fw_launch_argmax_finish(hipStream_t st, const unsigned long long *keys, int nblk, int ns, int32_t *tok,
@@ -998,13 +1007,13 @@ void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16
                        scale, pmax);
 }
 
-void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const int8_t *xq,
-                               const float *xqs, const int8_t *ck, const float *cks, const int8_t *cvt,
+void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,
+                               const float *lnw, const float *lnb, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
                                float scale, float *pmax) {
     size_t shm = sizeof(float) * ((T + 3) & ~3) + Tq;
-    hipLaunchKernelGGL(k_cross_attn_i8v2, dim3(H, ns), dim3(512), shm, st, wq, swq, bq, xq, xqs, ck, cks, cvt, cvs, att,
-                       d, T, Tq, H, L, layer, scale, pmax);
+    FW_ROWS_DISPATCH(k_cross_attn_i8v2, d, dim3(H, ns), dim3(512), shm, st, wq, swq, bq, x, lnw, lnb, ck, cks, cvt,
+                     cvs, att, d, T, Tq, H, L, layer, scale, pmax);
 }
 
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq) {

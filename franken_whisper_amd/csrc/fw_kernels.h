@@ -37,10 +37,10 @@ int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const 
 // that quantizes the rows itself (fw_launch_gemv_i8m with xf)
 void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
                           int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax = nullptr);
-// q = Wq xq: int8 cross q projection [d, d] with row scales swq and bias bq,
-// applied to the quantized LayerNorm rows xq / xqs
-void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const int8_t *xq,
-                               const float *xqs, const int8_t *ck, const float *cks, const int8_t *cvt,
+// q = Wq LN(x): the cross LayerNorm (lnw, lnb) of the residual rows x and the
+// int8 cross q projection [d, d] (row scales swq, bias bq) run in the kernel
+void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,
+                               const float *lnw, const float *lnb, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
                                float scale, float *pmax = nullptr);
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq);

@@ -573,21 +573,23 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
     for (int li = 0; li < L; li++) {
         const DecLayerDev &l = dd->layers[li];
         if (i8) {
+            // (the cross LayerNorm runs inside the cross-attention kernel; the
+            // GEMVs' 80-320 blocks would each redo a whole LayerNorm, which
+            // measured slower than this one-wave-per-row kernel)
             if (li > 0) fw_launch_ln_quant(s, st->x, nullptr, l.attn_ln_w, l.attn_ln_b, d, S, st->xq, st->xs);
             gemv_i8_all(st, s, l.qkv8, l.qkv8s, l.qkv_b, st->qkv, 3 * d, d, 3 * d, 0, nullptr);
             // attention writes per-head maxima; the o / co GEMVs quantize att themselves
             fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale,
                                  st->pmax);
             gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr, st->att);
-            fw_launch_ln_quant(s, st->x, nullptr, l.cross_ln_w, l.cross_ln_b, d, S, st->xq, st->xs);
-            // the cross q projection runs inside the cross-attention kernel
-            fw_launch_cross_attn_i8v2(s, l.cq8, l.cq8s, l.cq_b, st->xq, st->xs, st->ck8, st->ck8s, st->cvt8, st->cvt8s,
-                                      st->att, d, T, st->Tq, H, L, li, S, scale, st->pmax);
+            // the cross LayerNorm and q projection run inside the cross-attention kernel
+            fw_launch_cross_attn_i8v2(s, l.cq8, l.cq8s, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck8, st->ck8s,
+                                      st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li, S, scale, st->pmax);
             gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr, st->att);
-            fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs);
             // mode 4: GELU written block-interleaved for the block GEMV; prefill
             // rows take the f16 mlp_2 (the block-int8 arm has no batch form),
             // which reads natural order
+            fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs);
             gemv_i8_all(st, s, l.fc1_8, l.fc1_8s, l.fc1_b, st->ff, dff, d, dff, prefill ? 2 : 4, nullptr);
             if (prefill) fw_launch_gemv_f16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
             else if (!gemv_blk_all(st, s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, d))
