@@ -185,9 +185,6 @@ __device__ __forceinline__ bool dec_masked(int i, const fwhip_filter &f, int ini
 // quantization pass over the rows is needed.
 // 16 elements of a row whose length is a multiple of 8: all in the add-trunc
 // body of the quantizer.
-__device__ __forceinline__ uint32_t fw_q8_body(float v, float iv) {
-    return (uint32_t)(uint8_t)(int8_t)(int)fw_clamp(fw_round_add_trunc(v * iv), -127.0f, 127.0f);
-}
 __device__ __forceinline__ v4i fw_q8_chunk16(const float4 (&v)[4], float iv) {
     v4i q;
 #pragma unroll

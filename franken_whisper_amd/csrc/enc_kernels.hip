@@ -153,20 +153,23 @@ __global__ void __launch_bounds__(256) k_gelu_quant_i7_rows(const float *x, int 
             const int c4 = lane + 64 * k;
             v[k] = ((const float4 *)xr)[c4 < n4 ? c4 : 0];
         }
-        float m = 0.0f;
+        // all table reads first (groups past the row hold clamped, valid
+        // data), then the row max
+        if (gelu_tab) {
 #pragma unroll
-        for (int k = 0; k < GQ_V4; k++) {
-            if (lane + 64 * k < n4) {
-                if (gelu_tab) {
-                    v[k].x = fw_gelu(v[k].x, gelu_tab);
-                    v[k].y = fw_gelu(v[k].y, gelu_tab);
-                    v[k].z = fw_gelu(v[k].z, gelu_tab);
-                    v[k].w = fw_gelu(v[k].w, gelu_tab);
-                }
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+            for (int k = 0; k < GQ_V4; k++) {
+                v[k].x = fw_gelu(v[k].x, gelu_tab);
+                v[k].y = fw_gelu(v[k].y, gelu_tab);
+                v[k].z = fw_gelu(v[k].z, gelu_tab);
+                v[k].w = fw_gelu(v[k].w, gelu_tab);
             }
         }
-        m = fw_wave_max(m);
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < GQ_V4; k++)
+            if (lane + 64 * k < n4)
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+        m = fw_dpp_wave_max(m);
         const float sc = fmaxf(m, 1e-9f) / 127.0f;
         const float inv = 1.0f / sc;
 #pragma unroll
@@ -189,6 +192,72 @@ __global__ void __launch_bounds__(256) k_gelu_quant_i7_rows(const float *x, int 
     const float inv = 1.0f / sc;
     for (int i = lane; i < n; i += 64) q[r * n + i] = fw_q8_avx(gelu_tab ? fw_gelu(xr[i], gelu_tab) : xr[i], inv, i, n);
     if (lane == 0) qs[r] = sc;
+}
+
+// GELU + quantize_act of fc1 rows (the same arithmetic as the kernel above)
+// with the reference's f16-indexed GELU table held in LDS as f16 (its values
+// are f16-rounded): 64K x 2 B = 128 KB, loaded once per block.  The grid is
+// persistent (one block per CU, grid-stride over rows), one wave per row, NV4
+// float4 groups per lane, the wave's next row loading while the current one is
+// processed; rows of n % 8 == 0 values use the add-trunc rounding throughout.
+#define GQ_TAB_N 65536
+template <int NV4>
+__global__ void __launch_bounds__(512) k_gelu_quant_rows_lds(const float *x, int rows, int n, const float *gelu_tab,
+                                                             int8_t *q, float *qs) {
+    extern __shared__ uint16_t gtab[]; // [65536]
+    for (int i = threadIdx.x; i < GQ_TAB_N; i += blockDim.x) gtab[i] = fw_f2h(gelu_tab[i]); // values are f16-exact
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wpb = blockDim.x >> 6;
+    const int n4 = n >> 2;
+    auto load = [&](float4 (&v)[NV4], int r) {
+        const float4 *xr = (const float4 *)(x + (size_t)r * n);
+#pragma unroll
+        for (int k = 0; k < NV4; k++) {
+            const int c4 = lane + 64 * k;
+            v[k] = xr[c4 < n4 ? c4 : 0];
+        }
+    };
+    auto row = [&](float4 (&v)[NV4], int r) {
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV4; k++) {
+            float *e = &v[k].x;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float a = e[c];
+                const float t = fw_h2f(gtab[fw_f2h(a)]);
+                e[c] = a <= -10.0f ? 0.0f : (a >= 10.0f ? a : t);
+            }
+            if (lane + 64 * k < n4)
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+        }
+        m = fw_dpp_wave_max(m);
+        const float sc = fmaxf(m, 1e-9f) / 127.0f;
+        const float inv = 1.0f / sc;
+#pragma unroll
+        for (int k = 0; k < NV4; k++) {
+            const int c4 = lane + 64 * k;
+            if (c4 < n4) {
+                const uint32_t b0 = fw_q8_body(v[k].x, inv), b1 = fw_q8_body(v[k].y, inv);
+                const uint32_t b2 = fw_q8_body(v[k].z, inv), b3 = fw_q8_body(v[k].w, inv);
+                ((uint32_t *)(q + (size_t)r * n))[c4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
+        }
+        if (lane == 0) qs[r] = sc;
+    };
+    // two row buffers: the next row of this wave loads while this one is
+    // processed
+    const int step = gridDim.x * wpb;
+    float4 va[NV4], vb[NV4];
+    int r = blockIdx.x * wpb + (threadIdx.x >> 6);
+    if (r < rows) load(va, r);
+    for (; r < rows; r += 2 * step) {
+        if (r + step < rows) load(vb, r + step);
+        row(va, r);
+        if (r + step >= rows) break;
+        if (r + 2 * step < rows) load(va, r + 2 * step);
+        row(vb, r + step);
+    }
 }
 
 // im2col for conv1d (kernel 3, pad 1; conv1d_wt nn.rs:5006-5103) into the f16
@@ -526,6 +595,25 @@ void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n,
 }
 void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int n, const float *tab, int8_t *q,
                                   float *qs) {
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    const size_t shm = sizeof(uint16_t) * GQ_TAB_N;
+    const dim3 grid(n_cu), blk(512);
+    if (tab && (n & 7) == 0) {
+        switch ((n + 255) / 256) {
+        case 6: hipLaunchKernelGGL(k_gelu_quant_rows_lds<6>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+        case 8: hipLaunchKernelGGL(k_gelu_quant_rows_lds<8>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+        case 12: hipLaunchKernelGGL(k_gelu_quant_rows_lds<12>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+        case 16: hipLaunchKernelGGL(k_gelu_quant_rows_lds<16>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+        case 20: hipLaunchKernelGGL(k_gelu_quant_rows_lds<20>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+        default: break;
+        }
+    }
     hipLaunchKernelGGL(k_gelu_quant_i7_rows, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, tab, q, qs);
 }
 void fw_launch_im2col(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, int Kp,

@@ -39,6 +39,12 @@ __device__ __forceinline__ int8_t fw_q8_avx(float v, float inv, int i, int n) {
     return (int8_t)(int)fw_clamp(r, -127.0f, 127.0f);
 }
 
+// fw_q8_avx for an element of the add-trunc body (rows of n % 8 == 0), as an
+// unsigned byte ready for packing.
+__device__ __forceinline__ uint32_t fw_q8_body(float v, float inv) {
+    return (uint32_t)(uint8_t)(int8_t)(int)fw_clamp(fw_round_add_trunc(v * inv), -127.0f, 127.0f);
+}
+
 __device__ __forceinline__ float fw_expf(float x) {
     const uint64_t tab[32] = FW_EXP2F_TAB;
     return fw_expf_tab(x, tab);
@@ -46,7 +52,15 @@ __device__ __forceinline__ float fw_expf(float x) {
 
 // GELU of the reference (nn.rs:4603-4673): clamp +-10, else f16-indexed table.
 __device__ __forceinline__ float fw_gelu(float v, const float *tab) {
-    return v <= -10.0f ? 0.0f : (v >= 10.0f ? v : tab[fw_f2h(v)]);
+    // The table read is unconditional (every f16 pattern is a valid index) and
+    // the clamp cases are merged with bit masks the compiler cannot see
+    // through: written as a select, the read gets moved behind a branch of its
+    // own and each element waits for its data in turn.
+    const uint32_t t = __float_as_uint(tab[fw_f2h(v)]);
+    const bool lo = v <= -10.0f, hi = v >= 10.0f;
+    uint32_t mt = (!lo && !hi) ? 0xffffffffu : 0u, mv = hi ? 0xffffffffu : 0u;
+    asm volatile("" : "+v"(mt), "+v"(mv));
+    return __uint_as_float((t & mt) | (__float_as_uint(v) & mv));
 }
 
 // ---- wave / block reductions -------------------------------------------
