@@ -198,11 +198,11 @@ __global__ void __launch_bounds__(256) k_gelu_quant_i7_rows(const float *x, int 
 // with the reference's f16-indexed GELU table held in LDS as f16 (its values
 // are f16-rounded): 64K x 2 B = 128 KB, loaded once per block.  The grid is
 // persistent (one block per CU, grid-stride over rows), one wave per row, NV4
-// float4 groups per lane, the wave's next row loading while the current one is
-// processed; rows of n % 8 == 0 values use the add-trunc rounding throughout.
+// float4 groups per lane; rows of n % 8 == 0 values use the add-trunc rounding
+// throughout.
 #define GQ_TAB_N 65536
-template <int NV4>
-__global__ void __launch_bounds__(512) k_gelu_quant_rows_lds(const float *x, int rows, int n, const float *gelu_tab,
+template <int NV4, bool FULL>
+__global__ void __launch_bounds__(1024) k_gelu_quant_rows_lds(const float *x, int rows, int n, const float *gelu_tab,
                                                              int8_t *q, float *qs) {
     extern __shared__ uint16_t gtab[]; // [65536]
     for (int i = threadIdx.x; i < GQ_TAB_N; i += blockDim.x) gtab[i] = fw_f2h(gelu_tab[i]); // values are f16-exact
@@ -218,17 +218,30 @@ __global__ void __launch_bounds__(512) k_gelu_quant_rows_lds(const float *x, int
         }
     };
     auto row = [&](float4 (&v)[NV4], int r) {
+        // a row with every |x| < 10 (the usual case, decided for the whole
+        // wave) needs no clamp selects: GELU is the table value
+        float ax = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV4; k++)
+            if (FULL || lane + 64 * k < n4)
+                ax = fmaxf(ax, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+        const bool inner = fw_dpp_wave_max(ax) < 10.0f;
         float m = 0.0f;
 #pragma unroll
         for (int k = 0; k < NV4; k++) {
             float *e = &v[k].x;
+            if (inner) {
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const float a = e[c];
-                const float t = fw_h2f(gtab[fw_f2h(a)]);
-                e[c] = a <= -10.0f ? 0.0f : (a >= 10.0f ? a : t);
+                for (int c = 0; c < 4; c++) e[c] = fw_h2f(gtab[fw_f2h(e[c])]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float a = e[c];
+                    const float t = fw_h2f(gtab[fw_f2h(a)]);
+                    e[c] = a <= -10.0f ? 0.0f : (a >= 10.0f ? a : t);
+                }
             }
-            if (lane + 64 * k < n4)
+            if (FULL || lane + 64 * k < n4)
                 m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
         }
         m = fw_dpp_wave_max(m);
@@ -237,7 +250,7 @@ __global__ void __launch_bounds__(512) k_gelu_quant_rows_lds(const float *x, int
 #pragma unroll
         for (int k = 0; k < NV4; k++) {
             const int c4 = lane + 64 * k;
-            if (c4 < n4) {
+            if (FULL || c4 < n4) {
                 const uint32_t b0 = fw_q8_body(v[k].x, inv), b1 = fw_q8_body(v[k].y, inv);
                 const uint32_t b2 = fw_q8_body(v[k].z, inv), b3 = fw_q8_body(v[k].w, inv);
                 ((uint32_t *)(q + (size_t)r * n))[c4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
@@ -245,18 +258,10 @@ __global__ void __launch_bounds__(512) k_gelu_quant_rows_lds(const float *x, int
         }
         if (lane == 0) qs[r] = sc;
     };
-    // two row buffers: the next row of this wave loads while this one is
-    // processed
-    const int step = gridDim.x * wpb;
-    float4 va[NV4], vb[NV4];
-    int r = blockIdx.x * wpb + (threadIdx.x >> 6);
-    if (r < rows) load(va, r);
-    for (; r < rows; r += 2 * step) {
-        if (r + step < rows) load(vb, r + step);
-        row(va, r);
-        if (r + step >= rows) break;
-        if (r + 2 * step < rows) load(va, r + 2 * step);
-        row(vb, r + step);
+    for (int r = blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += gridDim.x * wpb) {
+        float4 v[NV4];
+        load(v, r);
+        row(v, r);
     }
 }
 
@@ -603,14 +608,22 @@ void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int 
             n_cu = 256;
     }
     const size_t shm = sizeof(uint16_t) * GQ_TAB_N;
-    const dim3 grid(n_cu), blk(512);
-    if (tab && (n & 7) == 0) {
-        switch ((n + 255) / 256) {
-        case 6: hipLaunchKernelGGL(k_gelu_quant_rows_lds<6>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
-        case 8: hipLaunchKernelGGL(k_gelu_quant_rows_lds<8>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
-        case 12: hipLaunchKernelGGL(k_gelu_quant_rows_lds<12>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
-        case 16: hipLaunchKernelGGL(k_gelu_quant_rows_lds<16>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
-        case 20: hipLaunchKernelGGL(k_gelu_quant_rows_lds<20>, grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+    const dim3 grid(n_cu), blk(1024);
+    // the MLP widths of the Whisper sizes (4 x 384 ... 4 x 1280) are whole
+    // multiples of 256: every lane's groups are in the row
+    if (tab && (n & 255) == 0) {
+        switch (n / 256) {
+        case 6: hipLaunchKernelGGL((k_gelu_quant_rows_lds<6, true>), grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+        case 8: hipLaunchKernelGGL((k_gelu_quant_rows_lds<8, true>), grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+        case 12:
+            hipLaunchKernelGGL((k_gelu_quant_rows_lds<12, true>), grid, blk, shm, st, x, rows, n, tab, q, qs);
+            return;
+        case 16:
+            hipLaunchKernelGGL((k_gelu_quant_rows_lds<16, true>), grid, blk, shm, st, x, rows, n, tab, q, qs);
+            return;
+        case 20:
+            hipLaunchKernelGGL((k_gelu_quant_rows_lds<20, true>), grid, blk, shm, st, x, rows, n, tab, q, qs);
+            return;
         default: break;
         }
     }
