@@ -151,11 +151,33 @@ __device__ __forceinline__ unsigned long long am_key(float v, int idx) {
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
 }
-__device__ __forceinline__ unsigned long long shfl_max_u64(unsigned long long k, int off) {
-    uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
-    uint32_t lo2 = __shfl_xor(lo, off, 64), hi2 = __shfl_xor(hi, off, 64);
-    unsigned long long o = ((unsigned long long)hi2 << 32) | lo2;
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_max_u64(unsigned long long k) {
+    const uint32_t lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)k, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(k >> 32), CTRL, 0xf, 0xf, false);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
     return o > k ? o : k;
+}
+// max over each 16-lane row (every lane of the row gets it), DPP moves only
+__device__ __forceinline__ unsigned long long row16_max_u64(unsigned long long k) {
+    k = dpp_max_u64<FW_DPP_XOR1>(k);
+    k = dpp_max_u64<FW_DPP_XOR2>(k);
+    k = dpp_max_u64<FW_DPP_HALF_MIRROR>(k);
+    return dpp_max_u64<FW_DPP_MIRROR>(k);
+}
+// max over the wave (every lane gets it)
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+    k = row16_max_u64(k);
+    const unsigned long long r0 = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), 0) << 32) |
+                                  (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 0);
+    const unsigned long long r1 = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), 16) << 32) |
+                                  (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 16);
+    const unsigned long long r2 = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), 32) << 32) |
+                                  (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 32);
+    const unsigned long long r3 = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), 48) << 32) |
+                                  (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 48);
+    const unsigned long long a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
+    return a > b ? a : b;
 }
 
 // The suppress set of process_logits in no-timestamps mode (decode.rs:702-867).
@@ -345,8 +367,7 @@ __global__ void __launch_bounds__(256) k_gemv_i8m(const int8_t *__restrict__ W, 
             }
             if (mode == 3) {
                 // max over the 16 lanes holding stream s (same lane>>4)
-#pragma unroll
-                for (int off = 1; off < 16; off <<= 1) key = shfl_max_u64(key, off);
+                key = row16_max_u64(key);
                 if ((lane & 15) == 0) ksh[g][s] = key;
             }
         }
@@ -382,8 +403,7 @@ __global__ void __launch_bounds__(1024) k_argmax_finish(const unsigned long long
             k = a0 > k ? a0 : k;
         }
         for (; i < nblk; i += 64) k = ks[i] > k ? ks[i] : k;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) k = shfl_max_u64(k, off);
+        k = wave_max_u64(k);
         if (lane == 0) {
             int t = k ? (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull)) : 0;
             tok[s] = t;
@@ -1031,8 +1051,7 @@ __global__ void __launch_bounds__(256) k_logits_keys(const float *logits, int V,
         unsigned long long c = am_key(l[i], i);
         k = c > k ? c : k;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) k = shfl_max_u64(k, off);
+    k = wave_max_u64(k);
     if (lane == 0) wk[wave] = k;
     __syncthreads();
     if (threadIdx.x == 0) {
