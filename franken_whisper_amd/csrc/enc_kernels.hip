@@ -313,9 +313,9 @@ __global__ void k_fill_u16(uint16_t *p, size_t n, uint16_t v) {
 // 4 x 8 KB) fed global -> LDS directly through an AT_NS-stage ring, one
 // barrier per tile.  Rows are 128 bytes; 16-byte chunk c of row r sits at
 // chunk c ^ (r & 7), which keeps the fragment reads free of bank conflicts.
-#define AT_NS 3
 #define AT_QW 8
-__global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
+template <int AT_QW_, int AT_NS>
+__global__ void __launch_bounds__(64 * AT_QW_) k_attention2(const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                                                            const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl,
                                                            int T, int Tp, int H, int d, int out_mode, float *of,
                                                            uint16_t *oh, uint16_t *ol) {
@@ -323,7 +323,7 @@ __global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, c
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = blockIdx.y, b = blockIdx.z;
     const size_t bh = (size_t)b * H + h;
-    const int q0 = blockIdx.x * 32 * AT_QW + wave * 32;
+    const int q0 = blockIdx.x * 32 * AT_QW_ + wave * 32;
     const int myq = q0 + (lane & 31);
     const int nt = (T + 63) >> 6;
     // this lane's Q^T fragments: q = myq, dims ks*16 + (l/32)*8 .. +8
@@ -341,8 +341,8 @@ __global__ void __launch_bounds__(64 * AT_QW) k_attention2(const uint16_t *qh, c
             }
         }
     }
-    // loader: 32 instructions of 1 KB per tile, AT_QW waves share them
-    constexpr int LPW = 32 / AT_QW;
+    // loader: 32 instructions of 1 KB per tile, AT_QW_ waves share them
+    constexpr int LPW = 32 / AT_QW_;
     const uint16_t *src[LPW];
     int dsto[LPW];
 #pragma unroll
@@ -648,6 +648,6 @@ void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql,
                          const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
                          int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol) {
     dim3 grid((T + 32 * AT_QW - 1) / (32 * AT_QW), H, B);
-    hipLaunchKernelGGL(k_attention2, grid, dim3(64 * AT_QW), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d, out_mode, of,
-                       oh, ol);
+    hipLaunchKernelGGL((k_attention2<AT_QW, 3>), grid, dim3(64 * AT_QW), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d,
+                       out_mode, of, oh, ol);
 }
