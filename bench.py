@@ -204,7 +204,7 @@ def main():
     ctx.timing(False)
     ms_per_step = elapsed * 1e3 / a.steps
 
-    names = {abi.K_ENC_GEMM_I8: ("encoder int8 GEMM (k_gemm2, int8 tiles)", "mfma", "int8"),
+    names = {abi.K_ENC_GEMM_I8: ("encoder int8 GEMM (k_gemm_pi8, persistent int8 tiles)", "mfma", "int8"),
              abi.K_ENC_GEMM_F32: ("encoder f16-pair GEMM (k_gemm2, f16-pair tiles)", "mfma", "f16"),
              abi.K_ENC_ATTN: ("encoder attention (k_attention2, f16 pairs)", "mfma", "f16"),
              abi.K_DEC_LOGITS: ("decoder logits GEMV (k_gemv_i8m)", "hbm", None)}

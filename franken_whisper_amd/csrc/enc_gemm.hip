@@ -38,6 +38,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 #define GEMM_LDSR 80 // LDS row stride in bytes (64 data + 16 pad)
 
@@ -481,6 +482,360 @@ __global__ void __launch_bounds__(256) k_gemm2(FwGemm g, int ntm, int ntn) {
 }
 
 // ---------------------------------------------------------------------------
+// Persistent int8 GEMM.  One block per CU walks its share of the tile sequence
+// through a single flattened (tile, k-step) pipeline: the operand stages of the
+// next tile are already in flight while the current tile's epilogue runs, and
+// its stores drain to memory under the next tile's MFMAs (a one-tile-per-block
+// launch leaves every CU storing at once and the MFMAs idle meanwhile).
+//
+// Block = NW = WGM x WGN waves (2 per SIMD); block tile BM x BN, wave tile
+// (BM/WGM) x (BN/WGN) of 32x32 i8 MFMA tiles; K advances 64 bytes per stage
+// through an NS-stage global -> LDS ring (16-byte chunks XOR-swizzled by
+// gsw(row)), one barrier per stage.
+//
+// vmcnt bookkeeping: stage s+1 is known to have landed once at most
+// LPW*(NS-2) of this wave's loads are outstanding, which holds while every
+// memory operation issued after stage s+1 is a load (loads return in order).
+// Stores may complete out of order with loads, so before a tile's epilogue
+// issues stores every outstanding load is waited for (vmcnt 0), and loads
+// issued after the stores are the only ones later waits count on.
+//
+// The per-tile row scales sx, column scales sw and bias are staged into LDS
+// with the tile's first stage (SCL 256-byte loads per wave, the same number
+// for every wave so the counts above stay uniform; a tile's scales sit in the
+// LDS half of its parity).
+//
+// Tile sequence: XCD x (blocks x, x+8, ...) owns a contiguous range of the
+// GM=8-grouped tile order, walked by its blocks in lockstep, so the tiles in
+// flight on one XCD share A row panels and B column panels in its L2.  With
+// `wrows` > 0 (the QKV epilogue) M tiles never straddle a window of wrows rows:
+// each window is tiled on its own, so every tile's rows share one window and
+// start at a multiple of BM within it.
+template <int EPI, int BM, int BN, int WGM, int WGN, int NS>
+__global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, int ntn, int ntw) {
+    constexpr int NW = WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+    constexpr int STAGE = (BM + BN) * 64, LPW = STAGE / 1024 / NW;
+    constexpr int SCL = (BM + 2 * BN + 64 * NW - 1) / (64 * NW); // scale loads per wave per tile
+    constexpr int SCLN = SCL * NW * 64;                           // floats per parity
+    constexpr bool QKV = EPI == FW_EPI_QKV;
+    constexpr int SLAB = 32 * 40;                                 // floats per wave (QKV transposes)
+    static_assert(STAGE % (1024 * NW) == 0, "stage loads must split evenly over waves");
+    __shared__ __align__(1024) unsigned char lds[NS * STAGE + 2 * SCLN * 4 + (QKV ? NW * SLAB * 4 : 0)];
+    float *scl = (float *)(lds + NS * STAGE);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int G = gridDim.x, xcd = blockIdx.x & 7, loc = blockIdx.x >> 3, nloc = G >> 3;
+    const int ntiles = ntm * ntn;
+    const int xs = (int)((long long)ntiles * xcd / 8), xe = (int)((long long)ntiles * (xcd + 1) / 8);
+    const int my_n = xe - xs > loc ? (xe - xs - loc + nloc - 1) / nloc : 0;
+    const int nsteps = g.K / 64;
+    const int total = my_n * nsteps;
+    if (total == 0) return;
+    // tile ti of this block -> first row, valid rows, first column
+    auto coords = [&](int ti, int &m0, int &mrows, int &n0) {
+        const int t = xs + loc + ti * nloc;
+        constexpr int GM = 8;
+        const int gsize = GM * ntn, grp = t / gsize, first_m = grp * GM;
+        const int gm = min(ntm - first_m, GM), rr = t - grp * gsize;
+        const int mt = first_m + rr % gm;
+        n0 = (rr / gm) * BN;
+        if (ntw > 0) {
+            const int w = mt / ntw, tt = mt - w * ntw;
+            m0 = w * g.T + tt * BM;
+            mrows = min(BM, g.T - tt * BM);
+        } else {
+            m0 = mt * BM;
+            mrows = min(BM, g.M - m0);
+        }
+    };
+    // issue side: tile and step of the next stage to load, per-lane sources
+    int it_tile = 0, it_step = 0;
+    const unsigned char *src[LPW];
+    const float *ssrc[SCL];
+    auto set_src = [&](int ti) {
+        int m0, mrows, n0;
+        coords(ti, m0, mrows, n0);
+#pragma unroll
+        for (int q = 0; q < LPW; q++) {
+            const int lr = (wave * LPW + q) * 16 + (lane >> 2);
+            const int c = (lane & 3) ^ gsw(lr);
+            if (lr < BM)
+                src[q] = (const unsigned char *)g.A + (size_t)(m0 + min(lr, mrows - 1)) * g.lda + c * 16;
+            else
+                src[q] = (const unsigned char *)g.B + (size_t)min(n0 + lr - BM, g.N - 1) * g.ldb + c * 16;
+        }
+#pragma unroll
+        for (int q = 0; q < SCL; q++) {
+            const int e = (q * NW + wave) * 64 + lane;
+            if (e < BM) ssrc[q] = g.sx + m0 + min(e, mrows - 1);
+            else if (e < BM + BN) ssrc[q] = g.sw + min(n0 + e - BM, g.N - 1);
+            else ssrc[q] = (g.bias ? g.bias : g.sw) + min(n0 + max(e - BM - BN, 0), g.N - 1);
+        }
+    };
+    set_src(0);
+    auto issue = [&](int gs) {
+        unsigned char *dst = lds + (gs % NS) * STAGE + wave * LPW * 1024;
+        const int sc = it_tile < my_n ? it_step : nsteps - 1; // past the last tile: in-bounds reload
+#pragma unroll
+        for (int q = 0; q < LPW; q++)
+            __builtin_amdgcn_global_load_lds((const void *)(src[q] + (size_t)sc * 64),
+                                             (void __attribute__((address_space(3))) *)(dst + q * 1024), 16, 0, 0);
+        if (it_step == 0) {
+            float *sd = scl + (it_tile & 1) * SCLN + wave * 64;
+#pragma unroll
+            for (int q = 0; q < SCL; q++)
+                __builtin_amdgcn_global_load_lds((const void *)ssrc[q],
+                                                 (void __attribute__((address_space(3))) *)(sd + q * NW * 64), 4,
+                                                 0, 0);
+        }
+        if (++it_step == nsteps) {
+            if (it_tile < my_n) {
+                it_step = 0;
+                if (++it_tile < my_n) set_src(it_tile);
+            } else {
+                it_step = nsteps - 1;
+            }
+        }
+    };
+
+    v16i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+    v4i fa[2][TM], fb[2][TN];
+    auto ldfrag = [&](int set, int stage, int ks) {
+        const unsigned char *tb = lds + (stage % NS) * STAGE;
+        const int c = ks * 2 + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int lr = wm * WM + i * 32 + (lane & 31);
+            fa[set][i] = *(const v4i *)(tb + lr * 64 + ((c ^ gsw(lr)) << 4));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int lr = BM + wn * WN + j * 32 + (lane & 31);
+            fb[set][j] = *(const v4i *)(tb + lr * 64 + ((c ^ gsw(lr)) << 4));
+        }
+    };
+    auto mfmas = [&](int set) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+    };
+
+#pragma unroll
+    for (int p = 0; p < NS - 1; p++) issue(p);
+    FW_WAIT_VM(0);
+    asm volatile("s_barrier" ::: "memory");
+    issue(NS - 1);
+    ldfrag(0, 0, 0);
+    const bool has_bias = g.bias != nullptr;
+    int tile = 0, s = 0;
+    for (int gs = 0; gs < total; gs++) {
+        FW_WAIT_LGKM0();
+        ldfrag(1, gs, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(0);
+        __builtin_amdgcn_sched_barrier(0);
+        FW_WAIT_VM_LGKM0(LPW * (NS - 2));
+        asm volatile("s_barrier" ::: "memory");
+        const bool last = s == nsteps - 1;
+        if (!last) issue(gs + NS);
+        ldfrag(0, gs + 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (!last) {
+            s++;
+            continue;
+        }
+        // ---- epilogue of this block's tile `tile` ----
+        FW_WAIT_VM(0);
+        int m0, mrows, n0;
+        coords(tile, m0, mrows, n0);
+        // lane-derived offsets recomputed here from an opaque copy of the lane
+        // id, so per-element addresses are not hoisted out of the tile loop
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const float *ssx = scl + (tile & 1) * SCLN, *ssw = ssx + BM, *sbi = ssw + BN;
+        if constexpr (EPI == FW_EPI_RESID) {
+            static_assert(TM * TN <= 4, "residual values of the wave tile are held in registers");
+            // residual values of every element first: one wait, then the stores
+            float cv[TM][TN][16];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int col = min(n0 + wn * WN + j * 32 + (ln & 31), g.N - 1);
+                    const int rl = wm * WM + i * 32 + (ln >> 5) * 4;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = m0 + min(rl + (r >> 2) * 8 + (r & 3), mrows - 1);
+                        cv[i][j][r] = g.C[(size_t)row * g.ldc + col];
+                    }
+                }
+            FW_WAIT_VM(0);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int cl = wn * WN + j * 32 + (ln & 31), col = n0 + cl;
+                    const int rl = wm * WM + i * 32 + (ln >> 5) * 4;
+                    const float s2 = ssw[cl], bb = sbi[cl];
+                    v4f sr[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sr[q] = *(const v4f *)(ssx + rl + q * 8);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int rw = rl + (r >> 2) * 8 + (r & 3);
+                        float v = (float)acc[i][j][r] * sr[r >> 2][r & 3] * s2;
+                        if (has_bias) v = v + bb;
+                        if (rw < mrows && col < g.N) g.C[(size_t)(m0 + rw) * g.ldc + col] = cv[i][j][r] + v;
+                    }
+                }
+        } else if constexpr (EPI == FW_EPI_F32 || EPI == FW_EPI_ACC32) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int cl = wn * WN + j * 32 + (ln & 31), col = n0 + cl;
+                    const int rl = wm * WM + i * 32 + (ln >> 5) * 4;
+                    const float s2 = ssw[cl], bb = sbi[cl];
+                    v4f sr[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sr[q] = *(const v4f *)(ssx + rl + q * 8);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int rw = rl + (r >> 2) * 8 + (r & 3);
+                        if (rw < mrows && col < g.N) {
+                            const size_t o = (size_t)(m0 + rw) * g.ldc + col;
+                            if constexpr (EPI == FW_EPI_ACC32) {
+                                ((int *)g.C)[o] = acc[i][j][r];
+                            } else {
+                                float v = (float)acc[i][j][r] * sr[r >> 2][r & 3] * s2;
+                                if (has_bias) v = v + bb;
+                                g.C[o] = v;
+                            }
+                        }
+                    }
+                }
+        } else if constexpr (QKV) {
+            // Q, K: [B, H, T, 64] f16 hi/lo rows, written through a wave-private
+            // LDS slab so each lane stores 16 consecutive dims (32-byte runs).
+            // V^T: [B, H, 64, Tp] at key positions fw_vt_pos(t); a lane's 8
+            // values r = 8c .. 8c+7 sit at 8 consecutive positions (window
+            // tiles start at multiples of 32), so they go out as 16-byte runs.
+            float *slab = (float *)(lds + NS * STAGE + 2 * SCLN * 4) + wave * SLAB;
+            const int d = g.ldc, wnd = m0 / g.T, tb0 = m0 - wnd * g.T;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int c0 = n0 + wn * WN + j * 32; // 32 columns of one head
+                    const int cl = c0 - n0 + (ln & 31), col = n0 + cl;
+                    const int rl = wm * WM + i * 32 + (ln >> 5) * 4;
+                    const float s2 = ssw[cl], bb = sbi[cl];
+                    v4f sr[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sr[q] = *(const v4f *)(ssx + rl + q * 8);
+                    float v[16];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        v[r] = (float)acc[i][j][r] * sr[r >> 2][r & 3] * s2;
+                        if (has_bias) v[r] = v[r] + bb;
+                    }
+                    if (c0 >= g.N) continue;
+                    const int which = c0 / d, cc = c0 - which * d, h = cc >> 6, dd0 = cc & 63;
+                    const int t0 = tb0 + wm * WM + i * 32; // window position of the tile's first row
+                    const int vrows = mrows - (wm * WM + i * 32);
+                    if (vrows <= 0) continue;
+                    if (which == 2) {
+                        const int dd = dd0 + (ln & 31);
+                        uint16_t *vh = g.o16[4] + (((size_t)wnd * g.H + h) * 64 + dd) * g.Tp;
+                        uint16_t *vl = g.o16[5] + (((size_t)wnd * g.H + h) * 64 + dd) * g.Tp;
+#pragma unroll
+                        for (int c = 0; c < 2; c++) {
+                            const int pb = t0 + 16 * c + 8 * (ln >> 5); // first of 8 positions
+                            uint16_t hi[8], lo[8];
+#pragma unroll
+                            for (int e = 0; e < 8; e++) fw_split2(v[8 * c + e], hi[e], lo[e]);
+                            if (16 * c + 16 <= vrows) {
+                                uint4 ph, pl;
+                                ph.x = hi[0] | ((uint32_t)hi[1] << 16);
+                                ph.y = hi[2] | ((uint32_t)hi[3] << 16);
+                                ph.z = hi[4] | ((uint32_t)hi[5] << 16);
+                                ph.w = hi[6] | ((uint32_t)hi[7] << 16);
+                                pl.x = lo[0] | ((uint32_t)lo[1] << 16);
+                                pl.y = lo[2] | ((uint32_t)lo[3] << 16);
+                                pl.z = lo[4] | ((uint32_t)lo[5] << 16);
+                                pl.w = lo[6] | ((uint32_t)lo[7] << 16);
+                                *(uint4 *)(vh + pb) = ph;
+                                *(uint4 *)(vl + pb) = pl;
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < 8; e++) {
+                                    // value e is key t0 + 16c + 8*(e/4) + 4*(lane/32) + e%4
+                                    const int rr = 16 * c + 8 * (e >> 2) + 4 * (ln >> 5) + (e & 3);
+                                    if (rr < vrows) {
+                                        const int p = fw_vt_pos(t0 + rr);
+                                        vh[p] = hi[e];
+                                        vl[p] = lo[e];
+                                    }
+                                }
+                            }
+                        }
+                    } else {
+                        // the slab is private to this wave and a wave's LDS accesses
+                        // run in order: only the compiler must not reorder them
+                        asm volatile("" ::: "memory");
+#pragma unroll
+                        for (int r = 0; r < 16; r++)
+                            slab[((r >> 2) * 8 + (ln >> 5) * 4 + (r & 3)) * 40 + (ln & 31)] = v[r];
+                        asm volatile("" ::: "memory");
+                        const int row = ln >> 1, half = ln & 1;
+                        v4f w4[4];
+#pragma unroll
+                        for (int q = 0; q < 4; q++) w4[q] = *(const v4f *)(slab + row * 40 + half * 16 + q * 4);
+                        asm volatile("" ::: "memory");
+                        if (row < vrows) {
+                            uint32_t ph[8], pl[8];
+#pragma unroll
+                            for (int q = 0; q < 8; q++) {
+                                uint16_t h0, l0, h1, l1;
+                                fw_split2(w4[q >> 1][(q & 1) * 2], h0, l0);
+                                fw_split2(w4[q >> 1][(q & 1) * 2 + 1], h1, l1);
+                                ph[q] = h0 | ((uint32_t)h1 << 16);
+                                pl[q] = l0 | ((uint32_t)l1 << 16);
+                            }
+                            const size_t o = (((size_t)wnd * g.H + h) * g.T + t0 + row) * 64 + dd0 + half * 16;
+                            uint4 *qh = (uint4 *)(g.o16[2 * which] + o), *ql = (uint4 *)(g.o16[2 * which + 1] + o);
+                            qh[0] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+                            qh[1] = make_uint4(ph[4], ph[5], ph[6], ph[7]);
+                            ql[0] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+                            ql[1] = make_uint4(pl[4], pl[5], pl[6], pl[7]);
+                        }
+                    }
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+        issue(gs + NS);
+        tile++;
+        s = 0;
+    }
+    FW_WAIT_VM(0);
+}
+
+// ---------------------------------------------------------------------------
 // Tile choice: register-staged tiles (r256x256, r256x128, r128x128) and the
 // pipelined direct-to-LDS tiles (p256x256, p256x128, p128x128 with 4 stages,
 // or 2-3 stages: n2, n3).  FWHIP_GEMM_TILE=<name> forces one (tuning sweeps).
@@ -540,6 +895,36 @@ static void launch_tiles(hipStream_t st, const FwGemm &g, int tile) {
     }
 }
 
+// Persistent int8 launch: 256x256 tiles (8 waves of 128x64) for wide outputs,
+// 256x128 (8 waves of 64x64) for N < 2048 and for the residual epilogue, whose
+// wave tile must fit its residual values in registers.  One block per CU
+// (LDS and registers admit no second); the grid is a multiple of 8 so block
+// b runs on XCD b % 8.
+template <int EPI, int BM, int BN, int WGM, int WGN>
+static void launch_pi8(hipStream_t st, const FwGemm &g, int ncu) {
+    int ntw = 0, ntm;
+    if (EPI == FW_EPI_QKV) {
+        ntw = (g.T + BM - 1) / BM;
+        ntm = (g.M / g.T) * ntw;
+    } else {
+        ntm = (g.M + BM - 1) / BM;
+    }
+    const int ntn = (g.N + BN - 1) / BN;
+    const int grid = ncu >= 8 ? ncu / 8 * 8 : 8;
+    hipLaunchKernelGGL((k_gemm_pi8<EPI, BM, BN, WGM, WGN, 3>), dim3(grid), dim3(64 * WGM * WGN), 0, st, g, ntm, ntn,
+                       ntw);
+}
+
+template <int EPI>
+static void launch_pi8_tiles(hipStream_t st, const FwGemm &g, int ncu) {
+    if constexpr (EPI != FW_EPI_RESID)
+        if (g.N >= 2048) {
+            launch_pi8<EPI, 256, 256, 2, 4>(st, g, ncu);
+            return;
+        }
+    launch_pi8<EPI, 256, 128, 4, 2>(st, g, ncu);
+}
+
 void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g0) {
     static int map = -1;
     if (map < 0) {
@@ -554,6 +939,20 @@ void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g0) {
         (void)hipGetDevice(&dev);
         (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
         if (ncu <= 0) ncu = 256;
+    }
+    static int pi8 = -1;
+    if (pi8 < 0) {
+        const char *e = getenv("FWHIP_GEMM_I8P");
+        pi8 = e ? atoi(e) : 1;
+    }
+    if (kind == FW_KIND_I8 && pi8 && g.K % 64 == 0 && (g.epi != FW_EPI_QKV || (g.T > 0 && g.M % g.T == 0))) {
+        switch (g.epi) {
+        case FW_EPI_F32: launch_pi8_tiles<FW_EPI_F32>(st, g, ncu); return;
+        case FW_EPI_RESID: launch_pi8_tiles<FW_EPI_RESID>(st, g, ncu); return;
+        case FW_EPI_QKV: launch_pi8_tiles<FW_EPI_QKV>(st, g, ncu); return;
+        case FW_EPI_ACC32: launch_pi8_tiles<FW_EPI_ACC32>(st, g, ncu); return;
+        default: break;
+        }
     }
     int tile = pick_tile(g.M, g.N, ncu);
     if (kind == FW_KIND_I8) {
