@@ -663,6 +663,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const float *ssx = scl + (tile & 1) * SCLN, *ssw = ssx + BM, *sbi = ssw + BN;
+        // Full-line f32 results (two 128-byte rows per store) are written
+        // non-temporally: they are not read again by this kernel and would only
+        // evict operand panels from L2.  The QKV epilogue's 16-byte runs stay
+        // cached so L2 can merge them into lines (non-temporal partial lines
+        // measured 1.6x slower).
         if constexpr (EPI == FW_EPI_RESID) {
             static_assert(TM * TN <= 4, "residual values of the wave tile are held in registers");
             // residual values of every element first: one wait, then the stores
@@ -695,7 +700,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
                         const int rw = rl + (r >> 2) * 8 + (r & 3);
                         float v = (float)acc[i][j][r] * sr[r >> 2][r & 3] * s2;
                         if (has_bias) v = v + bb;
-                        if (rw < mrows && col < g.N) g.C[(size_t)(m0 + rw) * g.ldc + col] = cv[i][j][r] + v;
+                        if (rw < mrows && col < g.N) __builtin_nontemporal_store(cv[i][j][r] + v, g.C + (size_t)(m0 + rw) * g.ldc + col);
                     }
                 }
         } else if constexpr (EPI == FW_EPI_F32 || EPI == FW_EPI_ACC32) {
@@ -719,7 +724,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
                             } else {
                                 float v = (float)acc[i][j][r] * sr[r >> 2][r & 3] * s2;
                                 if (has_bias) v = v + bb;
-                                g.C[o] = v;
+                                __builtin_nontemporal_store(v, g.C + o);
                             }
                         }
                     }
