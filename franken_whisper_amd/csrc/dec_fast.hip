@@ -35,17 +35,24 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // round trip; the reductions run on DPP lane moves.
 // Row r whose values xv (lane l: float4 groups l, l+64, ...; ok = in range)
 // are already loaded or in flight.
+// LayerNorm weight and bias groups of lane l (as the row values).
 template <int NV>
-__device__ __forceinline__ void fw_ln_quant_vals(float4 (&xv)[NV], const bool (&ok)[NV], float *y, const float *w,
-                                                 const float *b, int d, int r, int8_t *xq, float *xs, int lane) {
+__device__ __forceinline__ void fw_ln_load_wb(const bool (&ok)[NV], const float *w, const float *b, float4 (&wv)[NV],
+                                              float4 (&bv)[NV], int lane) {
     const float4 *w4 = (const float4 *)w, *b4 = (const float4 *)b;
-    float4 wv[NV], bv[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         const int c = ok[k] ? lane + k * 64 : 0;
         wv[k] = w4[c];
         bv[k] = b4[c];
     }
+}
+
+// The same with the weight and bias groups already loaded (or in flight).
+template <int NV>
+__device__ __forceinline__ void fw_ln_quant_core(float4 (&xv)[NV], const bool (&ok)[NV], const float4 (&wv)[NV],
+                                                 const float4 (&bv)[NV], float *y, int d, int r, int8_t *xq,
+                                                 float *xs, int lane) {
     double s = 0.0;
 #pragma unroll
     for (int k = 0; k < NV; k++)
@@ -92,6 +99,14 @@ __device__ __forceinline__ void fw_ln_quant_vals(float4 (&xv)[NV], const bool (&
         }
     }
     if (lane == 0) xs[r] = sc;
+}
+
+template <int NV>
+__device__ __forceinline__ void fw_ln_quant_vals(float4 (&xv)[NV], const bool (&ok)[NV], float *y, const float *w,
+                                                 const float *b, int d, int r, int8_t *xq, float *xs, int lane) {
+    float4 wv[NV], bv[NV];
+    fw_ln_load_wb<NV>(ok, w, b, wv, bv, lane);
+    fw_ln_quant_core<NV>(xv, ok, wv, bv, y, d, r, xq, xs, lane);
 }
 
 template <int NV>
@@ -691,13 +706,26 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
 // decoder.rs:1524-1716, int8 cross K/V — the default), including the head's
 // rows of the cross q projection: q = gemv_i8(Wq_h, xq) (+ bias); qh = q*s
 // quantized per vector; scores = gemv_i8(K_h, qh); softmax; p quantized per
-// vector; out = gemv_i8(Vt_h, p).  512 threads.  Vt rows have stride Tq (T rounded up
-// to 16, zero padded).  K (CA_KPT keys per thread) is loaded into registers at
-// entry and this wave's 8 Vt rows (CA_VPL 16-byte chunks per lane per row)
-// right after the q projection, so their latency overlaps the score/softmax
-// chain.
+// vector; out = gemv_i8(Vt_h, p).  512 threads.  Vt rows have stride Tq (T
+// rounded up to 16, zero padded).
+//
+// The register operands are requested at entry, in the order they are
+// consumed, so each phase waits only for its own (vector memory returns in
+// order): the LayerNorm row, weight and bias; the head's 64 q-projection rows;
+// the keys (CA_KPT per thread).  The head's Vt rows go straight into LDS (64 x
+// Tq bytes, global -> LDS without registers), issued by waves 1-7 while thread
+// 0 runs the softmax's sequential sum.
 #define CA_KPT 3
-#define CA_VPL 2
+#define CA_VKB 16 // 1 KB Vt loads per wave (7 waves): 64 * ca_vstride(Tq) <= 7 * CA_VKB KB
+// LDS row stride of the staged Vt rows: Tq rounded up to 16 mod 256
+__host__ __device__ __forceinline__ int ca_vstride(int Tq) { return Tq + ((16 - Tq % 256) + 256) % 256; }
+// Block barrier for LDS data (a plain barrier: __syncthreads would also wait
+// for the global -> LDS loads still in flight)
+#define CA_SYNC()                                                                                  \
+    do {                                                                                           \
+        FW_WAIT_LGKM0();                                                                           \
+        asm volatile("s_barrier" ::: "memory");                                                    \
+    } while (0)
 template <int NV>
 __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restrict__ wq, const float *__restrict__ swq,
                                                          const float *__restrict__ bq, const float *__restrict__ x,
@@ -706,8 +734,10 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
                                                          const float *cvs, float *att, int d, int T, int Tq, int H,
                                                          int L, int layer, float scale, float *pmax) {
     extern __shared__ __align__(16) unsigned char smc2[];
-    float *sc = (float *)smc2;                                       // [T]
-    int8_t *p8 = (int8_t *)(smc2 + sizeof(float) * ((T + 3) & ~3)); // [Tq]
+    const int vst = ca_vstride(Tq);                                               // LDS row stride of Vt
+    int8_t *vl = (int8_t *)smc2;                                                  // [64, vst]
+    float *sc = (float *)(smc2 + (size_t)64 * vst);                               // [T]
+    int8_t *p8 = (int8_t *)(smc2 + (size_t)64 * vst + sizeof(float) * ((T + 3) & ~3)); // [Tq]
     __shared__ __align__(16) int8_t q8[64];
     __shared__ float red[16];
     __shared__ float bc[2];
@@ -723,17 +753,24 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
     // arithmetic, into LDS), then this head's 64 rows of the cross q
     // projection (gemv_i8, nn.rs:3168-3231: exact i32 dots,
     // ((f32)acc * s_w) * s_x + b), 8 rows per wave, lane c taking 16-byte
-    // chunks c and c + 64 of the row (d <= 2048).  These operands are loaded
-    // first: the K/V prefetch behind them is not waited for until the scores.
+    // chunks c and c + 64 of the row (d <= 2048).
     __shared__ float qf[64];
     __shared__ __align__(16) int8_t xql[256 * NV];
     __shared__ float xsl;
-    float4 lv[NV];
+    float4 lv[NV], lw[NV], lb[NV];
     bool lok[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         lok[k] = lane + k * 64 < (d >> 2);
         lv[k] = ((const float4 *)(x + (size_t)s * d))[lok[k] ? lane + k * 64 : 0];
+    }
+    fw_ln_load_wb<NV>(lok, lnw, lnb, lw, lb, lane);
+    if (d < 0) {
+        // never taken: a use outside wave 0's LayerNorm branch, so the compiler
+        // issues these loads here, ahead of the other operands, instead of
+        // moving them into that branch behind everything else
+#pragma unroll
+        for (int k = 0; k < NV; k++) qf[k] = lv[k].x + lw[k].y + lb[k].z;
     }
     const int nq = d >> 4;
     const int qc0 = lane < nq ? lane : 0, qc1 = lane + 64 < nq ? lane + 64 : 0;
@@ -744,14 +781,16 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
         wa[rr] = *(const int4 *)(wr + qc0 * 16);
         wb[rr] = *(const int4 *)(wr + qc1 * 16);
     }
+    // per-row scales and biases are wave-uniform: scalar loads, which leave the
+    // vector-memory count (at most 63 outstanding) to the operands above and below
+    const float *bqp = bq ? bq : swq; // unconditional loads; the bias is added only when present
+    const int wrow0 = h * 64 + __builtin_amdgcn_readfirstlane(wave) * 8;
     float qsw[8], qb[8];
 #pragma unroll
     for (int rr = 0; rr < 8; rr++) {
-        const int row = h * 64 + wave * 8 + rr;
-        qsw[rr] = swq[row];
-        qb[rr] = bq ? bq[row] : 0.0f;
+        qsw[rr] = swq[wrow0 + rr];
+        qb[rr] = bqp[wrow0 + rr];
     }
-    // register prefetch: this thread's keys and this wave's value rows
     int4 kr[CA_KPT][4];
     float ksc[CA_KPT];
 #pragma unroll
@@ -763,8 +802,8 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
         for (int c = 0; c < 4; c++) kr[u][c] = kp[c];
         ksc[u] = Ks[jc];
     }
-    if (wave == 0) fw_ln_quant_vals<NV>(lv, lok, nullptr, lnw, lnb, d, 0, xql, &xsl, lane);
-    __syncthreads();
+    if (wave == 0) fw_ln_quant_core<NV>(lv, lok, lw, lb, nullptr, d, 0, xql, &xsl, lane);
+    CA_SYNC();
     {
         // chunks past the row read as zero
         const int4 xa = lane < nq ? *(const int4 *)(xql + qc0 * 16) : make_int4(0, 0, 0, 0);
@@ -782,22 +821,14 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
             acc = fw_sdot4(wb[rr].z, xb.z, acc);
             acc = fw_sdot4(wb[rr].w, xb.w, acc);
             acc = fw_dpp_wave_sum_i32(acc);
-            if (lane == 0) qf[wave * 8 + rr] = (float)acc * qsw[rr] * sx + qb[rr];
+            if (lane == 0) {
+                float q = (float)acc * qsw[rr] * sx;
+                if (bq) q = q + qb[rr];
+                qf[wave * 8 + rr] = q;
+            }
         }
     }
-    // this wave's value rows, needed only after the softmax (chunks past nch
-    // reload the last one; their p8 operand is zero)
-    int4 vr[8][CA_VPL];
-#pragma unroll
-    for (int rr = 0; rr < 8; rr++) {
-        const int8_t *vrow = Vp + (size_t)(wave * 8 + rr) * Tq;
-#pragma unroll
-        for (int u = 0; u < CA_VPL; u++) {
-            const int c = lane + u * 64;
-            vr[rr][u] = *(const int4 *)(vrow + (c < nch ? c : nch - 1) * 16);
-        }
-    }
-    __syncthreads();
+    CA_SYNC();
     if (wave == 0) {
         float v = qf[lane] * scale;
         float m = fw_dpp_wave_max(fabsf(v));
@@ -805,7 +836,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
         q8[lane] = fw_q8_avx(v, 1.0f / xs, lane, 64);
         if (lane == 0) bc[0] = xs;
     }
-    __syncthreads();
+    CA_SYNC();
     const float xs = bc[0];
     const int *qw = (const int *)q8;
     float mx = -INFINITY;
@@ -844,7 +875,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
     }
     mx = fw_dpp_wave_max(mx);
     if (lane == 0) red[wave] = mx;
-    __syncthreads();
+    CA_SYNC();
     mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
     const bool fin = isfinite(mx);
     // exp pass; am = max |stored value| (the exps, or the raw scores when the
@@ -861,12 +892,28 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
     }
     am = fw_dpp_wave_max(am);
     if (lane == 0) red[8 + wave] = am;
-    __syncthreads();
+    CA_SYNC();
     if (t == 0) {
         // softmax_rows' sequential sum (nn.rs:4880-4963)
         bc[1] = fin ? fw_seq_sum_inv(sc, T) : 0.0f;
+    } else if (wave > 0) {
+        // meanwhile waves 1-7 bring the head's Vt rows into LDS rows of stride
+        // vst, 1 KB of LDS per wave instruction: lane slot (row, col) takes
+        // Vt[row, col], pad slots (col >= Tq) an in-bounds dummy; the tail
+        // rewrites the last KB with the same bytes
+        const int nkb = (64 * vst + 1023) >> 10;
+#pragma unroll
+        for (int u = 0; u < CA_VKB; u++) {
+            const int kb = (wave - 1) + 7 * u, kc = kb < nkb ? kb : nkb - 1;
+            const int off = kc * 1024 + lane * 16, row = off / vst, col = off - row * vst;
+            const int8_t *src = row < 64 && col < Tq ? Vp + (size_t)row * Tq + col : Vp;
+            __builtin_amdgcn_global_load_lds((const void *)src,
+                                             (void __attribute__((address_space(3))) *)(vl + (size_t)kc * 1024), 16,
+                                             0, 0);
+        }
+        FW_WAIT_VM(0);
     }
-    __syncthreads();
+    CA_SYNC();
     const float inv = bc[1];
     am = fmaxf(fmaxf(fmaxf(red[8], red[9]), fmaxf(red[10], red[11])),
                fmaxf(fmaxf(red[12], red[13]), fmaxf(red[14], red[15])));
@@ -883,49 +930,35 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
         }
         p8[j] = q;
     }
-    __syncthreads();
-    // out[dd] = sum_j Vt[dd, j] * p8[j]: wave w owns rows dd = w*8 .. w*8+7
-    float om = 0.0f; // max |out| of this wave's rows (wave-uniform)
-    int4 pp[CA_VPL];
-#pragma unroll
-    for (int u = 0; u < CA_VPL; u++) {
-        const int c = lane + u * 64;
-        pp[u] = c < nch ? *(const int4 *)(p8 + c * 16) : make_int4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int rr = 0; rr < 8; rr++) {
-        const int dd = wave * 8 + rr;
+    CA_SYNC();
+    // out[dd] = sum_j Vt[dd, j] * p8[j] (exact i32 in any order): lane dd owns
+    // row dd, wave w the 16-byte chunks w, w + 8, ...  The row stride vst is 16
+    // mod 256, so the 16 lanes of a read group hit 16 different bank groups, and
+    // the p8 chunk is one broadcast address.  Partial sums meet in LDS.
+    __shared__ int pvp[8][64];
+    {
         int acc = 0;
-#pragma unroll
-        for (int u = 0; u < CA_VPL; u++) {
-            acc = fw_sdot4(vr[rr][u].x, pp[u].x, acc);
-            acc = fw_sdot4(vr[rr][u].y, pp[u].y, acc);
-            acc = fw_sdot4(vr[rr][u].z, pp[u].z, acc);
-            acc = fw_sdot4(vr[rr][u].w, pp[u].w, acc);
-        }
-        // rows longer than the prefetched chunks
-        for (int c = lane + CA_VPL * 64; c < nch; c += 64) {
-            int4 vv = *(const int4 *)(Vp + (size_t)dd * Tq + c * 16);
-            int4 q4 = *(const int4 *)(p8 + c * 16);
+        for (int ck = wave; ck < nch; ck += 8) {
+            const int4 vv = *(const int4 *)(vl + (size_t)lane * vst + ck * 16);
+            const int4 q4 = *(const int4 *)(p8 + ck * 16);
             acc = fw_sdot4(vv.x, q4.x, acc);
             acc = fw_sdot4(vv.y, q4.y, acc);
             acc = fw_sdot4(vv.z, q4.z, acc);
             acc = fw_sdot4(vv.w, q4.w, acc);
         }
-        acc = fw_dpp_wave_sum_i32(acc);
-        const float o = (float)acc * Vs[dd] * ps + 0.0f;
-        om = fmaxf(om, fabsf(o));
-        if (lane == 0) att[(size_t)s * d + h * 64 + dd] = o;
+        pvp[wave][lane] = acc;
     }
-    if (pmax) {
-        if (lane == 0) red[wave] = om;
-        __syncthreads();
-        if (t == 0) {
-            float m = red[0];
-            for (int w = 1; w < 8; w++) m = fmaxf(m, red[w]);
-            pmax[(size_t)s * H + h] = m;
-        }
+    CA_SYNC();
+    float om = 0.0f; // max |out| over the head's 64 rows (wave 0)
+    if (wave == 0) {
+        int acc = 0;
+#pragma unroll
+        for (int w = 0; w < 8; w++) acc += pvp[w][lane];
+        const float o = (float)acc * Vs[lane] * ps + 0.0f;
+        att[(size_t)s * d + h * 64 + lane] = o;
+        om = fw_dpp_wave_max(fabsf(o));
     }
+    if (pmax && t == 0) pmax[(size_t)s * H + h] = om;
 }
 
 // Per-row int8 quantization of f16 rows into a row stride ldq >= n (zero
@@ -1028,7 +1061,8 @@ void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *sw
                                const float *lnw, const float *lnb, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
                                float scale, float *pmax) {
-    size_t shm = sizeof(float) * ((T + 3) & ~3) + Tq;
+    if (64 * ca_vstride(Tq) > 7 * CA_VKB * 1024) return; // refused where the decoder is loaded (T <= 1536)
+    size_t shm = (size_t)64 * ca_vstride(Tq) + sizeof(float) * ((T + 3) & ~3) + Tq;
     FW_ROWS_DISPATCH(k_cross_attn_i8v2, d, dim3(H, ns), dim3(512), shm, st, wq, swq, bq, x, lnw, lnb, ck, cks, cvt,
                      cvs, att, d, T, Tq, H, L, layer, scale, pmax);
 }

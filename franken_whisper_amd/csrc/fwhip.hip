@@ -399,6 +399,9 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     if (!dd || !out) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_new: NULL argument");
     *out = nullptr;
     if (S <= 0 || T <= 0) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_new: n_streams and enc_frames must be > 0");
+    // the int8 cross-attention kernel stages a head's Vt rows (64 x T bytes) in LDS
+    if (dd->arm == FWHIP_DEC_INT8 && T > 1536)
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_new: enc_frames must be at most 1536 on the int8 arm");
     fwhip_ctx *c = dd->ctx;
     HIP_TRY(hipSetDevice(c->device));
     fwhip_dstate *st = new fwhip_dstate();
