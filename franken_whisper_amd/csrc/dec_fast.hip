@@ -702,6 +702,187 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
 }
 
 // ---------------------------------------------------------------------------
+// The int8 arm's whole self-attention sublayer for one (head, stream), up to
+// the output projection: the attention LayerNorm of stream s's residual row
+// (wave 0, k_ln_quant's arithmetic, into LDS), the head's 192 rows of the fused
+// q/k/v projection (gemv_i8, nn.rs:3168-3231: exact i32 dots,
+// ((f32)acc * s_w) * s_x + b, bias [q_b | 0 | v_b]), then k_self_attn2's
+// attention over the f16 cache with this token's k/v appended.  512 threads;
+// wave w computes projection rows 24w .. 24w+23 in three 8-row batches (a
+// batch never straddles the q/k/v boundary), lane c taking 16-byte chunks c
+// and c + 64 of each row (d <= 2048).  The LayerNorm operands are requested
+// first and two batches of weight rows right behind them; the third batch is
+// requested once the first has been used.
+template <int NV>
+__global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restrict__ wqkv, const float *__restrict__ sqkv,
+                                                         const float *__restrict__ bqkv, const float *__restrict__ x,
+                                                         const float *__restrict__ lnw, const float *__restrict__ lnb,
+                                                         uint16_t *kc, uint16_t *vc, float *att, const int *posp, int d,
+                                                         int nctx, int L, int layer, float scale, float *pmax) {
+    extern __shared__ __align__(16) unsigned char sm3[];
+    float *sc = (float *)sm3;                                              // [nctx]
+    uint16_t *vs = (uint16_t *)(sm3 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
+    __shared__ float qkvl[192];
+    __shared__ float qh[64];
+    __shared__ __align__(16) int8_t xql[256 * NV];
+    __shared__ float xsl;
+    __shared__ float red[8];
+    __shared__ float inv_s;
+    const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int base = h * 64;
+    float4 lv[NV], lw[NV], lb[NV];
+    bool lok[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        lok[k] = lane + k * 64 < (d >> 2);
+        lv[k] = ((const float4 *)(x + (size_t)s * d))[lok[k] ? lane + k * 64 : 0];
+    }
+    fw_ln_load_wb<NV>(lok, lnw, lnb, lw, lb, lane);
+    if (d < 0) {
+        // never taken: a use outside wave 0's LayerNorm branch, so the compiler
+        // issues these loads here, ahead of the weight rows, instead of moving
+        // them into that branch behind everything else
+#pragma unroll
+        for (int k = 0; k < NV; k++) qkvl[k] = lv[k].x + lw[k].y + lb[k].z;
+    }
+    const int nq = d >> 4;
+    const int qc0 = lane < nq ? lane : 0, qc1 = lane + 64 < nq ? lane + 64 : 0;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    // first global row of batch b of this wave (rows 24w + 8b .. +7 of the 192)
+    auto brow = [&](int b) {
+        const int r = wv * 24 + 8 * b;
+        return (r >> 6) * d + base + (r & 63);
+    };
+    int4 wa[2][8], wb[2][8];
+    auto loadb = [&](int set, int b) {
+        const int r0 = brow(b);
+#pragma unroll
+        for (int rr = 0; rr < 8; rr++) {
+            const int8_t *wr = wqkv + (size_t)(r0 + rr) * d;
+            wa[set][rr] = *(const int4 *)(wr + qc0 * 16);
+            wb[set][rr] = *(const int4 *)(wr + qc1 * 16);
+        }
+    };
+    loadb(0, 0);
+    loadb(1, 1);
+    // row scales and biases: wave-uniform, scalar loads
+    float rsc[3][8], rbi[3][8];
+#pragma unroll
+    for (int b = 0; b < 3; b++)
+#pragma unroll
+        for (int rr = 0; rr < 8; rr++) {
+            rsc[b][rr] = sqkv[brow(b) + rr];
+            rbi[b][rr] = bqkv[brow(b) + rr];
+        }
+    const int pos = *posp;
+    if (wave == 0) fw_ln_quant_core<NV>(lv, lok, lw, lb, nullptr, d, 0, xql, &xsl, lane);
+    __syncthreads();
+    {
+        // chunks past the row read as zero
+        const int4 xa = lane < nq ? *(const int4 *)(xql + qc0 * 16) : make_int4(0, 0, 0, 0);
+        const int4 xb = lane + 64 < nq ? *(const int4 *)(xql + qc1 * 16) : make_int4(0, 0, 0, 0);
+        const float sx = xsl;
+        auto rows = [&](int set, int b) {
+#pragma unroll
+            for (int rr = 0; rr < 8; rr++) {
+                int acc = 0;
+                acc = fw_sdot4(wa[set][rr].x, xa.x, acc);
+                acc = fw_sdot4(wa[set][rr].y, xa.y, acc);
+                acc = fw_sdot4(wa[set][rr].z, xa.z, acc);
+                acc = fw_sdot4(wa[set][rr].w, xa.w, acc);
+                acc = fw_sdot4(wb[set][rr].x, xb.x, acc);
+                acc = fw_sdot4(wb[set][rr].y, xb.y, acc);
+                acc = fw_sdot4(wb[set][rr].z, xb.z, acc);
+                acc = fw_sdot4(wb[set][rr].w, xb.w, acc);
+                acc = fw_dpp_wave_sum_i32(acc);
+                if (lane == 0) qkvl[wv * 24 + 8 * b + rr] = (float)acc * rsc[b][rr] * sx + rbi[b][rr];
+            }
+        };
+        rows(0, 0);
+        loadb(0, 2);
+        rows(1, 1);
+        rows(0, 2);
+    }
+    __syncthreads();
+    const size_t cbase = ((size_t)s * L + layer) * nctx * d;
+    if (t < 64) {
+        kc[cbase + (size_t)pos * d + base + t] = fw_f2h(qkvl[64 + t]);
+        vc[cbase + (size_t)pos * d + base + t] = fw_f2h(qkvl[128 + t]);
+        qh[t] = qkvl[t] * scale;
+    }
+    __syncthreads(); // this block's own cache row is visible to its threads
+    const int tk = pos + 1;
+    // stage V rows [0, tk) of this head (8 x 16 bytes per row), loads issued
+    // before the LDS stores
+    for (int c0 = 0; c0 < tk * 8; c0 += 512 * 2) {
+        uint4 v[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            int c = c0 + t + u * 512;
+            int cc = c < tk * 8 ? c : tk * 8 - 1;
+            v[u] = *(const uint4 *)(vc + cbase + (size_t)(cc >> 3) * d + base + (cc & 7) * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            int c = c0 + t + u * 512;
+            if (c < tk * 8) *(uint4 *)(vs + (c >> 3) * 64 + (c & 7) * 8) = v[u];
+        }
+    }
+    float mx = -INFINITY;
+    for (int j = t; j < tk; j += 512) {
+        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)j * d + base);
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            uint4 u = kr[c];
+            uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                acc += qh[c * 8 + 2 * e] * (fw_h2f(ww[e] & 0xffff) * scale);
+                acc += qh[c * 8 + 2 * e + 1] * (fw_h2f(ww[e] >> 16) * scale);
+            }
+        }
+        sc[j] = acc;
+        mx = fmaxf(mx, acc);
+    }
+    mx = fw_block_max(mx, red);
+    const bool fin = isfinite(mx);
+    if (fin)
+        for (int j = t; j < tk; j += 512) {
+            float e = fw_expf(sc[j] - mx);
+            sc[j] = isfinite(e) ? e : 0.0f;
+        }
+    __syncthreads();
+    if (t == 0) inv_s = fin ? fw_seq_sum_inv(sc, tk) : 0.0f;
+    __syncthreads();
+    const float inv = inv_s;
+    if (inv > 0.0f)
+        for (int j = t; j < tk; j += 512) sc[j] = sc[j] * inv;
+    __syncthreads();
+    if (t < 64) {
+        // ascending-j accumulation; operands for 8 keys are read before the adds
+        float acc = 0.0f;
+        int j = 0;
+        for (; j + 8 <= tk; j += 8) {
+            float pv[8], vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                pv[u] = sc[j + u];
+                vv[u] = fw_h2f(vs[(j + u) * 64 + t]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc += pv[u] * vv[u];
+        }
+        for (; j < tk; j++) acc += sc[j] * fw_h2f(vs[j * 64 + t]);
+        att[(size_t)s * d + base + t] = acc;
+        // this head's share of the row amax the int8 consumer needs
+        const float m = fw_dpp_wave_max(fabsf(acc));
+        if (pmax && t == 0) pmax[(size_t)s * gridDim.x + h] = m;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Cross-attention for one (head, stream) with int8 K/V (cross_attention,
 // decoder.rs:1524-1716, int8 cross K/V — the default), including the head's
 // rows of the cross q projection: q = gemv_i8(Wq_h, xq) (+ bias); qh = q*s
@@ -1055,6 +1236,15 @@ void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16
     size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
     hipLaunchKernelGGL(k_self_attn2, dim3(H, ns), dim3(256), shm, st, qkv, kc, vc, att, posp, d, nctx, L, layer,
                        scale, pmax);
+}
+
+void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *sqkv, const float *bqkv,
+                               const float *x, const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc,
+                               float *att, const int *posp, int d, int H, int nctx, int L, int layer, int ns,
+                               float scale, float *pmax) {
+    size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
+    FW_ROWS_DISPATCH(k_self_attn_fused, d, dim3(H, ns), dim3(512), shm, st, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc,
+                     att, posp, d, nctx, L, layer, scale, pmax);
 }
 
 void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,
