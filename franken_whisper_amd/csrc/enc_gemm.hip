@@ -518,9 +518,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
     constexpr int SCL = (BM + 2 * BN + 64 * NW - 1) / (64 * NW); // scale loads per wave per tile
     constexpr int SCLN = SCL * NW * 64;                           // floats per parity
     constexpr bool QKV = EPI == FW_EPI_QKV;
-    constexpr int SLAB = 32 * 40;                                 // floats per wave (QKV transposes)
+    // wave-private LDS slab: QKV turns 32 x 32 f32 tiles (rows of 40), the
+    // index epilogue sends 32 x WN u16 tiles out as whole rows
+    constexpr int SLABB = QKV ? 32 * 40 * 4 : (EPI == FW_EPI_F16IDX ? 32 * WN * 2 : 0); // bytes per wave
     static_assert(STAGE % (1024 * NW) == 0, "stage loads must split evenly over waves");
-    __shared__ __align__(1024) unsigned char lds[NS * STAGE + 2 * SCLN * 4 + (QKV ? NW * SLAB * 4 : 0)];
+    __shared__ __align__(1024) unsigned char lds[NS * STAGE + 2 * SCLN * 4 + NW * SLABB];
     float *scl = (float *)(lds + NS * STAGE);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
@@ -663,6 +665,30 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const float *ssx = scl + (tile & 1) * SCLN, *ssw = ssx + BM, *sbi = ssw + BN;
+        // A 32 x WN u16 tile (accumulator layout: element r of lane l is row
+        // (r/4)*8 + (l/32)*4 + r%4, column j*32 + l%32), put into this wave's
+        // slab one 32-column tile j at a time, then flushed to rows dst + row*ld,
+        // row < vrows, as 16-byte runs of whole rows (WN/8 lanes per row).  The
+        // slab is private to the wave and a wave's LDS accesses run in order:
+        // only the compiler must not reorder them.
+        uint16_t *const sl = (uint16_t *)(lds + NS * STAGE + 2 * SCLN * 4 + wave * SLABB);
+        auto slab_put = [&](int j, const uint16_t (&u)[16]) {
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int r = 0; r < 16; r++) sl[((r >> 2) * 8 + (ln >> 5) * 4 + (r & 3)) * WN + j * 32 + (ln & 31)] = u[r];
+            asm volatile("" ::: "memory");
+        };
+        auto slab_flush = [&](uint16_t *dst, size_t ld, int vrows) {
+            constexpr int LPR = WN / 8, RPI = 64 / LPR;
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int q = 0; q < 32 / RPI; q++) {
+                const int row = q * RPI + ln / LPR, ch = ln % LPR;
+                const uint4 w = *(const uint4 *)(sl + row * WN + ch * 8);
+                if (row < vrows) *(uint4 *)(dst + row * ld + ch * 8) = w;
+            }
+            asm volatile("" ::: "memory");
+        };
         // Full-line f32 results (two 128-byte rows per store) are written
         // non-temporally: they are not read again by this kernel and would only
         // evict operand panels from L2.  The QKV epilogue's 16-byte runs stay
@@ -703,6 +729,59 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
                         if (rw < mrows && col < g.N) __builtin_nontemporal_store(cv[i][j][r] + v, g.C + (size_t)(m0 + rw) * g.ldc + col);
                     }
                 }
+        } else if constexpr (EPI == FW_EPI_F16IDX) {
+            const bool wide = n0 + BN <= g.N;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int r0 = wm * WM + i * 32, vrows = mrows - r0;
+                uint16_t u[TN][16];
+                bool sent = false;
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int cl = wn * WN + j * 32 + (ln & 31);
+                    const int rl = r0 + (ln >> 5) * 4;
+                    const float s2 = ssw[cl], bb = sbi[cl];
+                    v4f sr[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sr[q] = *(const v4f *)(ssx + rl + q * 8);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        float v = (float)acc[i][j][r] * sr[r >> 2][r & 3] * s2;
+                        if (has_bias) v = v + bb;
+                        const bool in = fabsf(v) < FW_GIDX_LIM;
+                        u[j][r] = in ? fw_f2h(v) : (uint16_t)FW_GIDX_SENT;
+                        sent |= !in;
+                        acc[i][j][r] = __float_as_int(v); // kept for the rare side stores
+                    }
+                }
+                if (__builtin_amdgcn_ballot_w64(sent)) {
+                    // values beyond the table's range: exact f32 into the side array
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int rw = r0 + (r >> 2) * 8 + (ln >> 5) * 4 + (r & 3);
+                            const int col = n0 + wn * WN + j * 32 + (ln & 31);
+                            if (u[j][r] == (uint16_t)FW_GIDX_SENT && rw < mrows && col < g.N)
+                                g.C[(size_t)(m0 + rw) * g.ldc + col] = __int_as_float(acc[i][j][r]);
+                        }
+                }
+                if (vrows <= 0) continue;
+                if (wide) {
+#pragma unroll
+                    for (int j = 0; j < TN; j++) slab_put(j, u[j]);
+                    slab_flush(g.o16[0] + (size_t)(m0 + r0) * g.ldc + n0 + wn * WN, g.ldc, vrows);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int rw = (r >> 2) * 8 + (ln >> 5) * 4 + (r & 3);
+                            const int col = n0 + wn * WN + j * 32 + (ln & 31);
+                            if (rw < vrows && col < g.N) g.o16[0][(size_t)(m0 + r0 + rw) * g.ldc + col] = u[j][r];
+                        }
+                }
+            }
         } else if constexpr (EPI == FW_EPI_F32 || EPI == FW_EPI_ACC32) {
 #pragma unroll
             for (int i = 0; i < TM; i++)
@@ -735,7 +814,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
             // V^T: [B, H, 64, Tp] at key positions fw_vt_pos(t); a lane's 8
             // values r = 8c .. 8c+7 sit at 8 consecutive positions (window
             // tiles start at multiples of 32), so they go out as 16-byte runs.
-            float *slab = (float *)(lds + NS * STAGE + 2 * SCLN * 4) + wave * SLAB;
+            float *slab = (float *)(lds + NS * STAGE + 2 * SCLN * 4 + wave * SLABB);
             const int d = g.ldc, wnd = m0 / g.T, tb0 = m0 - wnd * g.T;
 #pragma unroll
             for (int i = 0; i < TM; i++)
@@ -930,7 +1009,7 @@ static void launch_pi8_tiles(hipStream_t st, const FwGemm &g, int ncu) {
     launch_pi8<EPI, 256, 128, 4, 2>(st, g, ncu);
 }
 
-void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g0) {
+bool fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g0) {
     static int map = -1;
     if (map < 0) {
         const char *e = getenv("FWHIP_GEMM_MAP");
@@ -952,31 +1031,32 @@ void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g0) {
     }
     if (kind == FW_KIND_I8 && pi8 && g.K % 64 == 0 && (g.epi != FW_EPI_QKV || (g.T > 0 && g.M % g.T == 0))) {
         switch (g.epi) {
-        case FW_EPI_F32: launch_pi8_tiles<FW_EPI_F32>(st, g, ncu); return;
-        case FW_EPI_RESID: launch_pi8_tiles<FW_EPI_RESID>(st, g, ncu); return;
-        case FW_EPI_QKV: launch_pi8_tiles<FW_EPI_QKV>(st, g, ncu); return;
-        case FW_EPI_ACC32: launch_pi8_tiles<FW_EPI_ACC32>(st, g, ncu); return;
+        case FW_EPI_F32: launch_pi8_tiles<FW_EPI_F32>(st, g, ncu); return true;
+        case FW_EPI_RESID: launch_pi8_tiles<FW_EPI_RESID>(st, g, ncu); return true;
+        case FW_EPI_QKV: launch_pi8_tiles<FW_EPI_QKV>(st, g, ncu); return true;
+        case FW_EPI_ACC32: launch_pi8_tiles<FW_EPI_ACC32>(st, g, ncu); return true;
+        case FW_EPI_F16IDX: launch_pi8_tiles<FW_EPI_F16IDX>(st, g, ncu); return true;
         default: break;
         }
     }
     int tile = pick_tile(g.M, g.N, ncu);
     if (kind == FW_KIND_I8) {
         switch (g.epi) {
-        case FW_EPI_F32: launch_tiles<FW_KIND_I8, FW_EPI_F32>(st, g, tile); break;
-        case FW_EPI_RESID: launch_tiles<FW_KIND_I8, FW_EPI_RESID>(st, g, tile); break;
-        case FW_EPI_QKV: launch_tiles<FW_KIND_I8, FW_EPI_QKV>(st, g, tile); break;
-        case FW_EPI_ACC32: launch_tiles<FW_KIND_I8, FW_EPI_ACC32>(st, g, tile); break;
-        default: break;
+        case FW_EPI_F32: launch_tiles<FW_KIND_I8, FW_EPI_F32>(st, g, tile); return true;
+        case FW_EPI_RESID: launch_tiles<FW_KIND_I8, FW_EPI_RESID>(st, g, tile); return true;
+        case FW_EPI_QKV: launch_tiles<FW_KIND_I8, FW_EPI_QKV>(st, g, tile); return true;
+        case FW_EPI_ACC32: launch_tiles<FW_KIND_I8, FW_EPI_ACC32>(st, g, tile); return true;
+        default: return false;
         }
     } else {
         switch (g.epi) {
-        case FW_EPI_F32: launch_tiles<FW_KIND_F16S, FW_EPI_F32>(st, g, tile); break;
-        case FW_EPI_RESID: launch_tiles<FW_KIND_F16S, FW_EPI_RESID>(st, g, tile); break;
-        case FW_EPI_GELU_F32: launch_tiles<FW_KIND_F16S, FW_EPI_GELU_F32>(st, g, tile); break;
-        case FW_EPI_GELU_SPLIT: launch_tiles<FW_KIND_F16S, FW_EPI_GELU_SPLIT>(st, g, tile); break;
-        case FW_EPI_CONV2: launch_tiles<FW_KIND_F16S, FW_EPI_CONV2>(st, g, tile); break;
-        case FW_EPI_QKV: launch_tiles<FW_KIND_F16S, FW_EPI_QKV>(st, g, tile); break;
-        default: break;
+        case FW_EPI_F32: launch_tiles<FW_KIND_F16S, FW_EPI_F32>(st, g, tile); return true;
+        case FW_EPI_RESID: launch_tiles<FW_KIND_F16S, FW_EPI_RESID>(st, g, tile); return true;
+        case FW_EPI_GELU_F32: launch_tiles<FW_KIND_F16S, FW_EPI_GELU_F32>(st, g, tile); return true;
+        case FW_EPI_GELU_SPLIT: launch_tiles<FW_KIND_F16S, FW_EPI_GELU_SPLIT>(st, g, tile); return true;
+        case FW_EPI_CONV2: launch_tiles<FW_KIND_F16S, FW_EPI_CONV2>(st, g, tile); return true;
+        case FW_EPI_QKV: launch_tiles<FW_KIND_F16S, FW_EPI_QKV>(st, g, tile); return true;
+        default: return false;
         }
     }
 }

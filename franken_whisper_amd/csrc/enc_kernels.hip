@@ -265,6 +265,75 @@ __global__ void __launch_bounds__(1024) k_gelu_quant_rows_lds(const float *x, in
     }
 }
 
+// The same GELU + quantization from rows of f16 table indices (the
+// FW_EPI_F16IDX epilogue of the fc1 GEMM): an index h is the f16 rounding of
+// an fc1 value v with |v| < FW_GIDX_LIM, whose GELU is the table entry
+// gtab[h] (the clamp cases need |v| >= 10); the sentinel marks a value whose
+// exact f32 sits at the same index of `side`, which takes the full
+// clamp-or-table path.  Half the bytes of the f32 rows; the output is the same.
+// One wave per row, persistent over rows; lane l holds the 8-index groups l,
+// l + 64, ... (NV8 of them: n == 512 * NV8).
+template <int NV8>
+__global__ void __launch_bounds__(1024) k_gelu_quant_h16(const uint16_t *hx, const float *side, int rows, int n,
+                                                        const float *gelu_tab, int8_t *q, float *qs) {
+    extern __shared__ uint16_t gtab[]; // [65536]
+    for (int i = threadIdx.x; i < GQ_TAB_N; i += blockDim.x) gtab[i] = fw_f2h(gelu_tab[i]); // values are f16-exact
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wpb = blockDim.x >> 6;
+    for (int r = blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += gridDim.x * wpb) {
+        const uint4 *hr = (const uint4 *)(hx + (size_t)r * n);
+        uint4 hv[NV8];
+#pragma unroll
+        for (int k = 0; k < NV8; k++) hv[k] = hr[lane + 64 * k];
+        float g[NV8][8];
+        bool sent = false;
+#pragma unroll
+        for (int k = 0; k < NV8; k++) {
+            const uint32_t w[4] = {hv[k].x, hv[k].y, hv[k].z, hv[k].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t lo = w[c] & 0xffffu, hi = w[c] >> 16;
+                sent |= lo == FW_GIDX_SENT || hi == FW_GIDX_SENT;
+                g[k][2 * c] = fw_h2f(gtab[lo]);
+                g[k][2 * c + 1] = fw_h2f(gtab[hi]);
+            }
+        }
+        if (__builtin_amdgcn_ballot_w64(sent)) {
+            // rare: values with |v| >= FW_GIDX_LIM, read back exactly
+#pragma unroll
+            for (int k = 0; k < NV8; k++) {
+                const uint32_t w[4] = {hv[k].x, hv[k].y, hv[k].z, hv[k].w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t h = (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                    if (h == FW_GIDX_SENT) {
+                        const float a = side[(size_t)r * n + (lane + 64 * k) * 8 + e];
+                        const float t = fw_h2f(gtab[fw_f2h(a)]);
+                        g[k][e] = a <= -10.0f ? 0.0f : (a >= 10.0f ? a : t);
+                    }
+                }
+            }
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV8; k++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) m = fmaxf(m, fabsf(g[k][e]));
+        m = fw_dpp_wave_max(m);
+        const float sc = fmaxf(m, 1e-9f) / 127.0f;
+        const float inv = 1.0f / sc;
+#pragma unroll
+        for (int k = 0; k < NV8; k++) {
+            uint32_t b[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) b[e] = fw_q8_body(g[k][e], inv);
+            ((uint2 *)(q + (size_t)r * n))[lane + 64 * k] =
+                make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+        }
+        if (lane == 0) qs[r] = sc;
+    }
+}
+
 // im2col for conv1d (kernel 3, pad 1; conv1d_wt nn.rs:5006-5103) into the f16
 // pair the GEMM consumes.  Column order kk*Cin + ci (weights are reordered to
 // match at load); columns >= 3*Cin are zero padding up to Kp.
@@ -628,6 +697,36 @@ void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int 
         }
     }
     hipLaunchKernelGGL(k_gelu_quant_i7_rows, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, tab, q, qs);
+}
+bool fw_launch_gelu_quant_h16(hipStream_t st, const uint16_t *hx, const float *side, int rows, int n,
+                              const float *tab, int8_t *q, float *qs) {
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    if (!tab || n <= 0 || n % 512) return false;
+    const size_t shm = sizeof(uint16_t) * GQ_TAB_N;
+    const dim3 grid(n_cu), blk(1024);
+#define GQH(NV8)                                                                                                     \
+    case NV8: hipLaunchKernelGGL((k_gelu_quant_h16<NV8>), grid, blk, shm, st, hx, side, rows, n, tab, q, qs); return true;
+    switch (n / 512) {
+        GQH(1)
+        GQH(2)
+        GQH(3)
+        GQH(4)
+        GQH(5)
+        GQH(6)
+        GQH(7)
+        GQH(8)
+        GQH(10)
+        GQH(12)
+        GQH(16)
+    default: return false;
+    }
+#undef GQH
 }
 void fw_launch_im2col(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, int Kp,
                       uint16_t *hi, uint16_t *lo) {

@@ -254,6 +254,12 @@ static bool ensure_bufs(fwhip_encoder *e, int B, int nf) {
     return hipStreamSynchronize(e->ctx->stream) == hipSuccess;
 }
 
+// MLP widths the index-form GELU quantizer handles (multiples of 512 up to 8192)
+static bool enc_h16_ok(int n) {
+    const int k = n / 512;
+    return n > 0 && n % 512 == 0 && (k <= 8 || k == 10 || k == 12 || k == 16);
+}
+
 static FwGemm gemm_args(const void *A, const void *A2, const void *B, int M, int N, int K, const float *sx,
                         const float *sw, const float *bias, int epi, float *C, int ldc) {
     FwGemm g;
@@ -347,11 +353,20 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
         fw_launch_enc_ln(st, b.x, l.mlp_ln_w, l.mlp_ln_b, M, d, i8 ? FW_LN_I7 : FW_LN_SPLIT, nullptr, b.hh, b.hl,
                          b.hq, b.hs);
         if (i8) {
-            g = gemm_args(b.hq, nullptr, l.fc1_7, M, dff, d, b.hs, l.fc1_7s, l.fc1_b, FW_EPI_F32, b.ff, dff);
+            // fc1 as f16 GELU-table indices (half the bytes of f32 rows; the
+            // rare |v| >= 9.98 values exactly in b.ff), then GELU + quantization;
+            // f32 rows where the index form has no kernel
+            g = gemm_args(b.hq, nullptr, l.fc1_7, M, dff, d, b.hs, l.fc1_7s, l.fc1_b, FW_EPI_F16IDX, b.ff, dff);
+            g.o16[0] = b.gh;
             fw_timed_begin(c, gcls, 2.0 * M * (double)dff * d, &ev);
-            fw_launch_gemm(st, kind, g);
+            bool idx = enc_h16_ok(dff) && fw_launch_gemm(st, kind, g);
+            if (!idx) {
+                g.epi = FW_EPI_F32;
+                fw_launch_gemm(st, kind, g);
+            }
             fw_timed_end(c, &ev);
-            fw_launch_gelu_quant_i7_rows(st, b.ff, M, dff, gt, b.gq, b.gs);
+            if (!idx || !fw_launch_gelu_quant_h16(st, b.gh, b.ff, M, dff, gt, b.gq, b.gs))
+                fw_launch_gelu_quant_i7_rows(st, b.ff, M, dff, gt, b.gq, b.gs);
             g = gemm_args(b.gq, nullptr, l.fc2_7, M, d, dff, b.gs, l.fc2_7s, l.fc2_b, FW_EPI_RESID, b.x, d);
         } else {
             g = gemm_args(b.hh, b.hl, l.fc1_16, M, dff, d, nullptr, nullptr, l.fc1_b, FW_EPI_GELU_SPLIT, nullptr,

@@ -14,6 +14,12 @@
 #define FW_EPI_CONV2 4
 #define FW_EPI_QKV 5
 #define FW_EPI_ACC32 6
+// int8 only: v = (acc * s_x) * s_w + b stored as its f16 bits (the index of
+// the f16 GELU table) when |v| < FW_GIDX_LIM, else FW_GIDX_SENT with the exact
+// v written at the same index of the f32 side array C
+#define FW_EPI_F16IDX 7
+#define FW_GIDX_LIM 9.98f
+#define FW_GIDX_SENT 0xffffu
 
 // Position of key t in a V^T row: bits 2 and 3 swapped, so the keys
 // {16g + 4h + 0..3, 16g + 8 + 4h + 0..3} one attention MFMA lane multiplies
@@ -40,12 +46,18 @@ struct FwGemm {
     int map; // tile order (set by fw_launch_gemm)
 };
 
-void fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g);
+// false when the operand kind / epilogue pair has no kernel (nothing launched)
+bool fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g);
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
                       float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs);
 void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs);
 void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int n, const float *tab, int8_t *q,
                                   float *qs);
+// The same GELU + quantization from FW_EPI_F16IDX rows (f16 table indices hx,
+// exact values of the sentinel elements in side); false when n is not a
+// supported width (a multiple of 512 up to 8192).
+bool fw_launch_gelu_quant_h16(hipStream_t st, const uint16_t *hx, const float *side, int rows, int n,
+                              const float *tab, int8_t *q, float *qs);
 void fw_launch_im2col(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, int Kp,
                       uint16_t *hi, uint16_t *lo);
 void fw_launch_mel_window(hipStream_t st, const float *mel, int n_mel, long long mel_frames, const long long *offs,
