@@ -85,7 +85,7 @@ def cpu_baseline(model, n_windows, n_tokens, threads, sample_windows):
     }
 
 
-TRAFFIC_FILE = "profiles/k_gemm2_int8_encoder_job.md"
+TRAFFIC_FILE = "profiles/k_gemm_pi8_int8_encoder_job.md"
 
 
 def measured_traffic():

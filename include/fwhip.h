@@ -229,7 +229,8 @@ void fwhip_decoder_free(fwhip_decoder *dec);
 
 /* A cohort of n_streams independent DecoderStates (decoder.rs:980-1027), each
  * with its own f16 self-attention KV cache (KvCache, nn.rs:5138) of
- * n_text_ctx tokens and its own cross K/V over enc_frames encoder rows. */
+ * n_text_ctx tokens and its own cross K/V over enc_frames encoder rows
+ * (FWHIP_DEC_INT8: enc_frames <= 1536; Whisper's encoder emits 1500). */
 fwhip_status fwhip_dstate_new(fwhip_decoder *dec, int32_t n_streams, int32_t enc_frames,
                               fwhip_dstate **out);
 void fwhip_dstate_free(fwhip_dstate *st);
