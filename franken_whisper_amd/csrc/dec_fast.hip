@@ -713,12 +713,17 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
 // and c + 64 of each row (d <= 2048).  The LayerNorm operands are requested
 // first and two batches of weight rows right behind them; the third batch is
 // requested once the first has been used.
-template <int NV>
+//
+// EMB (layer 0): the residual row is the token embedding first (embed_tokens,
+// decoder.rs:1323-1385: x = f16(E[tok]) + P[pos], as k_embed_ln), which every
+// block forms for its stream and the head-0 block also stores as x.
+template <int NV, bool EMB>
 __global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restrict__ wqkv, const float *__restrict__ sqkv,
-                                                         const float *__restrict__ bqkv, const float *__restrict__ x,
+                                                         const float *__restrict__ bqkv, float *x,
                                                          const float *__restrict__ lnw, const float *__restrict__ lnb,
                                                          uint16_t *kc, uint16_t *vc, float *att, const int *posp, int d,
-                                                         int nctx, int L, int layer, float scale, float *pmax) {
+                                                         int nctx, int L, int layer, float scale, float *pmax,
+                                                         const int32_t *tok, const uint16_t *emb, const float *pemb) {
     extern __shared__ __align__(16) unsigned char sm3[];
     float *sc = (float *)sm3;                                              // [nctx]
     uint16_t *vs = (uint16_t *)(sm3 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
@@ -733,10 +738,24 @@ __global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restric
     const int base = h * 64;
     float4 lv[NV], lw[NV], lb[NV];
     bool lok[NV];
+    if constexpr (EMB) {
+        const uint2 *er = (const uint2 *)(emb + (size_t)tok[s] * d);
+        const float4 *pr = (const float4 *)(pemb + (size_t)(*posp) * d);
 #pragma unroll
-    for (int k = 0; k < NV; k++) {
-        lok[k] = lane + k * 64 < (d >> 2);
-        lv[k] = ((const float4 *)(x + (size_t)s * d))[lok[k] ? lane + k * 64 : 0];
+        for (int k = 0; k < NV; k++) {
+            lok[k] = lane + k * 64 < (d >> 2);
+            const int c = lok[k] ? lane + k * 64 : 0;
+            const uint2 e = er[c];
+            const float4 p = pr[c];
+            lv[k] = make_float4(fw_h2f(e.x & 0xffff) + p.x, fw_h2f(e.x >> 16) + p.y, fw_h2f(e.y & 0xffff) + p.z,
+                                fw_h2f(e.y >> 16) + p.w);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            lok[k] = lane + k * 64 < (d >> 2);
+            lv[k] = ((const float4 *)(x + (size_t)s * d))[lok[k] ? lane + k * 64 : 0];
+        }
     }
     fw_ln_load_wb<NV>(lok, lnw, lnb, lw, lb, lane);
     if (d < 0) {
@@ -745,6 +764,13 @@ __global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restric
         // them into that branch behind everything else
 #pragma unroll
         for (int k = 0; k < NV; k++) qkvl[k] = lv[k].x + lw[k].y + lb[k].z;
+    }
+    if constexpr (EMB) {
+        if (h == 0 && wave == 0) {
+#pragma unroll
+            for (int k = 0; k < NV; k++)
+                if (lok[k]) ((float4 *)(x + (size_t)s * d))[lane + k * 64] = lv[k];
+        }
     }
     const int nq = d >> 4;
     const int qc0 = lane < nq ? lane : 0, qc1 = lane + 64 < nq ? lane + 64 : 0;
@@ -1240,13 +1266,46 @@ void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16
                        scale, pmax);
 }
 
-void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *sqkv, const float *bqkv,
-                               const float *x, const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc,
-                               float *att, const int *posp, int d, int H, int nctx, int L, int layer, int ns,
-                               float scale, float *pmax) {
+template <int NV>
+using k_self_attn_fused_e = void (*)(const int8_t *, const float *, const float *, float *, const float *,
+                                     const float *, uint16_t *, uint16_t *, float *, const int *, int, int, int, int,
+                                     float, float *, const int32_t *, const uint16_t *, const float *);
+template <int NV>
+static void launch_self_attn_fused(hipStream_t st, bool embed, dim3 grid, size_t shm, const int8_t *wqkv,
+                                   const float *sqkv, const float *bqkv, float *x, const float *lnw,
+                                   const float *lnb, uint16_t *kc, uint16_t *vc, float *att, const int *posp, int d,
+                                   int nctx, int L, int layer, float scale, float *pmax, const int32_t *tok,
+                                   const uint16_t *emb, const float *pemb) {
+    const k_self_attn_fused_e<NV> k = embed ? k_self_attn_fused<NV, true> : k_self_attn_fused<NV, false>;
+    hipLaunchKernelGGL(k, grid, dim3(512), shm, st, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,
+                       layer, scale, pmax, tok, emb, pemb);
+}
+
+void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *sqkv, const float *bqkv, float *x,
+                               const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
+                               const int *posp, int d, int H, int nctx, int L, int layer, int ns, float scale,
+                               float *pmax, const int32_t *tok, const uint16_t *emb, const float *pemb) {
     size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
-    FW_ROWS_DISPATCH(k_self_attn_fused, d, dim3(H, ns), dim3(512), shm, st, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc,
-                     att, posp, d, nctx, L, layer, scale, pmax);
+    const bool e = emb != nullptr;
+    const dim3 grid(H, ns);
+    switch ((d + 255) / 256) {
+#define SAF(NV)                                                                                                      \
+    case NV:                                                                                                         \
+        launch_self_attn_fused<NV>(st, e, grid, shm, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,    \
+                                   layer, scale, pmax, tok, emb, pemb);                                               \
+        break;
+        SAF(1)
+        SAF(2)
+        SAF(3)
+        SAF(4)
+        SAF(5)
+        SAF(6)
+        SAF(7)
+    default: launch_self_attn_fused<8>(st, e, grid, shm, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,
+                                       layer, scale, pmax, tok, emb, pemb);
+        break;
+#undef SAF
+    }
 }
 
 void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,

@@ -39,11 +39,14 @@ void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16
                           int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax = nullptr);
 // The int8 arm's self-attention sublayer: attention LayerNorm of the residual
 // rows x, the fused q/k/v projection (int8 rows wqkv [3d, d], row scales sqkv,
-// bias bqkv), cache append and attention; per-head output maxima into pmax
-void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *sqkv, const float *bqkv,
-                               const float *x, const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc,
-                               float *att, const int *posp, int d, int H, int nctx, int L, int layer, int ns,
-                               float scale, float *pmax);
+// bias bqkv), cache append and attention; per-head output maxima into pmax.
+// With emb (layer 0) the rows are first formed as the token embeddings
+// f16(emb[tok]) + pemb[pos] and stored to x.
+void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *sqkv, const float *bqkv, float *x,
+                               const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
+                               const int *posp, int d, int H, int nctx, int L, int layer, int ns, float scale,
+                               float *pmax, const int32_t *tok = nullptr, const uint16_t *emb = nullptr,
+                               const float *pemb = nullptr);
 // q = Wq LN(x): the cross LayerNorm (lnw, lnb) of the residual rows x and the
 // int8 cross q projection [d, d] (row scales swq, bias bq) run in the kernel
 void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,

@@ -566,12 +566,9 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
     bool i8 = dd->arm == FWHIP_DEC_INT8;
     float scale = powf(64.0f, -0.25f);
     const float *gt = c->gelu_tab;
-    // embedding (+ layer 0's attention LayerNorm on the f16 arm; the int8 arm's
-    // runs inside the self-attention kernel)
-    if (i8)
-        fw_launch_embed_ln(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S, nullptr, nullptr, nullptr, nullptr,
-                           nullptr);
-    else
+    // embedding + layer 0's attention LayerNorm (the int8 arm forms both inside
+    // layer 0's self-attention kernel)
+    if (!i8)
         fw_launch_embed_ln(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S, dd->layers[0].attn_ln_w,
                            dd->layers[0].attn_ln_b, st->h, nullptr, nullptr);
     for (int li = 0; li < L; li++) {
@@ -583,7 +580,9 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             // attention LayerNorm, q/k/v projection and attention in one kernel;
             // it writes per-head maxima; the o / co GEMVs quantize att themselves
             fw_launch_self_attn_fused(s, l.qkv8, l.qkv8s, l.qkv_b, st->x, l.attn_ln_w, l.attn_ln_b, st->kv_k,
-                                      st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale, st->pmax);
+                                      st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale, st->pmax,
+                                      li == 0 ? tok : nullptr, li == 0 ? dd->emb16 : nullptr,
+                                      li == 0 ? dd->pos_emb : nullptr);
             gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr, st->att);
             // the cross LayerNorm and q projection run inside the cross-attention kernel
             fw_launch_cross_attn_i8v2(s, l.cq8, l.cq8s, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck8, st->ck8s,
