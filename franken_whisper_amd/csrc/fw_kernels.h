@@ -25,6 +25,10 @@ void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w
 void fw_launch_embed_ln(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,
                         float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs);
 int fw_gemv_i8m_blocks(int N);
+// W of fw_launch_gemv_i8m is stored as MFMA operand fragments: bytes needed
+// for an [N, K] matrix (K % 64 == 0), and the repacking of a row-major one
+size_t fw_gemv_frag_bytes(int N, int K);
+void fw_launch_pack_gemv_frags(hipStream_t st, const int8_t *W, int8_t *Wf, int N, int K);
 void fw_launch_gemv_i8m(hipStream_t st, const int8_t *W, const float *sw, const float *bias, const int8_t *xq,
                         const float *xs, float *y, int N, int K, int ns, int ldy, int mode, const float *gelu_tab,
                         const fwhip_filter *filt, const int *initialp, unsigned long long *keys,

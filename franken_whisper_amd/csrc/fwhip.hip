@@ -198,6 +198,8 @@ void fw_free_all(std::vector<void *> &owned) {
 struct DecLayerDev {
     const float *attn_ln_w, *attn_ln_b, *cross_ln_w, *cross_ln_b, *mlp_ln_w, *mlp_ln_b;
     const float *qkv_b, *o_b, *cq_b, *co_b, *fc1_b, *fc2_b, *cv_b;
+    // o8, co8, fc1_8 (and the decoder's emb8) are in the int8 GEMV's fragment
+    // order; qkv8 and cq8 (read by the attention kernels) are row-major
     const int8_t *qkv8 = nullptr, *o8 = nullptr, *cq8 = nullptr, *co8 = nullptr, *fc1_8 = nullptr,
                  *fc2_b8 = nullptr;
     const float *qkv8s = nullptr, *o8s = nullptr, *cq8s = nullptr, *co8s = nullptr, *fc1_8s = nullptr,
@@ -240,19 +242,33 @@ struct fwhip_dstate {
     std::vector<void *> owned;
 };
 
-// Quantize a host f16 [out, inp] matrix to per-row int8 on the device.
+// Quantize a host f16 [out, inp] matrix to per-row int8 on the device; with
+// `frag` the int8 matrix is kept in the int8 GEMV's fragment order
+// (fw_launch_pack_gemv_frags) instead of row-major.
 static bool dev_quant_rows(fwhip_ctx *c, std::vector<void *> &owned, const uint16_t *host, int64_t out, int inp,
-                           const int8_t **q, const float **s) {
+                           const int8_t **q, const float **s, bool frag = false) {
     uint16_t *tmp = nullptr;
+    int8_t *rm = nullptr;
     size_t bytes = sizeof(uint16_t) * (size_t)out * inp;
-    if (hipMalloc(&tmp, bytes) != hipSuccess) return false;
-    if (hipMemcpy(tmp, host, bytes, hipMemcpyHostToDevice) != hipSuccess) return false;
-    int8_t *qq = (int8_t *)fw_dalloc(owned, (size_t)out * inp);
-    float *ss = (float *)fw_dalloc(owned, sizeof(float) * out);
-    if (!qq || !ss) return false;
-    fw_launch_quant_f16_rows(c->stream, tmp, qq, ss, (int)out, inp);
-    if (hipStreamSynchronize(c->stream) != hipSuccess) return false;
-    hipFree(tmp);
+    bool ok = hipMalloc(&tmp, bytes) == hipSuccess;
+    ok = ok && hipMemcpy(tmp, host, bytes, hipMemcpyHostToDevice) == hipSuccess;
+    int8_t *qq = nullptr;
+    float *ss = ok ? (float *)fw_dalloc(owned, sizeof(float) * out) : nullptr;
+    if (ok && frag) {
+        qq = (int8_t *)fw_dalloc(owned, fw_gemv_frag_bytes((int)out, inp));
+        ok = qq && hipMalloc(&rm, (size_t)out * inp) == hipSuccess;
+    } else if (ok) {
+        rm = qq = (int8_t *)fw_dalloc(owned, (size_t)out * inp);
+    }
+    ok = ok && ss && rm;
+    if (ok) {
+        fw_launch_quant_f16_rows(c->stream, tmp, rm, ss, (int)out, inp);
+        if (frag) fw_launch_pack_gemv_frags(c->stream, rm, qq, (int)out, inp);
+        ok = hipStreamSynchronize(c->stream) == hipSuccess;
+    }
+    if (tmp) hipFree(tmp);
+    if (frag && rm) hipFree(rm);
+    if (!ok) return false;
     *q = qq;
     *s = ss;
     return true;
@@ -334,7 +350,7 @@ extern "C" fwhip_status fwhip_decoder_load(fwhip_ctx *c, const fwhip_decoder_wei
     dd->pos_emb = up32(w->pos_emb, (size_t)dd->nctx * d);
     dd->ln_w = up32(w->ln_w, d);
     dd->ln_b = up32(w->ln_b, d);
-    if (ok && arm == FWHIP_DEC_INT8) ok = dev_quant_rows(c, own, w->tok_emb, dd->V, d, &dd->emb8, &dd->emb8s);
+    if (ok && arm == FWHIP_DEC_INT8) ok = dev_quant_rows(c, own, w->tok_emb, dd->V, d, &dd->emb8, &dd->emb8s, true);
     for (int li = 0; ok && li < dd->L; li++) {
         const fwhip_dec_layer &s = w->layers[li];
         DecLayerDev l;
@@ -364,10 +380,10 @@ extern "C" fwhip_status fwhip_decoder_load(fwhip_ctx *c, const fwhip_decoder_wei
         l.fc2_16 = up16(s.fc2_w, (size_t)d * dff); // prefill arm of mlp_2 in both arms
         if (arm == FWHIP_DEC_INT8) {
             ok = ok && dev_quant_rows(c, own, qkv.data(), 3 * d, d, &l.qkv8, &l.qkv8s);
-            ok = ok && dev_quant_rows(c, own, s.o_w, d, d, &l.o8, &l.o8s);
+            ok = ok && dev_quant_rows(c, own, s.o_w, d, d, &l.o8, &l.o8s, true);
             ok = ok && dev_quant_rows(c, own, s.cq_w, d, d, &l.cq8, &l.cq8s);
-            ok = ok && dev_quant_rows(c, own, s.co_w, d, d, &l.co8, &l.co8s);
-            ok = ok && dev_quant_rows(c, own, s.fc1_w, dff, d, &l.fc1_8, &l.fc1_8s);
+            ok = ok && dev_quant_rows(c, own, s.co_w, d, d, &l.co8, &l.co8s, true);
+            ok = ok && dev_quant_rows(c, own, s.fc1_w, dff, d, &l.fc1_8, &l.fc1_8s, true);
             ok = ok && dev_quant_blocked(c, own, s.fc2_w, d, dff, &l.fc2_b8, &l.fc2_b8s);
         } else {
             l.qkv16 = up16(qkv.data(), (size_t)3 * d * d);
