@@ -201,11 +201,22 @@ __global__ void __launch_bounds__(256) k_gelu_quant_i7_rows(const float *x, int 
 // float4 groups per lane; rows of n % 8 == 0 values use the add-trunc rounding
 // throughout.
 #define GQ_TAB_N 65536
+// The f16 GELU table into LDS: 16 bytes per thread and load, every load issued
+// before the first store (blockDim.x == 1024).
+__device__ __forceinline__ void fw_gtab_fill(uint16_t *gtab, const uint16_t *tab16) {
+    const uint4 *s = (const uint4 *)tab16;
+    uint4 *d = (uint4 *)gtab;
+    uint4 v[GQ_TAB_N / 8 / 1024];
+#pragma unroll
+    for (int u = 0; u < GQ_TAB_N / 8 / 1024; u++) v[u] = s[threadIdx.x + u * 1024];
+#pragma unroll
+    for (int u = 0; u < GQ_TAB_N / 8 / 1024; u++) d[threadIdx.x + u * 1024] = v[u];
+}
 template <int NV4, bool FULL>
-__global__ void __launch_bounds__(1024) k_gelu_quant_rows_lds(const float *x, int rows, int n, const float *gelu_tab,
+__global__ void __launch_bounds__(1024) k_gelu_quant_rows_lds(const float *x, int rows, int n, const uint16_t *tab16,
                                                              int8_t *q, float *qs) {
     extern __shared__ uint16_t gtab[]; // [65536]
-    for (int i = threadIdx.x; i < GQ_TAB_N; i += blockDim.x) gtab[i] = fw_f2h(gelu_tab[i]); // values are f16-exact
+    fw_gtab_fill(gtab, tab16);
     __syncthreads();
     const int lane = threadIdx.x & 63, wpb = blockDim.x >> 6;
     const int n4 = n >> 2;
@@ -275,9 +286,9 @@ __global__ void __launch_bounds__(1024) k_gelu_quant_rows_lds(const float *x, in
 // l + 64, ... (NV8 of them: n == 512 * NV8).
 template <int NV8>
 __global__ void __launch_bounds__(1024) k_gelu_quant_h16(const uint16_t *hx, const float *side, int rows, int n,
-                                                        const float *gelu_tab, int8_t *q, float *qs) {
+                                                        const uint16_t *tab16, int8_t *q, float *qs) {
     extern __shared__ uint16_t gtab[]; // [65536]
-    for (int i = threadIdx.x; i < GQ_TAB_N; i += blockDim.x) gtab[i] = fw_f2h(gelu_tab[i]); // values are f16-exact
+    fw_gtab_fill(gtab, tab16);
     __syncthreads();
     const int lane = threadIdx.x & 63, wpb = blockDim.x >> 6;
     for (int r = blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += gridDim.x * wpb) {
@@ -681,17 +692,18 @@ void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int 
     // the MLP widths of the Whisper sizes (4 x 384 ... 4 x 1280) are whole
     // multiples of 256: every lane's groups are in the row
     if (tab && (n & 255) == 0) {
+        const uint16_t *t16 = fw_gelu_tab16(tab);
         switch (n / 256) {
-        case 6: hipLaunchKernelGGL((k_gelu_quant_rows_lds<6, true>), grid, blk, shm, st, x, rows, n, tab, q, qs); return;
-        case 8: hipLaunchKernelGGL((k_gelu_quant_rows_lds<8, true>), grid, blk, shm, st, x, rows, n, tab, q, qs); return;
+        case 6: hipLaunchKernelGGL((k_gelu_quant_rows_lds<6, true>), grid, blk, shm, st, x, rows, n, t16, q, qs); return;
+        case 8: hipLaunchKernelGGL((k_gelu_quant_rows_lds<8, true>), grid, blk, shm, st, x, rows, n, t16, q, qs); return;
         case 12:
-            hipLaunchKernelGGL((k_gelu_quant_rows_lds<12, true>), grid, blk, shm, st, x, rows, n, tab, q, qs);
+            hipLaunchKernelGGL((k_gelu_quant_rows_lds<12, true>), grid, blk, shm, st, x, rows, n, t16, q, qs);
             return;
         case 16:
-            hipLaunchKernelGGL((k_gelu_quant_rows_lds<16, true>), grid, blk, shm, st, x, rows, n, tab, q, qs);
+            hipLaunchKernelGGL((k_gelu_quant_rows_lds<16, true>), grid, blk, shm, st, x, rows, n, t16, q, qs);
             return;
         case 20:
-            hipLaunchKernelGGL((k_gelu_quant_rows_lds<20, true>), grid, blk, shm, st, x, rows, n, tab, q, qs);
+            hipLaunchKernelGGL((k_gelu_quant_rows_lds<20, true>), grid, blk, shm, st, x, rows, n, t16, q, qs);
             return;
         default: break;
         }
@@ -711,7 +723,9 @@ bool fw_launch_gelu_quant_h16(hipStream_t st, const uint16_t *hx, const float *s
     const size_t shm = sizeof(uint16_t) * GQ_TAB_N;
     const dim3 grid(n_cu), blk(1024);
 #define GQH(NV8)                                                                                                     \
-    case NV8: hipLaunchKernelGGL((k_gelu_quant_h16<NV8>), grid, blk, shm, st, hx, side, rows, n, tab, q, qs); return true;
+    case NV8:                                                                                                        \
+        hipLaunchKernelGGL((k_gelu_quant_h16<NV8>), grid, blk, shm, st, hx, side, rows, n, fw_gelu_tab16(tab), q, qs); \
+        return true;
     switch (n / 512) {
         GQH(1)
         GQH(2)

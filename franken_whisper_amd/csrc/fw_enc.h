@@ -51,6 +51,9 @@ bool fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g);
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
                       float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs);
 void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs);
+// The f16 copy of the GELU table that follows the f32 one (65536 entries) in
+// the context's allocation; tab is the context's f32 table.
+inline const uint16_t *fw_gelu_tab16(const float *tab) { return (const uint16_t *)(tab + 65536); }
 void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int n, const float *tab, int8_t *q,
                                   float *qs);
 // The same GELU + quantization from FW_EPI_F16IDX rows (f16 table indices hx,

@@ -31,7 +31,9 @@ struct fwhip_ctx {
     bool timing = false;
     std::vector<fw_event_pair> pending;
     std::map<int, fw_kstat> stats;
-    float *gelu_tab = nullptr; // device [65536]
+    // device: the GELU table [65536] f32, followed in the same allocation by
+    // the same values as f16 (fw_gelu_tab16)
+    float *gelu_tab = nullptr;
 };
 
 fwhip_status fw_fail(fwhip_status code, const std::string &msg);

@@ -57,14 +57,21 @@ extern "C" fwhip_status fwhip_init(int32_t device, fwhip_ctx **out) {
     }
     // GELU table (gelu_table, nn.rs:4561-4575) built on the host with the
     // platform tanhf, exactly as the reference builds it.
+    // The f32 values are f16-exact; their f16 copy follows them in the same
+    // allocation (fw_gelu_tab16) for the kernels that keep the table in LDS.
     std::vector<float> tab(1 << 16);
+    std::vector<uint16_t> tab16(1 << 16);
     for (int i = 0; i < (1 << 16); i++) {
         float f = fw_host_h2f((uint16_t)i);
         float g = 0.5f * f * (1.0f + tanhf(0.7978846f * f * (1.0f + 0.044715f * f * f)));
-        tab[i] = fw_host_h2f(fw_host_f2h(g));
+        tab16[i] = fw_host_f2h(g);
+        tab[i] = fw_host_h2f(tab16[i]);
     }
-    if (hipMalloc(&c->gelu_tab, sizeof(float) * tab.size()) != hipSuccess ||
-        hipMemcpy(c->gelu_tab, tab.data(), sizeof(float) * tab.size(), hipMemcpyHostToDevice) != hipSuccess) {
+    const size_t tb = sizeof(float) * tab.size();
+    if (hipMalloc(&c->gelu_tab, tb + sizeof(uint16_t) * tab16.size()) != hipSuccess ||
+        hipMemcpy(c->gelu_tab, tab.data(), tb, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy((char *)c->gelu_tab + tb, tab16.data(), sizeof(uint16_t) * tab16.size(), hipMemcpyHostToDevice) !=
+            hipSuccess) {
         fwhip_destroy(c);
         return fw_fail(FWHIP_ERR_GENERIC, "gelu table upload failed");
     }
