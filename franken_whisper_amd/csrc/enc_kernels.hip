@@ -31,7 +31,8 @@ __device__ __forceinline__ void fw_split(float v, uint16_t &hi, uint16_t &lo) {
 // I7 (quantize_act_i7, nn.rs:1443-1466: per-row amax/127, add-trunc body /
 // exact tail, stored as the signed value q = u8 - 128).  One wave per row (4
 // rows per block), the row held in registers as float4s (d <= 2048, d % 4 ==
-// 0); every load is unconditional (clamped index).
+// 0); every load is unconditional (clamped index) and issued before the first
+// use: row, weight and bias together, so a row costs one memory round trip.
 #define ELN_V4 8
 __device__ __forceinline__ double eln_wave_sum(double v) {
 #pragma unroll
@@ -46,13 +47,20 @@ __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, 
     if (r >= (size_t)rows) return;
     const int n4 = d >> 2; // float4 per row; lane owns float4 slots lane + 64k
     const float4 *xr = (const float4 *)(x + r * d);
-    float4 xv[ELN_V4];
+    const float4 *wr = (const float4 *)w, *br = (const float4 *)b;
+    float4 xv[ELN_V4], wv4[ELN_V4], bv4[ELN_V4];
     bool ok[ELN_V4];
 #pragma unroll
     for (int k = 0; k < ELN_V4; k++) {
         const int c4 = lane + 64 * k;
         ok[k] = c4 < n4;
         xv[k] = xr[ok[k] ? c4 : 0];
+    }
+#pragma unroll
+    for (int k = 0; k < ELN_V4; k++) {
+        const int c4 = ok[k] ? lane + 64 * k : 0;
+        wv4[k] = wr[c4];
+        bv4[k] = br[c4];
     }
     double s = 0.0;
 #pragma unroll
@@ -69,13 +77,11 @@ __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, 
         }
     const double var = eln_wave_sum(v) / (double)d;
     const double inv = 1.0 / sqrt(var + (double)1e-5f);
-    const float4 *wr = (const float4 *)w, *br = (const float4 *)b;
     float yv[ELN_V4][4];
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < ELN_V4; k++) {
-        const int c4 = ok[k] ? lane + 64 * k : 0;
-        const float4 ww = wr[c4], bb = br[c4];
+        const float4 ww = wv4[k], bb = bv4[k];
         const float xs[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
         const float wv[4] = {ww.x, ww.y, ww.z, ww.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
 #pragma unroll
@@ -191,6 +197,35 @@ __global__ void __launch_bounds__(256) k_gelu_quant_i7_rows(const float *x, int 
     const float sc = fmaxf(m, 1e-9f) / 127.0f;
     const float inv = 1.0f / sc;
     for (int i = lane; i < n; i += 64) q[r * n + i] = fw_q8_avx(gelu_tab ? fw_gelu(xr[i], gelu_tab) : xr[i], inv, i, n);
+    if (lane == 0) qs[r] = sc;
+}
+
+// The same quantization with one wave per row (4 rows per block) for rows of
+// n % 4 == 0 values, n <= 256 * NV: lane l holds float4 groups l, l + 64, ...,
+// all loads issued before the first use, a DPP max, and 4-byte stores.
+template <int NV>
+__global__ void __launch_bounds__(256) k_quant_exact_rows_w(const float *x, int rows, int n, int8_t *q, float *qs) {
+    const int lane = threadIdx.x & 63;
+    const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= (size_t)rows) return;
+    const int n4 = n >> 2;
+    const float4 *xr = (const float4 *)(x + r * n);
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) v[k] = xr[lane + 64 * k < n4 ? lane + 64 * k : 0];
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; k++)
+        if (lane + 64 * k < n4) m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+    m = fw_dpp_wave_max(m);
+    const float sc = fmaxf(m, 1e-9f) / 127.0f;
+    const float inv = 1.0f / sc;
+    auto qe = [&](float t) { return (uint32_t)(uint8_t)(int8_t)(int)fw_clamp(fw_round_away(t * inv), -127.0f, 127.0f); };
+#pragma unroll
+    for (int k = 0; k < NV; k++)
+        if (lane + 64 * k < n4)
+            ((uint32_t *)(q + r * n))[lane + 64 * k] =
+                qe(v[k].x) | (qe(v[k].y) << 8) | (qe(v[k].z) << 16) | (qe(v[k].w) << 24);
     if (lane == 0) qs[r] = sc;
 }
 
@@ -676,6 +711,20 @@ void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const floa
     hipLaunchKernelGGL(k_enc_ln, dim3((rows + 3) / 4), dim3(256), 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs);
 }
 void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs) {
+    const dim3 g4((rows + 3) / 4), b4(256);
+    if (n % 4 == 0 && n > 0) {
+        switch ((n + 255) / 256) {
+        case 1: hipLaunchKernelGGL(k_quant_exact_rows_w<1>, g4, b4, 0, st, x, rows, n, q, qs); return;
+        case 2: hipLaunchKernelGGL(k_quant_exact_rows_w<2>, g4, b4, 0, st, x, rows, n, q, qs); return;
+        case 3: hipLaunchKernelGGL(k_quant_exact_rows_w<3>, g4, b4, 0, st, x, rows, n, q, qs); return;
+        case 4: hipLaunchKernelGGL(k_quant_exact_rows_w<4>, g4, b4, 0, st, x, rows, n, q, qs); return;
+        case 5: hipLaunchKernelGGL(k_quant_exact_rows_w<5>, g4, b4, 0, st, x, rows, n, q, qs); return;
+        case 6: hipLaunchKernelGGL(k_quant_exact_rows_w<6>, g4, b4, 0, st, x, rows, n, q, qs); return;
+        case 7: hipLaunchKernelGGL(k_quant_exact_rows_w<7>, g4, b4, 0, st, x, rows, n, q, qs); return;
+        case 8: hipLaunchKernelGGL(k_quant_exact_rows_w<8>, g4, b4, 0, st, x, rows, n, q, qs); return;
+        default: break;
+        }
+    }
     hipLaunchKernelGGL(k_quant_exact_rows, dim3(rows), dim3(256), 0, st, x, n, q, qs);
 }
 void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int n, const float *tab, int8_t *q,
