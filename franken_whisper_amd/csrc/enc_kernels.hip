@@ -30,18 +30,20 @@ __device__ __forceinline__ void fw_split(float v, uint16_t &hi, uint16_t &lo) {
 // GEMM consumes: mode F32 (ln_post), SPLIT (f16 hi/lo pair for the f32 path),
 // I7 (quantize_act_i7, nn.rs:1443-1466: per-row amax/127, add-trunc body /
 // exact tail, stored as the signed value q = u8 - 128).  One wave per row (4
-// rows per block), the row held in registers as float4s (d <= 2048, d % 4 ==
-// 0); every load is unconditional (clamped index) and issued before the first
-// use: row, weight and bias together, so a row costs one memory round trip.
-#define ELN_V4 8
+// rows per block), the row held in registers as NV float4s per lane (d <= 256
+// NV, d % 4 == 0); every load is unconditional (clamped index) and issued
+// before the first use: row, weight and bias together, so a row costs one
+// memory round trip.
 __device__ __forceinline__ double eln_wave_sum(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+template <int NV>
 __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, const float *b, int rows, int d,
                                                 int mode, float *yf, uint16_t *hi, uint16_t *lo, int8_t *q,
                                                 float *qs) {
+    constexpr int ELN_V4 = NV;
     const int lane = threadIdx.x & 63;
     const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= (size_t)rows) return;
@@ -708,7 +710,17 @@ void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qof
 // ---------------------------------------------------------------------------
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
                       float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs) {
-    hipLaunchKernelGGL(k_enc_ln, dim3((rows + 3) / 4), dim3(256), 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs);
+    const dim3 g((rows + 3) / 4), blk(256);
+    switch ((d + 255) / 256) {
+    case 1: hipLaunchKernelGGL(k_enc_ln<1>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    case 2: hipLaunchKernelGGL(k_enc_ln<2>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    case 3: hipLaunchKernelGGL(k_enc_ln<3>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    case 4: hipLaunchKernelGGL(k_enc_ln<4>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    case 5: hipLaunchKernelGGL(k_enc_ln<5>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    case 6: hipLaunchKernelGGL(k_enc_ln<6>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    case 7: hipLaunchKernelGGL(k_enc_ln<7>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    default: hipLaunchKernelGGL(k_enc_ln<8>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    }
 }
 void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs) {
     const dim3 g4((rows + 3) / 4), b4(256);
