@@ -757,6 +757,38 @@ __device__ __forceinline__ float fw_seq_sum_wave(const float *v, int n) {
 }
 
 // ---------------------------------------------------------------------------
+// sum_j p[j] * v[j*64 + t] (f16 values) in ascending j, one f32 chain per
+// thread (the attention value pass of one output column); the operands of 32
+// keys are read before their adds, so LDS latency is paid once per 32 keys.
+__device__ __forceinline__ float fw_pv_chain(const float *p, const uint16_t *v, int tk, int t) {
+    float acc = 0.0f;
+    int j = 0;
+    for (; j + 32 <= tk; j += 32) {
+        float pv[32], vv[32];
+#pragma unroll
+        for (int u = 0; u < 32; u++) {
+            pv[u] = p[j + u];
+            vv[u] = fw_h2f(v[(j + u) * 64 + t]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 32; u++) acc += pv[u] * vv[u];
+    }
+    for (; j + 8 <= tk; j += 8) {
+        float pv[8], vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            pv[u] = p[j + u];
+            vv[u] = fw_h2f(v[(j + u) * 64 + t]);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc += pv[u] * vv[u];
+    }
+    for (; j < tk; j++) acc += p[j] * fw_h2f(v[j * 64 + t]);
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
 // Self-attention over the f16 KV cache for one (head, stream), tq == 1
 // (attention_with_cache nn.rs:6267-6337 -> KvCache::append nn.rs:5352 ->
 // attention_decode_step_f16 nn.rs:6466-6540).  Appends this token's k/v (RNE
@@ -836,20 +868,7 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
         for (int j = t; j < tk; j += 256) sc[j] = sc[j] * inv;
     __syncthreads();
     if (t < 64) {
-        // ascending-j accumulation; operands for 8 keys are read before the adds
-        float acc = 0.0f;
-        int j = 0;
-        for (; j + 8 <= tk; j += 8) {
-            float pv[8], vv[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                pv[u] = sc[j + u];
-                vv[u] = fw_h2f(vs[(j + u) * 64 + t]);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc += pv[u] * vv[u];
-        }
-        for (; j < tk; j++) acc += sc[j] * fw_h2f(vs[j * 64 + t]);
+        const float acc = fw_pv_chain(sc, vs, tk, t);
         att[(size_t)s * d + base + t] = acc;
         // this head's share of the row amax the int8 consumer needs
         const float m = fw_dpp_wave_max(fabsf(acc));
@@ -1043,20 +1062,7 @@ __global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restric
         for (int j = t; j < tk; j += 512) sc[j] = sc[j] * inv;
     __syncthreads();
     if (t < 64) {
-        // ascending-j accumulation; operands for 8 keys are read before the adds
-        float acc = 0.0f;
-        int j = 0;
-        for (; j + 8 <= tk; j += 8) {
-            float pv[8], vv[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                pv[u] = sc[j + u];
-                vv[u] = fw_h2f(vs[(j + u) * 64 + t]);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc += pv[u] * vv[u];
-        }
-        for (; j < tk; j++) acc += sc[j] * fw_h2f(vs[j * 64 + t]);
+        const float acc = fw_pv_chain(sc, vs, tk, t);
         att[(size_t)s * d + base + t] = acc;
         // this head's share of the row amax the int8 consumer needs
         const float m = fw_dpp_wave_max(fabsf(acc));
