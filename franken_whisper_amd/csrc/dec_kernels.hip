@@ -14,12 +14,11 @@
 #define LN_EPS_F 1e-5f
 
 // ---------------------------------------------------------------------------
-// f16 GEMV in dot_f16c order (nn.rs:1983-2051), S streams per weight read.
+// f16 GEMV in dot_f16c order (nn.rs:1983-2051), MAXS streams per block.
 // Lane j (0..3) of a 4-lane group owns accumulator vector a_j (8 lanes of the
 // AVX register); chunk c covers elements [32c, 32c+32).
 // Block = 256 threads; 64 rows per block.
-#define GF16_U 4
-template <int MAXS>
+template <int MAXS, int U>
 __global__ void __launch_bounds__(256) k_gemv_f16(const uint16_t *__restrict__ W, const float *__restrict__ bias,
                                                   const float *__restrict__ x, float *y, int N, int K, int ns,
                                                   int ldy, int mode, const float *__restrict__ gelu_tab) {
@@ -68,9 +67,8 @@ __global__ void __launch_bounds__(256) k_gemv_f16(const uint16_t *__restrict__ W
             xc[s][1] = xp[1];
         }
     };
-    // the weight chunks of the next GF16_U iterations are in flight while the
+    // the weight chunks of the next U iterations are in flight while the
     // current ones are used (rows past N read row 0 and are never stored)
-    constexpr int U = GF16_U;
     uint4 wq[U];
 #pragma unroll
     for (int u = 0; u < U; u++) wq[u] = *(const uint4 *)(wr + (u < nc ? u : nc - 1) * 32 + j * 8);
@@ -292,17 +290,18 @@ __global__ void __launch_bounds__(64) k_quant_f16_rows(const uint16_t *src, int8
 // ---------------------------------------------------------------------------
 // launch wrappers
 
-// Streams go in groups of 4 over grid.y (one group per block keeps the grid
-// wide enough to fill the CUs; a weight chunk is still converted once per 4
-// streams).
+// Each thread's sequential chunk loop is latency-bound (a row's K/32 chunks in
+// order), so matrices up to 32 M weights run one stream per block row of the
+// grid (grid.y = ns) with 8 chunks of weights in flight per thread; larger ones
+// (the logits) keep 4 streams per block so the weights are read ns/4 times.
 void fw_launch_gemv_f16(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *y, int N,
                         int K, int ns, int ldy, int mode, const float *gelu_tab) {
-    if (ns == 1)
-        hipLaunchKernelGGL(k_gemv_f16<1>, dim3((N + 63) / 64, 1), dim3(256), 0, st, W, bias, x, y, N, K, ns, ldy, mode,
-                           gelu_tab);
+    if ((size_t)N * K <= ((size_t)32 << 20) || ns == 1)
+        hipLaunchKernelGGL((k_gemv_f16<1, 8>), dim3((N + 63) / 64, ns), dim3(256), 0, st, W, bias, x, y, N, K, ns,
+                           ldy, mode, gelu_tab);
     else
-        hipLaunchKernelGGL(k_gemv_f16<4>, dim3((N + 63) / 64, (ns + 3) / 4), dim3(256), 0, st, W, bias, x, y, N, K,
-                           ns, ldy, mode, gelu_tab);
+        hipLaunchKernelGGL((k_gemv_f16<4, 4>), dim3((N + 63) / 64, (ns + 3) / 4), dim3(256), 0, st, W, bias, x, y, N,
+                           K, ns, ldy, mode, gelu_tab);
 }
 
 void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,
