@@ -34,6 +34,11 @@ struct fwhip_ctx {
     // device: the GELU table [65536] f32, followed in the same allocation by
     // the same values as f16 (fw_gelu_tab16)
     float *gelu_tab = nullptr;
+    // log-mel: window and FFT twiddles (built on first use) and a scratch
+    // buffer grown on demand (filter ranges, per-block maxima, the floor)
+    void *mel_tab = nullptr;
+    void *mel_scratch = nullptr;
+    size_t mel_scratch_bytes = 0;
 };
 
 fwhip_status fw_fail(fwhip_status code, const std::string &msg);

@@ -88,6 +88,8 @@ extern "C" void fwhip_destroy(fwhip_ctx *c) {
         hipEventDestroy(e.b);
     }
     if (c->gelu_tab) hipFree(c->gelu_tab);
+    if (c->mel_tab) hipFree(c->mel_tab);
+    if (c->mel_scratch) hipFree(c->mel_scratch);
     hipStreamDestroy(c->stream);
     delete c;
 }

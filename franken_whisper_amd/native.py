@@ -55,6 +55,8 @@ SIGNATURES = {
     "fwhip_dstate_read": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_size_t]),
     "fwhip_decode_greedy": (C.c_int32, [_vp, _i32p, C.c_int32, C.c_int32, C.POINTER(abi.Filter), _i32p,
                                         _i32p]),
+    "fwhip_mel_frames": (C.c_int64, [C.c_int64]),
+    "fwhip_log_mel": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
 }
 
 _lib = None
@@ -113,6 +115,11 @@ class DeviceArray:
             self.ptr = None
 
 
+def mel_frames(n_samples: int) -> int:
+    """n_frames_for (src/native_engine/mel.rs:1127)."""
+    return int(lib().fwhip_mel_frames(n_samples))
+
+
 class Context:
     def __init__(self, device: int = 0):
         h = _vp()
@@ -140,6 +147,12 @@ class Context:
 
     def cancel(self):
         check(lib().fwhip_request_cancel(self.h))
+
+    def log_mel(self, samples_dev: DeviceArray, n_samples: int, filters_dev: DeviceArray, n_mel: int,
+                out_dev: DeviceArray, n_fft_bins: int = 201):
+        """log_mel (src/native_engine/mel.rs:1476): [n_mel, mel_frames(n)] into out_dev."""
+        check(lib().fwhip_log_mel(self.h, samples_dev.ptr if n_samples else None, n_samples,
+                                  filters_dev.ptr, n_mel, n_fft_bins, out_dev.ptr))
 
     def close(self):
         if self.h:

@@ -268,3 +268,33 @@ def mel_input(seed: int, n_windows: int, n_frames: int, n_mels: int) -> np.ndarr
     """Seeded N(0,1) time-major log-mel windows [n_windows, n_frames, n_mels]
     (an encoder input isolated from the log-mel frontend)."""
     return normal_f32(seed, "mel", (n_windows, n_frames, n_mels), std=1.0)
+
+
+def mel_filterbank(n_mel: int = 128, sample_rate: int = 16000, n_fft: int = 400) -> np.ndarray:
+    """Slaney-style triangular mel filterbank [n_mel, n_fft/2 + 1] f32 (the
+    construction of Whisper's mel_filters asset: Slaney mel scale, area
+    normalization), computed in f64 from the published formulas so the frontend
+    runs on a realistic sparse bank without the model file."""
+    n_bins = n_fft // 2 + 1
+    f_sp, min_log_hz = 200.0 / 3.0, 1000.0
+    min_log_mel = min_log_hz / f_sp
+    logstep = np.log(6.4) / 27.0
+
+    def hz_to_mel(f):
+        f = np.asarray(f, dtype=np.float64)
+        return np.where(f >= min_log_hz, min_log_mel + np.log(np.maximum(f, 1e-12) / min_log_hz) / logstep,
+                        f / f_sp)
+
+    def mel_to_hz(m):
+        m = np.asarray(m, dtype=np.float64)
+        return np.where(m >= min_log_mel, min_log_hz * np.exp(logstep * (m - min_log_mel)), f_sp * m)
+
+    fft_hz = np.linspace(0.0, sample_rate / 2.0, n_bins)
+    mel_hz = mel_to_hz(np.linspace(hz_to_mel(0.0), hz_to_mel(sample_rate / 2.0), n_mel + 2))
+    fdiff = np.diff(mel_hz)
+    ramps = mel_hz[:, None] - fft_hz[None, :]
+    lower = -ramps[:-2] / fdiff[:-1, None]
+    upper = ramps[2:] / fdiff[1:, None]
+    w = np.maximum(0.0, np.minimum(lower, upper))
+    w *= (2.0 / (mel_hz[2:] - mel_hz[:-2]))[:, None]
+    return w.astype(np.float32)

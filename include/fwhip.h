@@ -280,6 +280,23 @@ fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *prompt, int32_
                                  int32_t n_max_tokens, const fwhip_filter *filter,
                                  int32_t *out_tokens, int32_t *out_len);
 
+/* ---- log-mel frontend ---------------------------------------------------- */
+
+/* n_frames_for (src/native_engine/mel.rs:1127-1131): frames log_mel produces
+ * for n_samples raw 16 kHz samples, (n + 480000 + 400 - 400) / 160. */
+int64_t fwhip_mel_frames(int64_t n_samples);
+
+/* log_mel (src/native_engine/mel.rs:1476-1660, default two-for-one FFT path).
+ * samples_dev: n_samples f32 PCM on the device; filters_dev: the filterbank
+ * [n_mel, n_fft_bins] row-major f32 on the device (MelFilterbank,
+ * src/native_engine/mod.rs:143); mel_dev receives [n_mel, fwhip_mel_frames(n)]
+ * mel-major f32, bit-identical to the reference.  FWHIP_ERR_INVALID when
+ * n_fft_bins != 201 or n_mel == 0 (the reference's InvalidRequest cases), or
+ * n_mel > 256.  Enqueued on the context stream; fwhip_synchronize waits. */
+fwhip_status fwhip_log_mel(fwhip_ctx *ctx, const float *samples_dev, int64_t n_samples,
+                           const float *filters_dev, int32_t n_mel, int32_t n_fft_bins,
+                           float *mel_dev);
+
 #ifdef __cplusplus
 }
 #endif

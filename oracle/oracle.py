@@ -81,6 +81,11 @@ def lib():
         "ref_process_argmax": (C.c_int, [C.POINTER(abi.Filter), f32p, C.c_int, C.c_int]),
         "ref_decode_greedy": (C.c_int, [C.c_void_p, C.c_void_p, i32p, C.c_int, C.c_int,
                                         C.POINTER(abi.Filter), i32p, i32p]),
+        "ref_mel_frames": (C.c_int64, [C.c_int64]),
+        "ref_log_mel": (None, [f32p, C.c_int64, f32p, C.c_int, f32p]),
+        "ref_mel_fft400": (None, [f32p, f32p]),
+        "ref_log10_floor_approx": (C.c_float, [C.c_double]),
+        "ref_mel_hann": (None, [f32p]),
         "ref_num_threads": (C.c_int, []),
         "ref_set_num_threads": (None, [C.c_int]),
     }
@@ -257,6 +262,42 @@ def matmul_strict(a, b):
     c = np.empty((m, n), np.float32)
     lib().ref_matmul_strict(_p(a, C.c_float), _p(b, C.c_float), _p(c, C.c_float), m, k, n)
     return c
+
+
+def mel_frames(n_samples):
+    """n_frames_for, mel.rs:1127."""
+    return int(lib().ref_mel_frames(int(n_samples)))
+
+
+def log_mel(samples, filters):
+    """log_mel, mel.rs:1476-1660: mel-major [n_mel, mel_frames(n)], clamped and
+    normalized; filters [n_mel, 201] f32."""
+    x = _c(samples, np.float32)
+    f = _c(filters, np.float32)
+    n_mel = f.shape[0]
+    out = np.empty((n_mel, mel_frames(x.size)), dtype=np.float32)
+    lib().ref_log_mel(_p(x, C.c_float), x.size, _p(f, C.c_float), n_mel, _p(out, C.c_float))
+    return out
+
+
+def mel_fft400(frame):
+    """fft_twoforone, mel.rs:648-695, of one 400-sample frame: 400 complex bins."""
+    x = _c(frame, np.float32)
+    assert x.size == 400
+    out = np.empty(800, dtype=np.float32)
+    lib().ref_mel_fft400(_p(x, C.c_float), _p(out, C.c_float))
+    return out[0::2] + 1j * out[1::2].astype(np.float64)
+
+
+def log10_floor_approx(x):
+    """log10_floor_approx, mel.rs:1239-1249."""
+    return np.float32(lib().ref_log10_floor_approx(float(x)))
+
+
+def mel_hann():
+    out = np.empty(400, dtype=np.float32)
+    lib().ref_mel_hann(_p(out, C.c_float))
+    return out
 
 
 def argmax_first(x):

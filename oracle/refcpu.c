@@ -1132,3 +1132,223 @@ int ref_decode_greedy(const ref_decoder *dd, ref_dstate *s, const int32_t *promp
     free(logits);
     return rc;
 }
+
+
+/* ======================================================================
+ * log-mel frontend (mel.rs): periodic Hann window, the default two-for-one
+ * real FFT of 400 points (one complex FFT of 200 points: radix-2 splits
+ * 200 -> 100 -> 50 -> 25, radix-5 x 5 base), power spectrum, sparse f64 mel
+ * projection, log10 approximation, global clamp and normalization.
+ * ====================================================================== */
+#define MEL_NFFT 400
+#define MEL_HOP 160
+#define MEL_NBINS 201
+#define MEL_PAD1 480000 /* N_SAMPLES_30S */
+#define MEL_PAD2 200    /* N_FFT / 2 */
+
+static struct {
+    int ready;
+    float hann[MEL_NFFT];
+    float lcos[4][200], lnsin[4][200]; /* widths 400, 200, 100, 50 (half 200 >> l) */
+    float c5[25], s5[25], c25[25], s25[25];
+} mel_t;
+
+/* FftTwiddles::build / DftTable::build / hann_window (mel.rs:243-391):
+ * f64 transcendentals narrowed to f32 */
+static void mel_tables_init(void) {
+    if (mel_t.ready) return;
+    for (int i = 0; i < MEL_NFFT; i++)
+        mel_t.hann[i] = (float)(0.5 * (1.0 - cos((2.0 * M_PI * (double)i) / (double)MEL_NFFT)));
+    for (int l = 0; l < 4; l++) {
+        const int n = MEL_NFFT >> l, half = n / 2;
+        for (int k = 0; k < half; k++) {
+            const double th = (2.0 * M_PI * (double)k) / (double)n;
+            mel_t.lcos[l][k] = (float)cos(th);
+            mel_t.lnsin[l][k] = -(float)sin(th);
+        }
+    }
+    for (int k = 0; k < 5; k++)
+        for (int j = 0; j < 5; j++) {
+            const double th = (2.0 * M_PI * (double)(k * j)) / 5.0;
+            mel_t.c5[k * 5 + j] = (float)cos(th);
+            mel_t.s5[k * 5 + j] = (float)sin(th);
+            const double th2 = (2.0 * M_PI * (double)(k * j)) / 25.0;
+            mel_t.c25[k * 5 + j] = (float)cos(th2);
+            mel_t.s25[k * 5 + j] = (float)sin(th2);
+        }
+    mel_t.ready = 1;
+}
+
+/* radix5_cdft, mel.rs:533-577: complex 25-point DFT as 5 x 5 */
+static void mel_radix5_cdft(const float *in, float *out) {
+    float ir[5][5], ii[5][5], tr[5][5], ti[5][5];
+    for (int n2 = 0; n2 < 5; n2++)
+        for (int k1 = 0; k1 < 5; k1++) {
+            float re = 0.0f, im = 0.0f;
+            for (int n1 = 0; n1 < 5; n1++) {
+                const float xr = in[2 * (5 * n1 + n2)], xi = in[2 * (5 * n1 + n2) + 1];
+                const float c = mel_t.c5[k1 * 5 + n1], sn = mel_t.s5[k1 * 5 + n1];
+                re += xr * c + xi * sn;
+                im += xi * c - xr * sn;
+            }
+            ir[n2][k1] = re;
+            ii[n2][k1] = im;
+        }
+    for (int n2 = 0; n2 < 5; n2++)
+        for (int k1 = 0; k1 < 5; k1++) {
+            const float c = mel_t.c25[n2 * 5 + k1], sn = mel_t.s25[n2 * 5 + k1];
+            tr[n2][k1] = ir[n2][k1] * c + ii[n2][k1] * sn;
+            ti[n2][k1] = ii[n2][k1] * c - ir[n2][k1] * sn;
+        }
+    for (int k1 = 0; k1 < 5; k1++)
+        for (int k2 = 0; k2 < 5; k2++) {
+            float re = 0.0f, im = 0.0f;
+            for (int n2 = 0; n2 < 5; n2++) {
+                const float c = mel_t.c5[k2 * 5 + n2], sn = mel_t.s5[k2 * 5 + n2];
+                re += tr[n2][k1] * c + ti[n2][k1] * sn;
+                im += ti[n2][k1] * c - tr[n2][k1] * sn;
+            }
+            out[2 * (k1 + 5 * k2)] = re;
+            out[2 * (k1 + 5 * k2) + 1] = im;
+        }
+}
+
+/* cfft, mel.rs:604-646: recursive complex radix-2 DIT; level l has width 400 >> l */
+static void mel_cfft(const float *in, float *out, int n, int l) {
+    if (n == 1) {
+        out[0] = in[0];
+        out[1] = in[1];
+        return;
+    }
+    if (n % 2 == 1) { /* n == 25 */
+        mel_radix5_cdft(in, out);
+        return;
+    }
+    const int half = n / 2;
+    float even[400], odd[400], ef[400], of[400];
+    for (int i = 0; i < half; i++) {
+        even[2 * i] = in[2 * (2 * i)];
+        even[2 * i + 1] = in[2 * (2 * i) + 1];
+        odd[2 * i] = in[2 * (2 * i + 1)];
+        odd[2 * i + 1] = in[2 * (2 * i + 1) + 1];
+    }
+    mel_cfft(even, ef, half, l + 1);
+    mel_cfft(odd, of, half, l + 1);
+    for (int k = 0; k < half; k++) {
+        const float re = mel_t.lcos[l][k], im = mel_t.lnsin[l][k];
+        const float re_odd = of[2 * k], im_odd = of[2 * k + 1];
+        const float e_re = ef[2 * k], e_im = ef[2 * k + 1];
+        out[2 * k] = e_re + re * re_odd - im * im_odd;
+        out[2 * k + 1] = e_im + re * im_odd + im * re_odd;
+        out[2 * (k + half)] = e_re - re * re_odd + im * im_odd;
+        out[2 * (k + half) + 1] = e_im - re * im_odd - im * re_odd;
+    }
+}
+
+/* fft_twoforone, mel.rs:648-695 (the default FFT path) */
+void ref_mel_fft400(const float *in, float *out) {
+    mel_tables_init();
+    const int half = MEL_NFFT / 2;
+    float z[400], zf[400];
+    for (int m = 0; m < half; m++) {
+        z[2 * m] = in[2 * m];
+        z[2 * m + 1] = in[2 * m + 1];
+    }
+    mel_cfft(z, zf, half, 1);
+    for (int k = 0; k < half; k++) {
+        const int km = (half - k) % half;
+        const float ar = zf[2 * k], ai = zf[2 * k + 1], br = zf[2 * km], bi = zf[2 * km + 1];
+        const float e_re = 0.5f * (ar + br), e_im = 0.5f * (ai - bi);
+        const float o_re = 0.5f * (ai + bi), o_im = 0.5f * (br - ar);
+        const float re = mel_t.lcos[0][k], im = mel_t.lnsin[0][k];
+        out[2 * k] = e_re + re * o_re - im * o_im;
+        out[2 * k + 1] = e_im + re * o_im + im * o_re;
+        out[2 * (k + half)] = e_re - re * o_re + im * o_im;
+        out[2 * (k + half) + 1] = e_im - re * o_im - im * o_re;
+    }
+}
+
+/* log10_floor_approx, mel.rs:1239-1249 */
+float ref_log10_floor_approx(double x) {
+    x = x > 1e-10 ? x : 1e-10;
+    uint64_t bits;
+    memcpy(&bits, &x, 8);
+    const int64_t ex = (int64_t)((bits >> 52) & 0x7ff) - 1023;
+    const uint64_t mb = (bits & 0x000fffffffffffffull) | 0x3ff0000000000000ull;
+    double m;
+    memcpy(&m, &mb, 8);
+    const double t = (m - 1.0) / (m + 1.0);
+    const double t2 = t * t;
+    const double series = 1.0 + t2 * (1.0 / 3.0 + t2 * (1.0 / 5.0 + t2 * (1.0 / 7.0 + t2 * (1.0 / 9.0))));
+    const double ln_m = 2.0 * t * series;
+    return (float)(((double)ex * M_LN2 + ln_m) * (1.0 / M_LN10));
+}
+
+void ref_mel_hann(float *out400) {
+    mel_tables_init();
+    memcpy(out400, mel_t.hann, sizeof mel_t.hann);
+}
+
+int64_t ref_mel_frames(int64_t n_samples) {
+    return (n_samples + MEL_PAD1 + 2 * MEL_PAD2 - MEL_NFFT) / MEL_HOP;
+}
+
+/* log_mel, mel.rs:1476-1660 (build_padded 1096-1125, compute_frame_column
+ * 1167-1204, power_and_project 1206-1237, global clamp/normalize 1610-1650) */
+void ref_log_mel(const float *samples, int64_t n, const float *filters, int n_mel, float *out) {
+    mel_tables_init();
+    const int64_t plen = n + MEL_PAD1 + 2 * MEL_PAD2;
+    float *padded = (float *)calloc((size_t)plen, sizeof(float));
+    memcpy(padded + MEL_PAD2, samples, sizeof(float) * (size_t)n);
+    const int64_t refl = MEL_PAD2 < (n > 0 ? n - 1 : 0) ? MEL_PAD2 : (n > 0 ? n - 1 : 0);
+    for (int64_t j = 1; j <= refl; j++) padded[MEL_PAD2 - j] = samples[j];
+    const int64_t valid = n + MEL_PAD2;
+    const int64_t nf = (plen - MEL_NFFT) / MEL_HOP;
+    int *st = (int *)malloc(sizeof(int) * n_mel), *en = (int *)malloc(sizeof(int) * n_mel);
+    for (int m = 0; m < n_mel; m++) { /* SparseMelFilters::new */
+        const float *row = filters + (int64_t)m * MEL_NBINS;
+        int a = -1, b = -1;
+        for (int k = 0; k < MEL_NBINS; k++)
+            if (row[k] != 0.0f) {
+                if (a < 0) a = k;
+                b = k;
+            }
+        st[m] = a < 0 ? 0 : a;
+        en[m] = b < 0 ? 0 : b + 1;
+    }
+    const float floor10 = (float)log10(1e-10);
+#pragma omp parallel for schedule(static)
+    for (int64_t f = 0; f < nf; f++) {
+        const int64_t off = f * MEL_HOP;
+        if (off >= valid) {
+            for (int m = 0; m < n_mel; m++) out[(int64_t)m * nf + f] = floor10;
+            continue;
+        }
+        float in[MEL_NFFT], spec[2 * MEL_NFFT], pw[MEL_NBINS];
+        const int64_t avail = valid - off < MEL_NFFT ? valid - off : MEL_NFFT;
+        for (int j = 0; j < MEL_NFFT; j++) in[j] = j < avail ? mel_t.hann[j] * padded[off + j] : 0.0f;
+        ref_mel_fft400(in, spec);
+        for (int j = 0; j < MEL_NBINS; j++) {
+            const float re = spec[2 * j], im = spec[2 * j + 1];
+            pw[j] = re * re + im * im;
+        }
+        for (int m = 0; m < n_mel; m++) {
+            const float *row = filters + (int64_t)m * MEL_NBINS;
+            double sum = 0.0;
+            for (int k = st[m]; k < en[m]; k++) sum += (double)pw[k] * (double)row[k];
+            out[(int64_t)m * nf + f] = ref_log10_floor_approx(sum);
+        }
+    }
+    const int64_t tot = (int64_t)n_mel * nf;
+    float mx = -INFINITY;
+    for (int64_t i = 0; i < tot; i++)
+        if (out[i] > mx) mx = out[i];
+    const float fl = mx - 8.0f;
+    for (int64_t i = 0; i < tot; i++) {
+        float v = out[i] < fl ? fl : out[i];
+        out[i] = (v + 4.0f) / 4.0f;
+    }
+    free(st);
+    free(en);
+    free(padded);
+}

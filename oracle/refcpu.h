@@ -101,6 +101,18 @@ int ref_process_argmax(const fwhip_filter *f, const float *logits, int n_vocab, 
 int ref_decode_greedy(const ref_decoder *d, ref_dstate *s, const int32_t *prompt, int n_prompt,
                       int n_max, const fwhip_filter *f, int32_t *out_tokens, int32_t *out_len);
 
+/* ---- log-mel frontend (mel.rs:81-1660) ---- */
+int64_t ref_mel_frames(int64_t n_samples); /* n_frames_for, mel.rs:1127 */
+/* log_mel (mel.rs:1476): mel-major out [n_mel, ref_mel_frames(n)], clamped to
+ * max - 8 and normalized (x + 4) / 4.  filters: [n_mel, 201] f32. */
+void ref_log_mel(const float *samples, int64_t n_samples, const float *filters, int n_mel, float *out);
+/* pieces, for pinning: the default two-for-one real FFT of one 400-sample
+ * frame (out: 400 interleaved complex bins), the log10 approximation, and the
+ * Hann window */
+void ref_mel_fft400(const float *in, float *out);
+float ref_log10_floor_approx(double x);
+void ref_mel_hann(float *out400);
+
 int ref_num_threads(void);
 void ref_set_num_threads(int n);
 
