@@ -75,29 +75,42 @@ __device__ __forceinline__ float mel_log10_approx(double x) {
                    (1.0 / 2.302585092994045684017991454684364208));
 }
 
-// Nonzero [start, end) bin range of each filter (SparseMelFilters::new).
-__global__ void k_mel_ranges(const float *filters, int n_mel, int2 *ranges) {
-    const int m = blockIdx.x * blockDim.x + threadIdx.x;
+// Nonzero [start, end) bin range of each filter (SparseMelFilters::new), one
+// wave per filter: first and last nonzero bin by a wave min / max.
+__global__ void __launch_bounds__(256) k_mel_ranges(const float *filters, int n_mel, int2 *ranges) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (m >= n_mel) return;
     const float *row = filters + (size_t)m * MEL_NBINS;
-    int a = -1, b = -1;
-    for (int k = 0; k < MEL_NBINS; k++)
+    int a = MEL_NBINS, b = -1;
+    for (int k = lane; k < MEL_NBINS; k += 64)
         if (row[k] != 0.0f) {
-            if (a < 0) a = k;
+            a = a < k ? a : k;
             b = k;
         }
-    ranges[m] = make_int2(a < 0 ? 0 : a, b < 0 ? 0 : b + 1);
+    for (int o = 32; o > 0; o >>= 1) {
+        const int a2 = __shfl_xor(a, o, 64), b2 = __shfl_xor(b, o, 64);
+        a = a < a2 ? a : a2;
+        b = b > b2 ? b : b2;
+    }
+    if (lane == 0) ranges[m] = make_int2(b < 0 ? 0 : a, b < 0 ? 0 : b + 1);
 }
 
 // The frames kernel.  Buffers per wave (LDS, floats): A = the windowed frame
 // (= the packed complex input z, interleaved), B and C = work arrays.
 __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *samples, long long n, long long nf,
                                                              const float *filters, const int2 *ranges, int n_mel,
-                                                             const MelTables *__restrict__ tb, float floor10, float *out,
-                                                             float *pmax) {
+                                                             const MelTables *__restrict__ gtb, float floor10,
+                                                             float *out, float *pmax) {
+    // A (the frame) is dead after the leaf DFTs; it then holds the column of
+    // mel values for the coalesced mel-major store.
+    static_assert(MEL_MAXMEL <= 400, "mel column must fit the frame buffer");
     __shared__ float sh[MEL_FPB][3][400];
-    __shared__ float col[MEL_FPB][MEL_MAXMEL];
     __shared__ float wmax[MEL_FPB];
+    __shared__ MelTables stb;
+    const MelTables *tb = &stb;
+    for (int i = threadIdx.x; i < (int)(sizeof(MelTables) / 4); i += blockDim.x)
+        ((float *)&stb)[i] = ((const float *)gtb)[i];
+    __syncthreads();
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const long long f = (long long)blockIdx.x * MEL_FPB + w;
     float *A = sh[w][0], *B = sh[w][1], *Cb = sh[w][2];
@@ -217,7 +230,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
                 for (int k = rg.x; k < rg.y; k++) sum += (double)dst[k] * (double)row[k];
                 v = mel_log10_approx(sum);
             }
-            col[w][m] = v;
+            A[m] = v;
             mx = fmaxf(mx, v);
         }
     }
@@ -234,7 +247,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
     const long long f0 = (long long)blockIdx.x * MEL_FPB;
     for (int i = threadIdx.x; i < n_mel * MEL_FPB; i += blockDim.x) {
         const int m = i / MEL_FPB, fr = i % MEL_FPB;
-        if (f0 + fr < nf) out[(size_t)m * nf + f0 + fr] = col[fr][m];
+        if (f0 + fr < nf) out[(size_t)m * nf + f0 + fr] = sh[fr][0][m];
     }
 }
 
@@ -310,7 +323,7 @@ extern "C" fwhip_status fwhip_log_mel(fwhip_ctx *c, const float *samples, int64_
     float *flr = pmax + nb;
     const float floor10 = (float)log10(1e-10);
     hipStream_t st = c->stream;
-    hipLaunchKernelGGL(k_mel_ranges, dim3((n_mel + 63) / 64), dim3(64), 0, st, filters, (int)n_mel, ranges);
+    hipLaunchKernelGGL(k_mel_ranges, dim3((n_mel + 3) / 4), dim3(256), 0, st, filters, (int)n_mel, ranges);
     hipLaunchKernelGGL(k_mel_frames, dim3((unsigned)nb), dim3(64 * MEL_FPB), 0, st, samples, (long long)n, nf,
                        filters, (const int2 *)ranges, (int)n_mel, (const MelTables *)c->mel_tab, floor10, out, pmax);
     hipLaunchKernelGGL(k_mel_floor, dim3(1), dim3(1024), 0, st, (const float *)pmax, (int)nb, flr);
