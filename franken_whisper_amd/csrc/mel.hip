@@ -61,6 +61,16 @@ static void mel_tables_build(MelTables &t) {
         }
 }
 
+// Orders this wave's LDS writes before its later LDS reads of other lanes'
+// values.  The FFT stages of a frame touch only that wave's buffers, and a
+// wave's LDS operations execute in issue order, so the fences (which keep the
+// compiler from moving LDS accesses across) stand in for a block barrier.
+__device__ __forceinline__ void mel_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // log10_floor_approx (mel.rs:1239-1249), in f64 then narrowed.
 __device__ __forceinline__ float mel_log10_approx(double x) {
     x = x > 1e-10 ? x : 1e-10;
@@ -135,7 +145,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
             A[j] = v;
         }
     }
-    __syncthreads();
+    mel_wave_sync();
     if (fft) {
         // leaves: 8 radix-5 DFTs of 25 points, leaf r over z[r + 8 j]
         // step 1 (and its twiddle): item = (r, n2, k1)
@@ -154,7 +164,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
             B[2 * it + 1] = im * c - re * s; // ti
         }
     }
-    __syncthreads();
+    mel_wave_sync();
     if (fft) {
         // step 2: leaf r's output k1 + 5 k2 into C at [r][k] (25 complex per leaf)
         for (int it = lane; it < 200; it += 64) {
@@ -177,7 +187,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
     // source buffer; a combined node of width 2h is stored at its own index.
     float *src = Cb, *dst = B;
     for (int lvl = 3, h = 25, nodes = 4; lvl >= 1; lvl--, h <<= 1, nodes >>= 1) {
-        __syncthreads();
+        mel_wave_sync();
         if (fft) {
             for (int it = lane; it < nodes * h; it += 64) {
                 const int node = it / h, k = it % h;
@@ -197,7 +207,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
         src = dst;
         dst = tmp;
     }
-    __syncthreads();
+    mel_wave_sync();
     // src now holds Z (200 complex).  Unpack the two-for-one and take the power
     // of bins 0..200 into dst.
     if (fft) {
@@ -217,7 +227,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
             }
         }
     }
-    __syncthreads();
+    mel_wave_sync();
     // mel projection, one thread per filter
     float mx = -INFINITY;
     if (live) {
