@@ -111,10 +111,11 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
                                                              const float *filters, const int2 *ranges, int n_mel,
                                                              const MelTables *__restrict__ gtb, float floor10,
                                                              float *out, float *pmax) {
-    // A (the frame) is dead after the leaf DFTs; it then holds the column of
-    // mel values for the coalesced mel-major store.
-    static_assert(MEL_MAXMEL <= 400, "mel column must fit the frame buffer");
-    __shared__ float sh[MEL_FPB][3][400];
+    // Two buffers per wave, used in turn: frame A -> leaf pass 1 B -> leaf
+    // pass 2 A -> widths 50 B, 100 A, 200 B -> power A; the mel column then
+    // goes to B for the coalesced mel-major store.
+    static_assert(MEL_MAXMEL <= 400, "mel column must fit a frame buffer");
+    __shared__ float sh[MEL_FPB][2][400];
     __shared__ float wmax[MEL_FPB];
     __shared__ MelTables stb;
     const MelTables *tb = &stb;
@@ -123,7 +124,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
     __syncthreads();
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const long long f = (long long)blockIdx.x * MEL_FPB + w;
-    float *A = sh[w][0], *B = sh[w][1], *Cb = sh[w][2];
+    float *A = sh[w][0], *B = sh[w][1];
     const long long valid = n + MEL_PAD2;
     const bool live = f < nf;
     const long long off = f * MEL_HOP;
@@ -166,7 +167,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
     }
     mel_wave_sync();
     if (fft) {
-        // step 2: leaf r's output k1 + 5 k2 into C at [r][k] (25 complex per leaf)
+        // step 2: leaf r's output k1 + 5 k2 into A at [r][k] (25 complex per leaf)
         for (int it = lane; it < 200; it += 64) {
             const int r = it / 25, k1 = (it % 25) / 5, k2 = it % 5;
             float re = 0.0f, im = 0.0f;
@@ -177,15 +178,15 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
                 im += ti * c - tr * s;
             }
             const int k = k1 + 5 * k2;
-            Cb[2 * (r * 25 + k)] = re;
-            Cb[2 * (r * 25 + k) + 1] = im;
+            A[2 * (r * 25 + k)] = re;
+            A[2 * (r * 25 + k) + 1] = im;
         }
     }
     // combine levels: width 50 (level 3), 100 (level 2), 200 (level 1).  A node
     // at depth d is the path of its first d splits; its even child takes the
     // next split bit 0.  Leaf r = b1 + 2 b2 + 4 b3 sits at position r in the
     // source buffer; a combined node of width 2h is stored at its own index.
-    float *src = Cb, *dst = B;
+    float *src = A, *dst = B;
     for (int lvl = 3, h = 25, nodes = 4; lvl >= 1; lvl--, h <<= 1, nodes >>= 1) {
         mel_wave_sync();
         if (fft) {
@@ -240,7 +241,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
                 for (int k = rg.x; k < rg.y; k++) sum += (double)dst[k] * (double)row[k];
                 v = mel_log10_approx(sum);
             }
-            A[m] = v;
+            B[m] = v;
             mx = fmaxf(mx, v);
         }
     }
@@ -257,7 +258,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
     const long long f0 = (long long)blockIdx.x * MEL_FPB;
     for (int i = threadIdx.x; i < n_mel * MEL_FPB; i += blockDim.x) {
         const int m = i / MEL_FPB, fr = i % MEL_FPB;
-        if (f0 + fr < nf) out[(size_t)m * nf + f0 + fr] = sh[fr][0][m];
+        if (f0 + fr < nf) out[(size_t)m * nf + f0 + fr] = sh[fr][1][m];
     }
 }
 
