@@ -63,3 +63,37 @@ def test_log_mel_rejects_what_the_reference_rejects(ctx):
         ctx.log_mel(s_dev, 100, f_dev, 0, out)
     for a in (s_dev, f_dev, out):
         a.free()
+
+
+@pytest.mark.parametrize("cfg", [synth.MICRO, synth.Config("tiny-2L", 51864, 1500, 384, 6, 2, 448, 384, 6, 4, 80)],
+                         ids=lambda c: c.name)
+def test_audio_to_encoder_states_bitexact(ctx, cfg):
+    """The job's seam: audio -> fwhip_log_mel -> fwhip_encoder_forward on windows
+    sliced from the device mel (the last one past the end, padded with -1.5) ->
+    bit-identical to the oracle's log_mel, window slice and exact-mode encoder."""
+    import ctypes
+
+    from franken_whisper_amd import abi
+
+    print(f"audio->encoder {cfg.name}", flush=True)
+    m = synth.Model(cfg, seed=5, decoder=False)
+    nf = 2 * cfg.n_audio_ctx
+    samples = synth.audio(31, 2.0, gaps=True)
+    filters = synth.mel_filterbank(cfg.n_mels)
+    total = native.mel_frames(samples.size)
+    offs = [0, nf, total - nf // 2]
+    mel_dev = ctx.empty((cfg.n_mels, total), np.float32)
+    ctx.log_mel(ctx.array(samples), samples.size, ctx.array(filters), cfg.n_mels, mel_dev)
+    enc = native.Encoder(ctx, m, abi.ENC_INT8)
+    enc.set_exact(True)
+    out = ctx.empty((len(offs), cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+    enc.forward_mel(mel_dev, total, offs, nf, out)
+    got = out.download()
+    mel = O.log_mel(samples, filters)
+    oenc = O.Encoder(m, abi.ENC_INT8)
+    for b, off in enumerate(offs):
+        win = np.empty((nf, cfg.n_mels), np.float32)
+        O.lib().ref_mel_window(abi.ptr(mel, ctypes.c_float), cfg.n_mels, total, off, nf,
+                               abi.ptr(win, ctypes.c_float))
+        assert_bitexact(got[b], oenc.forward(win), f"{cfg.name} window at frame {off}")
+    enc.close()
