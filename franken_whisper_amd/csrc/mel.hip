@@ -111,9 +111,9 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
                                                              const float *filters, const int2 *ranges, int n_mel,
                                                              const MelTables *__restrict__ gtb, float floor10,
                                                              float *out, float *pmax) {
-    // Two buffers per wave, used in turn: frame A -> leaf pass 1 B -> leaf
-    // pass 2 A -> widths 50 B, 100 A, 200 B -> power A; the mel column then
-    // goes to B for the coalesced mel-major store.
+    // Two buffers per wave, used in turn: frame A -> leaves B -> widths 50 A,
+    // 100 B, 200 A -> power B; the mel column then goes to A for the coalesced
+    // mel-major store.
     static_assert(MEL_MAXMEL <= 400, "mel column must fit a frame buffer");
     __shared__ float sh[MEL_FPB][2][400];
     __shared__ float wmax[MEL_FPB];
@@ -147,12 +147,17 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
         }
     }
     mel_wave_sync();
-    if (fft) {
-        // leaves: 8 radix-5 DFTs of 25 points, leaf r over z[r + 8 j]
-        // step 1 (and its twiddle): item = (r, n2, k1)
-        for (int it = lane; it < 200; it += 64) {
-            const int r = it / 25, n2 = (it % 25) / 5, k1 = it % 5;
+    if (fft && lane < 40) {
+        // leaves: 8 radix-5 DFTs of 25 points, leaf r over z[r + 8 j].  Lane
+        // (r, k1) forms both 5-point passes of its column in registers: pass 1
+        // and its twiddle for every n2, then pass 2 for every k2 (the outputs
+        // k1 + 5 k2 of leaf r, into B at [r][k]).
+        const int r = lane / 5, k1 = lane % 5;
+        float tr[5], ti[5];
+#pragma unroll
+        for (int n2 = 0; n2 < 5; n2++) {
             float re = 0.0f, im = 0.0f;
+#pragma unroll
             for (int n1 = 0; n1 < 5; n1++) {
                 const int zi = r + 8 * (5 * n1 + n2);
                 const float xr = A[2 * zi], xi = A[2 * zi + 1];
@@ -161,32 +166,28 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
                 im += xi * c - xr * s;
             }
             const float c = tb->c25[n2 * 5 + k1], s = tb->s25[n2 * 5 + k1];
-            B[2 * it] = re * c + im * s;     // tr
-            B[2 * it + 1] = im * c - re * s; // ti
+            tr[n2] = re * c + im * s;
+            ti[n2] = im * c - re * s;
         }
-    }
-    mel_wave_sync();
-    if (fft) {
-        // step 2: leaf r's output k1 + 5 k2 into A at [r][k] (25 complex per leaf)
-        for (int it = lane; it < 200; it += 64) {
-            const int r = it / 25, k1 = (it % 25) / 5, k2 = it % 5;
+#pragma unroll
+        for (int k2 = 0; k2 < 5; k2++) {
             float re = 0.0f, im = 0.0f;
+#pragma unroll
             for (int n2 = 0; n2 < 5; n2++) {
-                const float tr = B[2 * (r * 25 + n2 * 5 + k1)], ti = B[2 * (r * 25 + n2 * 5 + k1) + 1];
                 const float c = tb->c5[k2 * 5 + n2], s = tb->s5[k2 * 5 + n2];
-                re += tr * c + ti * s;
-                im += ti * c - tr * s;
+                re += tr[n2] * c + ti[n2] * s;
+                im += ti[n2] * c - tr[n2] * s;
             }
             const int k = k1 + 5 * k2;
-            A[2 * (r * 25 + k)] = re;
-            A[2 * (r * 25 + k) + 1] = im;
+            B[2 * (r * 25 + k)] = re;
+            B[2 * (r * 25 + k) + 1] = im;
         }
     }
     // combine levels: width 50 (level 3), 100 (level 2), 200 (level 1).  A node
     // at depth d is the path of its first d splits; its even child takes the
     // next split bit 0.  Leaf r = b1 + 2 b2 + 4 b3 sits at position r in the
     // source buffer; a combined node of width 2h is stored at its own index.
-    float *src = A, *dst = B;
+    float *src = B, *dst = A;
     for (int lvl = 3, h = 25, nodes = 4; lvl >= 1; lvl--, h <<= 1, nodes >>= 1) {
         mel_wave_sync();
         if (fft) {
@@ -241,7 +242,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
                 for (int k = rg.x; k < rg.y; k++) sum += (double)dst[k] * (double)row[k];
                 v = mel_log10_approx(sum);
             }
-            B[m] = v;
+            A[m] = v;
             mx = fmaxf(mx, v);
         }
     }
@@ -258,7 +259,7 @@ __global__ void __launch_bounds__(64 * MEL_FPB) k_mel_frames(const float *sample
     const long long f0 = (long long)blockIdx.x * MEL_FPB;
     for (int i = threadIdx.x; i < n_mel * MEL_FPB; i += blockDim.x) {
         const int m = i / MEL_FPB, fr = i % MEL_FPB;
-        if (f0 + fr < nf) out[(size_t)m * nf + f0 + fr] = sh[fr][1][m];
+        if (f0 + fr < nf) out[(size_t)m * nf + f0 + fr] = sh[fr][0][m];
     }
 }
 
