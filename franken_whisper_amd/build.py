@@ -44,12 +44,26 @@ def build_synth():
     return out
 
 
-def build_hip():
+def build_hip(jobs: int | None = None):
+    """Each translation unit compiles to its own object in parallel (objects
+    under _build/, outside the package), then one link step."""
+    from concurrent.futures import ThreadPoolExecutor
+
     os.makedirs(LIBDIR, exist_ok=True)
+    objdir = os.path.join(ROOT, "_build", "hip")
+    os.makedirs(objdir, exist_ok=True)
     out = os.path.join(LIBDIR, "libfwhip.so")
     tmp = out + ".tmp"
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
-    _run([HIPCC] + HIP_FLAGS + srcs + ["-o", tmp])
+    cflags = [f for f in HIP_FLAGS if f != "-shared"]
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
+
+    def compile_one(i):
+        _run([HIPCC] + cflags + ["-c", os.path.join(CSRC, HIP_SOURCES[i]), "-o", objs[i]])
+
+    n = jobs or min(len(HIP_SOURCES), os.cpu_count() or 1, 16)
+    with ThreadPoolExecutor(max_workers=n) as ex:
+        list(ex.map(compile_one, range(len(HIP_SOURCES))))
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + objs + ["-o", tmp])
     os.replace(tmp, out)
     return out
 

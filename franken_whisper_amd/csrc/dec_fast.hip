@@ -159,10 +159,11 @@ __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *
 // ---------------------------------------------------------------------------
 // Order-preserving argmax key: larger value first, then smaller index; 0 means
 // "no candidate" (masked, -inf or NaN never compare greater, as in the
-// reference's strict '>' scan).
+// reference's strict '>' scan).  -0.0 and +0.0 compare equal under '>', so the
+// first of them wins (argmax_idx, decode.rs:1708-1770): both map to one key.
 __device__ __forceinline__ unsigned long long am_key(float v, int idx) {
     if (!(v > -INFINITY)) return 0ull;
-    uint32_t u = __float_as_uint(v);
+    uint32_t u = v == 0.0f ? 0u : __float_as_uint(v);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
 }

@@ -606,3 +606,54 @@ extern "C" fwhip_status fwhip_encoder_gemm_i8(fwhip_encoder *e, int32_t layer, i
     if (err != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, hipGetErrorString(err));
     return FWHIP_OK;
 }
+
+// Per-GEMM parity of the two fused int8 epilogues the forward runs (see
+// include/fwhip.h): the QKV GEMM's head-major f16 hi/lo split with V
+// transposed, and fc1 as f16 GELU-table indices with exact side values.
+extern "C" fwhip_status fwhip_encoder_gemm_i8_fused(fwhip_encoder *e, int32_t layer, int32_t which,
+                                                    const float *x_dev, int32_t n_windows, int32_t n_tokens,
+                                                    uint16_t *out16_dev, float *side_dev) {
+    if (!e || !x_dev || !out16_dev) return fw_fail(FWHIP_ERR_INVALID, "fwhip_encoder_gemm_i8_fused: NULL argument");
+    if (e->precision != FWHIP_ENC_INT8) return fw_fail(FWHIP_ERR_INVALID, "encoder is not on the int8 plan");
+    if (layer < 0 || layer >= e->L || (which != 0 && which != 4) || n_windows <= 0 || n_tokens <= 0 ||
+        (int64_t)n_windows * n_tokens > (1 << 30) / e->dff)
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_encoder_gemm_i8_fused: bad layer/which/size");
+    if (which == 4 && (!side_dev || !enc_h16_ok(e->dff)))
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_encoder_gemm_i8_fused: fc1 index form needs side_dev and a "
+                                          "supported MLP width");
+    fwhip_ctx *c = e->ctx;
+    HIP_TRY(hipSetDevice(c->device));
+    const int d = e->d, H = e->H, dff = e->dff, T = n_tokens, Tp = (T + 63) / 64 * 64, m = n_windows * n_tokens;
+    const EncLayerDev &l = e->layers[layer];
+    std::vector<void *> tmp;
+    int8_t *xq = (int8_t *)fw_dalloc(tmp, (size_t)m * d);
+    float *xs = (float *)fw_dalloc(tmp, sizeof(float) * m);
+    if (!xq || !xs) {
+        fw_free_all(tmp);
+        return fw_fail(FWHIP_ERR_GENERIC, "allocation failed");
+    }
+    hipStream_t st = c->stream;
+    fw_launch_gelu_quant_i7_rows(st, x_dev, m, d, nullptr, xq, xs); // quantize_act_i7
+    bool ok;
+    if (which == 0) {
+        const size_t qk = (size_t)n_windows * H * T * 64, vt = (size_t)n_windows * H * 64 * Tp;
+        FwGemm g = gemm_args(xq, nullptr, l.qkv7, m, 3 * d, d, xs, l.qkv7s, l.qkv_b, FW_EPI_QKV, nullptr, d);
+        for (int i = 0; i < 4; i++) g.o16[i] = out16_dev + i * qk;
+        g.o16[4] = out16_dev + 4 * qk;
+        g.o16[5] = out16_dev + 4 * qk + vt;
+        g.T = T;
+        g.H = H;
+        g.Tp = Tp;
+        fw_launch_fill_u16(st, g.o16[4], 2 * vt, 0);
+        ok = fw_launch_gemm(st, FW_KIND_I8, g);
+    } else {
+        FwGemm g = gemm_args(xq, nullptr, l.fc1_7, m, dff, d, xs, l.fc1_7s, l.fc1_b, FW_EPI_F16IDX, side_dev, dff);
+        g.o16[0] = out16_dev;
+        ok = fw_launch_gemm(st, FW_KIND_I8, g);
+    }
+    hipError_t err = hipStreamSynchronize(st);
+    fw_free_all(tmp);
+    if (!ok) return fw_fail(FWHIP_ERR_UNSUPPORTED, "fwhip_encoder_gemm_i8_fused: no kernel for this shape");
+    if (err != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, hipGetErrorString(err));
+    return FWHIP_OK;
+}

@@ -39,6 +39,9 @@ struct fwhip_ctx {
     void *mel_tab = nullptr;
     void *mel_scratch = nullptr;
     size_t mel_scratch_bytes = 0;
+    // fwhip_argmax_logits: per-block keys, tokens and the first-step flag
+    void *am_scratch = nullptr;
+    size_t am_scratch_bytes = 0;
 };
 
 fwhip_status fw_fail(fwhip_status code, const std::string &msg);

@@ -90,6 +90,7 @@ extern "C" void fwhip_destroy(fwhip_ctx *c) {
     if (c->gelu_tab) hipFree(c->gelu_tab);
     if (c->mel_tab) hipFree(c->mel_tab);
     if (c->mel_scratch) hipFree(c->mel_scratch);
+    if (c->am_scratch) hipFree(c->am_scratch);
     hipStreamDestroy(c->stream);
     delete c;
 }
@@ -851,5 +852,39 @@ extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *pro
         for (int k = 0; k < n_max; k++) out_tokens[(size_t)s * n_max + k] = k < n ? hist[(size_t)s * n_max + k] : 0;
     }
     st->len += n_prompt + steps - 1;
+    return FWHIP_OK;
+}
+
+// process_logits (no-timestamps mode) + argmax (decode.rs:702-867, 1708-1790)
+// over rows of logits already on the device: per-block keys, then the
+// first-index maximum of each row.
+extern "C" fwhip_status fwhip_argmax_logits(fwhip_ctx *c, const float *logits_dev, int32_t n_rows, int32_t n_vocab,
+                                            const fwhip_filter *filter, int32_t initial, int32_t *argmax_host) {
+    if (!c || !logits_dev || !argmax_host) return fw_fail(FWHIP_ERR_INVALID, "fwhip_argmax_logits: NULL argument");
+    if (n_rows <= 0 || n_rows > 65535 || n_vocab <= 0)
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_argmax_logits: n_rows must be in 1..65535 and n_vocab > 0");
+    HIP_TRY(hipSetDevice(c->device));
+    const int nblk = fw_logits_keys_blocks(n_vocab);
+    const size_t kb = sizeof(unsigned long long) * (size_t)n_rows * nblk;
+    const size_t need = kb + sizeof(int32_t) * (size_t)n_rows + 256;
+    if (need > c->am_scratch_bytes) {
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        if (c->am_scratch) HIP_TRY(hipFree(c->am_scratch));
+        c->am_scratch = nullptr;
+        c->am_scratch_bytes = 0;
+        HIP_TRY(hipMalloc(&c->am_scratch, need));
+        c->am_scratch_bytes = need;
+    }
+    unsigned long long *keys = (unsigned long long *)c->am_scratch;
+    int32_t *tok = (int32_t *)((char *)c->am_scratch + kb);
+    int *initp = (int *)(tok + n_rows);
+    int init = initial ? 1 : 0;
+    fwhip_status r = set_dev_ints(c, initp, &init, 1);
+    if (r != FWHIP_OK) return r;
+    fw_launch_logits_keys(c->stream, logits_dev, n_vocab, n_rows, filter, initp, keys);
+    fw_launch_argmax_finish(c->stream, keys, nblk, n_rows, tok, nullptr, 0, nullptr, nullptr, nullptr, 0);
+    HIP_TRY(hipMemcpyAsync(argmax_host, tok, sizeof(int32_t) * n_rows, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipGetLastError());
     return FWHIP_OK;
 }

@@ -43,6 +43,7 @@ SIGNATURES = {
                                                      C.POINTER(abi.ExecRecord)]),
     "fwhip_encoder_set_exact": (C.c_int32, [_vp, C.c_int32]),
     "fwhip_encoder_gemm_i8": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, _vp, _vp]),
+    "fwhip_encoder_gemm_i8_fused": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, C.c_int32, _vp, _vp]),
     "fwhip_decoder_load": (C.c_int32, [_vp, C.POINTER(abi.DecoderWeights), C.c_int32, C.POINTER(_vp)]),
     "fwhip_decoder_free": (None, [_vp]),
     "fwhip_dstate_new": (C.c_int32, [_vp, C.c_int32, C.c_int32, C.POINTER(_vp)]),
@@ -55,6 +56,7 @@ SIGNATURES = {
     "fwhip_dstate_read": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_size_t]),
     "fwhip_decode_greedy": (C.c_int32, [_vp, _i32p, C.c_int32, C.c_int32, C.POINTER(abi.Filter), _i32p,
                                         _i32p]),
+    "fwhip_argmax_logits": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.POINTER(abi.Filter), C.c_int32, _i32p]),
     "fwhip_mel_frames": (C.c_int64, [C.c_int64]),
     "fwhip_log_mel": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
 }
@@ -154,6 +156,16 @@ class Context:
         check(lib().fwhip_log_mel(self.h, samples_dev.ptr if n_samples else None, n_samples,
                                   filters_dev.ptr, n_mel, n_fft_bins, out_dev.ptr))
 
+    def argmax_logits(self, logits_dev: DeviceArray, filt=None, initial=False):
+        """process_logits + argmax (decode.rs:702-867, 1708-1790) of each row of
+        logits_dev [n_rows, n_vocab]."""
+        n_rows, n_vocab = logits_dev.shape
+        out = np.zeros(n_rows, np.int32)
+        check(lib().fwhip_argmax_logits(self.h, logits_dev.ptr, n_rows, n_vocab,
+                                        C.byref(filt) if filt is not None else None, 1 if initial else 0,
+                                        out.ctypes.data_as(_i32p)))
+        return out
+
     def close(self):
         if self.h:
             lib().fwhip_destroy(self.h)
@@ -190,6 +202,11 @@ class Encoder:
     def gemm_i8(self, layer: int, which: int, x_dev: DeviceArray, acc_dev: DeviceArray, y_dev: DeviceArray):
         check(lib().fwhip_encoder_gemm_i8(self.h, layer, which, x_dev.ptr, x_dev.shape[0], acc_dev.ptr,
                                           y_dev.ptr))
+
+    def gemm_i8_fused(self, layer: int, which: int, x_dev: DeviceArray, n_windows: int, n_tokens: int,
+                      out16_dev: DeviceArray, side_dev: DeviceArray | None = None):
+        check(lib().fwhip_encoder_gemm_i8_fused(self.h, layer, which, x_dev.ptr, n_windows, n_tokens, out16_dev.ptr,
+                                                side_dev.ptr if side_dev is not None else None))
 
     def close(self):
         if self.h:

@@ -220,6 +220,22 @@ fwhip_status fwhip_encoder_forward_time_major(fwhip_encoder *enc, const float *x
 fwhip_status fwhip_encoder_gemm_i8(fwhip_encoder *enc, int32_t layer, int32_t which, const float *x_dev,
                                    int32_t m, int32_t *acc_dev, float *y_dev);
 
+/* Per-GEMM parity of the fused epilogues the int8 forward runs, on rows x_dev
+ * [n_windows * n_tokens, d] quantized with quantize_act_i7 (nn.rs:1443):
+ *   which 0: the fused q/k/v GEMM (matmul_bias_i7_quantized nn.rs:1537-1771,
+ *     fused head-major as attention_from_i7_qkv nn.rs:5836-5877) with each
+ *     epilogue value v split into f16 hi = f16(v), lo = f16(v - hi).  out16_dev
+ *     receives Q hi, Q lo, K hi, K lo, each [n_windows, H, n_tokens, 64], then
+ *     V^T hi, V^T lo, each [n_windows, H, 64, Tp] (Tp = n_tokens rounded up to
+ *     64, zero padded; key t of a 16-key group at position t with bits 2 and 3
+ *     swapped).
+ *   which 4: fc1 in GELU-index form: out16_dev [m, 4d] holds the f16 bits of v
+ *     (the reference GELU's table index, nn.rs:4603-4687) when |v| < 9.98, else
+ *     0xffff with v itself in side_dev [m, 4d].
+ * A test entry point: it allocates its quantized operand per call. */
+fwhip_status fwhip_encoder_gemm_i8_fused(fwhip_encoder *enc, int32_t layer, int32_t which, const float *x_dev,
+                                         int32_t n_windows, int32_t n_tokens, uint16_t *out16_dev, float *side_dev);
+
 /* ---- decoder ------------------------------------------------------------ */
 
 /* Replaces DecoderWeights::from_ggml (decoder.rs:752-932).  arm = FWHIP_DEC_*. */
@@ -279,6 +295,15 @@ fwhip_status fwhip_dstate_read(const fwhip_dstate *st, int32_t what, int32_t str
 fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *prompt, int32_t n_prompt,
                                  int32_t n_max_tokens, const fwhip_filter *filter,
                                  int32_t *out_tokens, int32_t *out_len);
+
+/* process_logits in no-timestamps mode + argmax (decode.rs:702-867,
+ * 1708-1790) for `n_rows` rows of logits on the device (`logits_dev`
+ * [n_rows, n_vocab] f32): the suppress set of `filter` (NULL: raw argmax; with
+ * `initial` the first-step eot/blank suppression too), then the first index of
+ * the maximum under the reference's strict '>' (NaN and -inf never win, -0.0
+ * and +0.0 tie, a row with no candidate gives 0).  argmax_host is [n_rows]. */
+fwhip_status fwhip_argmax_logits(fwhip_ctx *ctx, const float *logits_dev, int32_t n_rows, int32_t n_vocab,
+                                 const fwhip_filter *filter, int32_t initial, int32_t *argmax_host);
 
 /* ---- log-mel frontend ---------------------------------------------------- */
 

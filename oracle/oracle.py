@@ -64,6 +64,9 @@ def lib():
         "ref_softmax_rows": (None, [f32p, C.c_int64, C.c_int]),
         "ref_matmul_strict": (None, [f32p, f32p, f32p, C.c_int64, C.c_int, C.c_int]),
         "ref_argmax_first": (C.c_int, [f32p, C.c_int]),
+        "ref_attention": (None, [f32p, C.c_int, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                 f32p]),
+        "ref_attention_decode_f16": (None, [f32p, u16p, u16p, C.c_int, C.c_int, C.c_int, f32p]),
         "ref_encoder_new": (C.c_void_p, [C.POINTER(abi.EncoderWeights), C.c_int]),
         "ref_encoder_free": (None, [C.c_void_p]),
         "ref_encoder_forward": (C.c_int, [C.c_void_p, f32p, C.c_int, f32p, C.c_int]),
@@ -297,6 +300,28 @@ def log10_floor_approx(x):
 def mel_hann():
     out = np.empty(400, dtype=np.float32)
     lib().ref_mel_hann(_p(out, C.c_float))
+    return out
+
+
+def attention(q, k, v, n_head, causal=False, cache_len=0):
+    """attention_raw's per-head path (nn.rs:6035-6131) on [tq, d] x [tk, d]."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    tq, d = q.shape
+    tk = k.shape[0]
+    out = np.empty((tq, d), np.float32)
+    lib().ref_attention(_p(q, C.c_float), tq, _p(k, C.c_float), _p(v, C.c_float), tk, d, n_head,
+                        1 if causal else 0, cache_len, _p(out, C.c_float))
+    return out
+
+
+def attention_decode_f16(q, kc16, vc16, n_head):
+    """attention_decode_step_f16 (nn.rs:6466-6540): one row over an f16 cache."""
+    q = _c(q, np.float32).ravel()
+    kc16, vc16 = _c(kc16, np.uint16), _c(vc16, np.uint16)
+    tk, d = kc16.shape
+    out = np.empty(d, np.float32)
+    lib().ref_attention_decode_f16(_p(q, C.c_float), _p(kc16, C.c_uint16), _p(vc16, C.c_uint16), tk, d, n_head,
+                                   _p(out, C.c_float))
     return out
 
 

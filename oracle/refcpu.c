@@ -527,6 +527,13 @@ static void attention_per_head(const float *q, int tq, const float *k, const flo
     free(kht);
 }
 
+/* Exported for the attention invariants (nn.rs:8472-8600): the per-head
+ * attention of attention_raw (causal: query i sees keys j <= cache_len + i). */
+void ref_attention(const float *q, int tq, const float *k, const float *v, int tk, int n_state,
+                   int n_head, int causal, int cache_len, float *out) {
+    attention_per_head(q, tq, k, v, tk, n_state, n_head, causal, cache_len, out);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Encoder                                                                  */
 /* ------------------------------------------------------------------------ */
@@ -999,6 +1006,13 @@ static void self_attn_f16(const float *q, const uint16_t *kc, const uint16_t *vc
         }
     }
     free(sc);
+}
+
+/* Exported for the KV-cache invariant (nn.rs:8559): one decode-step row
+ * attending to an f16 cache of tk rows. */
+void ref_attention_decode_f16(const float *q, const uint16_t *kc, const uint16_t *vc, int tk, int d,
+                              int H, float *out) {
+    self_attn_f16(q, kc, vc, tk, d, H, out);
 }
 
 /* cross_attention, decoder.rs:1524-1716 (FW_CROSS_F16 on; int8 K/V when the

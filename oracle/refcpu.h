@@ -69,6 +69,12 @@ void ref_softmax_rows(float *x, int64_t rows, int cols);
 void ref_matmul_strict(const float *a, const float *b, float *c, int64_t m, int k, int n);
 int ref_argmax_first(const float *l, int n);
 
+/* ---- attention (exported for the reference's attention invariants) ---- */
+void ref_attention(const float *q, int tq, const float *k, const float *v, int tk, int n_state,
+                   int n_head, int causal, int cache_len, float *out);
+void ref_attention_decode_f16(const float *q, const uint16_t *kc, const uint16_t *vc, int tk, int d,
+                              int H, float *out);
+
 /* ---- encoder ---- */
 typedef struct ref_encoder ref_encoder;
 ref_encoder *ref_encoder_new(const fwhip_encoder_weights *w, int precision);

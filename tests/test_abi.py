@@ -36,3 +36,23 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version():
     assert native.lib().fwhip_abi_version() == 1
+
+
+def test_init_without_gpu_names_the_cpu_route():
+    """No gfx950 device: fwhip_init returns FWHIP_ERR_UNSUPPORTED with a
+    `cpu:<reason>` message, so the caller falls back to its CPU route and records
+    why (the pattern of encoder.rs:1700-1725)."""
+    import pytest
+
+    from franken_whisper_amd import abi
+
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU driver is present; this checks the no-device route")
+    h = C.c_void_p()
+    rc = native.lib().fwhip_init(0, C.byref(h))
+    assert rc == abi.ERR_UNSUPPORTED
+    assert not h.value
+    assert native.lib().fwhip_last_error().decode().startswith("cpu:")
+    with __import__("pytest").raises(native.FwhipError) as e:
+        native.Context(0)
+    assert e.value.code == abi.ERR_UNSUPPORTED
