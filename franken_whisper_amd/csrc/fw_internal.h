@@ -50,6 +50,9 @@ void fw_timed_end(fwhip_ctx *c, fw_event_pair *ev);
 void *fw_dalloc(std::vector<void *> &owned, size_t bytes);
 void *fw_dupload(std::vector<void *> &owned, const void *host, size_t bytes);
 void fw_free_all(std::vector<void *> &owned);
+// Resolve the allocation-free log-mel's device scratch and tables on `device`
+// (the current device), once per device; called by fwhip_init.
+void fw_mel_noalloc_setup(int device);
 
 // IEEE binary16 <-> binary32 on the host (round-to-nearest-even).
 static inline float fw_host_h2f(uint16_t h) {

@@ -48,6 +48,7 @@ extern "C" fwhip_status fwhip_init(int32_t device, fwhip_ctx **out) {
     if (std::string(prop.gcnArchName).find("gfx950") == std::string::npos)
         return fw_fail(FWHIP_ERR_UNSUPPORTED, std::string("cpu:unsupported-arch:") + prop.gcnArchName);
     HIP_TRY(hipSetDevice(device));
+    fw_mel_noalloc_setup(device);
     fwhip_ctx *c = new fwhip_ctx();
     c->device = device;
     c->n_cu = prop.multiProcessorCount;

@@ -15,6 +15,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "fw_internal.h"
 
 #define MEL_NFFT 400
@@ -300,16 +302,42 @@ extern "C" int64_t fwhip_mel_frames(int64_t n_samples) {
     return (n_samples + MEL_PAD1 + 2 * MEL_PAD2 - MEL_NFFT) / MEL_HOP;
 }
 
-extern "C" fwhip_status fwhip_log_mel(fwhip_ctx *c, const float *samples, int64_t n, const float *filters,
-                                      int32_t n_mel, int32_t n_fft_bins, float *out) {
-    if (!c) return fw_fail(FWHIP_ERR_INVALID, "fwhip_log_mel: NULL ctx");
+// The four launches of one log-mel: filter ranges, the frames (log10 power of
+// the projection, per-block maxima), the global floor, the normalization.
+// `ranges`, `pmax` and `flr` are the scratch (n_mel int2, nb floats, 1 float).
+static void mel_launch(hipStream_t st, const float *samples, long long n, long long nf, long long nb,
+                       const float *filters, int n_mel, const MelTables *tab, int2 *ranges, float *pmax, float *flr,
+                       float *out) {
+    const float floor10 = (float)log10(1e-10);
+    hipLaunchKernelGGL(k_mel_ranges, dim3((n_mel + 3) / 4), dim3(256), 0, st, filters, n_mel, ranges);
+    hipLaunchKernelGGL(k_mel_frames, dim3((unsigned)nb), dim3(64 * MEL_FPB), 0, st, samples, n, nf, filters,
+                       (const int2 *)ranges, n_mel, tab, floor10, out, pmax);
+    hipLaunchKernelGGL(k_mel_floor, dim3(1), dim3(1024), 0, st, (const float *)pmax, (int)nb, flr);
+    const long long total = (long long)n_mel * nf;
+    long long g = (total + 255) / 256;
+    g = g < 4096 ? g : 4096;
+    hipLaunchKernelGGL(k_mel_norm, dim3((unsigned)g), dim3(256), 0, st, out, total, (const float *)flr);
+}
+
+// The reference's argument checks (log_mel's InvalidRequest cases) and this
+// build's limits, shared by both entry points.
+static fwhip_status mel_check(const char *who, fwhip_ctx *c, const float *samples, int64_t n, const float *filters,
+                              int32_t n_mel, int32_t n_fft_bins, const float *out) {
+    if (!c) return fw_fail(FWHIP_ERR_INVALID, std::string(who) + ": NULL ctx");
     if (n_fft_bins != MEL_NBINS)
         return fw_fail(FWHIP_ERR_INVALID, "mel filterbank has " + std::to_string(n_fft_bins) +
                                               " bins, expected 201 (N_FFT/2+1)");
     if (n_mel <= 0) return fw_fail(FWHIP_ERR_INVALID, "mel filterbank has zero mel bins");
-    if (n_mel > MEL_MAXMEL) return fw_fail(FWHIP_ERR_INVALID, "fwhip_log_mel: more than 256 mel bins");
+    if (n_mel > MEL_MAXMEL) return fw_fail(FWHIP_ERR_INVALID, std::string(who) + ": more than 256 mel bins");
     if (n < 0 || (n > 0 && !samples) || !filters || !out)
-        return fw_fail(FWHIP_ERR_INVALID, "fwhip_log_mel: NULL buffer or negative length");
+        return fw_fail(FWHIP_ERR_INVALID, std::string(who) + ": NULL buffer or negative length");
+    return FWHIP_OK;
+}
+
+extern "C" fwhip_status fwhip_log_mel(fwhip_ctx *c, const float *samples, int64_t n, const float *filters,
+                                      int32_t n_mel, int32_t n_fft_bins, float *out) {
+    fwhip_status r = mel_check("fwhip_log_mel", c, samples, n, filters, n_mel, n_fft_bins, out);
+    if (r != FWHIP_OK) return r;
     MEL_TRY(hipSetDevice(c->device));
     if (!c->mel_tab) {
         MelTables tb;
@@ -332,17 +360,87 @@ extern "C" fwhip_status fwhip_log_mel(fwhip_ctx *c, const float *samples, int64_
     }
     int2 *ranges = (int2 *)c->mel_scratch;
     float *pmax = (float *)((char *)c->mel_scratch + (size_t)n_mel * 8);
-    float *flr = pmax + nb;
-    const float floor10 = (float)log10(1e-10);
-    hipStream_t st = c->stream;
-    hipLaunchKernelGGL(k_mel_ranges, dim3((n_mel + 3) / 4), dim3(256), 0, st, filters, (int)n_mel, ranges);
-    hipLaunchKernelGGL(k_mel_frames, dim3((unsigned)nb), dim3(64 * MEL_FPB), 0, st, samples, (long long)n, nf,
-                       filters, (const int2 *)ranges, (int)n_mel, (const MelTables *)c->mel_tab, floor10, out, pmax);
-    hipLaunchKernelGGL(k_mel_floor, dim3(1), dim3(1024), 0, st, (const float *)pmax, (int)nb, flr);
-    const long long total = (long long)n_mel * nf;
-    long long g = (total + 255) / 256;
-    g = g < 4096 ? g : 4096;
-    hipLaunchKernelGGL(k_mel_norm, dim3((unsigned)g), dim3(256), 0, st, out, total, (const float *)flr);
+    mel_launch(c->stream, samples, (long long)n, nf, nb, filters, (int)n_mel, (const MelTables *)c->mel_tab, ranges,
+               pmax, pmax + nb, out);
+    MEL_TRY(hipGetLastError());
+    return FWHIP_OK;
+}
+
+// ---- allocation-free variant -------------------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph capture,
+// tight serving loops, harnesses that forbid it): the scratch of the log-mel
+// (filter ranges, per-block maxima, the floor) lives in the file-scope device
+// array `scratch`, and the window/twiddle tables in `mel_tables_dev`.  Each GPU
+// holds its own copy of both until the process ends.  fw_mel_noalloc_setup,
+// called by fwhip_init with the device current, resolves their device addresses
+// once per device (host code never passes the arrays' names to a kernel: on
+// the host they are stand-ins, not device addresses) and uploads the tables.
+// Every call on a device shares that device's scratch, which keeps the last
+// call's contents; nothing in it needs to start at zero (each launch writes
+// every entry it later reads).  Calls that overlap on one GPU race.
+#define MEL_SCRATCH_BYTES (512 * 1024)
+#define MEL_MAX_DEVICES 64
+static __device__ __align__(256) unsigned char scratch[MEL_SCRATCH_BYTES];
+static __device__ __align__(256) MelTables mel_tables_dev;
+
+static std::mutex g_noalloc_mu;
+static void *g_scratch_ptr[MEL_MAX_DEVICES];
+static const MelTables *g_tables_ptr[MEL_MAX_DEVICES];
+static int g_noalloc_state[MEL_MAX_DEVICES]; // 0 not set up, 1 ready, -1 set-up failed
+
+// The largest input the scratch holds: frames whose per-block maxima fit next
+// to 256 filter ranges and the floor.
+static long long mel_noalloc_max_frames() {
+    return (long long)((MEL_SCRATCH_BYTES - 256 - MEL_MAXMEL * 8) / 4) * MEL_FPB;
+}
+
+void fw_mel_noalloc_setup(int device) {
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (device < 0 || device >= MEL_MAX_DEVICES || g_noalloc_state[device] == 1) return;
+    void *p = nullptr, *t = nullptr;
+    MelTables tb;
+    mel_tables_build(tb);
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p ||
+        hipGetSymbolAddress(&t, HIP_SYMBOL(mel_tables_dev)) != hipSuccess || !t ||
+        hipMemcpy(t, &tb, sizeof(MelTables), hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        g_noalloc_state[device] = -1;
+        return;
+    }
+    g_scratch_ptr[device] = p;
+    g_tables_ptr[device] = (const MelTables *)t;
+    g_noalloc_state[device] = 1;
+}
+
+extern "C" fwhip_status fwhip_log_mel_noalloc(fwhip_ctx *c, const float *samples, int64_t n, const float *filters,
+                                              int32_t n_mel, int32_t n_fft_bins, float *out) {
+    fwhip_status r = mel_check("fwhip_log_mel_noalloc", c, samples, n, filters, n_mel, n_fft_bins, out);
+    if (r != FWHIP_OK) return r;
+    const int dev = c->device;
+    int state;
+    void *sp;
+    const MelTables *tp;
+    {
+        std::lock_guard<std::mutex> lk(g_noalloc_mu);
+        state = dev >= 0 && dev < MEL_MAX_DEVICES ? g_noalloc_state[dev] : -1;
+        sp = state == 1 ? g_scratch_ptr[dev] : nullptr;
+        tp = state == 1 ? g_tables_ptr[dev] : nullptr;
+    }
+    if (state != 1)
+        return fw_fail(FWHIP_ERR_GENERIC, "fwhip_log_mel_noalloc: the device scratch of device " +
+                                              std::to_string(dev) + " was not set up by fwhip_init");
+    const long long nf = fwhip_mel_frames(n);
+    const long long nb = (nf + MEL_FPB - 1) / MEL_FPB;
+    const size_t need = (size_t)n_mel * 8 + (size_t)nb * 4 + 256;
+    if (nf > mel_noalloc_max_frames() || need > (size_t)MEL_SCRATCH_BYTES)
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_log_mel_noalloc: " + std::to_string(nf) +
+                                              " frames exceed the allocation-free scratch (at most " +
+                                              std::to_string(mel_noalloc_max_frames()) + " frames, " +
+                                              std::to_string(MEL_SCRATCH_BYTES) + " bytes); use fwhip_log_mel");
+    MEL_TRY(hipSetDevice(dev));
+    int2 *ranges = (int2 *)sp;
+    float *pmax = (float *)((char *)sp + (size_t)n_mel * 8);
+    mel_launch(c->stream, samples, (long long)n, nf, nb, filters, (int)n_mel, tp, ranges, pmax, pmax + nb, out);
     MEL_TRY(hipGetLastError());
     return FWHIP_OK;
 }

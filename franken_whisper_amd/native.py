@@ -59,6 +59,7 @@ SIGNATURES = {
     "fwhip_argmax_logits": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.POINTER(abi.Filter), C.c_int32, _i32p]),
     "fwhip_mel_frames": (C.c_int64, [C.c_int64]),
     "fwhip_log_mel": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
+    "fwhip_log_mel_noalloc": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
 }
 
 _lib = None
@@ -165,6 +166,12 @@ class Context:
                                         C.byref(filt) if filt is not None else None, 1 if initial else 0,
                                         out.ctypes.data_as(_i32p)))
         return out
+
+    def log_mel_noalloc(self, samples_dev: DeviceArray, n_samples: int, filters_dev: DeviceArray, n_mel: int,
+                        out_dev: DeviceArray, n_fft_bins: int = 201):
+        """fwhip_log_mel with the library's static device scratch: no allocation."""
+        check(lib().fwhip_log_mel_noalloc(self.h, samples_dev.ptr if n_samples else None, n_samples,
+                                          filters_dev.ptr, n_mel, n_fft_bins, out_dev.ptr))
 
     def close(self):
         if self.h:

@@ -322,6 +322,18 @@ fwhip_status fwhip_log_mel(fwhip_ctx *ctx, const float *samples_dev, int64_t n_s
                            const float *filters_dev, int32_t n_mel, int32_t n_fft_bins,
                            float *mel_dev);
 
+/* fwhip_log_mel without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, result and errors as fwhip_log_mel, bit for bit; its scratch
+ * (filter ranges, per-block maxima, the floor: 512 KiB) is a device array each
+ * GPU holds from fwhip_init until the process ends, so inputs are limited to
+ * 1,043,968 frames (about 166 M samples, 2.9 hours at 16 kHz); longer inputs
+ * return FWHIP_ERR_INVALID.  All calls on one GPU share that scratch: calls that
+ * overlap on one GPU (two contexts, two threads) race. */
+fwhip_status fwhip_log_mel_noalloc(fwhip_ctx *ctx, const float *samples_dev, int64_t n_samples,
+                                   const float *filters_dev, int32_t n_mel, int32_t n_fft_bins, float *mel_dev);
+
 #ifdef __cplusplus
 }
 #endif
