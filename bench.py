@@ -5,9 +5,13 @@ architecture with seeded random-init weights, 300 s of seeded synthetic 16 kHz
 audio with silent gaps -> GPU log-mel (128 bins, Slaney filterbank; 33,000
 frames) -> 10 windows x 30 s (3000 frames each, offsets 0, 3000, ...), int8 encoder plan
 (FW_ENC_ATTN_OUT_I8I32: i7 q/k/v/fc1/fc2, i8 attn.out), cross K/V precompute,
-then greedy no-timestamps decode of every window as one cohort with the int8
-decoder arm and the f16 KV cache: 4-token prompt + 220 sampled tokens.
-One step = that whole job.  Prints one JSON line.
+then greedy no-timestamps decode of every window as one cohort with the f16
+decoder arm (--dec-arm int8 for the int8 arm) and the f16 KV cache: 4-token
+prompt + 220 sampled tokens.  One step = that whole job.  After the timed
+region the job runs once more in exact mode (bit-identical to the oracle) and
+the timed run's tokens are compared with it window by window; the int8 decoder
+arm is timed on the same job and reported beside the headline with its own
+token comparison.  Prints one JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload job|enc-f32|enc-int8|decode]
 """
@@ -31,6 +35,21 @@ ENC_GOP_PER_WINDOW = 2273.8  # all GEMMs + SDPA
 ENC_GEMM_GOP_PER_WINDOW = 1887.4
 
 
+def _classes():
+    from franken_whisper_amd import abi
+
+    # kernel class -> (name, roofline bound, MFMA operand type, traffic record)
+    return {
+        abi.K_ENC_GEMM_I8: ("encoder int8 GEMM (k_gemm_pi8, persistent int8 tiles)", "mfma", "int8", "enc_gemm_i8"),
+        abi.K_ENC_GEMM_F32: ("encoder f16-pair GEMM (k_gemm2, conv stem)", "mfma", "f16", None),
+        abi.K_ENC_ATTN: ("encoder attention (k_attention2, f16 pairs)", "mfma", "f16", None),
+        abi.K_DEC_CROSS: ("decoder cross K/V precompute (k_gemm2 f16 pairs, all layers)", "mfma", "f16", None),
+        abi.K_DEC_STEP: ("decoder step (graph replay of one sampled step: 30 kernels, weights + cross K/V + KV cache)",
+                         "hbm", None, "dec_step"),
+        abi.K_DEC_LOGITS: ("decoder logits GEMV of the prompt row (k_gemv_i8m)", "hbm", None, None),
+    }
+
+
 def _args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -41,23 +60,49 @@ def _args():
     p.add_argument("--tokens", type=int, default=220)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")))
-    p.add_argument("--cpu-windows", type=int, default=2, help="windows of the job the CPU baseline runs")
+    p.add_argument("--cpu-runs", type=int, default=3, help="end-to-end runs of one window for the CPU baseline")
     p.add_argument("--copy-mb", type=int, default=512)
+    p.add_argument("--exact", action="store_true", help="exact mode: bit-identical to the reference's strict mode")
+    p.add_argument("--dec-arm", default="f16", choices=["int8", "f16"],
+                   help="decoder arm (f16: the tied f16 logits head, token-stable; int8: the reference default)")
+    p.add_argument("--no-verify", action="store_true", help="skip the exact-mode token check of the job")
     return p.parse_args()
 
 
-def cpu_baseline(model, n_windows, n_tokens, threads, sample_windows):
+def host_topology():
+    """CPUs this process may use, and the host's sockets / cores / SMT (lscpu)."""
+    import subprocess
+
+    topo = {"nproc": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        keys = {"Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+                "Thread(s) per core": "threads_per_core", "Model name": "model"}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in keys:
+                v = v.strip()
+                topo[keys[k.strip()]] = int(v) if v.isdigit() else v
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return topo
+
+
+def cpu_baseline(model, n_windows, n_tokens, threads, runs, arm):
     """The oracle (C restatement of the reference CPU path, OpenMP) on a bounded
-    sample of the same job: `sample_windows` of the job's windows run end to end
+    sample of the same job: window 0 of the job run end to end `runs` times
     (int8-plan encoder over all layers, cross K/V precompute, prompt prefill and
-    greedy decode of n_tokens), timed, and scaled to audio-seconds per second."""
+    greedy decode of n_tokens) plus its share of the whole job's log-mel; the
+    median run, scaled to audio-seconds per second.  The runs alternate between
+    two halves whose medians give an A/A spread (the noise of the measurement).
+    Returns the baseline record and the sampled window's tokens."""
     from franken_whisper_amd import abi, synth
     from oracle import oracle as O
 
     O.lib().ref_set_num_threads(threads)
     cfg = model.cfg
     e = O.Encoder(model, abi.ENC_INT8)
-    d = O.Decoder(model, abi.DEC_INT8)
+    d = O.Decoder(model, arm)
     tk = model.tokens
     filt = tk.filter()
     prompt = tk.sot_sequence(language_id=0)
@@ -66,50 +111,90 @@ def cpu_baseline(model, n_windows, n_tokens, threads, sample_windows):
     filters = synth.mel_filterbank(cfg.n_mels)
     t0 = time.perf_counter()
     full = O.log_mel(samples, filters)
-    t_mel = (time.perf_counter() - t0) * sample_windows / n_windows
-    t_enc = t_dec = 0.0
-    n_tok = 0
-    for w in range(sample_windows):
+    t_mel = (time.perf_counter() - t0) / n_windows
+    win = np.ascontiguousarray(full[:, :nf].T)
+    times, t_enc, t_dec, toks = [], [], [], None
+    for _ in range(runs):
         t0 = time.perf_counter()
-        y = e.forward(np.ascontiguousarray(full[:, w * nf:(w + 1) * nf].T))
+        y = e.forward(win)
         t1 = time.perf_counter()
         toks = d.state(y).greedy(prompt, n_tokens, filt)
         t2 = time.perf_counter()
-        t_enc += t1 - t0
-        t_dec += t2 - t1
-        n_tok += len(toks)
-    total = t_mel + t_enc + t_dec
-    return {
-        "value": round(sample_windows * 30.0 / total, 4),
+        t_enc.append(t1 - t0)
+        t_dec.append(t2 - t1)
+        times.append(t_mel + t2 - t0)
+    med = float(np.median(times))
+    a, b = float(np.median(times[0::2])), float(np.median(times[1::2]))
+    topo = host_topology()
+    rec = {
+        "value": round(30.0 / med, 4),
         "unit": "audio-s/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle (C restatement of the reference CPU path, -O3 -march=x86-64-v3, {threads} OpenMP "
-                   f"threads) on {sample_windows} of the job's {n_windows} windows end to end: log-mel "
-                   f"{t_mel / sample_windows:.3f} s/window (share of the whole job's log-mel), int8-plan encoder "
-                   f"{t_enc / sample_windows:.2f} s/window, cross K/V + prefill + greedy decode "
-                   f"{t_dec / sample_windows:.2f} s/window ({n_tok} tokens); {total:.1f} s of CPU work"),
+        "sample": (f"oracle (C restatement of the reference CPU path in its strict-parity mode, -O3 "
+                   f"-march=x86-64-v3, {threads} OpenMP threads = this GPU's share of the host) on window 0 of the "
+                   f"job end to end, {runs} runs: median {med:.2f} s per 30 s window (log-mel share "
+                   f"{t_mel:.3f} s, int8-plan encoder {np.median(t_enc):.2f} s, cross K/V + prefill + greedy "
+                   f"decode of {len(toks)} tokens on the {'int8' if arm == abi.DEC_INT8 else 'f16'} decoder arm "
+                   f"{np.median(t_dec):.2f} s); A/A spread "
+                   f"{abs(a - b) / med * 100:.1f}%; the reference's own engine publishes ~1.44 s per turbo encoder "
+                   f"window (docs/PERF_FRONTIER.md:48-59)"),
+        "runs_s": [round(t, 3) for t in times],
+        "aa_spread": round(abs(a - b) / med, 4),
+        "host": topo,
     }
+    return rec, toks
 
 
 AUDIO_SEED = 1234
 
 
-TRAFFIC_FILE = "profiles/k_gemm_pi8_int8_encoder_job.md"
+# rocprofv3 counter measurements of the job's kernels, per class: file and the
+# key of its "key: bytes" line (the counters cannot be read inside a timed run)
+TRAFFIC = {"enc_gemm_i8": ("profiles/k_gemm_pi8_int8_encoder_job.md", "traffic_bytes_per_launch"),
+           "dec_step": ("profiles/decode_step_int8_10_streams.md", "traffic_bytes_per_step")}
 
 
-def measured_traffic():
-    """HBM bytes per int8 encoder GEMM dispatch on this job's shapes, as measured
-    with rocprofv3 counters and recorded in TRAFFIC_FILE (the counters cannot be
-    read from inside a timed run)."""
+def measured_traffic(which):
+    """HBM bytes per launch (or per decoder step) of a kernel class on this
+    job's shapes, as recorded from rocprofv3 FETCH_SIZE / WRITE_SIZE runs."""
     import re
 
+    path, key = TRAFFIC[which]
     try:
-        with open(os.path.join(ROOT, TRAFFIC_FILE)) as f:
-            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
-        return int(m.group(1)) if m else None
+        with open(os.path.join(ROOT, path)) as f:
+            m = re.search(r"^" + key + r":\s*(\d+)", f.read(), re.M)
+        return (int(m.group(1)), path) if m else (None, path)
     except OSError:
-        return None
+        return None, path
+
+
+def verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, n_tokens, filt, got):
+    """The job once more in exact mode (encoder and cross K/V in the reference's
+    strict-parity arithmetic, bit-identical to it), decoded on both arms; returns
+    per arm the exact tokens, and how many of the timed job's windows (got: arm ->
+    tokens) match them."""
+    from franken_whisper_amd import abi, native
+
+    cfg = model.cfg
+    enc = native.Encoder(ctx, model, abi.ENC_INT8)
+    enc.set_exact(True)
+    states = ctx.empty((W, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+    enc.forward_mel(mel_dev, mel_frames, offsets, nf, states)
+    enc.close()
+    out = {}
+    for arm, toks in got.items():
+        dec = native.Decoder(ctx, model, arm)
+        dec.set_exact(True)
+        st = dec.state(W, cfg.n_audio_ctx)
+        st.set_cross(states)
+        ref = st.greedy(prompt, n_tokens, filt)
+        st.close()
+        dec.close()
+        same = sum(int(np.array_equal(a, b)) for a, b in zip(toks, ref))
+        out[arm] = (ref, same)
+    states.free()
+    return out
 
 
 def copy_calibration(mb, reps):
@@ -172,11 +257,15 @@ def main():
         enc = native.Encoder(ctx, model, abi.ENC_INT8)
     elif a.workload == "enc-f32":
         enc = native.Encoder(ctx, model, abi.ENC_F32)
+    if enc is not None and a.exact:
+        enc.set_exact(True)
     tk = model.tokens
     filt = tk.filter()
     prompt = tk.sot_sequence(language_id=0)
     if a.workload in ("job", "decode"):
-        dec = native.Decoder(ctx, model, abi.DEC_INT8)
+        dec = native.Decoder(ctx, model, abi.DEC_INT8 if a.dec_arm == "int8" else abi.DEC_F16)
+        if a.exact:
+            dec.set_exact(True)
         st = dec.state(W, cfg.n_audio_ctx)
         if a.workload == "decode":
             enc_out.upload(synth.encoder_states(77, W, cfg.n_audio_ctx, cfg.n_audio_state))
@@ -185,6 +274,7 @@ def main():
     t_setup = time.perf_counter() - t_setup
 
     tokens_out = [0]
+    last_tokens = [None]
 
     def step():
         if enc is not None:
@@ -196,6 +286,7 @@ def main():
                 st.reset()
             toks = st.greedy(prompt, a.tokens, filt)
             tokens_out[0] = sum(len(t) for t in toks)
+            last_tokens[0] = toks
 
     for _ in range(a.warmup):
         step()
@@ -236,34 +327,60 @@ def main():
         step()
     ctx.synchronize()
     elapsed = time.perf_counter() - t0
-    stats = {k: ctx.kernel_stats(k) for k in (abi.K_ENC_GEMM_I8, abi.K_ENC_GEMM_F32, abi.K_ENC_ATTN,
-                                              abi.K_DEC_LOGITS)}
+    CLASSES = _classes()
+    stats = {k: ctx.kernel_stats(k) for k in CLASSES}
     ctx.timing(False)
     ms_per_step = elapsed * 1e3 / a.steps
 
-    names = {abi.K_ENC_GEMM_I8: ("encoder int8 GEMM (k_gemm_pi8, persistent int8 tiles)", "mfma", "int8"),
-             abi.K_ENC_GEMM_F32: ("encoder f16-pair GEMM (k_gemm2, f16-pair tiles)", "mfma", "f16"),
-             abi.K_ENC_ATTN: ("encoder attention (k_attention2, f16 pairs)", "mfma", "f16"),
-             abi.K_DEC_LOGITS: ("decoder logits GEMV (k_gemv_i8m)", "hbm", None)}
-    kclass = max(stats, key=lambda k: stats[k][1])
-    n, ms, units = stats[kclass]
-    name, bound, op = names[kclass]
-    if bound == "mfma":
-        achieved = units / (ms * 1e-3) / 1e12
-        roof = {"kernel": name, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS[op],
-                "unit": "TFLOP/s", "op_dtype": op, "frac": round(achieved / PEAK_TFLOPS[op], 4), "traffic": None,
-                "launches": n, "avg_launch_ms": round(ms / max(n, 1), 4)}
-    else:
-        achieved = units / (ms * 1e-3) / 1e9
-        roof = {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "launches": n,
-                "avg_launch_ms": round(ms / max(n, 1), 4)}
-    kernel_classes = {names[k][0]: {"launches": v[0], "total_ms": round(v[1], 3)} for k, v in stats.items() if v[0]}
-    if kclass == abi.K_ENC_GEMM_I8 and a.workload == "job" and W == 10:
-        tb = measured_traffic()
-        if tb:
-            roof["traffic"] = tb
-            roof["traffic_source"] = TRAFFIC_FILE + " (rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0, per dispatch)"
+    rooflines = []
+    for k, (n, ms, units) in stats.items():
+        if not n:
+            continue
+        name, bound, op, tkey = CLASSES[k]
+        r = {"kernel": name, "bound": bound, "launches": n, "avg_launch_ms": round(ms / n, 4),
+             "total_ms": round(ms, 3)}
+        if bound == "mfma":
+            ach = units / (ms * 1e-3) / 1e12
+            r.update(achieved=round(ach, 2), peak=PEAK_TFLOPS[op], unit="TFLOP/s", op_dtype=op,
+                     frac=round(ach / PEAK_TFLOPS[op], 4), traffic=None)
+        else:
+            ach = units / (ms * 1e-3) / 1e9
+            r.update(achieved=round(ach, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
+                     traffic=None, algorithmic_bytes=round(units / n))
+        if tkey and a.workload == "job" and W == 10:
+            tb, path = measured_traffic(tkey)
+            if tb:
+                r["traffic"] = tb
+                r["traffic_source"] = path + " (rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0)"
+        rooflines.append(r)
+    rooflines.sort(key=lambda r: -r["total_ms"])
+    roof = dict(rooflines[0]) if rooflines else None
+
+    # the int8 decoder arm (the reference's default arm) on the same job:
+    # timed the same way, reported beside the headline with its token check
+    int8_arm = None
+    if a.workload == "job" and a.dec_arm == "f16" and not a.no_verify:
+        dec8 = native.Decoder(ctx, model, abi.DEC_INT8)
+        st8 = dec8.state(W, cfg.n_audio_ctx)
+        toks8 = None
+        for i in range(a.warmup + a.steps):
+            if i == a.warmup:
+                ctx.synchronize()
+                t8 = time.perf_counter()
+            encode()
+            st8.set_cross(enc_out)
+            toks8 = st8.greedy(prompt, a.tokens, filt)
+        ctx.synchronize()
+        ms8 = (time.perf_counter() - t8) * 1e3 / a.steps
+        int8_arm = {"value": round(30.0 * W / (ms8 * 1e-3), 2), "ms_per_step": round(ms8, 3), "tokens": toks8}
+        st8.close()
+        dec8.close()
+    verify = None
+    if a.workload == "job" and not a.no_verify:
+        got = {abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8: last_tokens[0]}
+        if int8_arm:
+            got[abi.DEC_INT8] = int8_arm.pop("tokens")
+        verify = verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, a.tokens, filt, got)
 
     audio_s = 30.0 * W
     out = {
@@ -283,15 +400,20 @@ def main():
                  "synthetic (seeded random-init weights N(0,0.02), seeded synthetic log-mel input)"),
         "config": {},
         "roofline": roof,
+        "rooflines": rooflines,
     }
     if a.workload == "job":
         out["value"] = round(audio_s / (ms_per_step * 1e-3), 2)
+        arm_txt = ("f16 decoder arm (every GEMV f16 in dot_f16c order, f16 cross K/V, tied f16 logits head)"
+                   if a.dec_arm == "f16" else "int8 decoder arm")
         out["config"] = {"workload": f"large-v3-turbo whole job: {W} x 30 s windows, int8 encoder "
                                      f"(FW_ENC_ATTN_OUT_I8I32 plan, dense, no ToMe), cross K/V, greedy no-timestamps "
-                                     f"decode of {a.tokens} tokens/window (cohort of {W} streams), int8 decoder arm, "
+                                     f"decode of {a.tokens} tokens/window (cohort of {W} streams), {arm_txt}, "
                                      f"f16 KV cache; log-mel (128 bins) of {30 * W} s of seeded synthetic 16 kHz audio with "
                                      f"silent gaps computed inside the step", "windows": W, "audio_s": audio_s,
-                         "n_frames": nf, "prompt_tokens": len(prompt), "max_tokens": a.tokens}
+                         "n_frames": nf, "prompt_tokens": len(prompt), "max_tokens": a.tokens,
+                         "mode": "exact" if a.exact else "fast"}
+        out["dtype"] = "int8+f16" if a.dec_arm == "f16" else "int8+f32"
     elif a.workload.startswith("enc"):
         out["value"] = round(audio_s / (ms_per_step * 1e-3), 2)
         out["dtype"] = "int8+f32" if a.workload == "enc-int8" else "f32 (f16-pair MFMA)"
@@ -301,18 +423,30 @@ def main():
         out["unit"] = "tok/s"
         out["value"] = round(tokens_out[0] / (ms_per_step * 1e-3), 1)
         out["config"] = {"workload": f"large-v3-turbo decoder: {W} streams, prompt + {a.tokens} greedy steps, "
-                                     f"int8 arm, f16 KV cache", "streams": W}
+                                     f"{a.dec_arm} arm, f16 KV cache", "streams": W}
     enc_ms = comp.get("encoder_ms")
     out["enc_tflops"] = round(ENC_GOP_PER_WINDOW * W / enc_ms, 1) if enc_ms else None
     if "decode_ms" in comp:
         out["decode_tok_s"] = round(comp["decode_tokens"] / (comp["decode_ms"] * 1e-3), 1)
     out["components_ms"] = {k: round(v, 2) if isinstance(v, float) else v for k, v in comp.items()}
-    out["kernel_classes"] = kernel_classes
+    arm_main = abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8
+    if verify:
+        out["tokens_identical_to_exact"] = f"{verify[arm_main][1]}/{W} windows"
+        out["tokens_match"] = verify[arm_main][1] == W
+    if int8_arm:
+        int8_arm["tokens_identical_to_exact"] = f"{verify[abi.DEC_INT8][1]}/{W} windows"
+        int8_arm["note"] = ("int8 decoder arm (the reference's default): every linear re-quantizes its input to int8, "
+                            "so the sub-ulp f32 reordering of fast mode moves tokens; exact mode is bit-identical")
+        out["int8_decoder_arm"] = int8_arm
     out["setup_s"] = round(t_setup, 1)
     if a.workload == "job" and not a.no_cpu_baseline:
-        cb = cpu_baseline(model, W, a.tokens, a.cpu_threads, a.cpu_windows)
+        cb, cpu_toks = cpu_baseline(model, W, a.tokens, a.cpu_threads, a.cpu_runs, arm_main)
         out["cpu_baseline"] = cb
         out["gpu_over_cpu"] = round(out["value"] / cb["value"], 1)
+        g0 = last_tokens[0][0] if last_tokens[0] else None
+        out["tokens_match_cpu_oracle"] = {
+            "window": 0, "identical": bool(g0 is not None and np.array_equal(np.asarray(g0), np.asarray(cpu_toks))),
+            "gpu_tokens": int(len(g0)) if g0 is not None else 0, "cpu_tokens": int(len(cpu_toks))}
     for x in (st, dec, enc):
         if x is not None:
             x.close()

@@ -22,6 +22,8 @@ K_ENC_GEMM_F32 = 2
 K_ENC_ATTN = 3
 K_DEC_GEMV = 4
 K_DEC_LOGITS = 5
+K_DEC_CROSS = 6
+K_DEC_STEP = 7
 
 DS_CROSS_K_F16 = 1
 DS_CROSS_VT_F16 = 2

@@ -157,6 +157,256 @@ __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *
 }
 
 // ---------------------------------------------------------------------------
+// The same GEMV on weights repacked so each lane's share of a row is
+// contiguous ("fragment order", fw_launch_pack_gemv_f16): lane q of the LPR
+// lanes of a row owns lane-local elements li = c * CPL + e (chunk c, element e
+// of its CPL), stored in 16-byte groups g = li / 8 at row offset
+// (g * LPR + q) * 8 + li % 8.  Wave load g then reads LPR * 16 contiguous bytes
+// of each of its rows, and a lane issues R = 8 groups per round, the next round
+// in flight while the current one is used (a row of 1280 needs one round at 32
+// lanes per row).  Needs K % (8 * LPR) == 0.
+template <int LPR, int SG, bool LN>
+__global__ void __launch_bounds__(256) k_gemv_f16f(const uint16_t *__restrict__ Wf, const float *__restrict__ bias,
+                                                   const float *__restrict__ x, float *y, int N, int K, int ns,
+                                                   int ldy, int mode, const float *__restrict__ gelu_tab, int cps,
+                                                   int spb, const float *__restrict__ lnw,
+                                                   const float *__restrict__ lnb) {
+    constexpr int CPL = 32 / LPR, RPB = 256 / LPR, R = 8, CPG = 8 / CPL;
+    extern __shared__ __align__(16) float xs[]; // [cps][SG][32]
+    const int q = threadIdx.x % LPR;
+    const int nc = K >> 5, G = K / (8 * LPR), nslab = (nc + cps - 1) / cps, ntile = (N + RPB - 1) / RPB;
+    auto stage = [&](int s0, int sn, int c0, int cn) {
+        const int n4 = cn * 8, tot = SG * n4;
+        for (int b0 = 0; b0 < tot; b0 += 256 * 8) {
+            float4 tmp[8];
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                int i = b0 + r * 256 + (int)threadIdx.x;
+                i = i < tot ? i : tot - 1;
+                const int sl = i / n4, c4 = i - sl * n4;
+                const int sv = sl < sn ? sl : sn - 1;
+                const float4 v = ((const float4 *)(x + (size_t)(s0 + sv) * K + (size_t)c0 * 32))[c4];
+                tmp[r] = sl < sn ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                const int i = b0 + r * 256 + (int)threadIdx.x;
+                if (i < tot) {
+                    const int sl = i / n4, c4 = i - sl * n4;
+                    ((float4 *)xs)[((c4 >> 3) * SG + sl) * 8 + (c4 & 7)] = tmp[r];
+                }
+            }
+        }
+    };
+    // this block's streams [sb0, sb1), SG per pass; with lnw the staged rows are
+    // LayerNorm(x) (k_ln_quant's arithmetic: one wave per row, whole rows of
+    // K <= 1280 in one slab)
+    const int sb0 = blockIdx.y * spb, sb1 = ns < sb0 + spb ? ns : sb0 + spb;
+    auto stage_ln = [&](int s0, int sn) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n4 = K >> 2;
+        for (int sl = wave; sl < SG; sl += 4) {
+            float4 xv[5];
+            bool okk[5];
+#pragma unroll
+            for (int kk = 0; kk < 5; kk++) {
+                const int i = lane + kk * 64;
+                okk[kk] = i < n4;
+                xv[kk] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (sl < sn) xv[kk] = ((const float4 *)(x + (size_t)(s0 + sl) * K))[okk[kk] ? i : 0];
+            }
+            if (sl < sn) fw_ln_quant_vals<5>(xv, okk, nullptr, lnw, lnb, K, 0, nullptr, nullptr, lane);
+#pragma unroll
+            for (int kk = 0; kk < 5; kk++) {
+                if (okk[kk]) {
+                    const int i = (lane + kk * 64) * 4;
+                    *(float4 *)(xs + ((i >> 5) * SG + sl) * 32 + (i & 31)) =
+                        sl < sn ? xv[kk] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+            }
+        }
+    };
+    for (int s0 = sb0; s0 < sb1; s0 += SG) {
+        const int sn = sb1 - s0 < SG ? sb1 - s0 : SG;
+        bool staged = false;
+        for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+            const int row = tile * RPB + threadIdx.x / LPR;
+            const bool ok = row < N;
+            const uint4 *wl = (const uint4 *)(Wf + (size_t)(ok ? row : 0) * K) + q;
+            float a[SG][CPL];
+#pragma unroll
+            for (int sl = 0; sl < SG; sl++)
+#pragma unroll
+                for (int e = 0; e < CPL; e++) a[sl][e] = 0.0f;
+            for (int sb = 0; sb < nslab; sb++) {
+                const int c0 = sb * cps, cn = nc - c0 < cps ? nc - c0 : cps;
+                const int gs0 = c0 / CPG, gn = cn / CPG;
+                uint4 nxt[R];
+#pragma unroll
+                for (int i = 0; i < R; i++) nxt[i] = wl[(size_t)(gs0 + i < G ? gs0 + i : G - 1) * LPR];
+                if (nslab > 1 || !staged) {
+                    __syncthreads();
+                    if constexpr (LN) stage_ln(s0, sn);
+                    else stage(s0, sn, c0, cn);
+                    __syncthreads();
+                    staged = true;
+                }
+                for (int gg = 0; gg < gn; gg += R) {
+                    uint4 cur[R];
+#pragma unroll
+                    for (int i = 0; i < R; i++) {
+                        cur[i] = nxt[i];
+                        const int gx = gs0 + gg + R + i;
+                        nxt[i] = wl[(size_t)(gx < G ? gx : G - 1) * LPR];
+                    }
+#pragma unroll
+                    for (int i = 0; i < R; i++) {
+                        if (gg + i < gn) {
+                            const uint32_t u[4] = {cur[i].x, cur[i].y, cur[i].z, cur[i].w};
+#pragma unroll
+                            for (int cc = 0; cc < CPG; cc++) {
+                                float wf[CPL];
+#pragma unroll
+                                for (int e = 0; e < CPL; e++) {
+                                    const int f = cc * CPL + e;
+                                    wf[e] = fw_h2f((uint16_t)(u[f >> 1] >> ((f & 1) * 16)));
+                                }
+                                const float *xc = xs + ((gg + i) * CPG + cc) * SG * 32 + q * CPL;
+                                float xv[SG][CPL];
+#pragma unroll
+                                for (int sl = 0; sl < SG; sl++) {
+                                    if constexpr (CPL >= 4) {
+#pragma unroll
+                                        for (int e = 0; e < CPL; e += 4) {
+                                            const float4 t = *(const float4 *)(xc + sl * 32 + e);
+                                            xv[sl][e] = t.x; xv[sl][e + 1] = t.y; xv[sl][e + 2] = t.z; xv[sl][e + 3] = t.w;
+                                        }
+                                    } else if constexpr (CPL == 2) {
+                                        const float2 t = *(const float2 *)(xc + sl * 32);
+                                        xv[sl][0] = t.x; xv[sl][1] = t.y;
+                                    } else {
+                                        xv[sl][0] = xc[sl * 32];
+                                    }
+                                }
+#pragma unroll
+                                for (int sl = 0; sl < SG; sl++)
+#pragma unroll
+                                    for (int e = 0; e < CPL; e++) a[sl][e] = __builtin_fmaf(wf[e], xv[sl][e], a[sl][e]);
+                            }
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int sl = 0; sl < SG; sl++) {
+                if (sl < sn) {
+                    float t[CPL];
+#pragma unroll
+                    for (int e = 0; e < CPL; e++) {
+                        float v = a[sl][e];
+                        v = v + __shfl_xor(v, 8 / CPL, 64);
+                        v = v + __shfl_xor(v, 16 / CPL, 64);
+                        t[e] = v;
+                    }
+#pragma unroll
+                    for (int w = 1; w < CPL; w <<= 1)
+#pragma unroll
+                        for (int e = 0; e < CPL; e += 2 * w) t[e] = t[e] + t[e + w];
+                    float acc = t[0];
+#pragma unroll
+                    for (int m = 1; m < 8 / CPL; m <<= 1) acc = acc + __shfl_xor(acc, m, 64);
+                    if (q == 0 && ok) {
+                        const float v = bias ? acc + bias[row] : acc;
+                        float *yp = y + (size_t)(s0 + sl) * ldy + row;
+                        if (mode == 1) *yp = *yp + v;
+                        else if (mode == 2) *yp = fw_gelu(v, gelu_tab);
+                        else *yp = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+int fw_gemv_f16_lpr(int N) { return N <= 2048 ? 32 : N <= 8192 ? 16 : 8; }
+bool fw_gemv_f16_frag_ok(int N, int K) { return K > 0 && K % (8 * fw_gemv_f16_lpr(N)) == 0; }
+
+__global__ void __launch_bounds__(256) k_pack_gemv_f16(const uint16_t *W, uint16_t *Wf, int N, int K, int LPR) {
+    const int CPL = 32 / LPR;
+    const size_t total = (size_t)N * K;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        const size_t r = i / K;
+        const int k = (int)(i - r * K);
+        const int c = k >> 5, within = k & 31, q = within / CPL, e = within % CPL;
+        const int li = c * CPL + e;
+        Wf[r * K + (size_t)((li >> 3) * LPR + q) * 8 + (li & 7)] = W[i];
+    }
+}
+
+void fw_launch_pack_gemv_f16(hipStream_t st, const uint16_t *W, uint16_t *Wf, int N, int K) {
+    const size_t total = (size_t)N * K;
+    size_t g = (total + 255) / 256;
+    g = g < 65536 ? g : 65536;
+    hipLaunchKernelGGL(k_pack_gemv_f16, dim3((unsigned)g), dim3(256), 0, st, W, Wf, N, K, fw_gemv_f16_lpr(N));
+}
+
+// W in fragment order (fw_launch_pack_gemv_f16); K % (8 * lanes per row) == 0
+void fw_launch_gemv_f16f(hipStream_t st, const uint16_t *Wf, const float *bias, const float *x, float *y, int N,
+                         int K, int ns, int ldy, int mode, const float *gelu_tab, const float *lnw,
+                         const float *lnb) {
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    const int LPR = fw_gemv_f16_lpr(N), CPG = LPR / 4;
+    const int nc = K >> 5;
+    // streams per block: all of them when their rows fit the LDS budget in one
+    // slab, else split over grid.y (fc2's 5120-wide rows)
+    constexpr size_t LDS_BUDGET = 128 * 1024;
+    int spb = ns < 16 ? ns : 16;
+    while (spb > 1 && (size_t)spb * nc * 128 > LDS_BUDGET) spb = (spb + 1) / 2;
+    const int nby = (ns + spb - 1) / spb;
+    const int spass = spb > 12 ? 16 : spb > 10 ? 12 : spb > 8 ? 10 : spb > 5 ? 8 : spb > 4 ? 5 : spb > 2 ? 4 : spb;
+    int cps = (int)(LDS_BUDGET / ((size_t)spass * 128));
+    cps = cps / CPG * CPG; // whole weight groups per slab
+    cps = cps < nc ? cps : nc;
+    const size_t shm = sizeof(float) * (size_t)spass * cps * 32;
+    const bool one = cps >= nc;
+    if (lnw && (!one || K > 1280)) return; // LayerNorm staging needs the whole row (callers check)
+#define GF_GO(LPR_, SG)                                                                                      \
+    do {                                                                                                     \
+        const int ntile = (N + 256 / LPR_ - 1) / (256 / LPR_);                                               \
+        const int grid = one && ntile > 2 * n_cu ? 2 * n_cu : ntile;                                        \
+        if (lnw)                                                                                            \
+            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, true>), dim3(grid, nby), dim3(256), shm, st, Wf, bias, x, y, \
+                               N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);                          \
+        else                                                                                                \
+            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, false>), dim3(grid, nby), dim3(256), shm, st, Wf, bias, x,   \
+                               y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);                       \
+    } while (0)
+#define GF_SG(LPR_)                      \
+    do {                                 \
+        switch (spass) {                 \
+        case 1: GF_GO(LPR_, 1); break;   \
+        case 2: GF_GO(LPR_, 2); break;   \
+        case 4: GF_GO(LPR_, 4); break;   \
+        case 5: GF_GO(LPR_, 5); break;   \
+        case 8: GF_GO(LPR_, 8); break;   \
+        case 10: GF_GO(LPR_, 10); break; \
+        case 12: GF_GO(LPR_, 12); break; \
+        default: GF_GO(LPR_, 16); break; \
+        }                                \
+    } while (0)
+    if (LPR == 32) GF_SG(32);
+    else if (LPR == 16) GF_SG(16);
+    else GF_SG(8);
+#undef GF_SG
+#undef GF_GO
+}
+
+// ---------------------------------------------------------------------------
 // Order-preserving argmax key: larger value first, then smaller index; 0 means
 // "no candidate" (masked, -inf or NaN never compare greater, as in the
 // reference's strict '>' scan).  -0.0 and +0.0 compare equal under '>', so the
@@ -755,6 +1005,150 @@ __device__ __forceinline__ float fw_seq_sum_wave(const float *v, int n) {
         }
     }
     return s;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-attention for one (head, stream) with f16 K/V (cross_attention,
+// decoder.rs:1524-1716, FRANKEN_WHISPER_INT8_CROSS_KV=0): qh = q*s; scores =
+// gemv_f16(K_h, qh) and out = gemv_f16(Vt_h, p), both in dot_f16c order
+// (nn.rs:1983-2051); softmax with glibc-exact expf and the sequential sum
+// (nn.rs:4880-4963), formed by one wave (fw_seq_sum_wave) when T <= 1536.
+// 512 threads.  Scores: a key row (64 f16) per thread per round, read as eight
+// 16-byte loads.  Values: 8 lanes per output column dd, lane q owning chains
+// 4q .. 4q+3 of each 32-key chunk (vector q/2, lanes 4(q%2) .. +3), then the
+// dot_f16c reduction by butterflies; V^T rows need T % 4 == 0 for 8-byte loads
+// (VEC), else they are read element by element.
+#define XA_MAXC 48 // 32-key chunks of V^T a thread holds in registers (T <= 1536)
+template <bool VEC>
+__global__ void __launch_bounds__(512) k_cross_attn_f16v2(const float *qc, const uint16_t *ck, const uint16_t *cvt,
+                                                          float *att, int d, int T, int H, int L, int layer,
+                                                          float scale) {
+    extern __shared__ __align__(16) float scf[]; // [(T + 3) & ~3]
+    __shared__ float qh[64];
+    __shared__ float red[8];
+    __shared__ float inv_s;
+    const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const size_t lh = ((size_t)s * L + layer) * H + h;
+    const uint16_t *K = ck + lh * (size_t)T * 64;
+    const uint16_t *V = cvt + lh * (size_t)T * 64;
+    // VEC: this thread's V^T chunks (row dd = t / 8, 4 keys at 32c + 4(t % 8))
+    // requested first, so they arrive under the scores and the softmax
+    const int nc = T >> 5;
+    uint2 vreg[VEC ? XA_MAXC : 1];
+    if constexpr (VEC) {
+        const uint16_t *vr0 = V + (size_t)(t >> 3) * T + (t & 7) * 4;
+#pragma unroll
+        for (int c = 0; c < XA_MAXC; c++) vreg[c] = *(const uint2 *)(vr0 + (size_t)(c < nc ? c : 0) * 32);
+    }
+    if (t < 64) qh[t] = qc[(size_t)s * d + h * 64 + t] * scale;
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = t; j < T; j += 512) {
+        const uint4 *kr = (const uint4 *)(K + (size_t)j * 64);
+        uint4 kv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) kv[i] = kr[i];
+        float a[4][8];
+#pragma unroll
+        for (int jv = 0; jv < 4; jv++)
+#pragma unroll
+            for (int l = 0; l < 8; l++) a[jv][l] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int jv = 0; jv < 4; jv++) {
+                const uint4 u = kv[c * 4 + jv];
+                const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int l = 0; l < 8; l++)
+                    a[jv][l] = __builtin_fmaf(fw_h2f((uint16_t)(uw[l >> 1] >> ((l & 1) * 16))),
+                                              qh[c * 32 + jv * 8 + l], a[jv][l]);
+            }
+        float tt[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) tt[l] = (a[0][l] + a[1][l]) + (a[2][l] + a[3][l]);
+        const float v = ((tt[0] + tt[1]) + (tt[2] + tt[3])) + ((tt[4] + tt[5]) + (tt[6] + tt[7]));
+        scf[j] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = fw_block_max(mx, red);
+    const bool fin = isfinite(mx);
+    if (fin)
+        for (int j = t; j < T; j += 512) {
+            const float e = fw_expf(scf[j] - mx);
+            scf[j] = isfinite(e) ? e : 0.0f;
+        }
+    __syncthreads();
+    if (t < 64) {
+        float sum = 0.0f;
+        if (fin) {
+            if (T <= 64 * SW_MAXC) {
+                sum = fw_seq_sum_wave(scf, T);
+            } else if (t == 0) {
+                for (int j = 0; j < T; j++) sum += scf[j];
+            }
+        }
+        if (t == 0) inv_s = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    if (inv > 0.0f)
+        for (int j = t; j < T; j += 512) scf[j] = scf[j] * inv;
+    __syncthreads();
+    const int dd = t >> 3, q = t & 7;
+    const uint16_t *vr = V + (size_t)dd * T;
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (VEC) {
+#pragma unroll
+        for (int c = 0; c < XA_MAXC; c++) {
+            if (c < nc) {
+                const float4 p = *(const float4 *)(scf + c * 32 + q * 4);
+                const uint2 u = vreg[c];
+                a[0] = __builtin_fmaf(fw_h2f((uint16_t)(u.x & 0xffff)), p.x, a[0]);
+                a[1] = __builtin_fmaf(fw_h2f((uint16_t)(u.x >> 16)), p.y, a[1]);
+                a[2] = __builtin_fmaf(fw_h2f((uint16_t)(u.y & 0xffff)), p.z, a[2]);
+                a[3] = __builtin_fmaf(fw_h2f((uint16_t)(u.y >> 16)), p.w, a[3]);
+            }
+        }
+    } else {
+        for (int c = 0; c < nc; c++) {
+            const int i0 = c * 32 + q * 4;
+            const float4 p = *(const float4 *)(scf + i0);
+            a[0] = __builtin_fmaf(fw_h2f(vr[i0]), p.x, a[0]);
+            a[1] = __builtin_fmaf(fw_h2f(vr[i0 + 1]), p.y, a[1]);
+            a[2] = __builtin_fmaf(fw_h2f(vr[i0 + 2]), p.z, a[2]);
+            a[3] = __builtin_fmaf(fw_h2f(vr[i0 + 3]), p.w, a[3]);
+        }
+    }
+    // (a0 + a1) + (a2 + a3): vectors 2 lanes apart; then the 8-lane tree
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        a[e] = a[e] + __shfl_xor(a[e], 2, 64);
+        a[e] = a[e] + __shfl_xor(a[e], 4, 64);
+    }
+    float acc = (a[0] + a[1]) + (a[2] + a[3]);
+    acc = acc + __shfl_xor(acc, 1, 64);
+    if (q == 0) {
+        int i = nc * 32;
+        for (; i + 8 <= T; i += 8) {
+            float pp[8];
+            for (int l = 0; l < 8; l++) pp[l] = fw_h2f(vr[i + l]) * scf[i + l];
+            acc += ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
+        }
+        for (; i < T; i++) acc += fw_h2f(vr[i]) * scf[i];
+        att[(size_t)s * d + h * 64 + dd] = acc;
+    }
+}
+
+void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt, float *att,
+                              int d, int T, int H, int L, int layer, int ns, float scale) {
+    const size_t shm = sizeof(float) * (size_t)((T + 3) & ~3);
+    if ((T & 3) == 0 && (T >> 5) <= XA_MAXC)
+        hipLaunchKernelGGL(k_cross_attn_f16v2<true>, dim3(H, ns), dim3(512), shm, st, qc, ck, cvt, att, d, T, H, L,
+                           layer, scale);
+    else
+        hipLaunchKernelGGL(k_cross_attn_f16v2<false>, dim3(H, ns), dim3(512), shm, st, qc, ck, cvt, att, d, T, H, L,
+                           layer, scale);
 }
 
 // ---------------------------------------------------------------------------

@@ -14,194 +14,181 @@
 #define LN_EPS_F 1e-5f
 
 // ---------------------------------------------------------------------------
-// f16 GEMV in dot_f16c order (nn.rs:1983-2051), MAXS streams per block.
-// Lane j (0..3) of a 4-lane group owns accumulator vector a_j (8 lanes of the
-// AVX register); chunk c covers elements [32c, 32c+32).
-// Block = 256 threads; 64 rows per block.
-template <int MAXS, int U>
-__global__ void __launch_bounds__(256) k_gemv_f16(const uint16_t *__restrict__ W, const float *__restrict__ bias,
-                                                  const float *__restrict__ x, float *y, int N, int K, int ns,
-                                                  int ldy, int mode, const float *__restrict__ gelu_tab) {
-    // blockIdx.y selects the stream group [s0, s0 + MAXS)
-    const int s0 = blockIdx.y * MAXS;
-    x += (size_t)s0 * K;
-    y += (size_t)s0 * ldy;
-    ns = ns - s0 < MAXS ? ns - s0 : MAXS;
-    int j = threadIdx.x & 3;
-    int row = blockIdx.x * 64 + (threadIdx.x >> 2);
-    bool ok = row < N;
-    const uint16_t *wr = W + (size_t)(ok ? row : 0) * K;
-    float a[MAXS][8];
+// f16 GEMV in dot_f16c order (nn.rs:1983-2051), every stream in one launch so
+// the weights are read once.
+//
+// dot_f16c keeps 4 accumulator vectors of 8 lanes: chain ch = 8 * jv + l
+// (vector jv, lane l) takes element 32c + ch of each 32-element chunk c, FMA,
+// in chunk order.  Here LPR lanes share a row and lane q owns the CPL = 32/LPR
+// chains q*CPL .. q*CPL + CPL - 1 (contiguous elements of every chunk), for
+// every stream of the pass.  Then the reference's reduction: lane-wise
+// (a0 + a1) + (a2 + a3) by butterflies over the lanes holding the same l of
+// other vectors, the 8-lane tree ((t0+t1)+(t2+t3))+((t4+t5)+(t6+t7)) (in-lane
+// over a lane's aligned block of t, then butterflies), then the K % 32 tail
+// (8-element chunks, each reduced the same way, then scalar mul + add) by the
+// row's first lane.  Every add is commutative, so a butterfly leaves the same
+// bits on both lanes.  The streams' x rows are staged in LDS by K-slabs.
+template <int LPR, int SG>
+__global__ void __launch_bounds__(256) k_gemv_f16m(const uint16_t *__restrict__ W, const float *__restrict__ bias,
+                                                   const float *__restrict__ x, float *y, int N, int K, int ns,
+                                                   int ldy, int mode, const float *__restrict__ gelu_tab, int cps) {
+    // U chunks of weights in flight per lane: narrow per-lane loads need more
+    // of them to cover the memory latency
+    constexpr int CPL = 32 / LPR, RPB = 256 / LPR, U = CPL <= 2 ? 16 : CPL == 4 ? 8 : 4, NW = (CPL + 1) / 2;
+    // a K-slab of every stream of the pass, chunk-major [cps][SG][32], so the
+    // streams of one chunk sit at small constant offsets from one address
+    extern __shared__ __align__(16) float xs[];
+    const int q = threadIdx.x % LPR;
+    const int nc = K >> 5, nslab = (nc + cps - 1) / cps, ntile = (N + RPB - 1) / RPB;
+    // stage chunks [c0, c0 + cn) of streams [s0, s0 + sn): every load of a round
+    // is issued before its LDS stores
+    // (streams past sn of the pass are staged as zeros: the FMA loop runs all SG)
+    auto stage = [&](int s0, int sn, int c0, int cn) {
+        const int n4 = cn * 8, tot = SG * n4;
+        for (int b0 = 0; b0 < tot; b0 += 256 * 8) {
+            // unconditional loads from clamped (valid) addresses, so all eight
+            // are in flight before the first wait
+            float4 tmp[8];
 #pragma unroll
-    for (int s = 0; s < MAXS; s++)
-#pragma unroll
-        for (int l = 0; l < 8; l++) a[s][l] = 0.0f;
-    const int nc = K >> 5;
-    // fma of one 32-chunk (8 weights per lane) into the MAXS accumulators
-    auto chunk = [&](const uint4 wv, const float4 (&xc)[MAXS][2]) {
-        float wf[8];
-        wf[0] = fw_h2f(wv.x & 0xffff); wf[1] = fw_h2f(wv.x >> 16);
-        wf[2] = fw_h2f(wv.y & 0xffff); wf[3] = fw_h2f(wv.y >> 16);
-        wf[4] = fw_h2f(wv.z & 0xffff); wf[5] = fw_h2f(wv.z >> 16);
-        wf[6] = fw_h2f(wv.w & 0xffff); wf[7] = fw_h2f(wv.w >> 16);
-#pragma unroll
-        for (int s = 0; s < MAXS; s++) {
-            if (s < ns) {
-                const float4 x0 = xc[s][0], x1 = xc[s][1];
-                a[s][0] = __builtin_fmaf(wf[0], x0.x, a[s][0]);
-                a[s][1] = __builtin_fmaf(wf[1], x0.y, a[s][1]);
-                a[s][2] = __builtin_fmaf(wf[2], x0.z, a[s][2]);
-                a[s][3] = __builtin_fmaf(wf[3], x0.w, a[s][3]);
-                a[s][4] = __builtin_fmaf(wf[4], x1.x, a[s][4]);
-                a[s][5] = __builtin_fmaf(wf[5], x1.y, a[s][5]);
-                a[s][6] = __builtin_fmaf(wf[6], x1.z, a[s][6]);
-                a[s][7] = __builtin_fmaf(wf[7], x1.w, a[s][7]);
+            for (int r = 0; r < 8; r++) {
+                int i = b0 + r * 256 + (int)threadIdx.x;
+                i = i < tot ? i : tot - 1;
+                const int sl = i / n4, c4 = i - sl * n4;
+                const int sv = sl < sn ? sl : sn - 1;
+                const float4 v = ((const float4 *)(x + (size_t)(s0 + sv) * K + (size_t)c0 * 32))[c4];
+                tmp[r] = sl < sn ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
-        }
-    };
-    auto load_x = [&](int c, float4 (&xc)[MAXS][2]) {
 #pragma unroll
-        for (int s = 0; s < MAXS; s++) {
-            const float4 *xp = (const float4 *)(x + (size_t)(s < ns ? s : ns - 1) * K + c * 32 + j * 8);
-            xc[s][0] = xp[0];
-            xc[s][1] = xp[1];
-        }
-    };
-    // the weight chunks of the next U iterations are in flight while the
-    // current ones are used (rows past N read row 0 and are never stored)
-    uint4 wq[U];
-#pragma unroll
-    for (int u = 0; u < U; u++) wq[u] = *(const uint4 *)(wr + (u < nc ? u : nc - 1) * 32 + j * 8);
-    int c = 0;
-    for (; c + U <= nc; c += U) {
-        uint4 wc[U];
-        float4 xc[U][MAXS][2];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            wc[u] = wq[u];
-            const int cn = c + U + u < nc ? c + U + u : nc - 1;
-            wq[u] = *(const uint4 *)(wr + cn * 32 + j * 8);
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) load_x(c + u, xc[u]);
-#pragma unroll
-        for (int u = 0; u < U; u++) chunk(wc[u], xc[u]);
-    }
-    for (; c < nc; c++) {
-        float4 xc[MAXS][2];
-        load_x(c, xc);
-        chunk(*(const uint4 *)(wr + c * 32 + j * 8), xc);
-    }
-    int tail8 = nc * 32;
-#pragma unroll
-    for (int s = 0; s < MAXS; s++) {
-        if (s >= ns) continue;
-        float t[8];
-#pragma unroll
-        for (int l = 0; l < 8; l++) {
-            float v = a[s][l];
-            v = v + __shfl_xor(v, 1, 64); // (a0+a1) | (a2+a3)
-            v = v + __shfl_xor(v, 2, 64); // (a0+a1)+(a2+a3)
-            t[l] = v;
-        }
-        float acc = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
-        if (j == 0 && ok) {
-            const float *xr = x + (size_t)s * K;
-            int i = tail8;
-            for (; i + 8 <= K; i += 8) {
-                float p[8];
-                for (int l = 0; l < 8; l++) p[l] = fw_h2f(wr[i + l]) * xr[i + l];
-                acc += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-            }
-            for (; i < K; i++) acc += fw_h2f(wr[i]) * xr[i];
-            float v = bias ? acc + bias[row] : acc;
-            float *yp = y + (size_t)s * ldy + row;
-            if (mode == 1) *yp = *yp + v;
-            else if (mode == 2) *yp = fw_gelu(v, gelu_tab);
-            else *yp = v;
-        }
-    }
-}
-
-// Cross-attention, f16 K/V (FRANKEN_WHISPER_INT8_CROSS_KV=0 arm): scores =
-// gemv_f16(K_h, qh) and out = gemv_f16(Vt_h, p), both in dot_f16c order.
-__global__ void __launch_bounds__(256) k_cross_attn_f16(const float *qc, const uint16_t *ck,
-                                                        const uint16_t *cvt, float *att, int d, int T, int H,
-                                                        int L, int layer, float scale) {
-    extern __shared__ float scf[]; // [T]
-    __shared__ float qh[64];
-    __shared__ float red[4];
-    __shared__ float bc[1];
-    int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
-    size_t lh = ((size_t)s * L + layer) * H + h;
-    const uint16_t *K = ck + lh * (size_t)T * 64;
-    const uint16_t *V = cvt + lh * (size_t)T * 64;
-    if (t < 64) qh[t] = qc[(size_t)s * d + h * 64 + t] * scale;
-    __syncthreads();
-    float mx = -INFINITY;
-    for (int jj = t; jj < T; jj += 256) {
-        const uint16_t *kr = K + (size_t)jj * 64;
-        float a[4][8];
-        for (int q = 0; q < 4; q++)
-            for (int l = 0; l < 8; l++) a[q][l] = 0.0f;
-        for (int c = 0; c < 2; c++)
-            for (int q = 0; q < 4; q++)
-                for (int l = 0; l < 8; l++) {
-                    int i = c * 32 + q * 8 + l;
-                    a[q][l] = __builtin_fmaf(fw_h2f(kr[i]), qh[i], a[q][l]);
+            for (int r = 0; r < 8; r++) {
+                const int i = b0 + r * 256 + (int)threadIdx.x;
+                if (i < tot) {
+                    const int sl = i / n4, c4 = i - sl * n4;
+                    ((float4 *)xs)[((c4 >> 3) * SG + sl) * 8 + (c4 & 7)] = tmp[r];
                 }
-        float tt[8];
-        for (int l = 0; l < 8; l++) tt[l] = (a[0][l] + a[1][l]) + (a[2][l] + a[3][l]);
-        float v = ((tt[0] + tt[1]) + (tt[2] + tt[3])) + ((tt[4] + tt[5]) + (tt[6] + tt[7]));
-        scf[jj] = v;
-        mx = fmaxf(mx, v);
-    }
-    mx = fw_block_max(mx, red);
-    bool fin = isfinite(mx);
-    if (fin)
-        for (int jj = t; jj < T; jj += 256) {
-            float e = fw_expf(scf[jj] - mx);
-            scf[jj] = isfinite(e) ? e : 0.0f;
+            }
         }
-    __syncthreads();
-    if (t == 0) {
-        float sum = 0.0f;
-        if (fin) for (int jj = 0; jj < T; jj++) sum += scf[jj];
-        bc[0] = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
-    }
-    __syncthreads();
-    float inv = bc[0];
-    if (inv > 0.0f)
-        for (int jj = t; jj < T; jj += 256) scf[jj] = scf[jj] * inv;
-    __syncthreads();
-    // out[dd] = dot_f16c(V[dd, :T], p): lane j of the 4-lane group owns a_j
-    int dd = t >> 2, j = t & 3;
-    const uint16_t *vr = V + (size_t)dd * T;
-    float a[8];
-    for (int l = 0; l < 8; l++) a[l] = 0.0f;
-    int nc = T >> 5;
-    for (int c = 0; c < nc; c++)
-        for (int l = 0; l < 8; l++) {
-            int i = c * 32 + j * 8 + l;
-            a[l] = __builtin_fmaf(fw_h2f(vr[i]), scf[i], a[l]);
+    };
+    for (int s0 = 0; s0 < ns; s0 += SG) {
+        const int sn = ns - s0 < SG ? ns - s0 : SG;
+        if (nslab == 1) {
+            __syncthreads();
+            stage(s0, sn, 0, nc);
+            __syncthreads();
         }
-    float tt[8];
-    for (int l = 0; l < 8; l++) {
-        float v = a[l];
-        v = v + __shfl_xor(v, 1, 64);
-        v = v + __shfl_xor(v, 2, 64);
-        tt[l] = v;
-    }
-    float acc = ((tt[0] + tt[1]) + (tt[2] + tt[3])) + ((tt[4] + tt[5]) + (tt[6] + tt[7]));
-    if (j == 0) {
-        int i = nc * 32;
-        for (; i + 8 <= T; i += 8) {
-            float p[8];
-            for (int l = 0; l < 8; l++) p[l] = fw_h2f(vr[i + l]) * scf[i + l];
-            acc += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+            const int row = tile * RPB + threadIdx.x / LPR;
+            const bool ok = row < N;
+            const uint16_t *wr = W + (size_t)(ok ? row : 0) * K + q * CPL;
+            // CPL f16 weights of chunk c (rows past N read row 0, never stored)
+            auto ldw = [&](int c, uint32_t (&u)[NW]) {
+                const uint16_t *p = wr + (size_t)c * 32;
+                if constexpr (CPL == 8) {
+                    const uint4 v = *(const uint4 *)p;
+                    u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
+                } else if constexpr (CPL == 4) {
+                    const uint2 v = *(const uint2 *)p;
+                    u[0] = v.x; u[1] = v.y;
+                } else if constexpr (CPL == 2) {
+                    u[0] = *(const uint32_t *)p;
+                } else {
+                    u[0] = *p;
+                }
+            };
+            float a[SG][CPL];
+#pragma unroll
+            for (int sl = 0; sl < SG; sl++)
+#pragma unroll
+                for (int e = 0; e < CPL; e++) a[sl][e] = 0.0f;
+            for (int sb = 0; sb < nslab; sb++) {
+                const int c0 = sb * cps, cn = nc - c0 < cps ? nc - c0 : cps;
+                if (nslab > 1) {
+                    __syncthreads();
+                    stage(s0, sn, c0, cn);
+                    __syncthreads();
+                }
+                uint32_t wq[U][NW];
+#pragma unroll
+                for (int u = 0; u < U; u++) ldw(c0 + (u < cn ? u : cn - 1), wq[u]);
+                for (int c = 0; c < cn; c += U) {
+                    uint32_t wc[U][NW];
+#pragma unroll
+                    for (int u = 0; u < U; u++) {
+#pragma unroll
+                        for (int e = 0; e < NW; e++) wc[u][e] = wq[u][e];
+                        ldw(c0 + (c + U + u < cn ? c + U + u : cn - 1), wq[u]);
+                    }
+#pragma unroll
+                    for (int u = 0; u < U; u++) {
+                        if (c + u < cn) {
+                            float wf[CPL];
+#pragma unroll
+                            for (int e = 0; e < CPL; e++)
+                                wf[e] = fw_h2f((uint16_t)(CPL == 1 ? wc[u][0] : (wc[u][e >> 1] >> ((e & 1) * 16))));
+                            const float *xc = xs + (c + u) * SG * 32 + q * CPL;
+                            float xv[SG][CPL];
+#pragma unroll
+                            for (int sl = 0; sl < SG; sl++) {
+                                if constexpr (CPL >= 4) {
+#pragma unroll
+                                    for (int e = 0; e < CPL; e += 4) {
+                                        const float4 t = *(const float4 *)(xc + sl * 32 + e);
+                                        xv[sl][e] = t.x; xv[sl][e + 1] = t.y; xv[sl][e + 2] = t.z; xv[sl][e + 3] = t.w;
+                                    }
+                                } else if constexpr (CPL == 2) {
+                                    const float2 t = *(const float2 *)(xc + sl * 32);
+                                    xv[sl][0] = t.x; xv[sl][1] = t.y;
+                                } else {
+                                    xv[sl][0] = xc[sl * 32];
+                                }
+                            }
+#pragma unroll
+                            for (int sl = 0; sl < SG; sl++)
+#pragma unroll
+                                for (int e = 0; e < CPL; e++) a[sl][e] = __builtin_fmaf(wf[e], xv[sl][e], a[sl][e]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int sl = 0; sl < SG; sl++) {
+                if (sl < sn) {
+                    // (a0 + a1) + (a2 + a3): vectors jv and jv ^ 1 sit 8 / CPL lanes apart
+                    float t[CPL];
+#pragma unroll
+                    for (int e = 0; e < CPL; e++) {
+                        float v = a[sl][e];
+                        v = v + __shfl_xor(v, 8 / CPL, 64);
+                        v = v + __shfl_xor(v, 16 / CPL, 64);
+                        t[e] = v;
+                    }
+                    // ((t0+t1)+(t2+t3))+((t4+t5)+(t6+t7)): in-lane over this lane's
+                    // aligned block of CPL values, then across the 8 / CPL lanes
+#pragma unroll
+                    for (int w = 1; w < CPL; w <<= 1)
+#pragma unroll
+                        for (int e = 0; e < CPL; e += 2 * w) t[e] = t[e] + t[e + w];
+                    float acc = t[0];
+#pragma unroll
+                    for (int m = 1; m < 8 / CPL; m <<= 1) acc = acc + __shfl_xor(acc, m, 64);
+                    if (q == 0 && ok) {
+                        const float *xr = x + (size_t)(s0 + sl) * K;
+                        const uint16_t *w0 = W + (size_t)row * K;
+                        int i = nc * 32;
+                        for (; i + 8 <= K; i += 8) {
+                            float p[8];
+                            for (int l = 0; l < 8; l++) p[l] = fw_h2f(w0[i + l]) * xr[i + l];
+                            acc += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                        }
+                        for (; i < K; i++) acc += fw_h2f(w0[i]) * xr[i];
+                        const float v = bias ? acc + bias[row] : acc;
+                        float *yp = y + (size_t)(s0 + sl) * ldy + row;
+                        if (mode == 1) *yp = *yp + v;
+                        else if (mode == 2) *yp = fw_gelu(v, gelu_tab);
+                        else *yp = v;
+                    }
+                }
+            }
         }
-        for (; i < T; i++) acc += fw_h2f(vr[i]) * scf[i];
-        att[(size_t)s * d + h * 64 + dd] = acc;
     }
 }
 
@@ -290,24 +277,52 @@ __global__ void __launch_bounds__(64) k_quant_f16_rows(const uint16_t *src, int8
 // ---------------------------------------------------------------------------
 // launch wrappers
 
-// Each thread's sequential chunk loop is latency-bound (a row's K/32 chunks in
-// order), so matrices up to 32 M weights run one stream per block row of the
-// grid (grid.y = ns) with 8 chunks of weights in flight per thread; larger ones
-// (the logits) keep 4 streams per block so the weights are read ns/4 times.
+// Lanes per row: enough waves for narrow matrices (N <= 2048: 32 lanes, up to
+// 8192: 16), 8 for the vocabulary-wide logits; streams go 16 per pass.  The
+// streams' x rows sit in LDS (at most 96 KB: a K-slab of cps 32-chunks); when
+// the whole row fits, the grid is persistent (two blocks per CU walk the row
+// tiles, x staged once per block), else each block takes one row tile and
+// stages the slabs in turn.
 void fw_launch_gemv_f16(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *y, int N,
                         int K, int ns, int ldy, int mode, const float *gelu_tab) {
-    if ((size_t)N * K <= ((size_t)32 << 20) || ns == 1)
-        hipLaunchKernelGGL((k_gemv_f16<1, 8>), dim3((N + 63) / 64, ns), dim3(256), 0, st, W, bias, x, y, N, K, ns,
-                           ldy, mode, gelu_tab);
-    else
-        hipLaunchKernelGGL((k_gemv_f16<4, 4>), dim3((N + 63) / 64, (ns + 3) / 4), dim3(256), 0, st, W, bias, x, y, N,
-                           K, ns, ldy, mode, gelu_tab);
-}
-
-void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,
-                              float *att, int d, int T, int H, int L, int layer, int ns, float scale) {
-    hipLaunchKernelGGL(k_cross_attn_f16, dim3(H, ns), dim3(256), sizeof(float) * T, st, qc, ck, cvt, att, d, T,
-                       H, L, layer, scale);
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    const int nc = K >> 5;
+    // streams per pass: the next of 1, 2, 4, 8, 10, 12, 16 (padding rows are zeros)
+    const int spass = ns > 12 ? 16 : ns > 10 ? 12 : ns > 8 ? 10 : ns > 4 ? 8 : ns > 2 ? 4 : ns;
+    int cps = (96 * 1024) / (spass * 128);
+    cps = cps < nc ? cps : (nc > 0 ? nc : 1);
+    const size_t shm = sizeof(float) * (size_t)spass * cps * 32;
+    const bool one = cps >= nc;
+#define GF_GO(LPR, SG)                                                                                      \
+    do {                                                                                                    \
+        const int ntile = (N + 256 / LPR - 1) / (256 / LPR);                                                \
+        const int grid = one && ntile > 2 * n_cu ? 2 * n_cu : ntile;                                       \
+        hipLaunchKernelGGL((k_gemv_f16m<LPR, SG>), dim3(grid), dim3(256), shm, st, W, bias, x, y, N, K, ns, \
+                           ldy, mode, gelu_tab, cps);                                                      \
+    } while (0)
+#define GF_SG(LPR)                      \
+    do {                                \
+        switch (spass) {                \
+        case 1: GF_GO(LPR, 1); break;   \
+        case 2: GF_GO(LPR, 2); break;   \
+        case 4: GF_GO(LPR, 4); break;   \
+        case 8: GF_GO(LPR, 8); break;   \
+        case 10: GF_GO(LPR, 10); break; \
+        case 12: GF_GO(LPR, 12); break; \
+        default: GF_GO(LPR, 16); break; \
+        }                               \
+    } while (0)
+    if (N <= 2048) GF_SG(32);
+    else if (N <= 8192) GF_SG(16);
+    else GF_SG(8);
+#undef GF_SG
+#undef GF_GO
 }
 
 // Greedy bookkeeping after a sampling step: record the sampled tokens, advance

@@ -51,11 +51,47 @@ __device__ __forceinline__ void fw_split2(float v, uint16_t &hi, uint16_t &lo) {
     lo = __builtin_bit_cast(uint16_t, (_Float16)r);
 }
 
+__global__ void __launch_bounds__(256) k_split_f16(const float4 *x, size_t n4, uint2 *hi, uint2 *lo) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        const float4 v = x[i];
+        uint16_t h[4], l[4];
+        fw_split2(v.x, h[0], l[0]);
+        fw_split2(v.y, h[1], l[1]);
+        fw_split2(v.z, h[2], l[2]);
+        fw_split2(v.w, h[3], l[3]);
+        hi[i] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+        lo[i] = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+    }
+}
+
+// n must be a multiple of 4 (rows of d, d % 128 == 0)
+void fw_launch_split_f16(hipStream_t st, const float *x, size_t n, uint16_t *hi, uint16_t *lo) {
+    const size_t n4 = n / 4;
+    size_t g = (n4 + 255) / 256;
+    g = g < 8192 ? g : 8192;
+    hipLaunchKernelGGL(k_split_f16, dim3((unsigned)g), dim3(256), 0, st, (const float4 *)x, n4, (uint2 *)hi,
+                       (uint2 *)lo);
+}
+
 // Epilogue for the 4 consecutive rows row0..row0+3 of one column.
 template <int KIND, int EPI>
 __device__ __forceinline__ void gemm_store4(const FwGemm &g, int row0, int col, const float (&a)[4]) {
     if (col >= g.N) return;
-    if constexpr (EPI == FW_EPI_QKV) {
+    if constexpr (EPI == FW_EPI_XKV) {
+        const int d = g.ldc, l = col / (2 * d), r = col - l * 2 * d, kv = r >= d ? 1 : 0, c = r - kv * d;
+        const int h = c >> 6, dd = c & 63;
+        const float bias = g.bias ? g.bias[col] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int row = row0 + e;
+            if (row >= g.M) continue;
+            const int s = row / g.T, t = row - s * g.T;
+            const size_t lh = ((size_t)s * g.L + l) * g.H + h;
+            if (kv == 0) g.o16[0][(lh * g.T + t) * 64 + dd] = fw_f2h(a[e] * g.scale);
+            else g.o16[1][(lh * 64 + dd) * g.T + t] = fw_f2h(a[e] + bias);
+        }
+        return;
+    } else if constexpr (EPI == FW_EPI_QKV) {
         // head-major split outputs: Q, K as [B, H, T, 64]; V as [B, H, 64, Tp]
         const int d = g.ldc, which = col / d, cc = col - which * d, h = cc >> 6, dd = cc & 63;
         float bias = g.bias ? g.bias[col] : 0.0f;
@@ -159,7 +195,7 @@ __device__ __forceinline__ void gemm_epilogue(const FwGemm &g, accT (&acc)[BM / 
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    if constexpr (EPI == FW_EPI_QKV || EPI == FW_EPI_CONV2) {
+    if constexpr (EPI == FW_EPI_QKV || EPI == FW_EPI_CONV2 || EPI == FW_EPI_XKV) {
         // Heavy epilogues: written once, in a runtime loop over this wave's
         // tiles, reading each tile back from a wave-private LDS slab (a fully
         // unrolled copy of such an epilogue per tile is too large to unroll,
@@ -1056,6 +1092,7 @@ bool fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g0) {
         case FW_EPI_GELU_SPLIT: launch_tiles<FW_KIND_F16S, FW_EPI_GELU_SPLIT>(st, g, tile); return true;
         case FW_EPI_CONV2: launch_tiles<FW_KIND_F16S, FW_EPI_CONV2>(st, g, tile); return true;
         case FW_EPI_QKV: launch_tiles<FW_KIND_F16S, FW_EPI_QKV>(st, g, tile); return true;
+        case FW_EPI_XKV: launch_tiles<FW_KIND_F16S, FW_EPI_XKV>(st, g, tile); return true;
         default: return false;
         }
     }

@@ -20,6 +20,12 @@
 #define FW_EPI_F16IDX 7
 #define FW_GIDX_LIM 9.98f
 #define FW_GIDX_SENT 0xffffu
+// f16-pair only: the decoder's cross K/V of every layer from one GEMM
+// (DecoderState::new, decoder.rs:1040-1222).  Column col = (l * 2 + kv) * d + c
+// (d = ldc, head h = c / 64, dd = c % 64), row = s * T + t: K (kv 0) goes to
+// o16[0] at [s, l, h, t, dd] as f16(v * scale), V (kv 1) to o16[1] at
+// [s, l, h, dd, t] as f16(v + bias[col]).
+#define FW_EPI_XKV 8
 
 // Position of key t in a V^T row: bits 2 and 3 swapped, so the keys
 // {16g + 4h + 0..3, 16g + 8 + 4h + 0..3} one attention MFMA lane multiplies
@@ -43,7 +49,9 @@ struct FwGemm {
     const float *pos;
     const float *gelu_tab;
     int T, H, Tp;
-    int map; // tile order (set by fw_launch_gemm)
+    int L;       // FW_EPI_XKV: decoder layers
+    float scale; // FW_EPI_XKV: the key scale
+    int map;     // tile order (set by fw_launch_gemm)
 };
 
 // false when the operand kind / epilogue pair has no kernel (nothing launched)
@@ -66,6 +74,8 @@ void fw_launch_im2col(hipStream_t st, const float *x, int B, int Tin, int Cin, i
 void fw_launch_mel_window(hipStream_t st, const float *mel, int n_mel, long long mel_frames, const long long *offs,
                           int n_frames, float *out, int B);
 void fw_launch_fill_u16(hipStream_t st, uint16_t *p, size_t n, uint16_t v);
+// f32 -> f16 pair (hi = f16(x), lo = f16(x - hi)): the A operand of an f16-pair GEMM
+void fw_launch_split_f16(hipStream_t st, const float *x, size_t n, uint16_t *hi, uint16_t *lo);
 void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                          const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
                          int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol);

@@ -30,6 +30,7 @@ struct fwhip_ctx {
     std::atomic<int> cancel{0};
     bool timing = false;
     std::vector<fw_event_pair> pending;
+    std::vector<hipEvent_t> ev_pool; // events of drained timings, reused
     std::map<int, fw_kstat> stats;
     // device: the GELU table [65536] f32, followed in the same allocation by
     // the same values as f16 (fw_gelu_tab16)

@@ -10,6 +10,16 @@
 // decoder (dec_kernels.hip)
 void fw_launch_gemv_f16(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *y, int N,
                         int K, int ns, int ldy, int mode, const float *gelu_tab);
+// f16 GEMV on weights in fragment order (repacked once by
+// fw_launch_pack_gemv_f16 when fw_gemv_f16_frag_ok(N, K)); same results
+int fw_gemv_f16_lpr(int N);
+bool fw_gemv_f16_frag_ok(int N, int K);
+void fw_launch_pack_gemv_f16(hipStream_t st, const uint16_t *W, uint16_t *Wf, int N, int K);
+// With lnw / lnb (K <= 1280) the rows x are first put through LayerNorm
+// (k_ln_quant's arithmetic), so the GEMV consumes LN(x).
+void fw_launch_gemv_f16f(hipStream_t st, const uint16_t *Wf, const float *bias, const float *x, float *y, int N,
+                         int K, int ns, int ldy, int mode, const float *gelu_tab, const float *lnw = nullptr,
+                         const float *lnb = nullptr);
 void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,
                               float *att, int d, int T, int H, int L, int layer, int ns, float scale);
 void fw_launch_gemm_strict(hipStream_t st, const float *A, const uint16_t *B, int m, int n, int k, int epi,

@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "fw_enc.h"
 #include "fw_internal.h"
 #include "fw_kernels.h"
 
@@ -88,6 +89,7 @@ extern "C" void fwhip_destroy(fwhip_ctx *c) {
         hipEventDestroy(e.a);
         hipEventDestroy(e.b);
     }
+    for (hipEvent_t e : c->ev_pool) hipEventDestroy(e);
     if (c->gelu_tab) hipFree(c->gelu_tab);
     if (c->mel_tab) hipFree(c->mel_tab);
     if (c->mel_scratch) hipFree(c->mel_scratch);
@@ -142,8 +144,15 @@ void fw_timed_begin(fwhip_ctx *c, int cls, double units, fw_event_pair *ev) {
     if (!ev->active) return;
     ev->cls = cls;
     ev->units = units;
-    hipEventCreate(&ev->a);
-    hipEventCreate(&ev->b);
+    hipEvent_t *e[2] = {&ev->a, &ev->b};
+    for (hipEvent_t *p : e) {
+        if (!c->ev_pool.empty()) {
+            *p = c->ev_pool.back();
+            c->ev_pool.pop_back();
+        } else {
+            hipEventCreate(p);
+        }
+    }
     hipEventRecord(ev->a, c->stream);
 }
 void fw_timed_end(fwhip_ctx *c, fw_event_pair *ev) {
@@ -161,8 +170,8 @@ static void fw_drain_events(fwhip_ctx *c) {
         s.launches += 1;
         s.ms += ms;
         s.units += e.units;
-        hipEventDestroy(e.a);
-        hipEventDestroy(e.b);
+        c->ev_pool.push_back(e.a);
+        c->ev_pool.push_back(e.b);
     }
     c->pending.clear();
 }
@@ -224,10 +233,16 @@ struct fwhip_decoder {
     int arm;
     fwhip_hparams hp;
     int d, H, L, V, nctx, dff;
-    const uint16_t *emb16 = nullptr;
+    const uint16_t *emb16 = nullptr;  // natural order (the token embedding gather)
+    const uint16_t *emb16f = nullptr; // f16 arm: the tied logits head in GEMV fragment order
     const int8_t *emb8 = nullptr;
     const float *emb8s = nullptr;
     const float *pos_emb = nullptr, *ln_w = nullptr, *ln_b = nullptr;
+    // cross K and V weights of every layer, [L][K rows; V rows][d] f16, and the
+    // matching bias [L][0 | cv_b] (one f16-pair GEMM makes every layer's cross K/V)
+    const uint16_t *ckv16 = nullptr;
+    const float *ckv_b = nullptr;
+    int exact = 0; // 1: strict sequential-k cross K/V precompute
     std::vector<DecLayerDev> layers;
     std::vector<void *> owned;
 };
@@ -246,6 +261,7 @@ struct fwhip_dstate {
     int32_t *tok, *hist, *rows;
     int *pos, *initial, *stepc;
     float *pmax;            // [S, H] per-head max |attention output|
+    uint16_t *ench, *encl;  // [S * T, d] f16 pair of the encoder states (fast cross K/V)
     int hist_cap;
     // captured sampling step (forward of st->tok + argmax + bookkeeping)
     hipGraphExec_t graph = nullptr;
@@ -301,6 +317,45 @@ static bool dev_quant_blocked(fwhip_ctx *c, std::vector<void *> &owned, const ui
     *q = qq;
     *s = ss;
     return true;
+}
+
+// An f16 GEMV weight [N, K] in the GEMV's fragment order when the kernel takes
+// that shape (fw_gemv_f16_frag_ok), else natural order: fw_gemv16 launches the
+// matching kernel.  `nat` (device, natural order) is freed when repacked unless
+// keep_nat.
+static const uint16_t *frag16(fwhip_ctx *c, std::vector<void *> &owned, const uint16_t *nat, int N, int K,
+                              bool keep_nat = false) {
+    if (!nat || !fw_gemv_f16_frag_ok(N, K)) return nat;
+    uint16_t *f = (uint16_t *)fw_dalloc(owned, sizeof(uint16_t) * (size_t)N * K);
+    if (!f) return nullptr;
+    fw_launch_pack_gemv_f16(c->stream, nat, f, N, K);
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return nullptr;
+    if (!keep_nat) {
+        for (auto it = owned.begin(); it != owned.end(); ++it)
+            if (*it == (const void *)nat) {
+                owned.erase(it);
+                break;
+            }
+        hipFree((void *)nat);
+    }
+    return f;
+}
+static void fw_gemv16(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *y, int N, int K,
+                      int ns, int ldy, int mode, const float *gelu_tab) {
+    if (fw_gemv_f16_frag_ok(N, K)) fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab);
+    else fw_launch_gemv_f16(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab);
+}
+// y = W LayerNorm(x) (+ bias): the LayerNorm inside the GEMV where its kernel
+// stages whole rows (fragment order, K <= 1280), else a LayerNorm pass into h.
+static void fw_gemv16_ln(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *h,
+                         const float *lnw, const float *lnb, float *y, int N, int K, int ns, int ldy, int mode,
+                         const float *gelu_tab) {
+    if (fw_gemv_f16_frag_ok(N, K) && K <= 1280) {
+        fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb);
+    } else {
+        fw_launch_ln_quant(st, x, h, lnw, lnb, K, ns, nullptr, nullptr);
+        fw_gemv16(st, W, bias, h, y, N, K, ns, ldy, mode, gelu_tab);
+    }
 }
 
 static bool hp_decoder_ok(const fwhip_hparams &hp, std::string &why) {
@@ -361,7 +416,22 @@ extern "C" fwhip_status fwhip_decoder_load(fwhip_ctx *c, const fwhip_decoder_wei
     dd->pos_emb = up32(w->pos_emb, (size_t)dd->nctx * d);
     dd->ln_w = up32(w->ln_w, d);
     dd->ln_b = up32(w->ln_b, d);
+    {
+        std::vector<uint16_t> ckv((size_t)dd->L * 2 * d * d);
+        std::vector<float> ckvb((size_t)dd->L * 2 * d, 0.0f);
+        for (int li = 0; li < dd->L; li++) {
+            memcpy(ckv.data() + (size_t)li * 2 * d * d, w->layers[li].ck_w, sizeof(uint16_t) * d * d);
+            memcpy(ckv.data() + ((size_t)li * 2 + 1) * d * d, w->layers[li].cv_w, sizeof(uint16_t) * d * d);
+            memcpy(ckvb.data() + ((size_t)li * 2 + 1) * d, w->layers[li].cv_b, sizeof(float) * d);
+        }
+        dd->ckv16 = up16(ckv.data(), ckv.size());
+        dd->ckv_b = up32(ckvb.data(), ckvb.size());
+    }
     if (ok && arm == FWHIP_DEC_INT8) ok = dev_quant_rows(c, own, w->tok_emb, dd->V, d, &dd->emb8, &dd->emb8s, true);
+    if (ok && arm == FWHIP_DEC_F16) {
+        dd->emb16f = frag16(c, own, dd->emb16, dd->V, d, true);
+        ok = dd->emb16f != nullptr;
+    }
     for (int li = 0; ok && li < dd->L; li++) {
         const fwhip_dec_layer &s = w->layers[li];
         DecLayerDev l;
@@ -386,9 +456,9 @@ extern "C" fwhip_status fwhip_decoder_load(fwhip_ctx *c, const fwhip_decoder_wei
         l.fc1_b = up32(s.fc1_b, dff);
         l.fc2_b = up32(s.fc2_b, d);
         l.cv_b = up32(s.cv_b, d);
-        l.ck16w = up16(s.ck_w, (size_t)d * d);
-        l.cv16w = up16(s.cv_w, (size_t)d * d);
-        l.fc2_16 = up16(s.fc2_w, (size_t)d * dff); // prefill arm of mlp_2 in both arms
+        l.ck16w = dd->ckv16 ? dd->ckv16 + (size_t)li * 2 * d * d : nullptr;
+        l.cv16w = dd->ckv16 ? dd->ckv16 + ((size_t)li * 2 + 1) * d * d : nullptr;
+        l.fc2_16 = frag16(c, own, up16(s.fc2_w, (size_t)d * dff), d, dff); // prefill arm of mlp_2 in both arms
         if (arm == FWHIP_DEC_INT8) {
             ok = ok && dev_quant_rows(c, own, qkv.data(), 3 * d, d, &l.qkv8, &l.qkv8s);
             ok = ok && dev_quant_rows(c, own, s.o_w, d, d, &l.o8, &l.o8s, true);
@@ -397,11 +467,12 @@ extern "C" fwhip_status fwhip_decoder_load(fwhip_ctx *c, const fwhip_decoder_wei
             ok = ok && dev_quant_rows(c, own, s.fc1_w, dff, d, &l.fc1_8, &l.fc1_8s, true);
             ok = ok && dev_quant_blocked(c, own, s.fc2_w, d, dff, &l.fc2_b8, &l.fc2_b8s);
         } else {
-            l.qkv16 = up16(qkv.data(), (size_t)3 * d * d);
-            l.o16 = up16(s.o_w, (size_t)d * d);
-            l.cq16 = up16(s.cq_w, (size_t)d * d);
-            l.co16 = up16(s.co_w, (size_t)d * d);
-            l.fc1_16 = up16(s.fc1_w, (size_t)dff * d);
+            l.qkv16 = frag16(c, own, up16(qkv.data(), (size_t)3 * d * d), 3 * d, d);
+            l.o16 = frag16(c, own, up16(s.o_w, (size_t)d * d), d, d);
+            l.cq16 = frag16(c, own, up16(s.cq_w, (size_t)d * d), d, d);
+            l.co16 = frag16(c, own, up16(s.co_w, (size_t)d * d), d, d);
+            l.fc1_16 = frag16(c, own, up16(s.fc1_w, (size_t)dff * d), dff, d);
+            ok = ok && l.qkv16 && l.o16 && l.cq16 && l.co16 && l.fc1_16;
         }
         dd->layers.push_back(l);
     }
@@ -473,8 +544,10 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     st->initial = st->pos + 1;
     st->stepc = st->pos + 2;
     st->pmax = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * dd->H);
+    st->ench = (uint16_t *)fw_dalloc(own, sizeof(uint16_t) * (size_t)S * T * d);
+    st->encl = (uint16_t *)fw_dalloc(own, sizeof(uint16_t) * (size_t)S * T * d);
     ok = ok && st->x && st->h && st->qkv && st->att && st->y && st->ff && st->logits && st->xq && st->xs &&
-         st->keys && st->tok && st->rows && st->hist && st->pos && st->pmax;
+         st->keys && st->tok && st->rows && st->hist && st->pos && st->pmax && st->ench && st->encl;
     // padding rows of the quantized activations must read as zeros
     ok = ok && hipMemset(st->xq, 0, (size_t)st->Sp * d) == hipSuccess && hipMemset(st->pos, 0, sizeof(int) * 4) == hipSuccess;
     if (!ok) {
@@ -524,9 +597,17 @@ extern "C" fwhip_status fwhip_dstate_read(const fwhip_dstate *st, int32_t what, 
     return FWHIP_OK;
 }
 
-// DecoderState::new (decoder.rs:1040-1285) for every stream: strict f32
-// projection GEMMs writing per-head f16 K (scaled) and transposed f16 V, then
-// per-row int8 copies for the default arm.
+extern "C" fwhip_status fwhip_decoder_set_exact(fwhip_decoder *dd, int32_t exact) {
+    if (!dd) return fw_fail(FWHIP_ERR_INVALID, "NULL decoder");
+    dd->exact = exact != 0;
+    return FWHIP_OK;
+}
+
+// DecoderState::new (decoder.rs:1040-1285) for every stream: the cross K/V
+// projections written as per-head f16 K (scaled) and transposed f16 V, then
+// per-row int8 copies for the default arm.  Exact mode: the strict
+// sequential-k f32 GEMM, layer by layer; fast mode: every layer's K and V in
+// one f16-pair MFMA GEMM over the states split into f16 (hi, lo) pairs.
 extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *enc_dev) {
     if (!st || !enc_dev) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_set_cross: NULL argument");
     fwhip_decoder *dd = st->dec;
@@ -535,14 +616,41 @@ extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *en
     int d = dd->d, H = dd->H, L = dd->L, T = st->T, S = st->S;
     float kscale = powf(64.0f, -0.25f);
     fw_event_pair ev;
-    for (int li = 0; li < L; li++) {
-        const DecLayerDev &l = dd->layers[li];
-        fw_timed_begin(c, FWHIP_K_DEC_GEMV, 2.0 * S * T * (double)d * d, &ev);
-        fw_launch_gemm_strict(c->stream, enc_dev, l.ck16w, S * T, d, d, 1, nullptr, nullptr, kscale, st->ck16, T,
-                              H, L, li);
+    if (dd->exact) {
+        for (int li = 0; li < L; li++) {
+            const DecLayerDev &l = dd->layers[li];
+            fw_timed_begin(c, FWHIP_K_DEC_GEMV, 2.0 * S * T * (double)d * d, &ev);
+            fw_launch_gemm_strict(c->stream, enc_dev, l.ck16w, S * T, d, d, 1, nullptr, nullptr, kscale, st->ck16,
+                                  T, H, L, li);
+            fw_timed_end(c, &ev);
+            fw_launch_gemm_strict(c->stream, enc_dev, l.cv16w, S * T, d, d, 2, nullptr, l.cv_b, 1.0f, st->cvt16, T,
+                                  H, L, li);
+        }
+    } else {
+        fw_launch_split_f16(c->stream, enc_dev, (size_t)S * T * d, st->ench, st->encl);
+        FwGemm g;
+        memset(&g, 0, sizeof g);
+        g.A = st->ench;
+        g.A2 = st->encl;
+        g.B = dd->ckv16;
+        g.M = S * T;
+        g.N = L * 2 * d;
+        g.K = d;
+        g.lda = d;
+        g.ldb = d;
+        g.bias = dd->ckv_b;
+        g.epi = FW_EPI_XKV;
+        g.ldc = d;
+        g.o16[0] = st->ck16;
+        g.o16[1] = st->cvt16;
+        g.T = T;
+        g.H = H;
+        g.L = L;
+        g.scale = kscale;
+        fw_timed_begin(c, FWHIP_K_DEC_CROSS, 2.0 * 2.0 * S * T * (double)L * d * d, &ev);
+        const bool ok = fw_launch_gemm(c->stream, FW_KIND_F16S, g);
         fw_timed_end(c, &ev);
-        fw_launch_gemm_strict(c->stream, enc_dev, l.cv16w, S * T, d, d, 2, nullptr, l.cv_b, 1.0f, st->cvt16, T,
-                              H, L, li);
+        if (!ok) return fw_fail(FWHIP_ERR_GENERIC, "cross K/V GEMM has no kernel");
     }
     if (dd->arm == FWHIP_DEC_INT8) {
         fw_launch_quant_f16_rows(c->stream, st->ck16, st->ck8, st->ck8s, S * L * H * T, 64);
@@ -620,21 +728,23 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             // which reads natural order
             fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs);
             gemv_i8_all(st, s, l.fc1_8, l.fc1_8s, l.fc1_b, st->ff, dff, d, dff, prefill ? 2 : 4, nullptr);
-            if (prefill) fw_launch_gemv_f16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
+            if (prefill) fw_gemv16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
             else if (!gemv_blk_all(st, s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, d))
                 return fw_fail(FWHIP_ERR_INVALID, "block GEMV: unsupported mlp width");
         } else {
-            if (li > 0) fw_launch_ln_quant(s, st->x, st->h, l.attn_ln_w, l.attn_ln_b, d, S, nullptr, nullptr);
-            fw_launch_gemv_f16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
+            // (layer 0's attention LayerNorm ran with the embedding, into h)
+            if (li > 0)
+                fw_gemv16_ln(s, l.qkv16, l.qkv_b, st->x, st->h, l.attn_ln_w, l.attn_ln_b, st->qkv, 3 * d, d, S, 3 * d,
+                             0, gt);
+            else
+                fw_gemv16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
             fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
-            fw_launch_gemv_f16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
-            fw_launch_ln_quant(s, st->x, st->h, l.cross_ln_w, l.cross_ln_b, d, S, nullptr, nullptr);
-            fw_launch_gemv_f16(s, l.cq16, l.cq_b, st->h, st->y, d, d, S, d, 0, gt);
+            fw_gemv16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
+            fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0, gt);
             fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
-            fw_launch_gemv_f16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
-            fw_launch_ln_quant(s, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, d, S, nullptr, nullptr);
-            fw_launch_gemv_f16(s, l.fc1_16, l.fc1_b, st->h, st->ff, dff, d, S, dff, 2, gt);
-            fw_launch_gemv_f16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
+            fw_gemv16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
+            fw_gemv16_ln(s, l.fc1_16, l.fc1_b, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, st->ff, dff, d, S, dff, 2, gt);
+            fw_gemv16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
         }
     }
     if (want_logits) {
@@ -646,9 +756,9 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             gemv_i8_all(st, s, dd->emb8, dd->emb8s, nullptr, st->logits, dd->V, d, dd->V, 3, filt);
             if (timed) fw_timed_end(c, &ev);
         } else {
-            fw_launch_ln_quant(s, st->x, st->h, dd->ln_w, dd->ln_b, d, S, nullptr, nullptr);
             if (timed) fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d * 2.0, &ev);
-            fw_launch_gemv_f16(s, dd->emb16, nullptr, st->h, st->logits, dd->V, d, S, dd->V, 0, gt);
+            fw_gemv16_ln(s, dd->emb16f, nullptr, st->x, st->h, dd->ln_w, dd->ln_b, st->logits, dd->V, d, S, dd->V, 0,
+                         gt);
             if (timed) fw_timed_end(c, &ev);
             fw_launch_logits_keys(s, st->logits, dd->V, S, filt, st->initial, st->keys);
         }
@@ -742,9 +852,17 @@ static fwhip_status greedy_step(fwhip_dstate *st, const fwhip_filter *filt, bool
 // replays for every step of this state).  Returns false when capture is
 // unavailable; the loop then launches the same kernels directly.
 static bool capture_step_impl(fwhip_dstate *st, const fwhip_filter *filt);
+// Graph capture is skipped under a profiler that intercepts the HIP runtime
+// (rocprofv3 preloads librocprofiler-sdk-tool): a kernel trace of replayed
+// graphs has ended in a SIGSEGV inside the runtime's graph launch path, so
+// profiled runs launch the same kernels directly.
+static bool profiler_preloaded() {
+    const char *p = getenv("LD_PRELOAD");
+    return p && strstr(p, "rocprofiler-sdk") != nullptr;
+}
 static bool capture_step(fwhip_dstate *st, const fwhip_filter *filt) {
     static int disabled = -1, debug = -1;
-    if (disabled < 0) disabled = getenv("FWHIP_NO_GRAPH") != nullptr;
+    if (disabled < 0) disabled = getenv("FWHIP_NO_GRAPH") != nullptr || profiler_preloaded();
     if (debug < 0) debug = getenv("FWHIP_DEBUG") != nullptr;
     if (disabled) return false;
     bool ok = capture_step_impl(st, filt);
@@ -775,6 +893,27 @@ static bool capture_step_impl(fwhip_dstate *st, const fwhip_filter *filt) {
     st->graph = ge;
     st->graph_filter = *filt;
     return true;
+}
+
+// Algorithmic HBM bytes of one sampled decoder step of every stream at cache
+// length tk: the weights once (int8 rows + f32 row scales, mlp_2 as 32-blocks
+// with an f32 scale each, or f16), and per stream its cross K/V (int8 + scales,
+// or f16) and self-attention cache (K and V rows [0, tk) read, one row each
+// written, f16).
+static double dec_step_bytes(const fwhip_dstate *st, int tk) {
+    const fwhip_decoder *dd = st->dec;
+    const double d = dd->d, L = dd->L, V = dd->V, T = st->T, S = st->S, H = dd->H;
+    double w, cross;
+    if (dd->arm == FWHIP_DEC_INT8) {
+        w = L * (3 * d * d + 3 * d * d + 4 * d * d + 4 * (3 * d + d + d + d + 4 * d) + 4 * d * d * (1.0 + 4.0 / 32.0)) +
+            V * d + 4 * V;
+        cross = L * (2 * T * d + 4 * H * T + 4 * d);
+    } else {
+        w = 2.0 * (L * 12 * d * d + V * d);
+        cross = L * 2 * T * d * 2;
+    }
+    const double kv = L * 2 * ((double)tk + 1) * d * 2;
+    return w + S * (cross + kv);
 }
 
 // Greedy no-timestamps loop (decode.rs:3429-3566): prefill the prompt, then
@@ -818,11 +957,14 @@ extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *pro
             st->len += n_prompt + steps - 1;
             return r;
         }
+        fw_event_pair ev;
+        fw_timed_begin(c, FWHIP_K_DEC_STEP, dec_step_bytes(st, st->len + n_prompt + i), &ev);
         if (use_graph) HIP_TRY(hipGraphLaunch(st->graph, c->stream));
         else {
             r = greedy_step(st, filter, false);
             if (r != FWHIP_OK) return r;
         }
+        fw_timed_end(c, &ev);
         steps = i + 1;
         if (steps % poll == 0 && steps < n_max) {
             HIP_TRY(hipMemcpy2DAsync(hist.data(), sizeof(int32_t) * n_max, st->hist, sizeof(int32_t) * st->hist_cap,

@@ -46,6 +46,7 @@ SIGNATURES = {
     "fwhip_encoder_gemm_i8_fused": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, C.c_int32, _vp, _vp]),
     "fwhip_decoder_load": (C.c_int32, [_vp, C.POINTER(abi.DecoderWeights), C.c_int32, C.POINTER(_vp)]),
     "fwhip_decoder_free": (None, [_vp]),
+    "fwhip_decoder_set_exact": (C.c_int32, [_vp, C.c_int32]),
     "fwhip_dstate_new": (C.c_int32, [_vp, C.c_int32, C.c_int32, C.POINTER(_vp)]),
     "fwhip_dstate_free": (None, [_vp]),
     "fwhip_dstate_set_cross": (C.c_int32, [_vp, _vp]),
@@ -231,6 +232,11 @@ class Decoder:
         check(lib().fwhip_decoder_load(ctx.h, C.byref(self._desc), arm, C.byref(h)))
         self.h = h
         self.arm = arm
+
+    def set_exact(self, exact: bool):
+        """Strict sequential-k cross K/V precompute (bit-exact logits) or the fast
+        f16-pair MFMA one (the default)."""
+        check(lib().fwhip_decoder_set_exact(self.h, 1 if exact else 0))
 
     def state(self, n_streams: int, enc_frames: int) -> "DecoderState":
         return DecoderState(self, n_streams, enc_frames)

@@ -171,6 +171,8 @@ fwhip_status fwhip_request_cancel(fwhip_ctx *ctx);
 #define FWHIP_K_ENC_ATTN 3
 #define FWHIP_K_DEC_GEMV 4
 #define FWHIP_K_DEC_LOGITS 5
+#define FWHIP_K_DEC_CROSS 6  /* cross K/V precompute (fast mode) */
+#define FWHIP_K_DEC_STEP 7   /* one sampled decoder step of the greedy loop */
 fwhip_status fwhip_kernel_timing(fwhip_ctx *ctx, int32_t enable);
 fwhip_status fwhip_kernel_stats(fwhip_ctx *ctx, int32_t kclass, int64_t *launches,
                                 double *total_ms, double *work_units);
@@ -242,6 +244,16 @@ fwhip_status fwhip_encoder_gemm_i8_fused(fwhip_encoder *enc, int32_t layer, int3
 fwhip_status fwhip_decoder_load(fwhip_ctx *ctx, const fwhip_decoder_weights *w, int32_t arm,
                                 fwhip_decoder **out);
 void fwhip_decoder_free(fwhip_decoder *dec);
+
+/* Exact mode (exact = 1): the cross K/V precompute of fwhip_dstate_set_cross
+ * (DecoderState::new, decoder.rs:1049-1069) is the strict-parity sequential-k
+ * f32 GEMM (FT_SGEMM_STRICT_PARITY=1, nn.rs:587-604), so logits are
+ * bit-identical to the reference's strict mode.  Fast mode (exact = 0, the
+ * default) makes every layer's cross K and V in one f16-pair MFMA GEMM (each
+ * K/V value within ~1e-7 relative before its f16 rounding; the reference's
+ * default ft sgemm has no pinned summation order either).  The token step is
+ * the same in both modes. */
+fwhip_status fwhip_decoder_set_exact(fwhip_decoder *dec, int32_t exact);
 
 /* A cohort of n_streams independent DecoderStates (decoder.rs:980-1027), each
  * with its own f16 self-attention KV cache (KvCache, nn.rs:5138) of

@@ -2,7 +2,8 @@
 the reference's decoder, src/native_engine/decoder.rs + nn.rs).
 
 Both arms are built to reproduce the reference's per-output arithmetic order,
-so logits are compared BIT-EXACTLY (the only documented deviation is the f64
+so logits are compared BIT-EXACTLY (exact mode: the strict cross K/V
+precompute) (the only documented deviation is the f64
 LayerNorm reduction order, which changes an f32 output only when a sum lands
 within 2^-53 relative of a rounding boundary — none is expected at these
 sizes; a failure here would print the differing count)."""
@@ -22,6 +23,7 @@ def _run_steps(ctx, name, arm, n_streams, n_steps, seed=0, T=None):
     T = T or cfg.n_audio_ctx
     enc = enc_states(seed + 7, n_streams, T, cfg.n_text_state)
     dec = native.Decoder(ctx, m, arm)
+    dec.set_exact(True)
     st = dec.state(n_streams, T)
     st.set_cross(ctx.array(enc))
     logits_dev = ctx.empty((n_streams, cfg.n_vocab), np.float32)
@@ -85,6 +87,7 @@ def test_greedy_tokens_match(ctx, arm):
     S, T = 3, cfg.n_audio_ctx
     enc = enc_states(11, S, T, cfg.n_text_state)
     dec = native.Decoder(ctx, m, arm)
+    dec.set_exact(True)
     st = dec.state(S, T)
     st.set_cross(ctx.array(enc))
     tk = m.tokens

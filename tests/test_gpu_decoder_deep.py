@@ -7,7 +7,8 @@ Each stream's cache is filled by prompt prefills through fwhip_decoder_step
 (tq > 1) and single steps are checked at cache depths 65, 129, 224 and 447, so
 the self-attention kernels run their multi-chunk key loops (more than 64 and
 128 keys) and the sequential softmax sums at every length class.  Streams 0 and
-S-1 are compared BIT-EXACTLY with the oracle; every stream of the cohort is
+S-1 are compared BIT-EXACTLY with the oracle (exact mode: the strict cross
+K/V precompute); every stream of the cohort is
 compared bit for bit with the same stream decoded alone (the cohort invariant
 forward_step_batch_matches_independent_states, decoder.rs:2680, including the
 continuation of each stream's private cache)."""
@@ -63,6 +64,7 @@ def test_turbo_deep_cache_bitexact(ctx, arm, S):
     enc = enc_states(21, S, cfg.n_audio_ctx, cfg.n_text_state)
     toks = _tokens(5 + S, S, 447, cfg.n_vocab)
     dec = native.Decoder(ctx, m, arm)
+    dec.set_exact(True)
     got = _gpu_run(ctx, dec, enc, toks)
     odec = O.Decoder(m, arm)
     for s in sorted({0, S - 1}):
@@ -89,6 +91,7 @@ def test_turbo_greedy_16_streams_match_oracle(ctx, arm):
     S = 16
     enc = enc_states(33, S, cfg.n_audio_ctx, cfg.n_text_state)
     dec = native.Decoder(ctx, m, arm)
+    dec.set_exact(True)
     st = dec.state(S, cfg.n_audio_ctx)
     st.set_cross(ctx.array(enc))
     got = st.greedy(tk.sot_sequence(), 32, tk.filter())
@@ -109,6 +112,7 @@ def test_cohort_continuation_after_batched_step(ctx):
     S = 3
     enc = enc_states(41, S, cfg.n_audio_ctx, cfg.n_text_state)
     dec = native.Decoder(ctx, m, abi.DEC_INT8)
+    dec.set_exact(True)
     coh = dec.state(S, cfg.n_audio_ctx)
     coh.set_cross(ctx.array(enc))
     lg = ctx.empty((S, cfg.n_vocab), np.float32)

@@ -126,6 +126,7 @@ def test_encoder_int8_end_to_end_tokens(ctx, cfg):
     m = synth.Model(cfg, seed=2, encoder=False)
     tk = m.tokens
     dec = native.Decoder(ctx, m, abi.DEC_INT8)
+    dec.set_exact(True)
     st = dec.state(2, cfg.n_audio_ctx)
     st.set_cross(ctx.array(got))
     toks = st.greedy(tk.sot_sequence(), 24, tk.filter())
