@@ -319,16 +319,24 @@ static bool dev_quant_blocked(fwhip_ctx *c, std::vector<void *> &owned, const ui
     return true;
 }
 
-// An f16 GEMV weight [N, K] in the GEMV's fragment order when the kernel takes
-// that shape (fw_gemv_f16_frag_ok), else natural order: fw_gemv16 launches the
-// matching kernel.  `nat` (device, natural order) is freed when repacked unless
-// keep_nat.
+// The f16 arm's logits head forms its argmax keys inside the GEMV when that
+// GEMV takes the shape (slot order, the final LayerNorm fused: d <= 1280).
+static bool f16_fused_keys(const fwhip_decoder *dd) {
+    return dd->arm == FWHIP_DEC_F16 && fw_gemv16_ok(dd->V, dd->d) && dd->d <= 1280;
+}
+
+// An f16 GEMV weight [N, K] repacked for the cohort GEMV: slot order when
+// fw_gemv16_ok(N, K) (dec_gemv16.hip), else the fragment order of
+// fw_gemv_f16_frag_ok, else natural order; fw_gemv16 launches the matching
+// kernel.  `nat` (device, natural order) is freed when repacked unless keep_nat.
 static const uint16_t *frag16(fwhip_ctx *c, std::vector<void *> &owned, const uint16_t *nat, int N, int K,
                               bool keep_nat = false) {
-    if (!nat || !fw_gemv_f16_frag_ok(N, K)) return nat;
+    const bool slot = fw_gemv16_ok(N, K);
+    if (!nat || (!slot && !fw_gemv_f16_frag_ok(N, K))) return nat;
     uint16_t *f = (uint16_t *)fw_dalloc(owned, sizeof(uint16_t) * (size_t)N * K);
     if (!f) return nullptr;
-    fw_launch_pack_gemv_f16(c->stream, nat, f, N, K);
+    if (slot) fw_launch_pack_gemv16(c->stream, nat, f, N, K);
+    else fw_launch_pack_gemv_f16(c->stream, nat, f, N, K);
     if (hipStreamSynchronize(c->stream) != hipSuccess) return nullptr;
     if (!keep_nat) {
         for (auto it = owned.begin(); it != owned.end(); ++it)
@@ -342,15 +350,18 @@ static const uint16_t *frag16(fwhip_ctx *c, std::vector<void *> &owned, const ui
 }
 static void fw_gemv16(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *y, int N, int K,
                       int ns, int ldy, int mode, const float *gelu_tab) {
-    if (fw_gemv_f16_frag_ok(N, K)) fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab);
+    if (fw_gemv16_ok(N, K)) fw_launch_gemv16(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab);
+    else if (fw_gemv_f16_frag_ok(N, K)) fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab);
     else fw_launch_gemv_f16(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab);
 }
 // y = W LayerNorm(x) (+ bias): the LayerNorm inside the GEMV where its kernel
-// stages whole rows (fragment order, K <= 1280), else a LayerNorm pass into h.
+// stages whole rows (K <= 1280), else a LayerNorm pass into h.
 static void fw_gemv16_ln(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *h,
                          const float *lnw, const float *lnb, float *y, int N, int K, int ns, int ldy, int mode,
                          const float *gelu_tab) {
-    if (fw_gemv_f16_frag_ok(N, K) && K <= 1280) {
+    if (fw_gemv16_ok(N, K) && K <= 1280) {
+        fw_launch_gemv16(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb);
+    } else if (fw_gemv_f16_frag_ok(N, K) && K <= 1280) {
         fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb);
     } else {
         fw_launch_ln_quant(st, x, h, lnw, lnb, K, ns, nullptr, nullptr);
@@ -534,7 +545,9 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     st->logits = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * dd->V);
     st->xq = (int8_t *)fw_dalloc(own, (size_t)st->Sp * d);
     st->xs = (float *)fw_dalloc(own, sizeof(float) * st->Sp);
-    st->nkeys = dd->arm == FWHIP_DEC_INT8 ? fw_gemv_i8m_blocks(dd->V) : fw_logits_keys_blocks(dd->V);
+    st->nkeys = dd->arm == FWHIP_DEC_INT8 ? fw_gemv_i8m_blocks(dd->V)
+                : f16_fused_keys(dd)         ? fw_gemv16_key_blocks(dd->V, d)
+                                             : fw_logits_keys_blocks(dd->V);
     st->keys = (unsigned long long *)fw_dalloc(own, sizeof(unsigned long long) * (size_t)S * st->nkeys);
     st->tok = (int32_t *)fw_dalloc(own, sizeof(int32_t) * S);
     st->rows = (int32_t *)fw_dalloc(own, sizeof(int32_t) * (size_t)S * nctx);
@@ -757,10 +770,17 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             if (timed) fw_timed_end(c, &ev);
         } else {
             if (timed) fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d * 2.0, &ev);
-            fw_gemv16_ln(s, dd->emb16f, nullptr, st->x, st->h, dd->ln_w, dd->ln_b, st->logits, dd->V, d, S, dd->V, 0,
-                         gt);
-            if (timed) fw_timed_end(c, &ev);
-            fw_launch_logits_keys(s, st->logits, dd->V, S, filt, st->initial, st->keys);
+            if (f16_fused_keys(dd)) {
+                // final LayerNorm, tied f16 logits head and per-tile argmax keys in one kernel
+                fw_launch_gemv16(s, dd->emb16f, nullptr, st->x, st->logits, dd->V, d, S, dd->V, 0, gt, dd->ln_w,
+                                 dd->ln_b, filt, st->initial, st->keys);
+                if (timed) fw_timed_end(c, &ev);
+            } else {
+                fw_gemv16_ln(s, dd->emb16f, nullptr, st->x, st->h, dd->ln_w, dd->ln_b, st->logits, dd->V, d, S, dd->V,
+                             0, gt);
+                if (timed) fw_timed_end(c, &ev);
+                fw_launch_logits_keys(s, st->logits, dd->V, S, filt, st->initial, st->keys);
+            }
         }
     }
     return FWHIP_OK;
