@@ -1019,6 +1019,233 @@ void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *c
 }
 
 // ---------------------------------------------------------------------------
+// The same cross attention on K and V^T stored in slot order
+// (fw_launch_pack_cross_f16): in a 64-wide group of a row, element
+// 32cc + 8k + l sits at l*8 + cc*4 + k, so lane l of an 8-lane row group reads
+// its four dot_f16c slots (k = 0..3, lane l) of two chunks as one 16-byte load
+// and a row group's load is one whole 128-byte line.  Key rows are one group
+// (64 values: the score chains are lane-local, then the slot tree's last
+// three steps are lane exchanges).  V^T rows (stride Tv = T rounded up to 64)
+// hold nc / 2 groups, an odd last chunk as l*4 + k, and the n % 32 tail in
+// natural order.  512 threads: the value pass gives each of the 64 output
+// rows one row group.  A lane requests all its key rows at entry (T <= 1536:
+// 24 rounds of 64 keys) and its V^T groups after its scores; every request is
+// a whole 128-byte line.
+#define XP_MAXG 24 // full 64-key groups of V^T a lane holds in registers
+__device__ __forceinline__ int fw_xp_pos(int e) { return (e & 7) * 8 + (e >> 5) * 4 + ((e >> 3) & 3); }
+
+__global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const uint16_t *ckp, const uint16_t *cvtp,
+                                                         float *att, int d, int T, int Tv, int H, int L, int layer,
+                                                         float scale) {
+    extern __shared__ __align__(16) float scf[]; // [Tv]: scores, then p in the value pass order
+    __shared__ float red[8];
+    __shared__ float inv_s;
+    const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6, l = lane & 7, rg = lane >> 3;
+    const size_t lh = ((size_t)s * L + layer) * H + h;
+    const uint16_t *K = ckp + lh * (size_t)T * 64;
+    const uint16_t *V = cvtp + lh * (size_t)Tv * 64;
+    const int nc = T >> 5, ng = nc >> 1, ntail = T - nc * 32;
+    // loads retire in order (vmcnt), so the first requests are the ones used
+    // first: q, then every key row this lane multiplies (key j = r * 64 +
+    // wave * 8 + rg)
+    const float *qs = qc + (size_t)s * d + h * 64;
+    float q0[4], q1[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        q0[k] = qs[8 * k + l];
+        q1[k] = qs[32 + 8 * k + l];
+    }
+    // (no load sits behind a branch: addresses past the end are clamped to
+    // the last row and the values unused, so the waits count loads exactly)
+    const int nr = (T + 63) >> 6;
+    uint4 kv[XP_MAXG];
+#pragma unroll
+    for (int r = 0; r < XP_MAXG; r++) {
+        const int j = r * 64 + wave * 8 + rg;
+        kv[r] = *(const uint4 *)(K + (size_t)(j < T ? j : T - 1) * 64 + l * 8);
+    }
+    // qh = q * s, this lane's slots of both chunks
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        q0[k] = q0[k] * scale;
+        q1[k] = q1[k] * scale;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < XP_MAXG; r++) {
+        if (r < nr) {
+            const int j = r * 64 + wave * 8 + rg;
+            const uint32_t u[4] = {kv[r].x, kv[r].y, kv[r].z, kv[r].w};
+            float a[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float w0 = fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16)));
+                const float w1 = fw_h2f((uint16_t)(u[2 + (k >> 1)] >> ((k & 1) * 16)));
+                a[k] = __builtin_fmaf(w1, q1[k], __builtin_fmaf(w0, q0[k], 0.0f));
+            }
+            float v = (a[0] + a[1]) + (a[2] + a[3]);
+            v = v + __shfl_xor(v, 1, 64);
+            v = v + __shfl_xor(v, 2, 64);
+            v = v + __shfl_xor(v, 4, 64);
+            if (j < T) {
+                if (l == 0) scf[j] = v;
+                mx = fmaxf(mx, v);
+            }
+        }
+    }
+    // the value rows are requested once this wave's scores are formed: a
+    // CU's memory queue serves the block's key rows first, and the softmax
+    // (with its 1500-long sequential sum) runs while the values stream in
+    __builtin_amdgcn_sched_barrier(0);
+    const int dd = wave * 8 + rg;
+    const uint16_t *vr = V + (size_t)dd * Tv;
+    uint4 vreg[XP_MAXG];
+#pragma unroll
+    for (int g = 0; g < XP_MAXG; g++) vreg[g] = *(const uint4 *)(vr + (g < ng ? g : 0) * 64 + l * 8);
+    // the odd last chunk (when nc is odd, ng * 64 + 32 <= nc * 32 <= Tv)
+    const uint2 vodd = *(const uint2 *)(vr + ((nc & 1) ? ng * 64 : 0) + l * 4);
+    // the n % 32 tail (rows are Tv >= nc * 32 + 32 long; used by lane 0 only)
+    uint4 vtail[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) vtail[i] = *(const uint4 *)(vr + (ntail > 0 ? nc * 32 : 0) + i * 8);
+    mx = fw_block_max(mx, red);
+    const bool fin = isfinite(mx);
+    if (fin)
+        for (int j = t; j < T; j += 512) {
+            const float e = fw_expf(scf[j] - mx);
+            scf[j] = isfinite(e) ? e : 0.0f;
+        }
+    __syncthreads();
+    if (t < 64) {
+        float sum = 0.0f;
+        if (fin) {
+            if (T <= 64 * SW_MAXC) {
+                sum = fw_seq_sum_wave(scf, T);
+            } else if (t == 0) {
+                for (int j = 0; j < T; j++) sum += scf[j];
+            }
+        }
+        if (t == 0) inv_s = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    // p (normalized when the sum is positive; a non-finite max leaves the raw
+    // scores, as softmax_rows does), moved to the value pass order: within
+    // chunk c, element 8k + l to 4l + k; the tail stays in place
+    const float inv = inv_s;
+    float pv[3];
+#pragma unroll
+    for (int u = 0; u < 3; u++) {
+        const int j = t + u * 512;
+        pv[u] = j < T ? (inv > 0.0f ? scf[j] * inv : scf[j]) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 3; u++) {
+        const int j = t + u * 512;
+        if (j < T) {
+            const int e = j & 31;
+            scf[j < nc * 32 ? (j & ~31) + (e & 7) * 4 + (e >> 3) : j] = pv[u];
+        }
+    }
+    __syncthreads();
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < XP_MAXG; g++) {
+        if (g < ng) {
+            const float4 p0 = *(const float4 *)(scf + g * 64 + l * 4);
+            const float4 p1 = *(const float4 *)(scf + g * 64 + 32 + l * 4);
+            const uint32_t u[4] = {vreg[g].x, vreg[g].y, vreg[g].z, vreg[g].w};
+            const float pa[4] = {p0.x, p0.y, p0.z, p0.w}, pb[4] = {p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16))), pa[k], a[k]);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[2 + (k >> 1)] >> ((k & 1) * 16))), pb[k], a[k]);
+        }
+    }
+    if (nc & 1) {
+        const float4 p0 = *(const float4 *)(scf + (nc - 1) * 32 + l * 4);
+        const float pa[4] = {p0.x, p0.y, p0.z, p0.w};
+        const uint32_t u[2] = {vodd.x, vodd.y};
+#pragma unroll
+        for (int k = 0; k < 4; k++) a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16))), pa[k], a[k]);
+    }
+    float acc = (a[0] + a[1]) + (a[2] + a[3]);
+    acc = acc + __shfl_xor(acc, 1, 64);
+    acc = acc + __shfl_xor(acc, 2, 64);
+    acc = acc + __shfl_xor(acc, 4, 64);
+    if (l == 0) {
+        // dot_f16c's tails: whole 8-wide chunks (products, then their tree), then scalars
+        const uint32_t tw[16] = {vtail[0].x, vtail[0].y, vtail[0].z, vtail[0].w, vtail[1].x, vtail[1].y,
+                                 vtail[1].z, vtail[1].w, vtail[2].x, vtail[2].y, vtail[2].z, vtail[2].w,
+                                 vtail[3].x, vtail[3].y, vtail[3].z, vtail[3].w};
+        const float *pt = scf + nc * 32;
+        int i = 0;
+#pragma unroll
+        for (int c8 = 0; c8 < 4; c8++) {
+            if (i + 8 <= ntail) {
+                float pp[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int ii = c8 * 8 + e;
+                    pp[e] = fw_h2f((uint16_t)(tw[ii >> 1] >> ((ii & 1) * 16))) * pt[ii];
+                }
+                acc += ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
+                i += 8;
+            }
+        }
+#pragma unroll
+        for (int ii = 0; ii < 32; ii++)
+            if (ii >= i && ii < ntail) acc += fw_h2f((uint16_t)(tw[ii >> 1] >> ((ii & 1) * 16))) * pt[ii];
+        att[(size_t)s * d + h * 64 + dd] = acc;
+    }
+}
+
+// K [rows_k, 64] and V^T [rows_v, T] (natural order) to the slot order of
+// k_cross_attn_f16p; V^T rows take stride Tv (pad left as it is).
+__global__ void __launch_bounds__(256) k_pack_cross_f16(const uint16_t *ck, const uint16_t *cvt, uint16_t *ckp,
+                                                        uint16_t *cvtp, size_t rows_k, size_t rows_v, int T, int Tv) {
+    const size_t nk = rows_k * 64, nv = rows_v * (size_t)T;
+    const int nc = T >> 5, ng = nc >> 1;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < nk + nv; i += (size_t)gridDim.x * 256) {
+        if (i < nk) {
+            ckp[(i & ~(size_t)63) + fw_xp_pos((int)(i & 63))] = ck[i];
+        } else {
+            const size_t iv = i - nk, r = iv / T;
+            const int e = (int)(iv - r * T);
+            int pos;
+            if (e < ng * 64) pos = (e & ~63) + fw_xp_pos(e & 63);
+            else if (e < nc * 32) pos = ng * 64 + ((e - ng * 64) & 7) * 4 + ((e - ng * 64) >> 3);
+            else pos = e;
+            cvtp[r * Tv + pos] = cvt[iv];
+        }
+    }
+}
+
+// the value pass holds <= XP_MAXG groups per lane and p in 3 values per thread;
+// the sum needs T <= 64 * SW_MAXC
+bool fw_cross_f16p_ok(int T) { return T > 0 && T <= 1536 && T <= 64 * SW_MAXC && T <= 64 * XP_MAXG; }
+int fw_cross_f16p_tv(int T) { return (T + 63) & ~63; }
+
+void fw_launch_pack_cross_f16(hipStream_t st, const uint16_t *ck, const uint16_t *cvt, uint16_t *ckp, uint16_t *cvtp,
+                              size_t rows_k, size_t rows_v, int T) {
+    const size_t tot = rows_k * 64 + rows_v * (size_t)T;
+    size_t g = (tot + 255) / 256;
+    g = g < 65536 ? g : 65536;
+    hipLaunchKernelGGL(k_pack_cross_f16, dim3((unsigned)g), dim3(256), 0, st, ck, cvt, ckp, cvtp, rows_k, rows_v, T,
+                       fw_cross_f16p_tv(T));
+}
+
+void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp, float *att,
+                               int d, int T, int H, int L, int layer, int ns, float scale) {
+    const int Tv = fw_cross_f16p_tv(T);
+    hipLaunchKernelGGL(k_cross_attn_f16p, dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st, qc, ckp, cvtp, att,
+                       d, T, Tv, H, L, layer, scale);
+}
+
+// ---------------------------------------------------------------------------
 // sum_j p[j] * v[j*64 + t] (f16 values) in ascending j, one f32 chain per
 // thread (the attention value pass of one output column); the operands of 32
 // keys are read before their adds, so LDS latency is paid once per 32 keys.

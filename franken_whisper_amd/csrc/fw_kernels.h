@@ -34,6 +34,15 @@ void fw_launch_gemv16(hipStream_t st, const uint16_t *Wp, const float *bias, con
                       unsigned long long *keys = nullptr, int r = 0, int sb_cap = 0, int grid_cap = 0);
 void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,
                               float *att, int d, int T, int H, int L, int layer, int ns, float scale);
+// The f16 arm's cross attention on slot-order K / V^T copies (dec_fast.hip):
+// fw_launch_pack_cross_f16 repacks natural-order K [rows_k, 64] and V^T
+// [rows_v, T] once per DecoderState::new (V^T rows at stride fw_cross_f16p_tv(T)).
+bool fw_cross_f16p_ok(int T);
+int fw_cross_f16p_tv(int T);
+void fw_launch_pack_cross_f16(hipStream_t st, const uint16_t *ck, const uint16_t *cvt, uint16_t *ckp, uint16_t *cvtp,
+                              size_t rows_k, size_t rows_v, int T);
+void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp, float *att,
+                               int d, int T, int H, int L, int layer, int ns, float scale);
 void fw_launch_gemm_strict(hipStream_t st, const float *A, const uint16_t *B, int m, int n, int k, int epi,
                            float *C, const float *bias, float scale, uint16_t *out16, int T, int H, int L,
                            int layer, int ldc = 0, const float *gelu_tab = nullptr, const float *pos = nullptr);

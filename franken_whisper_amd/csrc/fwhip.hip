@@ -251,6 +251,7 @@ struct fwhip_dstate {
     fwhip_decoder *dec;
     int S, T, Tq, Sp, len;
     uint16_t *kv_k, *kv_v, *ck16, *cvt16;
+    uint16_t *ck16p = nullptr, *cvt16p = nullptr; // f16 arm: slot-order copies for the cross attention
     int8_t *ck8 = nullptr, *cvt8 = nullptr; // cvt8 rows have stride Tq (T rounded up to 16)
     float *ck8s = nullptr, *cvt8s = nullptr;
     float *x, *h, *qkv, *att, *y, *ff, *logits;
@@ -529,6 +530,13 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     st->ck16 = (uint16_t *)fw_dalloc(own, crn * 2);
     st->cvt16 = (uint16_t *)fw_dalloc(own, crn * 2);
     bool ok = st->kv_k && st->kv_v && st->ck16 && st->cvt16;
+    if (dd->arm == FWHIP_DEC_F16 && fw_cross_f16p_ok(T)) {
+        st->ck16p = (uint16_t *)fw_dalloc(own, crn * 2);
+        const size_t vpn = (size_t)S * L * dd->H * 64 * fw_cross_f16p_tv(T);
+        st->cvt16p = (uint16_t *)fw_dalloc(own, vpn * 2);
+        ok = ok && st->ck16p && st->cvt16p;
+        if (ok) ok = hipMemset(st->cvt16p, 0, vpn * 2) == hipSuccess;
+    }
     if (dd->arm == FWHIP_DEC_INT8) {
         st->ck8 = (int8_t *)fw_dalloc(own, crn);
         st->cvt8 = (int8_t *)fw_dalloc(own, (size_t)S * L * dd->H * 64 * st->Tq);
@@ -665,6 +673,9 @@ extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *en
         fw_timed_end(c, &ev);
         if (!ok) return fw_fail(FWHIP_ERR_GENERIC, "cross K/V GEMM has no kernel");
     }
+    if (st->ck16p)
+        fw_launch_pack_cross_f16(c->stream, st->ck16, st->cvt16, st->ck16p, st->cvt16p, (size_t)S * L * H * T,
+                                 (size_t)S * L * H * 64, T);
     if (dd->arm == FWHIP_DEC_INT8) {
         fw_launch_quant_f16_rows(c->stream, st->ck16, st->ck8, st->ck8s, S * L * H * T, 64);
         fw_launch_quant_f16_rows_ld(c->stream, st->cvt16, st->cvt8, st->cvt8s, S * L * H * 64, T, st->Tq);
@@ -754,7 +765,8 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
             fw_gemv16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
             fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0, gt);
-            fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
+            if (st->ck16p) fw_launch_cross_attn_f16p(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S, scale);
+            else fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
             fw_gemv16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
             fw_gemv16_ln(s, l.fc1_16, l.fc1_b, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, st->ff, dff, d, S, dff, 2, gt);
             fw_gemv16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
