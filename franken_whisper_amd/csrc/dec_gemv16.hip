@@ -41,7 +41,10 @@
 
 namespace {
 
-constexpr int G16_BG = 4; // weight groups per pipelined batch
+#ifndef G16_BG_N
+#define G16_BG_N 4
+#endif
+constexpr int G16_BG = G16_BG_N; // weight groups per pipelined batch
 
 template <int LPR>
 struct G16 {
@@ -74,6 +77,30 @@ __global__ void __launch_bounds__(64 * WPB) k_gemv16(const uint16_t *__restrict_
     const int nc = K >> 5, G = nc / CPG;
     const int s0 = blockIdx.y * SB, sn = ns - s0 < SB ? ns - s0 : SB;
     const int ntile = (N + RPT - 1) / RPT;
+
+    // ---- the first tile's weights are requested before the rows are staged
+    const int initial = KEYS && use_filter ? *initialp : 0;
+    const int nb = (G + BG - 1) / BG; // batches per tile
+    int tile = blockIdx.x;
+    auto wptr = [&](int t, int r) -> const uint4 * {
+        const int row = t * RPT + wave * RPW + r * RG + rg;
+        return (const uint4 *)(Wp + (size_t)(row < N ? row : N - 1) * K) + p;
+    };
+    uint4 nxt[BG][R];
+    auto load_batch = [&](int t, int b) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint4 *w = wptr(t, r);
+#pragma unroll
+            for (int i = 0; i < BG; i++) {
+                const int g = b * BG + i;
+                // (unconditional: a partial last batch re-reads group G - 1, unused,
+                // so no load sits behind a branch and the waits count exactly)
+                nxt[i][r] = w[(size_t)(g < G ? g : G - 1) * LPR];
+            }
+        }
+    };
+    if (tile < ntile) load_batch(tile, 0);
 
     // ---- stage the block's stream rows (or their LayerNorm) into LDS
     if constexpr (LN) {
@@ -116,27 +143,6 @@ __global__ void __launch_bounds__(64 * WPB) k_gemv16(const uint16_t *__restrict_
         }
     }
 
-    // ---- tiles: weights stream through a batch pipeline that crosses tiles
-    const int initial = KEYS && use_filter ? *initialp : 0;
-    const int nb = (G + BG - 1) / BG; // batches per tile
-    int tile = blockIdx.x;
-    auto wptr = [&](int t, int r) -> const uint4 * {
-        const int row = t * RPT + wave * RPW + r * RG + rg;
-        return (const uint4 *)(Wp + (size_t)(row < N ? row : N - 1) * K) + p;
-    };
-    uint4 nxt[BG][R];
-    auto load_batch = [&](int t, int b) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint4 *w = wptr(t, r);
-#pragma unroll
-            for (int i = 0; i < BG; i++) {
-                const int g = b * BG + i;
-                if (g < G) nxt[i][r] = w[(size_t)g * LPR];
-            }
-        }
-    };
-    if (tile < ntile) load_batch(tile, 0);
     __syncthreads();
     for (; tile < ntile; tile += gridDim.x) {
         const int rowb = tile * RPT + wave * RPW + rg;
@@ -176,18 +182,11 @@ __global__ void __launch_bounds__(64 * WPB) k_gemv16(const uint16_t *__restrict_
                 }
             }
         };
-        // one batch of weight groups; a full batch has no guards (fixed
-        // registers, straight-line FMAs), the tail batch skips groups past G
-        auto batch = [&](int b, int nbg, auto tail_tag) {
+        // multiply the groups of one batch (weights wb in registers); a full
+        // batch has no guards (fixed registers, straight-line FMAs), the tail
+        // batch skips groups past G
+        auto mul = [&](const uint4 (&wb)[BG][R], int b, int nbg, auto tail_tag) {
             constexpr bool TAIL = decltype(tail_tag)::value;
-            uint4 cur[BG][R];
-#pragma unroll
-            for (int i = 0; i < BG; i++)
-#pragma unroll
-                for (int r = 0; r < R; r++) cur[i][r] = nxt[i][r];
-            // next batch: this tile's, or the first of the block's next tile
-            if (b + 1 < nb) load_batch(tile, b + 1);
-            else if (tile + (int)gridDim.x < ntile) load_batch(tile + gridDim.x, 0);
             load_x(b * BG * CPG, xv[0]);
 #pragma unroll
             for (int i = 0; i < BG; i++) {
@@ -200,7 +199,7 @@ __global__ void __launch_bounds__(64 * WPB) k_gemv16(const uint16_t *__restrict_
                     float wf[R][CPL];
 #pragma unroll
                     for (int r = 0; r < R; r++) {
-                        const uint32_t u[4] = {cur[i][r].x, cur[i][r].y, cur[i][r].z, cur[i][r].w};
+                        const uint32_t u[4] = {wb[i][r].x, wb[i][r].y, wb[i][r].z, wb[i][r].w};
 #pragma unroll
                         for (int kk = 0; kk < CPL; kk++) {
                             const int f = cc * CPL + kk;
@@ -216,6 +215,19 @@ __global__ void __launch_bounds__(64 * WPB) k_gemv16(const uint16_t *__restrict_
                                 acc[r][sl][kk] = __builtin_fmaf(wf[r][kk], xv[cur_x][sl][kk], acc[r][sl][kk]);
                 }
             }
+        };
+        // one pipelined batch: its weights move out of the in-flight buffer
+        // and the next batch (this tile's, or the block's next tile's first) is
+        // requested before the multiply
+        auto batch = [&](int b, int nbg, auto tail_tag) {
+            uint4 cur[BG][R];
+#pragma unroll
+            for (int i = 0; i < BG; i++)
+#pragma unroll
+                for (int r = 0; r < R; r++) cur[i][r] = nxt[i][r];
+            if (b + 1 < nb) load_batch(tile, b + 1);
+            else if (tile + (int)gridDim.x < ntile) load_batch(tile + gridDim.x, 0);
+            mul(cur, b, nbg, tail_tag);
         };
         const int nfull = G / BG;
         for (int b = 0; b < nfull; b++) batch(b, BG, std::false_type{});
@@ -333,62 +345,67 @@ int fw_gemv16_key_blocks(int N, int K) {
 
 namespace {
 
+struct G16Args {
+    const uint16_t *Wp;
+    const float *bias, *x;
+    float *y;
+    int N, K, ns, ldy, mode;
+    const float *gelu_tab, *lnw, *lnb;
+    fwhip_filter filt;
+    int use_filter;
+    const int *initialp;
+    unsigned long long *keys;
+};
+
 template <int LPR, int R, int SB, int WPB>
-void g16_go(hipStream_t st, int grid, int nsg, size_t shm, const uint16_t *Wp, const float *bias, const float *x,
-            float *y, int N, int K, int ns, int ldy, int mode, const float *gelu_tab, const float *lnw,
-            const float *lnb, const fwhip_filter *filt, const int *initialp, unsigned long long *keys) {
-    fwhip_filter ff;
-    if (filt) ff = *filt;
-    else memset(&ff, 0, sizeof ff);
-    const int use = filt != nullptr;
+void g16_go(hipStream_t st, int grid, int nsg, const G16Args &a) {
+    const size_t shm = (size_t)SB * a.K * 4;
     dim3 g(grid, nsg), b(64 * WPB);
-    if (keys) {
+#define G16_L(LN_, KEYS_)                                                                                          \
+    hipLaunchKernelGGL((k_gemv16<LPR, R, SB, WPB, LN_, KEYS_>), g, b, shm, st, a.Wp, a.bias, a.x, a.y, a.N, a.K, \
+                       a.ns, a.ldy, a.mode, a.gelu_tab, a.lnw, a.lnb, a.filt, a.use_filter, a.initialp, a.keys)
+    if (a.keys) {
         if constexpr (R == 1) { // the tiling fw_gemv16_key_blocks assumes
-            if (lnw)
-                hipLaunchKernelGGL((k_gemv16<LPR, R, SB, WPB, true, true>), g, b, shm, st, Wp, bias, x, y, N, K, ns,
-                                   ldy, mode, gelu_tab, lnw, lnb, ff, use, initialp, keys);
-            else
-                hipLaunchKernelGGL((k_gemv16<LPR, R, SB, WPB, false, true>), g, b, shm, st, Wp, bias, x, y, N, K, ns,
-                                   ldy, mode, gelu_tab, lnw, lnb, ff, use, initialp, keys);
+            if (a.lnw) G16_L(true, true);
+            else G16_L(false, true);
         }
-    } else if (lnw) {
-        hipLaunchKernelGGL((k_gemv16<LPR, R, SB, WPB, true, false>), g, b, shm, st, Wp, bias, x, y, N, K, ns, ldy, mode,
-                           gelu_tab, lnw, lnb, ff, use, initialp, keys);
+    } else if (a.lnw) {
+        G16_L(true, false);
     } else {
-        hipLaunchKernelGGL((k_gemv16<LPR, R, SB, WPB, false, false>), g, b, shm, st, Wp, bias, x, y, N, K, ns, ldy,
-                           mode, gelu_tab, lnw, lnb, ff, use, initialp, keys);
+        G16_L(false, false);
     }
+#undef G16_L
 }
 
 // streams per block for a cohort of ns: the LDS copy of the rows must fit;
 // the cohort splits into equal groups of at most sb_cap
-template <int LPR, int R, int WPB>
-void g16_sb(hipStream_t st, int grid_cap, const uint16_t *Wp, const float *bias, const float *x, float *y, int N,
-            int K, int ns, int ldy, int mode, const float *gelu_tab, const float *lnw, const float *lnb,
-            const fwhip_filter *filt, const int *initialp, unsigned long long *keys, int sb_cap) {
-    constexpr int RPT = (64 / LPR) * R * WPB;
-    const int ntile = (N + RPT - 1) / RPT;
+int g16_pick_sb(int ns, int K, int sb_cap, int *nsg) {
     while (sb_cap > 1 && (size_t)sb_cap * K * 4 > 96 * 1024) sb_cap = (sb_cap + 1) / 2;
-    int nsg = (ns + sb_cap - 1) / sb_cap;
-    const int want = (ns + nsg - 1) / nsg;
+    int n = (ns + sb_cap - 1) / sb_cap;
+    const int want = (ns + n - 1) / n;
     const int sb = want <= 1 ? 1 : want <= 2 ? 2 : want <= 4 ? 4 : want <= 5 ? 5 : want <= 8 ? 8 : want <= 10 ? 10
                  : want <= 12 ? 12 : 16;
-    nsg = (ns + sb - 1) / sb;
+    *nsg = (ns + sb - 1) / sb;
+    return sb;
+}
+
+template <int LPR, int R, int WPB>
+void g16_pipe(hipStream_t st, int grid_cap, int sb_cap, const G16Args &a) {
+    constexpr int RPT = (64 / LPR) * R * WPB;
+    const int ntile = (a.N + RPT - 1) / RPT;
+    int nsg;
+    const int sb = g16_pick_sb(a.ns, a.K, sb_cap, &nsg);
     const int grid = ntile < grid_cap ? ntile : grid_cap;
-#define G16_SB(S_) \
-    g16_go<LPR, R, S_, WPB>(st, grid, nsg, (size_t)S_ * K * 4, Wp, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, \
-                            lnb, filt, initialp, keys)
     switch (sb) {
-    case 1: G16_SB(1); break;
-    case 2: G16_SB(2); break;
-    case 4: G16_SB(4); break;
-    case 5: G16_SB(5); break;
-    case 8: G16_SB(8); break;
-    case 10: G16_SB(10); break;
-    case 12: G16_SB(12); break;
-    default: G16_SB(16); break;
+    case 1: g16_go<LPR, R, 1, WPB>(st, grid, nsg, a); break;
+    case 2: g16_go<LPR, R, 2, WPB>(st, grid, nsg, a); break;
+    case 4: g16_go<LPR, R, 4, WPB>(st, grid, nsg, a); break;
+    case 5: g16_go<LPR, R, 5, WPB>(st, grid, nsg, a); break;
+    case 8: g16_go<LPR, R, 8, WPB>(st, grid, nsg, a); break;
+    case 10: g16_go<LPR, R, 10, WPB>(st, grid, nsg, a); break;
+    case 12: g16_go<LPR, R, 12, WPB>(st, grid, nsg, a); break;
+    default: g16_go<LPR, R, 16, WPB>(st, grid, nsg, a); break;
     }
-#undef G16_SB
 }
 
 } // namespace
@@ -396,7 +413,7 @@ void g16_sb(hipStream_t st, int grid_cap, const uint16_t *Wp, const float *bias,
 // y[s, :N] (mode 0 store, 1 add to y, 2 GELU) = W x_s + b for the ns rows of
 // x [ns, K] (with lnw/lnb: LN(x_s), K <= 1280); W in slot order
 // (fw_launch_pack_gemv16, lanes per row fw_gemv16_lpr(N, K)).  With keys (the
-// logits head) the per-tile argmax keys [ns, fw_gemv16_key_blocks(N)] of the
+// logits head) the per-tile argmax keys [ns, fw_gemv16_key_blocks(N, K)] of the
 // filtered row are written too.  r / sb_cap / grid_cap <= 0 take the tuned
 // defaults for the shape.
 void fw_launch_gemv16(hipStream_t st, const uint16_t *Wp, const float *bias, const float *x, float *y, int N, int K,
@@ -405,9 +422,13 @@ void fw_launch_gemv16(hipStream_t st, const uint16_t *Wp, const float *bias, con
                       int grid_cap) {
     const int n_cu = g_n_cu();
     const int lpr = fw_gemv16_lpr(N, K);
+    G16Args a{Wp, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb, {}, filt != nullptr, initialp, keys};
+    if (filt) a.filt = *filt;
+    else memset(&a.filt, 0, sizeof a.filt);
     // shapes measured on MI355X for cohorts of 1, 10 and 16 streams:
     //  - the logits head (51866 rows): one row per lane, 10 streams a block
-    //    (VALU-bound: ~1 FMA per weight element per stream), 2 blocks per CU;
+    //    (VALU-bound: ~1 FMA per weight element per stream), 2 blocks per CU,
+    //    weights through the batch pipeline;
     //  - d x d (o, cross q/o): one stream per block, one row per lane (the
     //    most blocks; each re-reads the 3.3 MB matrix from L2 or the MALL);
     //  - q/k/v, fc1, fc2: 2 streams a block, 2 rows per lane.
@@ -416,8 +437,7 @@ void fw_launch_gemv16(hipStream_t st, const uint16_t *Wp, const float *bias, con
     if (sb_cap <= 0) sb_cap = big ? (ns >= 16 ? 5 : 10) : small ? 1 : 2;
     if (grid_cap <= 0) grid_cap = big ? (ns == 1 ? 4 * n_cu : ns >= 16 ? n_cu : 2 * n_cu) : 1 << 30;
     if (keys) r = 1; // the key layout (fw_gemv16_key_blocks) assumes one row per lane
-#define G16_GO(L_, R_) \
-    g16_sb<L_, R_, 4>(st, grid_cap, Wp, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb, filt, initialp, keys, sb_cap)
+#define G16_GO(L_, R_) g16_pipe<L_, R_, 4>(st, grid_cap, sb_cap, a)
     if (lpr == 8) {
         if (r >= 2) G16_GO(8, 2);
         else G16_GO(8, 1);
