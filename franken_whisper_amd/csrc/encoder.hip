@@ -32,6 +32,10 @@ struct EncBufs {
     int8_t *hq, *aq, *gq;
     float *hs, *as, *gs;
     long long *offs;
+    // ToMe: merged rows, unmerge map, merge workspace
+    float *xm;
+    int32_t *umap;
+    void *tws;
     std::vector<void *> owned;
 };
 
@@ -45,6 +49,10 @@ struct fwhip_encoder {
     fwhip_ctx *ctx;
     int precision;
     int exact = 0;
+    // ToMe (FW_TOME_R / FW_TOME_LAYER): merge tome_r rows after block
+    // tome_after; 0 = the un-merged encoder (the strict-parity setting)
+    int tome_r = 0, tome_after = 3;
+    int tome_min_rows = 0; // the default rule merges full 30 s windows only (1500 rows)
     const uint16_t *conv1n = nullptr, *conv2n = nullptr; // natural [d, Cin*3] (exact mode)
     EncExactBufs xbuf;
     fwhip_hparams hp;
@@ -246,6 +254,9 @@ static bool ensure_bufs(fwhip_encoder *e, int B, int nf) {
     b.gq = (int8_t *)A(M * dff);
     b.gs = (float *)A(4 * M);
     b.offs = (long long *)A(sizeof(long long) * B);
+    b.xm = (float *)A(4 * M * d);
+    b.umap = (int32_t *)A(sizeof(int32_t) * M);
+    b.tws = A(fw_tome_ws_bytes(B, (int)T2));
     for (void *p : o)
         if (!p) return false;
     // V^T padding columns (keys >= T) must be finite zeros
@@ -258,6 +269,13 @@ static bool ensure_bufs(fwhip_encoder *e, int B, int nf) {
 static bool enc_h16_ok(int n) {
     const int k = n / 512;
     return n > 0 && n % 512 == 0 && (k <= 8 || k == 10 || k == 12 || k == 16);
+}
+
+// The single-shot schedule of forward_time_major (encoder.rs:1590-1632): merge
+// after block tome_after when rows > r + 2 and rows - r >= 128 (the floor).
+static bool tome_due(const fwhip_encoder *e, int li, int rows, bool merged) {
+    return !merged && e->tome_r > 0 && li == e->tome_after && rows >= e->tome_min_rows && rows > e->tome_r + 2 &&
+           rows - e->tome_r >= 128 && fw_tome_ok(rows, e->d);
 }
 
 static FwGemm gemm_args(const void *A, const void *A2, const void *B, int M, int N, int K, const float *sx,
@@ -316,72 +334,86 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
         fw_timed_end(c, &ev);
     }
     int gcls = i8 ? FWHIP_K_ENC_GEMM_I8 : FWHIP_K_ENC_GEMM_F32;
+    // the current rows: b.x [B, T2, d], or after a ToMe merge b.xm [B, Tc, d]
+    float *X = b.x;
+    int Tc = T2, Mc = M, Tpc = Tp;
+    bool merged = false;
     int kind = i8 ? FW_KIND_I8 : FW_KIND_F16S;
     for (int li = 0; li < e->L; li++) {
         const EncLayerDev &l = e->layers[li];
         // self-attention residual (encoder_block, encoder.rs:2608-2681)
-        fw_launch_enc_ln(st, b.x, l.attn_ln_w, l.attn_ln_b, M, d, i8 ? FW_LN_I7 : FW_LN_SPLIT, nullptr, b.hh, b.hl,
+        fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, i8 ? FW_LN_I7 : FW_LN_SPLIT, nullptr, b.hh, b.hl,
                          b.hq, b.hs);
-        FwGemm g = i8 ? gemm_args(b.hq, nullptr, l.qkv7, M, 3 * d, d, b.hs, l.qkv7s, l.qkv_b, FW_EPI_QKV, nullptr, d)
-                      : gemm_args(b.hh, b.hl, l.qkv16, M, 3 * d, d, nullptr, nullptr, l.qkv_b, FW_EPI_QKV, nullptr, d);
+        FwGemm g = i8 ? gemm_args(b.hq, nullptr, l.qkv7, Mc, 3 * d, d, b.hs, l.qkv7s, l.qkv_b, FW_EPI_QKV, nullptr, d)
+                      : gemm_args(b.hh, b.hl, l.qkv16, Mc, 3 * d, d, nullptr, nullptr, l.qkv_b, FW_EPI_QKV, nullptr, d);
         g.o16[0] = b.qh;
         g.o16[1] = b.ql;
         g.o16[2] = b.kh;
         g.o16[3] = b.kl;
         g.o16[4] = b.vth;
         g.o16[5] = b.vtl;
-        g.T = T2;
+        g.T = Tc;
         g.H = H;
-        g.Tp = Tp;
-        fw_timed_begin(c, gcls, 2.0 * M * 3.0 * d * d, &ev);
+        g.Tp = Tpc;
+        fw_timed_begin(c, gcls, 2.0 * Mc * 3.0 * d * d, &ev);
         fw_launch_gemm(st, kind, g);
         fw_timed_end(c, &ev);
-        fw_timed_begin(c, FWHIP_K_ENC_ATTN, 4.0 * B * H * (double)T2 * T2 * 64, &ev);
-        fw_launch_attention(st, b.qh, b.ql, b.kh, b.kl, b.vth, b.vtl, B, T2, Tp, H, d, i8 ? 0 : 1, b.att, b.ath,
+        fw_timed_begin(c, FWHIP_K_ENC_ATTN, 4.0 * B * H * (double)Tc * Tc * 64, &ev);
+        fw_launch_attention(st, b.qh, b.ql, b.kh, b.kl, b.vth, b.vtl, B, Tc, Tpc, H, d, i8 ? 0 : 1, b.att, b.ath,
                             b.atl);
         fw_timed_end(c, &ev);
         if (i8) {
-            fw_launch_quant_exact_rows(st, b.att, M, d, b.aq, b.as);
-            g = gemm_args(b.aq, nullptr, l.o8, M, d, d, b.as, l.o8s, l.o_b, FW_EPI_RESID, b.x, d);
+            fw_launch_quant_exact_rows(st, b.att, Mc, d, b.aq, b.as);
+            g = gemm_args(b.aq, nullptr, l.o8, Mc, d, d, b.as, l.o8s, l.o_b, FW_EPI_RESID, X, d);
         } else {
-            g = gemm_args(b.ath, b.atl, l.o16, M, d, d, nullptr, nullptr, l.o_b, FW_EPI_RESID, b.x, d);
+            g = gemm_args(b.ath, b.atl, l.o16, Mc, d, d, nullptr, nullptr, l.o_b, FW_EPI_RESID, X, d);
         }
-        fw_timed_begin(c, gcls, 2.0 * M * (double)d * d, &ev);
+        fw_timed_begin(c, gcls, 2.0 * Mc * (double)d * d, &ev);
         fw_launch_gemm(st, kind, g);
         fw_timed_end(c, &ev);
         // MLP residual (encoder.rs:2684-2735)
-        fw_launch_enc_ln(st, b.x, l.mlp_ln_w, l.mlp_ln_b, M, d, i8 ? FW_LN_I7 : FW_LN_SPLIT, nullptr, b.hh, b.hl,
+        fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, i8 ? FW_LN_I7 : FW_LN_SPLIT, nullptr, b.hh, b.hl,
                          b.hq, b.hs);
         if (i8) {
             // fc1 as f16 GELU-table indices (half the bytes of f32 rows; the
             // rare |v| >= 9.98 values exactly in b.ff), then GELU + quantization;
             // f32 rows where the index form has no kernel
-            g = gemm_args(b.hq, nullptr, l.fc1_7, M, dff, d, b.hs, l.fc1_7s, l.fc1_b, FW_EPI_F16IDX, b.ff, dff);
+            g = gemm_args(b.hq, nullptr, l.fc1_7, Mc, dff, d, b.hs, l.fc1_7s, l.fc1_b, FW_EPI_F16IDX, b.ff, dff);
             g.o16[0] = b.gh;
-            fw_timed_begin(c, gcls, 2.0 * M * (double)dff * d, &ev);
+            fw_timed_begin(c, gcls, 2.0 * Mc * (double)dff * d, &ev);
             bool idx = enc_h16_ok(dff) && fw_launch_gemm(st, kind, g);
             if (!idx) {
                 g.epi = FW_EPI_F32;
                 fw_launch_gemm(st, kind, g);
             }
             fw_timed_end(c, &ev);
-            if (!idx || !fw_launch_gelu_quant_h16(st, b.gh, b.ff, M, dff, gt, b.gq, b.gs))
-                fw_launch_gelu_quant_i7_rows(st, b.ff, M, dff, gt, b.gq, b.gs);
-            g = gemm_args(b.gq, nullptr, l.fc2_7, M, d, dff, b.gs, l.fc2_7s, l.fc2_b, FW_EPI_RESID, b.x, d);
+            if (!idx || !fw_launch_gelu_quant_h16(st, b.gh, b.ff, Mc, dff, gt, b.gq, b.gs))
+                fw_launch_gelu_quant_i7_rows(st, b.ff, Mc, dff, gt, b.gq, b.gs);
+            g = gemm_args(b.gq, nullptr, l.fc2_7, Mc, d, dff, b.gs, l.fc2_7s, l.fc2_b, FW_EPI_RESID, X, d);
         } else {
-            g = gemm_args(b.hh, b.hl, l.fc1_16, M, dff, d, nullptr, nullptr, l.fc1_b, FW_EPI_GELU_SPLIT, nullptr,
+            g = gemm_args(b.hh, b.hl, l.fc1_16, Mc, dff, d, nullptr, nullptr, l.fc1_b, FW_EPI_GELU_SPLIT, nullptr,
                           dff);
             g.gelu_tab = gt;
             g.o16[0] = b.gh;
             g.o16[1] = b.gl;
-            fw_timed_begin(c, gcls, 2.0 * M * (double)dff * d, &ev);
+            fw_timed_begin(c, gcls, 2.0 * Mc * (double)dff * d, &ev);
             fw_launch_gemm(st, kind, g);
             fw_timed_end(c, &ev);
-            g = gemm_args(b.gh, b.gl, l.fc2_16, M, d, dff, nullptr, nullptr, l.fc2_b, FW_EPI_RESID, b.x, d);
+            g = gemm_args(b.gh, b.gl, l.fc2_16, Mc, d, dff, nullptr, nullptr, l.fc2_b, FW_EPI_RESID, X, d);
         }
-        fw_timed_begin(c, gcls, 2.0 * M * (double)d * dff, &ev);
+        fw_timed_begin(c, gcls, 2.0 * Mc * (double)d * dff, &ev);
         fw_launch_gemm(st, kind, g);
         fw_timed_end(c, &ev);
+        if (tome_due(e, li, Tc, merged)) {
+            Tc = fw_launch_tome_merge(st, X, B, Tc, d, e->tome_r, b.tws, b.xm, b.umap);
+            X = b.xm;
+            Mc = B * Tc;
+            Tpc = (Tc + 63) / 64 * 64;
+            merged = true;
+            // V^T rows now have stride Tpc: their padding keys must be finite
+            fw_launch_tome_vpad(st, b.vth, (size_t)B * H * 64, Tc, Tpc);
+            fw_launch_tome_vpad(st, b.vtl, (size_t)B * H * 64, Tc, Tpc);
+        }
         if (c->cancel.exchange(0)) {
             hipStreamSynchronize(st);
             hipEventDestroy(e0);
@@ -389,6 +421,8 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
             return fw_fail(FWHIP_ERR_CANCELLED, "cancelled");
         }
     }
+    // tome_unmerge before ln_post (encoder.rs:1629-1631)
+    if (merged) fw_launch_tome_unmerge(st, X, B, Tc, b.umap, T2, d, b.x);
     // ln_post (encoder.rs:1636)
     fw_launch_enc_ln(st, b.x, e->lnpw, e->lnpb, M, d, FW_LN_F32, out_dev, nullptr, nullptr, nullptr, nullptr);
     hipEventRecord(e1, st);
@@ -452,43 +486,53 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
     fw_launch_im2col_f32(st, x.a1, B, T1, d, 2, T2, x.c2);
     fw_launch_gemm_strict(st, x.c2, e->conv2n, M, d, 3 * d, 4, b.x, e->conv2b, 1.0f, nullptr, T2, 0, 0, 0, d, gt,
                           e->pos);
+    float *X = b.x;
+    int Tc = T2, Mc = M;
+    bool merged = false;
     for (int li = 0; li < e->L; li++) {
         const EncLayerDev &l = e->layers[li];
         if (i8) {
-            fw_launch_enc_ln(st, b.x, l.attn_ln_w, l.attn_ln_b, M, d, FW_LN_I7, nullptr, nullptr, nullptr, b.hq, b.hs);
-            FwGemm g = gemm_args(b.hq, nullptr, l.qkv7, M, 3 * d, d, b.hs, l.qkv7s, l.qkv_b, FW_EPI_F32, x.qkv, 3 * d);
+            fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_I7, nullptr, nullptr, nullptr, b.hq, b.hs);
+            FwGemm g = gemm_args(b.hq, nullptr, l.qkv7, Mc, 3 * d, d, b.hs, l.qkv7s, l.qkv_b, FW_EPI_F32, x.qkv, 3 * d);
             fw_launch_gemm(st, FW_KIND_I8, g);
         } else {
-            fw_launch_enc_ln(st, b.x, l.attn_ln_w, l.attn_ln_b, M, d, FW_LN_F32, x.h, nullptr, nullptr, nullptr,
+            fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_F32, x.h, nullptr, nullptr, nullptr,
                              nullptr);
-            fw_launch_gemm_strict(st, x.h, l.qkv16, M, 3 * d, d, 0, x.qkv, l.qkv_b, 1.0f, nullptr, T2, 0, 0, 0,
+            fw_launch_gemm_strict(st, x.h, l.qkv16, Mc, 3 * d, d, 0, x.qkv, l.qkv_b, 1.0f, nullptr, Tc, 0, 0, 0,
                                   3 * d, nullptr, nullptr);
         }
-        fw_launch_attention_exact(st, x.qkv, 3 * d, 0, d, 2 * d, B, T2, H, d, x.S, x.att);
+        fw_launch_attention_exact(st, x.qkv, 3 * d, 0, d, 2 * d, B, Tc, H, d, x.S, x.att);
         if (i8) {
-            fw_launch_quant_exact_rows(st, x.att, M, d, b.aq, b.as);
-            FwGemm g = gemm_args(b.aq, nullptr, l.o8, M, d, d, b.as, l.o8s, l.o_b, FW_EPI_RESID, b.x, d);
+            fw_launch_quant_exact_rows(st, x.att, Mc, d, b.aq, b.as);
+            FwGemm g = gemm_args(b.aq, nullptr, l.o8, Mc, d, d, b.as, l.o8s, l.o_b, FW_EPI_RESID, X, d);
             fw_launch_gemm(st, FW_KIND_I8, g);
-            fw_launch_enc_ln(st, b.x, l.mlp_ln_w, l.mlp_ln_b, M, d, FW_LN_I7, nullptr, nullptr, nullptr, b.hq, b.hs);
-            g = gemm_args(b.hq, nullptr, l.fc1_7, M, dff, d, b.hs, l.fc1_7s, l.fc1_b, FW_EPI_F32, b.ff, dff);
+            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_I7, nullptr, nullptr, nullptr, b.hq, b.hs);
+            g = gemm_args(b.hq, nullptr, l.fc1_7, Mc, dff, d, b.hs, l.fc1_7s, l.fc1_b, FW_EPI_F32, b.ff, dff);
             fw_launch_gemm(st, FW_KIND_I8, g);
-            fw_launch_gelu_quant_i7_rows(st, b.ff, M, dff, gt, b.gq, b.gs);
-            g = gemm_args(b.gq, nullptr, l.fc2_7, M, d, dff, b.gs, l.fc2_7s, l.fc2_b, FW_EPI_RESID, b.x, d);
+            fw_launch_gelu_quant_i7_rows(st, b.ff, Mc, dff, gt, b.gq, b.gs);
+            g = gemm_args(b.gq, nullptr, l.fc2_7, Mc, d, dff, b.gs, l.fc2_7s, l.fc2_b, FW_EPI_RESID, X, d);
             fw_launch_gemm(st, FW_KIND_I8, g);
         } else {
-            fw_launch_gemm_strict(st, x.att, l.o16, M, d, d, 5, b.x, l.o_b, 1.0f, nullptr, T2, 0, 0, 0, d, nullptr,
+            fw_launch_gemm_strict(st, x.att, l.o16, Mc, d, d, 5, X, l.o_b, 1.0f, nullptr, Tc, 0, 0, 0, d, nullptr,
                                   nullptr);
-            fw_launch_enc_ln(st, b.x, l.mlp_ln_w, l.mlp_ln_b, M, d, FW_LN_F32, x.h, nullptr, nullptr, nullptr, nullptr);
-            fw_launch_gemm_strict(st, x.h, l.fc1_16, M, dff, d, 3, x.ff, l.fc1_b, 1.0f, nullptr, T2, 0, 0, 0, dff, gt,
+            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_F32, x.h, nullptr, nullptr, nullptr, nullptr);
+            fw_launch_gemm_strict(st, x.h, l.fc1_16, Mc, dff, d, 3, x.ff, l.fc1_b, 1.0f, nullptr, Tc, 0, 0, 0, dff, gt,
                                   nullptr);
-            fw_launch_gemm_strict(st, x.ff, l.fc2_16, M, d, dff, 5, b.x, l.fc2_b, 1.0f, nullptr, T2, 0, 0, 0, d,
+            fw_launch_gemm_strict(st, x.ff, l.fc2_16, Mc, d, dff, 5, X, l.fc2_b, 1.0f, nullptr, Tc, 0, 0, 0, d,
                                   nullptr, nullptr);
+        }
+        if (tome_due(e, li, Tc, merged)) {
+            Tc = fw_launch_tome_merge(st, X, B, Tc, d, e->tome_r, b.tws, b.xm, b.umap);
+            X = b.xm;
+            Mc = B * Tc;
+            merged = true;
         }
         if (c->cancel.exchange(0)) {
             hipStreamSynchronize(st);
             return fw_fail(FWHIP_ERR_CANCELLED, "cancelled");
         }
     }
+    if (merged) fw_launch_tome_unmerge(st, X, B, Tc, b.umap, T2, d, b.x);
     fw_launch_enc_ln(st, b.x, e->lnpw, e->lnpb, M, d, FW_LN_F32, out_dev, nullptr, nullptr, nullptr, nullptr);
     hipError_t err = hipStreamSynchronize(st);
     if (err == hipSuccess) err = hipGetLastError();
@@ -515,6 +559,41 @@ extern "C" fwhip_status fwhip_encoder_set_exact(fwhip_encoder *e, int32_t exact)
     if (exact && e->precision == FWHIP_ENC_F32 && e->layers.size() && !e->layers[0].qkv16)
         return fw_fail(FWHIP_ERR_INVALID, "exact f32 mode needs the f32 plan's weights");
     e->exact = exact != 0;
+    return FWHIP_OK;
+}
+
+// FW_TOME_R / FW_TOME_LAYER (encoder.rs:1264-1337): merge r rows after block
+// `after` (0-based) of every full window; r = 0 restores the un-merged
+// encoder; r < 0 takes the reference's default for the model (tome_r_for:
+// 500 after block 3 on the 20-head large class, else 0).
+extern "C" fwhip_status fwhip_encoder_set_tome(fwhip_encoder *e, int32_t r, int32_t after) {
+    if (!e) return fw_fail(FWHIP_ERR_INVALID, "NULL encoder");
+    int min_rows = 0;
+    if (r < 0) {
+        r = e->H >= 20 ? 500 : 0;
+        after = 3;
+        min_rows = 1500; // shorter (tail) windows keep every row
+    }
+    if (r > 0 && (after < 0 || after >= e->L)) return fw_fail(FWHIP_ERR_INVALID, "ToMe layer out of range");
+    e->tome_r = r;
+    e->tome_after = after;
+    e->tome_min_rows = min_rows;
+    return FWHIP_OK;
+}
+
+extern "C" fwhip_status fwhip_tome_merge(fwhip_ctx *c, const float *x_dev, int32_t n_windows, int32_t T, int32_t d,
+                                         int32_t r, float *merged_dev, int32_t *umap_dev, int32_t *out_rows) {
+    if (!c || !x_dev || !merged_dev || !umap_dev || !out_rows) return fw_fail(FWHIP_ERR_INVALID, "fwhip_tome_merge: NULL argument");
+    if (n_windows <= 0 || r < 0 || !fw_tome_ok(T, d))
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_tome_merge: needs n_windows > 0, r >= 0, 2 <= T <= 4096, d % 32 == 0");
+    HIP_TRY(hipSetDevice(c->device));
+    void *ws = nullptr;
+    HIP_TRY(hipMalloc(&ws, fw_tome_ws_bytes(n_windows, T)));
+    *out_rows = fw_launch_tome_merge(c->stream, x_dev, n_windows, T, d, r, ws, merged_dev, umap_dev);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) e = hipGetLastError();
+    hipFree(ws);
+    if (e != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("fwhip_tome_merge: ") + hipGetErrorString(e));
     return FWHIP_OK;
 }
 

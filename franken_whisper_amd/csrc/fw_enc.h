@@ -82,3 +82,12 @@ void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql,
 void fw_launch_im2col_f32(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, float *out);
 void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qoff, int koff, int voff, int B, int T,
                                int H, int d, float *S, float *out);
+// ToMe (enc_tome.hip): merge x [B, T, d] into xm [B, T - r', d] with the
+// unmerge map umap [B, T] (workspace fw_tome_ws_bytes(B, T)); returns T - r'
+bool fw_tome_ok(int T, int d);
+size_t fw_tome_ws_bytes(int B, int T);
+int fw_launch_tome_merge(hipStream_t st, const float *x, int B, int T, int d, int r, void *ws, float *xm,
+                         int32_t *umap);
+void fw_launch_tome_unmerge(hipStream_t st, const float *xm, int B, int Tm, const int32_t *umap, int T, int d,
+                            float *out);
+void fw_launch_tome_vpad(hipStream_t st, uint16_t *vt, size_t rows, int T, int Tp);

@@ -42,6 +42,8 @@ SIGNATURES = {
     "fwhip_encoder_forward_time_major": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, _vp,
                                                      C.POINTER(abi.ExecRecord)]),
     "fwhip_encoder_set_exact": (C.c_int32, [_vp, C.c_int32]),
+    "fwhip_encoder_set_tome": (C.c_int32, [_vp, C.c_int32, C.c_int32]),
+    "fwhip_tome_merge": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _vp, _vp, _i32p]),
     "fwhip_encoder_gemm_i8": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, _vp, _vp]),
     "fwhip_encoder_gemm_i8_fused": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, C.c_int32, _vp, _vp]),
     "fwhip_decoder_load": (C.c_int32, [_vp, C.POINTER(abi.DecoderWeights), C.c_int32, C.POINTER(_vp)]),
@@ -168,6 +170,22 @@ class Context:
                                         out.ctypes.data_as(_i32p)))
         return out
 
+    def tome_merge(self, x_dev: DeviceArray, r: int):
+        """tome_merge (encoder.rs:1403-1506) of every window of x_dev [n_windows,
+        T, d]: returns (merged [n_windows, T - r', d], umap [n_windows, T])."""
+        nw, T, d = x_dev.shape
+        merged = self.empty((nw, T, d), np.float32)
+        umap = self.empty((nw, T), np.int32)
+        rows = C.c_int32(0)
+        check(lib().fwhip_tome_merge(self.h, x_dev.ptr, nw, T, d, r, merged.ptr, umap.ptr, C.byref(rows)))
+        m = merged.download().reshape(nw, T, d)
+        # the device rows are packed [n_windows, T - r', d]
+        flat = m.reshape(-1)[: nw * rows.value * d].reshape(nw, rows.value, d)
+        out = (flat.copy(), umap.download().reshape(nw, T))
+        merged.free()
+        umap.free()
+        return out
+
     def log_mel_noalloc(self, samples_dev: DeviceArray, n_samples: int, filters_dev: DeviceArray, n_mel: int,
                         out_dev: DeviceArray, n_fft_bins: int = 201):
         """fwhip_log_mel with the library's static device scratch: no allocation."""
@@ -206,6 +224,10 @@ class Encoder:
 
     def set_exact(self, exact: bool):
         check(lib().fwhip_encoder_set_exact(self.h, 1 if exact else 0))
+
+    def set_tome(self, r: int, after: int = 3):
+        """FW_TOME_R / FW_TOME_LAYER; r < 0 takes the reference's default rule."""
+        check(lib().fwhip_encoder_set_tome(self.h, r, after))
 
     def gemm_i8(self, layer: int, which: int, x_dev: DeviceArray, acc_dev: DeviceArray, y_dev: DeviceArray):
         check(lib().fwhip_encoder_gemm_i8(self.h, layer, which, x_dev.ptr, x_dev.shape[0], acc_dev.ptr,

@@ -205,6 +205,28 @@ fwhip_status fwhip_encoder_forward(fwhip_encoder *enc, const float *mel_dev, int
  * tolerance; int8 accumulators are exact in both). */
 fwhip_status fwhip_encoder_set_exact(fwhip_encoder *enc, int32_t exact);
 
+/* ToMe token merging (FW_TOME_R / FW_TOME_LAYER, encoder.rs:1264-1337 and
+ * 1590-1632, single-shot schedule): merge r of the rows of every window after
+ * block `after` (0-based) by bipartite soft matching (tome_merge,
+ * encoder.rs:1403-1506), run the later blocks on the merged rows and unmerge
+ * before ln_post (tome_unmerge, encoder.rs:1509-1517).  The merge runs when
+ * rows > r + 2 and rows - r >= 128.  r = 0 (the initial setting) is the
+ * un-merged encoder, FW_TOME_R=0; r < 0 applies the reference's default for
+ * the model (tome_r_for: 500 after block 3 on the 20-head large class for full
+ * 1500-row windows, none otherwise).  The merge itself is computed in the
+ * strict-parity arithmetic in both modes (its similarity GEMM in ascending-k
+ * sequential f32), so in exact mode the whole forward stays bit-identical to
+ * the reference's strict mode with the same FW_TOME_R. */
+fwhip_status fwhip_encoder_set_tome(fwhip_encoder *enc, int32_t r, int32_t after);
+
+/* tome_merge of rows x_dev [n_windows, T, d] (f32) per window: merged rows
+ * into merged_dev [n_windows, T - r', d] (r' = min(r, ceil(T/2), T - 1)) and
+ * the unmerge map umap_dev [n_windows, T] (original row -> merged row);
+ * *out_rows = T - r'.  A parity entry point for the encoder's merge step; it
+ * allocates its workspace per call. */
+fwhip_status fwhip_tome_merge(fwhip_ctx *ctx, const float *x_dev, int32_t n_windows, int32_t T, int32_t d, int32_t r,
+                              float *merged_dev, int32_t *umap_dev, int32_t *out_rows);
+
 /* Same contract, time-major input already windowed: `x_dev` is
  * [n_windows, n_frames, n_mels] (the Mat that forward_time_major consumes,
  * encoder.rs:1520). */

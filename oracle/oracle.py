@@ -70,6 +70,9 @@ def lib():
         "ref_encoder_new": (C.c_void_p, [C.POINTER(abi.EncoderWeights), C.c_int]),
         "ref_encoder_free": (None, [C.c_void_p]),
         "ref_encoder_forward": (C.c_int, [C.c_void_p, f32p, C.c_int, f32p, C.c_int]),
+        "ref_encoder_forward_tome": (C.c_int, [C.c_void_p, f32p, C.c_int, f32p, C.c_int, C.c_int, C.c_int]),
+        "ref_tome_merge": (C.c_int, [f32p, C.c_int, C.c_int, C.c_int, f32p, i32p]),
+        "ref_tome_unmerge": (None, [f32p, i32p, C.c_int, C.c_int, f32p]),
         "ref_mel_window": (None, [f32p, C.c_int, C.c_int64, C.c_int64, C.c_int, f32p]),
         "ref_enc_i7_gemm": (None, [C.c_void_p, C.c_int, C.c_int, f32p, C.c_int64, i32p, f32p]),
         "ref_decoder_new": (C.c_void_p, [C.POINTER(abi.DecoderWeights), C.c_int]),
@@ -338,12 +341,14 @@ class Encoder:
         self.h = lib().ref_encoder_new(C.byref(self.desc), precision)
         self.cfg = model.cfg
 
-    def forward(self, x_time_major, n_layers=-1):
+    def forward(self, x_time_major, n_layers=-1, tome_r=0, tome_after=3):
+        """forward_time_major; tome_r > 0 merges tome_r rows after block
+        tome_after (0-based), as FW_TOME_R / FW_TOME_LAYER do."""
         x = _c(x_time_major, np.float32)
         n_frames = x.shape[0]
         out = np.empty((n_frames // 2, self.cfg.n_audio_state), np.float32)
-        rc = lib().ref_encoder_forward(self.h, _p(x, C.c_float), n_frames, _p(out, C.c_float),
-                                       n_layers)
+        rc = lib().ref_encoder_forward_tome(self.h, _p(x, C.c_float), n_frames, _p(out, C.c_float),
+                                            n_layers, tome_r, tome_after)
         if rc != 0:
             raise ValueError(f"ref_encoder_forward rc={rc}")
         return out
@@ -364,6 +369,26 @@ class Encoder:
             lib().ref_encoder_free(self.h)
         except Exception:
             pass
+
+
+def tome_merge(x, r):
+    """tome_merge (encoder.rs:1403-1506) of the rows x [seq, d]: returns the
+    merged rows [seq - r', d] and the unmerge map [seq]."""
+    x = _c(x, np.float32)
+    seq, d = x.shape
+    merged = np.zeros((seq, d), np.float32)
+    umap = np.zeros(seq, np.int32)
+    n = lib().ref_tome_merge(_p(x, C.c_float), seq, d, r, _p(merged, C.c_float), _p(umap, C.c_int32))
+    return merged[:n].copy(), umap
+
+
+def tome_unmerge(merged, umap):
+    merged = _c(merged, np.float32)
+    umap = _c(umap, np.int32)
+    out = np.empty((umap.size, merged.shape[1]), np.float32)
+    lib().ref_tome_unmerge(_p(merged, C.c_float), _p(umap, C.c_int32), umap.size, merged.shape[1],
+                           _p(out, C.c_float))
+    return out
 
 
 class Decoder:

@@ -770,9 +770,109 @@ static void encoder_block(const ref_encoder *e, const enc_layer_t *l, float *x, 
     free(h); free(q); free(k); free(v); free(att); free(f);
 }
 
-/* forward_time_major, encoder.rs:1520-1677 (CPU blocks, no ToMe). */
-int ref_encoder_forward(const ref_encoder *e, const float *x, int n_frames, float *out,
-                        int n_layers_run) {
+/* tome_merge, encoder.rs:1403-1506 (bipartite soft matching), in the
+ * strict-parity arithmetic: A = rows 0, 2, 4, ..., B = rows 1, 3, ...;
+ * sim = A @ B^T by the strict matmul; row norms sqrt of the sequential f32 sum
+ * of v*v, floored at 1e-9 (f32::max); cos = s / (na * nb); per A row the first
+ * strict maximum over B (start -inf); the r = min(r, n_a, seq - 1) A rows with
+ * the largest best similarity (a stable descending sort: ties keep the lower
+ * A index) are added to their B partner in ascending A order and each B row
+ * with count c > 1 is divided by c; merged = the B rows, then the kept A rows
+ * in ascending order.  umap[seq]: original row -> merged row.  Returns the
+ * merged row count seq - r. */
+int ref_tome_merge(const float *x, int seq, int d, int r, float *merged, int32_t *umap) {
+    int n_a = (seq + 1) / 2, n_b = seq / 2;
+    if (r > n_a) r = n_a;
+    if (r > seq - 1) r = seq - 1 > 0 ? seq - 1 : 0;
+    float *a = (float *)malloc(sizeof(float) * ((size_t)n_a * d + 1));
+    float *bt = (float *)malloc(sizeof(float) * ((size_t)n_b * d + 1));
+    float *sim = (float *)malloc(sizeof(float) * ((size_t)n_a * (n_b > 0 ? n_b : 1) + 1));
+    float *an = (float *)malloc(sizeof(float) * (n_a + 1));
+    float *bn = (float *)malloc(sizeof(float) * (n_b + 1));
+    float *best_sim = (float *)malloc(sizeof(float) * (n_a + 1));
+    int *best_b = (int *)malloc(sizeof(int) * (n_a + 1));
+    int *rank = (int *)malloc(sizeof(int) * (n_a + 1));
+    int *counts = (int *)malloc(sizeof(int) * (n_b + 1));
+    for (int i = 0; i < n_a; i++) memcpy(a + (size_t)i * d, x + (size_t)(2 * i) * d, sizeof(float) * d);
+    /* b_t = transpose(B) [d, n_b] */
+    for (int i = 0; i < n_b; i++)
+        for (int k = 0; k < d; k++) bt[(size_t)k * n_b + i] = x[(size_t)(2 * i + 1) * d + k];
+    if (n_b > 0) ref_matmul_strict(a, bt, sim, n_a, d, n_b);
+    else for (int i = 0; i < n_a; i++) sim[i] = 0.0f; /* the reference's [n_a, 1] zero fallback */
+    for (int i = 0; i < n_a; i++) {
+        float s = 0.0f;
+        for (int k = 0; k < d; k++) s += a[(size_t)i * d + k] * a[(size_t)i * d + k];
+        s = sqrtf(s);
+        an[i] = s > 1e-9f ? s : 1e-9f; /* f32::max (NaN -> 1e-9) */
+    }
+    for (int i = 0; i < n_b; i++) {
+        const float *row = x + (size_t)(2 * i + 1) * d;
+        float s = 0.0f;
+        for (int k = 0; k < d; k++) s += row[k] * row[k];
+        s = sqrtf(s);
+        bn[i] = s > 1e-9f ? s : 1e-9f;
+    }
+    for (int i = 0; i < n_a; i++) {
+        int bb = 0;
+        float bs = -INFINITY;
+        for (int j = 0; j < n_b; j++) {
+            float cs = sim[(size_t)i * n_b + j] / (an[i] * bn[j]);
+            if (cs > bs) {
+                bs = cs;
+                bb = j;
+            }
+        }
+        best_b[i] = bb;
+        best_sim[i] = bs;
+    }
+    /* stable descending sort: rank = #greater + #equal at a lower index */
+    for (int i = 0; i < n_a; i++) {
+        int rk = 0;
+        for (int j = 0; j < n_a; j++)
+            if (best_sim[j] > best_sim[i] || (j < i && best_sim[j] == best_sim[i])) rk++;
+        rank[i] = rk;
+    }
+    for (int i = 0; i < n_b; i++) {
+        memcpy(merged + (size_t)i * d, x + (size_t)(2 * i + 1) * d, sizeof(float) * d);
+        counts[i] = 1;
+    }
+    for (int i = 0; i < n_a; i++)
+        if (rank[i] < r) {
+            float *m = merged + (size_t)best_b[i] * d;
+            for (int k = 0; k < d; k++) m[k] += a[(size_t)i * d + k];
+            counts[best_b[i]]++;
+        }
+    for (int i = 0; i < n_b; i++)
+        if (counts[i] > 1) {
+            float c = (float)counts[i];
+            for (int k = 0; k < d; k++) merged[(size_t)i * d + k] /= c;
+        }
+    for (int i = 0; i < n_b; i++) umap[2 * i + 1] = i;
+    int slot = n_b;
+    for (int i = 0; i < n_a; i++) {
+        if (rank[i] < r) {
+            umap[2 * i] = best_b[i];
+        } else {
+            memcpy(merged + (size_t)slot * d, a + (size_t)i * d, sizeof(float) * d);
+            umap[2 * i] = slot++;
+        }
+    }
+    free(a); free(bt); free(sim); free(an); free(bn); free(best_sim); free(best_b); free(rank); free(counts);
+    return seq - r;
+}
+
+/* tome_unmerge, encoder.rs:1509-1517: out[pos] = merged[umap[pos]]. */
+void ref_tome_unmerge(const float *merged, const int32_t *umap, int seq, int d, float *out) {
+    for (int p = 0; p < seq; p++) memcpy(out + (size_t)p * d, merged + (size_t)umap[p] * d, sizeof(float) * d);
+}
+
+/* forward_time_major, encoder.rs:1520-1677 (CPU blocks).  ToMe (encoder.rs:
+ * 1590-1632, single-shot schedule): with tome_r > 0, after block tome_after
+ * (0-based) the rows merge by ref_tome_merge when seq > r + 2 and
+ * seq - r >= 128 (the floor), the later blocks run on the merged rows and
+ * ln_post follows the unmerge. */
+int ref_encoder_forward_tome(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run,
+                             int tome_r, int tome_after) {
     if (n_frames <= 0 || n_frames % 2 || n_frames > 2 * e->nctx) return FWHIP_ERR_INVALID;
     int d = e->d, t1, t2;
     float *a = (float *)malloc(sizeof(float) * (size_t)n_frames * d);
@@ -784,12 +884,31 @@ int ref_encoder_forward(const ref_encoder *e, const float *x, int n_frames, floa
     for (int64_t r = 0; r < t2; r++)
         for (int j = 0; j < d; j++) out[r * d + j] += e->pos_emb[r * d + j];
     int n_run = n_layers_run < 0 || n_layers_run > e->L ? e->L : n_layers_run;
-    for (int li = 0; li < n_run; li++) encoder_block(e, &e->layers[li], out, t2);
+    float *xm = NULL;
+    int32_t *umap = NULL;
+    int rows = t2;
+    for (int li = 0; li < n_run; li++) {
+        encoder_block(e, &e->layers[li], xm ? xm : out, rows);
+        if (tome_r > 0 && !xm && li == tome_after && rows > tome_r + 2 && rows - tome_r >= 128) {
+            xm = (float *)malloc(sizeof(float) * (size_t)t2 * d);
+            umap = (int32_t *)malloc(sizeof(int32_t) * t2);
+            rows = ref_tome_merge(out, t2, d, tome_r, xm, umap);
+        }
+    }
+    if (xm) {
+        ref_tome_unmerge(xm, umap, t2, d, out);
+        free(xm);
+        free(umap);
+    }
     float *y = (float *)malloc(sizeof(float) * (size_t)t2 * d);
     ref_layer_norm(out, y, t2, d, e->ln_post_w, e->ln_post_b, LN_EPS);
     memcpy(out, y, sizeof(float) * (size_t)t2 * d);
     free(y);
     return FWHIP_OK;
+}
+
+int ref_encoder_forward(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run) {
+    return ref_encoder_forward_tome(e, x, n_frames, out, n_layers_run, 0, 0);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -83,6 +83,10 @@ void ref_encoder_free(ref_encoder *e);
  * runs every block (encoder_layer_limit semantics otherwise). */
 int ref_encoder_forward(const ref_encoder *e, const float *x, int n_frames, float *out,
                         int n_layers_run);
+int ref_encoder_forward_tome(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run,
+                             int tome_r, int tome_after);
+int ref_tome_merge(const float *x, int seq, int d, int r, float *merged, int32_t *umap);
+void ref_tome_unmerge(const float *merged, const int32_t *umap, int seq, int d, float *out);
 void ref_mel_window(const float *full_mel, int n_mel, int64_t mel_frames, int64_t frame_offset,
                     int n_frames, float *out);
 /* one encoder int8 GEMM, for per-GEMM parity: i32 accumulators and epilogue */

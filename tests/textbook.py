@@ -47,6 +47,9 @@ MUTATIONS = (
     "pos_emb_shift",      # decoder positional embedding off by one
     "ln_eps_1e-3",        # LayerNorm epsilon 1e-3 instead of 1e-5
     "gelu_erf",           # erf GELU instead of the tanh approximation
+    "tome_no_average",    # ToMe adds merged rows into their partner without dividing by the count
+    "tome_merge_lowest",  # ToMe merges the r least similar A rows instead of the most similar
+    "tome_dot_not_cos",   # ToMe ranks by the raw dot product instead of the cosine
 )
 
 
@@ -119,6 +122,57 @@ def mha(q, k, v, n_head, nm: Numerics, causal_offset=None, kv_round=None):
     return out
 
 
+def tome_merge(x, r, nm: Numerics | None = None):
+    """Token merging by bipartite soft matching (Bolya et al. 2023, "Token
+    Merging: Your ViT but Faster"), single shot: even rows form set A, odd rows
+    set B; each A row's edge goes to its most cosine-similar B row (the first
+    one on a tie); the r A rows with the most similar edges are averaged into
+    their B partners (a B row's result is the mean of itself and every A row
+    merged into it); the merged sequence is the B rows followed by the kept A
+    rows in their order.  Returns the merged rows, the map from each original
+    row to its merged row, and the decision margins (how far the r-th best edge
+    is from the next, and the smallest best-vs-second-best gap of a merged row)
+    so a caller can check that float32 and float64 must agree on the decisions."""
+    nm = nm or Numerics()
+    x = np.asarray(x, np.float64)
+    seq = x.shape[0]
+    A, B = x[0::2], x[1::2]
+    n_a, n_b = A.shape[0], B.shape[0]
+    r = min(r, n_a, seq - 1)
+    sim = A @ B.T
+    if not nm.m("tome_dot_not_cos"):
+        sim = sim / np.maximum(np.linalg.norm(A, axis=1), 1e-9)[:, None]
+        sim = sim / np.maximum(np.linalg.norm(B, axis=1), 1e-9)[None, :]
+    best_b = np.argmax(sim, axis=1)
+    best = sim[np.arange(n_a), best_b]
+    order = sorted(range(n_a), key=lambda a: (best[a] if nm.m("tome_merge_lowest") else -best[a], a))
+    chosen = set(order[:r])
+    merged = [B[b].copy() for b in range(n_b)]
+    count = [1] * n_b
+    for a in range(n_a):
+        if a in chosen:
+            merged[best_b[a]] = merged[best_b[a]] + A[a]
+            count[best_b[a]] += 1
+    if not nm.m("tome_no_average"):
+        merged = [merged[b] / count[b] for b in range(n_b)]
+    umap = np.zeros(seq, np.int64)
+    umap[1::2] = np.arange(n_b)
+    kept = []
+    for a in range(n_a):
+        if a in chosen:
+            umap[2 * a] = best_b[a]
+        else:
+            umap[2 * a] = n_b + len(kept)
+            kept.append(A[a])
+    out = np.array(merged + kept).reshape(seq - r, x.shape[1])
+    sb = np.sort(best)[::-1]
+    second = np.sort(sim, axis=1)[:, -2] if n_b > 1 else best - 1.0
+    info = {"rank_margin": float(sb[r - 1] - sb[r]) if 0 < r < n_a else float("inf"),
+            "edge_margin": float(np.min((best - second)[sorted(chosen)])) if chosen else float("inf"),
+            "umap": umap.copy()}
+    return out, umap, info
+
+
 class Encoder:
     """Whisper audio encoder: two GELU convs (k=3, pad 1; strides 1, 2), sinusoid
     slot filled by the file's positional embedding, pre-LN transformer blocks,
@@ -169,7 +223,7 @@ class Encoder:
         f = nm.gelu(self.linear(h, p + ".mlp.0", bias=not nm.m("no_fc1_bias")))
         return x + self.linear(f, p + ".mlp.2", bias=not nm.m("no_fc2_bias"))
 
-    def forward(self, mel_time_major, n_layers=None):
+    def forward(self, mel_time_major, n_layers=None, tome_r=0, tome_after=3, info=None):
         nm = self.nm
         x = np.asarray(mel_time_major, np.float64)
         x = nm.gelu(self.conv(x, "encoder.conv1.weight", "encoder.conv1.bias", 1))
@@ -177,8 +231,16 @@ class Encoder:
         if not nm.m("no_pos_emb"):
             x = x + self._g("encoder.positional_embedding")[: x.shape[0]]
         L = self.cfg.n_audio_layer if n_layers is None else n_layers
+        umap = None
         for i in range(L):
             x = self.block(x, i)
+            if tome_r > 0 and umap is None and i == tome_after and x.shape[0] > tome_r + 2 \
+                    and x.shape[0] - tome_r >= 128:
+                x, umap, tinfo = tome_merge(x, tome_r, nm)
+                if info is not None:
+                    info.update(tinfo)
+        if umap is not None:
+            x = x[umap]
         if nm.m("no_ln_post"):
             return x
         return nm.ln(x, self._g("encoder.ln_post.weight"), self._g("encoder.ln_post.bias"))
