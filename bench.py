@@ -60,12 +60,17 @@ def _args():
     p.add_argument("--tokens", type=int, default=220)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")))
-    p.add_argument("--cpu-runs", type=int, default=3, help="end-to-end runs of one window for the CPU baseline")
+    p.add_argument("--cpu-runs", type=int, default=5, help="end-to-end runs of one window for the CPU baseline")
     p.add_argument("--copy-mb", type=int, default=512)
     p.add_argument("--exact", action="store_true", help="exact mode: bit-identical to the reference's strict mode")
     p.add_argument("--dec-arm", default="f16", choices=["int8", "f16"],
                    help="decoder arm (f16: the tied f16 logits head, token-stable; int8: the reference default)")
     p.add_argument("--no-verify", action="store_true", help="skip the exact-mode token check of the job")
+    p.add_argument("--tome", type=int, default=0,
+                   help="ToMe rows merged after encoder block 3 (FW_TOME_R; -1: the reference's default rule, "
+                        "500 for large-v3-turbo); 0 = the un-merged encoder")
+    p.add_argument("--no-tome-run", action="store_true",
+                   help="skip the job's second timed run with the reference's default ToMe")
     return p.parse_args()
 
 
@@ -169,16 +174,17 @@ def measured_traffic(which):
         return None, path
 
 
-def verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, n_tokens, filt, got):
+def verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, n_tokens, filt, got, tome=0):
     """The job once more in exact mode (encoder and cross K/V in the reference's
-    strict-parity arithmetic, bit-identical to it), decoded on both arms; returns
-    per arm the exact tokens, and how many of the timed job's windows (got: arm ->
-    tokens) match them."""
+    strict-parity arithmetic, bit-identical to it; tome: the same ToMe setting
+    as the timed job), decoded on each arm; returns per arm the exact tokens, and
+    how many of the timed job's windows (got: arm -> tokens) match them."""
     from franken_whisper_amd import abi, native
 
     cfg = model.cfg
     enc = native.Encoder(ctx, model, abi.ENC_INT8)
     enc.set_exact(True)
+    enc.set_tome(tome, 3)
     states = ctx.empty((W, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
     enc.forward_mel(mel_dev, mel_frames, offsets, nf, states)
     enc.close()
@@ -259,6 +265,8 @@ def main():
         enc = native.Encoder(ctx, model, abi.ENC_F32)
     if enc is not None and a.exact:
         enc.set_exact(True)
+    if enc is not None:
+        enc.set_tome(a.tome, 3)
     tk = model.tokens
     filt = tk.filter()
     prompt = tk.sot_sequence(language_id=0)
@@ -331,6 +339,7 @@ def main():
     stats = {k: ctx.kernel_stats(k) for k in CLASSES}
     ctx.timing(False)
     ms_per_step = elapsed * 1e3 / a.steps
+    last_tokens_main = last_tokens[0]
 
     rooflines = []
     for k, (n, ms, units) in stats.items():
@@ -375,12 +384,42 @@ def main():
         int8_arm = {"value": round(30.0 * W / (ms8 * 1e-3), 2), "ms_per_step": round(ms8, 3), "tokens": toks8}
         st8.close()
         dec8.close()
+    # the same job with the reference's shipped large-v3-turbo encoder (ToMe on
+    # by default: 500 of 1500 rows merged after block 3, encoder.rs:1264-1337),
+    # timed the same way, with its own exact-mode token check
+    tome_run = None
+    if a.workload == "job" and a.tome == 0 and not a.no_tome_run and not a.no_verify:
+        enc.set_tome(-1, 3)
+        for i in range(a.warmup + a.steps):
+            if i == a.warmup:
+                ctx.synchronize()
+                tt = time.perf_counter()
+            step()
+        ctx.synchronize()
+        mst = (time.perf_counter() - tt) * 1e3 / a.steps
+        tome_run = {"value": round(30.0 * W / (mst * 1e-3), 2), "ms_per_step": round(mst, 3),
+                    "tokens": last_tokens[0]}
+        t = time.perf_counter()
+        encode()
+        ctx.synchronize()
+        tome_run["encoder_ms"] = round((time.perf_counter() - t) * 1e3, 2)
+        enc.set_tome(0, 3)
     verify = None
     if a.workload == "job" and not a.no_verify:
-        got = {abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8: last_tokens[0]}
+        got = {abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8: last_tokens_main}
         if int8_arm:
             got[abi.DEC_INT8] = int8_arm.pop("tokens")
-        verify = verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, a.tokens, filt, got)
+        verify = verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, a.tokens, filt, got,
+                               tome=a.tome)
+        if tome_run:
+            arm_m = abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8
+            vt = verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, a.tokens, filt,
+                               {arm_m: tome_run.pop("tokens")}, tome=-1)
+            tome_run["tokens_identical_to_exact"] = f"{vt[arm_m][1]}/{W} windows"
+            tome_run["note"] = ("the reference's default large-v3-turbo encoder: ToMe merges 500 of 1500 rows per "
+                                "window after block 3 (tome_r_for, encoder.rs:1264-1337; not byte-exact against "
+                                "the un-merged encoder, WER-certified there); tokens checked against exact mode "
+                                "with the same ToMe")
 
     audio_s = 30.0 * W
     out = {
@@ -438,12 +477,14 @@ def main():
         int8_arm["note"] = ("int8 decoder arm (the reference's default): every linear re-quantizes its input to int8, "
                             "so the sub-ulp f32 reordering of fast mode moves tokens; exact mode is bit-identical")
         out["int8_decoder_arm"] = int8_arm
+    if tome_run:
+        out["tome_default_job"] = tome_run
     out["setup_s"] = round(t_setup, 1)
     if a.workload == "job" and not a.no_cpu_baseline:
         cb, cpu_toks = cpu_baseline(model, W, a.tokens, a.cpu_threads, a.cpu_runs, arm_main)
         out["cpu_baseline"] = cb
         out["gpu_over_cpu"] = round(out["value"] / cb["value"], 1)
-        g0 = last_tokens[0][0] if last_tokens[0] else None
+        g0 = last_tokens_main[0] if last_tokens_main else None
         out["tokens_match_cpu_oracle"] = {
             "window": 0, "identical": bool(g0 is not None and np.array_equal(np.asarray(g0), np.asarray(cpu_toks))),
             "gpu_tokens": int(len(g0)) if g0 is not None else 0, "cpu_tokens": int(len(cpu_toks))}
