@@ -44,7 +44,7 @@ def _classes():
         abi.K_ENC_GEMM_F32: ("encoder f16-pair GEMM (k_gemm2, conv stem)", "mfma", "f16", None),
         abi.K_ENC_ATTN: ("encoder attention (k_attention2, f16 pairs)", "mfma", "f16", None),
         abi.K_DEC_CROSS: ("decoder cross K/V precompute (k_gemm2 f16 pairs, all layers)", "mfma", "f16", None),
-        abi.K_DEC_STEP: ("decoder step (graph replay of one sampled step: 30 kernels, weights + cross K/V + KV cache)",
+        abi.K_DEC_STEP: ("decoder step (graph replay of one sampled step: weights + cross K/V + KV cache)",
                          "hbm", None, "dec_step"),
         abi.K_DEC_LOGITS: ("decoder logits GEMV of the prompt row (k_gemv_i8m)", "hbm", None, None),
     }
@@ -157,7 +157,8 @@ AUDIO_SEED = 1234
 # rocprofv3 counter measurements of the job's kernels, per class: file and the
 # key of its "key: bytes" line (the counters cannot be read inside a timed run)
 TRAFFIC = {"enc_gemm_i8": ("profiles/k_gemm_pi8_int8_encoder_job.md", "traffic_bytes_per_launch"),
-           "dec_step": ("profiles/decode_step_int8_10_streams.md", "traffic_bytes_per_step")}
+           "dec_step_int8": ("profiles/decode_step_int8_10_streams.md", "traffic_bytes_per_step"),
+           "dec_step_f16": ("profiles/decode_step_f16_10_streams.md", "traffic_bytes_per_step")}
 
 
 def measured_traffic(which):
@@ -356,7 +357,9 @@ def main():
             ach = units / (ms * 1e-3) / 1e9
             r.update(achieved=round(ach, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
                      traffic=None, algorithmic_bytes=round(units / n))
-        if tkey and a.workload == "job" and W == 10:
+        if tkey == "dec_step":
+            tkey = "dec_step_f16" if a.dec_arm == "f16" else "dec_step_int8"
+        if tkey and a.workload in ("job", "decode") and W == 10:
             tb, path = measured_traffic(tkey)
             if tb:
                 r["traffic"] = tb
