@@ -63,6 +63,22 @@ SIGNATURES = {
     "fwhip_mel_frames": (C.c_int64, [C.c_int64]),
     "fwhip_log_mel": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
     "fwhip_log_mel_noalloc": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
+    "fwhip_ggml_open": (C.c_int32, [C.c_char_p, C.POINTER(_vp)]),
+    "fwhip_ggml_open_bytes": (C.c_int32, [C.c_char_p, C.c_uint64, C.POINTER(_vp)]),
+    "fwhip_ggml_close": (None, [_vp]),
+    "fwhip_ggml_header": (C.c_int32, [_vp, _i32p]),
+    "fwhip_ggml_filters": (C.c_int32, [_vp, _i32p, _i32p, C.POINTER(C.POINTER(C.c_float))]),
+    "fwhip_ggml_vocab_count": (C.c_int32, [_vp]),
+    "fwhip_ggml_vocab_token": (C.c_int32, [_vp, C.c_int32, C.POINTER(C.POINTER(C.c_uint8)),
+                                           C.POINTER(C.c_uint32)]),
+    "fwhip_ggml_tensor_count": (C.c_int32, [_vp]),
+    "fwhip_ggml_tensor_name": (C.c_char_p, [_vp, C.c_int32]),
+    "fwhip_ggml_tensor_info": (C.c_int32, [_vp, C.c_char_p, _i32p, _i32p, _i64p, C.POINTER(C.c_uint64)]),
+    "fwhip_ggml_tensor_raw": (C.c_int32, [_vp, C.c_char_p, _vp, C.c_uint64]),
+    "fwhip_ggml_tensor_f32": (C.c_int32, [_vp, _vp, C.c_char_p, _vp, C.c_int64]),
+    "fwhip_dequant": (C.c_int32, [_vp, C.c_int32, _vp, C.c_uint64, C.c_int64, _vp]),
+    "fwhip_encoder_load_ggml": (C.c_int32, [_vp, _vp, C.c_int32, C.POINTER(_vp)]),
+    "fwhip_decoder_load_ggml": (C.c_int32, [_vp, _vp, C.c_int32, C.POINTER(_vp)]),
 }
 
 _lib = None
@@ -198,16 +214,98 @@ class Context:
             self.h = None
 
 
+class GgmlFile:
+    """A ggml model file (GgmlModel, ggml.rs:582-600): the directory is scanned
+    on open, payloads are read on demand.  `source` is a path, or bytes for
+    GgmlModel::from_bytes."""
+
+    def __init__(self, source):
+        h = _vp()
+        if isinstance(source, (bytes, bytearray, memoryview)):
+            data = bytes(source)
+            check(lib().fwhip_ggml_open_bytes(data, len(data), C.byref(h)))
+        else:
+            check(lib().fwhip_ggml_open(os.fsencode(source), C.byref(h)))
+        self.h = h
+
+    @property
+    def hparams(self) -> list:
+        hp = (C.c_int32 * 11)()
+        check(lib().fwhip_ggml_header(self.h, hp))
+        return list(hp)
+
+    @property
+    def cfg(self):
+        """The model shape as the attribute names of WhisperHParams."""
+        from types import SimpleNamespace
+        keys = ("n_vocab", "n_audio_ctx", "n_audio_state", "n_audio_head", "n_audio_layer", "n_text_ctx",
+                "n_text_state", "n_text_head", "n_text_layer", "n_mels", "ftype")
+        return SimpleNamespace(name="ggml", **dict(zip(keys, self.hparams)))
+
+    def filters(self) -> np.ndarray:
+        nm, nf, p = C.c_int32(), C.c_int32(), C.POINTER(C.c_float)()
+        check(lib().fwhip_ggml_filters(self.h, C.byref(nm), C.byref(nf), C.byref(p)))
+        n = nm.value * nf.value
+        out = np.empty((nm.value, nf.value), np.float32)
+        if n:
+            C.memmove(out.ctypes.data, p, 4 * n)
+        return out
+
+    def vocab(self) -> list:
+        out = []
+        for i in range(lib().fwhip_ggml_vocab_count(self.h)):
+            p, n = C.POINTER(C.c_uint8)(), C.c_uint32()
+            check(lib().fwhip_ggml_vocab_token(self.h, i, C.byref(p), C.byref(n)))
+            out.append(C.string_at(p, n.value) if n.value else b"")
+        return out
+
+    def names(self) -> list:
+        return [lib().fwhip_ggml_tensor_name(self.h, i).decode() for i in range(lib().fwhip_ggml_tensor_count(self.h))]
+
+    def info(self, name: str):
+        """(logical shape, element type, payload bytes)"""
+        t, nd, n = C.c_int32(), C.c_int32(), C.c_uint64()
+        shape = (C.c_int64 * 4)()
+        check(lib().fwhip_ggml_tensor_info(self.h, name.encode(), C.byref(t), C.byref(nd), shape, C.byref(n)))
+        return [int(shape[i]) for i in range(nd.value)], t.value, n.value
+
+    def raw(self, name: str) -> bytes:
+        _, _, n = self.info(name)
+        buf = C.create_string_buffer(max(n, 1))
+        check(lib().fwhip_ggml_tensor_raw(self.h, name.encode(), buf, n))
+        return buf.raw[:n]
+
+    def tensor_f32(self, ctx: "Context", name: str) -> "DeviceArray":
+        shape, _, _ = self.info(name)
+        out = ctx.empty(tuple(shape), np.float32)
+        check(lib().fwhip_ggml_tensor_f32(ctx.h, self.h, name.encode(), out.ptr, int(np.prod(shape))))
+        return out
+
+    def close(self):
+        if self.h:
+            lib().fwhip_ggml_close(self.h)
+            self.h = None
+
+
+def dequant(ctx: "Context", dtype: int, raw_dev: "DeviceArray", raw_bytes: int, n: int, out_dev: "DeviceArray"):
+    """fwhip_dequant: decode a payload already on the device."""
+    check(lib().fwhip_dequant(ctx.h, dtype, raw_dev.ptr, raw_bytes, n, out_dev.ptr))
+
+
 class Encoder:
     """EncoderWeights + forward (encoder.rs:764, 1224) on the GPU."""
 
     def __init__(self, ctx: Context, model, precision: int):
         self.ctx, self.cfg = ctx, model.cfg
-        self._desc = model.encoder_weights()
-        h = _vp()
-        check(lib().fwhip_encoder_load(ctx.h, C.byref(self._desc), precision, C.byref(h)))
-        self.h = h
         self.precision = precision
+        h = _vp()
+        if isinstance(model, GgmlFile):
+            self.cfg = model.cfg
+            check(lib().fwhip_encoder_load_ggml(ctx.h, model.h, precision, C.byref(h)))
+        else:
+            self._desc = model.encoder_weights()
+            check(lib().fwhip_encoder_load(ctx.h, C.byref(self._desc), precision, C.byref(h)))
+        self.h = h
 
     def forward_time_major(self, x_dev: DeviceArray, n_windows: int, n_frames: int, out_dev: DeviceArray):
         rec = abi.ExecRecord()
@@ -248,12 +346,17 @@ class Decoder:
     """DecoderWeights (decoder.rs:752-932) resident on the GPU."""
 
     def __init__(self, ctx: Context, model, arm: int):
-        self.ctx, self.cfg = ctx, model.cfg
-        self._desc = model.decoder_weights()
-        h = _vp()
-        check(lib().fwhip_decoder_load(ctx.h, C.byref(self._desc), arm, C.byref(h)))
-        self.h = h
         self.arm = arm
+        h = _vp()
+        if isinstance(model, GgmlFile):
+            self.cfg = model.cfg
+            check(lib().fwhip_decoder_load_ggml(ctx.h, model.h, arm, C.byref(h)))
+        else:
+            self.ctx, self.cfg = ctx, model.cfg
+            self._desc = model.decoder_weights()
+            check(lib().fwhip_decoder_load(ctx.h, C.byref(self._desc), arm, C.byref(h)))
+        self.ctx = ctx
+        self.h = h
 
     def set_exact(self, exact: bool):
         """Strict sequential-k cross K/V precompute (bit-exact logits) or the fast

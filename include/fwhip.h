@@ -173,6 +173,7 @@ fwhip_status fwhip_request_cancel(fwhip_ctx *ctx);
 #define FWHIP_K_DEC_LOGITS 5
 #define FWHIP_K_DEC_CROSS 6  /* cross K/V precompute (fast mode) */
 #define FWHIP_K_DEC_STEP 7   /* one sampled decoder step of the greedy loop */
+#define FWHIP_K_DEQUANT 8    /* ggml payload decode (fwhip_dequant, fwhip_ggml_tensor_f32) */
 fwhip_status fwhip_kernel_timing(fwhip_ctx *ctx, int32_t enable);
 fwhip_status fwhip_kernel_stats(fwhip_ctx *ctx, int32_t kclass, int64_t *launches,
                                 double *total_ms, double *work_units);
@@ -367,6 +368,89 @@ fwhip_status fwhip_log_mel(fwhip_ctx *ctx, const float *samples_dev, int64_t n_s
  * overlap on one GPU (two contexts, two threads) race. */
 fwhip_status fwhip_log_mel_noalloc(fwhip_ctx *ctx, const float *samples_dev, int64_t n_samples,
                                    const float *filters_dev, int32_t n_mel, int32_t n_fft_bins, float *mel_dev);
+
+/* ---- ggml model files ---------------------------------------------------- */
+
+/* A whisper.cpp ggml model file (src/native_engine/ggml.rs:1-47 layout: magic,
+ * eleven i32 hparams, mel filterbank, byte-level vocab, tensor directory with
+ * ggml-order dims, no padding).  Opening scans the directory only; payloads
+ * stay in the file and are read when a tensor is asked for. */
+typedef struct fwhip_ggml fwhip_ggml;
+
+/* Tensor element types (the file's ttype codes, ggml.rs:1068-1087). */
+#define FWHIP_GGML_F32 0
+#define FWHIP_GGML_F16 1
+#define FWHIP_GGML_Q4_0 2
+#define FWHIP_GGML_Q4_1 3
+#define FWHIP_GGML_Q5_0 6
+#define FWHIP_GGML_Q5_1 7
+#define FWHIP_GGML_Q8_0 8
+#define FWHIP_GGML_Q2_K 10
+#define FWHIP_GGML_Q3_K 11
+#define FWHIP_GGML_Q4_K 12
+#define FWHIP_GGML_Q5_K 13
+#define FWHIP_GGML_Q6_K 14
+
+/* Replaces GgmlModel::load (ggml.rs:903-950, the streamed pread scan of
+ * 1160-1220): FWHIP_ERR_INVALID with the reference's message for a bad magic,
+ * a truncated or malformed structure (negative counts, n_dims outside 1..=4,
+ * element counts that are not a multiple of the type's block), and
+ * FWHIP_ERR_UNSUPPORTED for an ftype or tensor type the reference does not
+ * decode; FWHIP_ERR_GENERIC ("io: ...") when the file cannot be opened. */
+fwhip_status fwhip_ggml_open(const char *path, fwhip_ggml **out);
+/* GgmlModel::from_bytes (ggml.rs:953-955): the same parse over a copy of `len`
+ * bytes of caller memory. */
+fwhip_status fwhip_ggml_open_bytes(const void *data, uint64_t len, fwhip_ggml **out);
+void fwhip_ggml_close(fwhip_ggml *g);
+
+/* hparams11: n_vocab, n_audio_ctx, n_audio_state, n_audio_head, n_audio_layer,
+ * n_text_ctx, n_text_state, n_text_head, n_text_layer, n_mels, ftype
+ * (WhisperHParams, mod.rs:56-77). */
+fwhip_status fwhip_ggml_header(const fwhip_ggml *g, int32_t *hparams11);
+/* GgmlModel::filters (MelFilterbank, [n_mel, n_fft_bins] row-major); `data`
+ * stays valid until fwhip_ggml_close. */
+fwhip_status fwhip_ggml_filters(const fwhip_ggml *g, int32_t *n_mel, int32_t *n_fft_bins, const float **data);
+/* GgmlModel::vocab_tokens: the count stored in the file and token `id`'s raw
+ * bytes (valid until fwhip_ggml_close). */
+int32_t fwhip_ggml_vocab_count(const fwhip_ggml *g);
+fwhip_status fwhip_ggml_vocab_token(const fwhip_ggml *g, int32_t id, const uint8_t **bytes, uint32_t *len);
+/* GgmlModel::tensor_names (ggml.rs:1416, sorted) and tensor (ggml.rs:1424):
+ * logical row-major shape (ggml's ne[] reversed; unused trailing entries 1),
+ * element type and payload bytes.  Unknown names: FWHIP_ERR_INVALID
+ * "unknown tensor '<name>'". */
+int32_t fwhip_ggml_tensor_count(const fwhip_ggml *g);
+const char *fwhip_ggml_tensor_name(const fwhip_ggml *g, int32_t i);
+fwhip_status fwhip_ggml_tensor_info(const fwhip_ggml *g, const char *name, int32_t *dtype, int32_t *n_dims,
+                                    int64_t *shape4, uint64_t *byte_len);
+/* The payload bytes as stored (TensorBytes, ggml.rs:689-740) into `host` (cap
+ * bytes at least byte_len). */
+fwhip_status fwhip_ggml_tensor_raw(const fwhip_ggml *g, const char *name, void *host, uint64_t cap);
+
+/* GgmlModel::tensor_f32 (ggml.rs:1478-1632) on the GPU: the payload is read
+ * into pinned staging, copied to the device and decoded there into out_dev
+ * (n_elements f32, 4-byte aligned) in the reference's arithmetic, bit for bit. */
+fwhip_status fwhip_ggml_tensor_f32(fwhip_ctx *ctx, const fwhip_ggml *g, const char *name, float *out_dev,
+                                   int64_t n_elements);
+/* The decode step alone: `raw_dev` holds a payload of element type `dtype`
+ * already on the device (raw_bytes must equal the type's byte length for
+ * n_elements, ggml_byte_len ggml.rs:386-474; both pointers 4-byte aligned).
+ * Enqueued on the context stream. */
+fwhip_status fwhip_dequant(fwhip_ctx *ctx, int32_t dtype, const void *raw_dev, uint64_t raw_bytes,
+                           int64_t n_elements, float *out_dev);
+
+/* EncoderWeights::from_ggml (encoder.rs:764-1029) into fwhip_encoder_load:
+ * the reference's tensor names, shapes and messages.  Vectors may be stored in
+ * any type (decoded as tensor_f32 does).  Linears and conv kernels are taken
+ * as binary16: f16-stored ones as they are, others when every value is a
+ * binary16 value (the reference then computes on the same numbers), else
+ * FWHIP_ERR_UNSUPPORTED "cpu:ggml-<type>-linear: ..." (the caller's CPU route).
+ * Cancellation (fwhip_request_cancel) is checked between blocks. */
+fwhip_status fwhip_encoder_load_ggml(fwhip_ctx *ctx, const fwhip_ggml *g, int32_t precision, fwhip_encoder **out);
+/* DecoderWeights::from_ggml (decoder.rs:752-932) into fwhip_decoder_load.  The
+ * GPU arms are the reference's f16-stored arms (load_linear / load_embedding,
+ * decoder.rs:599-720), so every linear and the token embedding must be stored
+ * as f16 (else FWHIP_ERR_UNSUPPORTED "cpu:ggml-<type>-linear: ..."). */
+fwhip_status fwhip_decoder_load_ggml(fwhip_ctx *ctx, const fwhip_ggml *g, int32_t arm, fwhip_decoder **out);
 
 #ifdef __cplusplus
 }
