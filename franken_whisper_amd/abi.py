@@ -87,6 +87,15 @@ class Filter(C.Structure):
         "translate", "transcribe", "timestamp_begin", "space_token", "n_languages")]
 
 
+class WindowCfg(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("timestamps", "max_initial_tid", "max_tokens", "n_max", "exact")]
+
+
+class WindowStream(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("seek_cs", "seek_end_cs", "has_prior_segments", "n_tokens", "result_len",
+                                         "has_ts", "seek_delta_cs", "n_exact")] + [("no_speech_logprob", C.c_float)]
+
+
 class ExecRecord(C.Structure):
     _fields_ = [("route", C.c_char * 48), ("precision", C.c_int32), ("n_windows", C.c_int32),
                 ("device_ms", C.c_double)]

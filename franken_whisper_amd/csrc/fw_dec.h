@@ -140,3 +140,151 @@ __device__ __forceinline__ bool dec_masked(int i, const fwhip_filter &f, int ini
     if (i >= f.sot + 1 && i <= f.sot + f.n_languages) return true;
     return false;
 }
+
+// ---------------------------------------------------------------------------
+// The same sequential f32 sum ((0 + v[0]) + v[1]) + ... of n <= 64 * SW_MAXC
+// values v[i] >= 0 (finite, in LDS, readable up to index (n+3) & ~3), by one
+// whole wave, bit-identical to the one-thread loop.
+//
+// While a running sum s stays in one binade [2^k, 2^(k+1)] its bit pattern
+// moves by integers: s + e rounds to the grid of ulp 2^(k-23), and the step
+// depends on s only through the parity of its last bit (ties go to even).  So
+// a lane's chunk of c consecutive values acts, on any start in binade k, as
+// bits -> bits + D[bits & 1], and running the chunk's own f32 adds from the
+// two lowest starts 2^k and 2^k + ulp gives D[0] and D[1] exactly.
+//  1. lane l takes values [l*c, l*c + c) (c = n/64 rounded up to 4), sums
+//     them roughly and a wave scan gives its rough start P;
+//  2. a lane whose rough range [P, P + chunk] sits inside one binade with a
+//     2^-10 margin runs its chunk from both starts (else it is left to step 4);
+//  3. consecutive such lanes of one binade compose their (D[0], D[1]) maps in
+//     a segmented wave scan: run [a, b] maps parity p to D[p] of the whole run;
+//  4. walking the runs in order, a run applies when the exact s lies in its
+//     binade and s + D stays <= 2^(k+1) (monotone sums: then every partial
+//     sum of the run stayed in the binade); otherwise its values are added one
+//     by one, as the reference does.
+// Correctness rests on step 4's exact check alone; steps 1-2 only choose
+// which lanes to try.  Every lane of the wave must call it (n uniform).
+#define SW_MAXC 24
+__device__ __forceinline__ float fw_seq_sum_wave(const float *v, int n) {
+    const int lane = threadIdx.x & 63;
+    const int c = ((((n + 63) >> 6) + 3) & ~3) > 0 ? ((((n + 63) >> 6) + 3) & ~3) : 4; // values per lane, <= SW_MAXC
+    const int n4 = (n + 3) >> 2;                                                     // readable float4 groups
+    float e[SW_MAXC];
+#pragma unroll
+    for (int q = 0; q < SW_MAXC / 4; q++) {
+        const int g = (lane * c >> 2) + q; // float4 group of this lane's chunk
+        float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (4 * q < c && g < n4) x = ((const float4 *)v)[g];
+        const int i0 = lane * c + 4 * q;
+        e[4 * q + 0] = 4 * q + 0 < c && i0 + 0 < n ? x.x : 0.0f;
+        e[4 * q + 1] = 4 * q + 1 < c && i0 + 1 < n ? x.y : 0.0f;
+        e[4 * q + 2] = 4 * q + 2 < c && i0 + 2 < n ? x.z : 0.0f;
+        e[4 * q + 3] = 4 * q + 3 < c && i0 + 3 < n ? x.w : 0.0f;
+    }
+    // 1. rough chunk sum and rough start
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SW_MAXC; i++) t += e[i];
+    float inc = t;
+#pragma unroll
+    for (int dlt = 1; dlt < 64; dlt <<= 1) {
+        const float y = __shfl_up(inc, dlt, 64);
+        if (lane >= dlt) inc += y;
+    }
+    const float P = inc - t;
+    // 2. the chunk's map on its guessed binade
+    const uint32_t pb = __float_as_uint(P);
+    const int ex = (int)(pb >> 23);
+    const uint32_t lo = (uint32_t)ex << 23, hi = (uint32_t)(ex + 1) << 23;
+    bool ok = ex >= 1 && ex <= 253 && P >= __uint_as_float(lo) * 1.0009765625f &&
+              P + t <= __uint_as_float(hi) * 0.9990234375f;
+    float s0 = __uint_as_float(lo), s1 = __uint_as_float(lo + 1);
+#pragma unroll
+    for (int i = 0; i < SW_MAXC; i++) {
+        s0 = s0 + e[i];
+        s1 = s1 + e[i];
+    }
+    ok = ok && __float_as_uint(s0) <= hi && __float_as_uint(s1) <= hi;
+    int d0 = (int)(__float_as_uint(s0) - lo), d1 = (int)(__float_as_uint(s1) - (lo + 1));
+    // 3. runs: consecutive ok lanes of one binade; any other lane is a run of its own
+    const uint32_t key = ok ? lo : (0x80000000u | (uint32_t)lane);
+    const uint32_t kprev = __shfl_up(key, 1, 64);
+    const bool head = lane == 0 || key != kprev;
+    int rs = head ? lane : 0; // first lane of this lane's run
+#pragma unroll
+    for (int dlt = 1; dlt < 64; dlt <<= 1) {
+        const int y = __shfl_up(rs, dlt, 64);
+        if (lane >= dlt) rs = max(rs, y);
+    }
+#pragma unroll
+    for (int dlt = 1; dlt < 64; dlt <<= 1) {
+        const int a0 = __shfl_up(d0, dlt, 64), a1 = __shfl_up(d1, dlt, 64);
+        if (lane - dlt >= rs) {
+            // [.., lane - dlt] then [.., lane]
+            const int n0 = a0 + ((a0 & 1) ? d1 : d0);
+            const int n1 = a1 + (((1 + a1) & 1) ? d1 : d0);
+            d0 = n0;
+            d1 = n1;
+        }
+    }
+    // 4. walk the runs (uniform)
+    unsigned long long heads = __builtin_amdgcn_ballot_w64(head);
+    float s = 0.0f;
+    while (heads) {
+        const int a = __builtin_ctzll(heads);
+        heads &= heads - 1;
+        const int b = heads ? __builtin_ctzll(heads) - 1 : 63;
+        const bool rok = __builtin_amdgcn_readlane((int)ok, b) != 0;
+        bool done = false;
+        if (rok) {
+            const uint32_t rlo = (uint32_t)__builtin_amdgcn_readlane((int)lo, b), rhi = rlo + (1u << 23);
+            const uint32_t sb = __float_as_uint(s);
+            const uint32_t D = (uint32_t)((sb & 1) ? __builtin_amdgcn_readlane(d1, b) : __builtin_amdgcn_readlane(d0, b));
+            if (sb >= rlo && sb < rhi && sb + D <= rhi) {
+                s = __uint_as_float(sb + D);
+                done = true;
+            }
+        }
+        if (!done) {
+            // the run's values one by one, in order: each lane's chunk is read
+            // again from LDS (one broadcast address per read, all reads issued
+            // before the adds); values past the chunk or past n count as +0,
+            // which leaves the non-negative s unchanged
+            for (int q = a; q <= b; q++) {
+                float4 r[SW_MAXC / 4];
+                if (c == SW_MAXC && (q + 1) * c <= n) {
+                    // a whole chunk of SW_MAXC values (the usual case)
+#pragma unroll
+                    for (int i = 0; i < SW_MAXC / 4; i++) r[i] = ((const float4 *)v)[(q * c >> 2) + i];
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < SW_MAXC / 4; i++) {
+                        s = s + r[i].x;
+                        s = s + r[i].y;
+                        s = s + r[i].z;
+                        s = s + r[i].w;
+                    }
+                    continue;
+                }
+#pragma unroll
+                for (int i = 0; i < SW_MAXC / 4; i++) {
+                    const int g = (q * c >> 2) + i;
+                    r[i] = 4 * i < c && g < n4 ? ((const float4 *)v)[g] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+                float x[SW_MAXC];
+#pragma unroll
+                for (int i = 0; i < SW_MAXC / 4; i++) {
+                    const int i0 = q * c + 4 * i;
+                    x[4 * i + 0] = i0 + 0 < n ? r[i].x : 0.0f;
+                    x[4 * i + 1] = i0 + 1 < n ? r[i].y : 0.0f;
+                    x[4 * i + 2] = i0 + 2 < n ? r[i].z : 0.0f;
+                    x[4 * i + 3] = i0 + 3 < n ? r[i].w : 0.0f;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < SW_MAXC; i++) s = s + x[i];
+            }
+        }
+    }
+    return s;
+}

@@ -50,6 +50,11 @@ __device__ __forceinline__ float fw_expf(float x) {
     return fw_expf_tab(x, tab);
 }
 
+__device__ __forceinline__ float fw_logf(float x) {
+    const double tab[32] = FW_LOGF_TAB;
+    return fw_logf_tab(x, tab);
+}
+
 // GELU of the reference (nn.rs:4603-4673): clamp +-10, else f16-indexed table.
 __device__ __forceinline__ float fw_gelu(float v, const float *tab) {
     // The table read is unconditional (every f16 pattern is a valid index) and

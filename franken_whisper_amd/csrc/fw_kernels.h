@@ -50,6 +50,29 @@ void fw_launch_quant_f16_rows(hipStream_t st, const uint16_t *src, int8_t *q, fl
 void fw_launch_step_bookkeeping(hipStream_t st, int *posp, int *initialp, const int32_t *tok, int32_t *hist,
                                 int hist_stride, int step, int ns);
 
+// the window decode loop (dec_window.hip): process_logits in full + argmax +
+// the loop's state per stream, and the post-loop log-probabilities
+#define WIN_MAXTS 1536 // timestamp tokens the forcing rule's sequential sum takes
+struct FwWinCfg {
+    int V, beg, eot, sot, sot_prev, solm, no_speech, no_ts, translate, transcribe, space, n_lang;
+    int timestamps;      // 0: no-timestamps mode (every timestamp masked)
+    int max_initial_tid; // < 0: no initial-timestamp cap
+    int max_tokens;      // the user token budget (min with n_max); <= 0: none
+    int n_max;           // sampled-token cap of the loop
+    int exact;           // decide the forcing rule from the exact log-sum-exp every step
+    int ldr;             // row stride (floats) of the stored rows
+};
+struct FwWinStream {
+    int seek_cs, seek_end_cs, has_prior;                               // set by the host
+    int n_dec, has_ts, seek_delta_cs, result_len, done, n_exact;       // loop state
+};
+void fw_launch_win_select(hipStream_t st, const float *logits, int ldl, const FwWinCfg &c, FwWinStream *ws,
+                          int32_t *hist, int hist_cap, float *rows, uint8_t *forced, float *scratch, int32_t *tok,
+                          int *posp, int *ndone, int ns);
+void fw_launch_win_plogs(hipStream_t st, const float *rows, const float *nsrow, const FwWinCfg &c,
+                         const FwWinStream *ws, const int32_t *hist, int hist_cap, const uint8_t *forced,
+                         float *plogs, float *nslp, int ns);
+
 // int8 decoder arm (dec_fast.hip)
 void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d, int rows,
                         int8_t *xq, float *xs);

@@ -10,6 +10,16 @@
 // range-reduction steps and the three polynomial steps.  An exhaustive
 // comparison over every float in [-110, 90] against the host's expf pins this
 // (zero mismatches; the unfused range reduction differs on 2 inputs).
+//
+// fw_logf: single-precision natural log restated from the same library's
+// published table method (the logf glibc >= 2.28 ships): x = 2^k z with z in
+// [0x1.66p-1, 0x1.66p0), z split into 16 subintervals each with a table pair
+// (1/c, log c), log1p(z/c - 1) from a degree-4 polynomial in double
+// (r + A2 r^2 + A1 r^3 + A0 r^4, evaluated as ((A1 r + A2) + A0 r^2) r^2 +
+// (k ln2 + log c + r)), one final rounding to float.  The reference's
+// log-softmax calls the platform logf (f32::ln -> glibc logf,
+// decode.rs:1690).  An exhaustive comparison over every float in [0, +inf]
+// against the host's logf pins this (zero mismatches, fused and unfused).
 #pragma once
 #include <stdint.h>
 #include <string.h>
@@ -83,7 +93,52 @@ FW_HD static inline float fw_expf_tab(float x, const uint64_t *tab) {
     return (float)y;
 }
 
+// (1/c, log c) of the 16 subintervals, as doubles
+#define FW_LOGF_TAB                                                                                      \
+    {0x1.661ec79f8f3bep+0, -0x1.57bf7808caadep-2, 0x1.571ed4aaf883dp+0, -0x1.2bef0a7c06ddbp-2,          \
+     0x1.49539f0f010bp+0,  -0x1.01eae7f513a67p-2, 0x1.3c995b0b80385p+0, -0x1.b31d8a68224e9p-3,          \
+     0x1.30d190c8864a5p+0, -0x1.6574f0ac07758p-3, 0x1.25e227b0b8eap+0,  -0x1.1aa2bc79c81p-3,            \
+     0x1.1bb4a4a1a343fp+0, -0x1.a4e76ce8c0e5ep-4, 0x1.12358f08ae5bap+0, -0x1.1973c5a611cccp-4,          \
+     0x1.0953f419900a7p+0, -0x1.252f438e10c1ep-5, 0x1p+0,               0x0p+0,                         \
+     0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5,  0x1.ca4b31f026aap-1,  0x1.c5e53aa362eb4p-4,           \
+     0x1.b2036576afce6p-1, 0x1.526e57720db08p-3,  0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3,            \
+     0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2,  0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2}
+
+FW_HD static inline float fw_u2f(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+FW_HD static inline float fw_logf_tab(float x, const double *tab) {
+    const double ln2 = 0x1.62e42fefa39efp-1;
+    const double a0 = -0x1.00ea348b88334p-2, a1 = 0x1.5575b0be00b6ap-2, a2 = -0x1.ffffef20a4123p-2;
+    uint32_t ix = fw_f2u(x);
+    if (ix == 0x3f800000u) return 0.0f;
+    if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+        if (ix * 2 == 0) return -__builtin_inff();                          /* +-0 */
+        if (ix == 0x7f800000u) return x;                                    /* +inf */
+        if ((ix & 0x80000000u) || ix * 2 >= 0xff000000u) return __builtin_nanf(""); /* x < 0, nan */
+        ix = fw_f2u(x * 0x1p23f) - (23u << 23);                             /* subnormal: normalize */
+    }
+    const uint32_t tmp = ix - 0x3f330000u;
+    const int i = (int)((tmp >> 19) % 16);
+    const int k = (int32_t)tmp >> 23;
+    const uint32_t iz = ix - (tmp & 0xff800000u);
+    const double invc = tab[2 * i], logc = tab[2 * i + 1];
+    const double z = (double)fw_u2f(iz);
+    const double r = FW_FMA(z, invc, -1.0);
+    const double y0 = FW_FMA((double)k, ln2, logc);
+    const double r2 = r * r;
+    double y = FW_FMA(a1, r, a2);
+    y = FW_FMA(a0, r2, y);
+    y = FW_FMA(y, r2, y0 + r);
+    return (float)y;
+}
+
 #if !defined(__HIP_DEVICE_COMPILE__)
+static const double fw_logf_tab_host[32] = FW_LOGF_TAB;
+static inline float fw_logf_host(float x) { return fw_logf_tab(x, fw_logf_tab_host); }
 static const uint64_t fw_exp2f_tab_host[32] = FW_EXP2F_TAB;
 static inline float fw_expf_host(float x) { return fw_expf_tab(x, fw_exp2f_tab_host); }
 #endif

@@ -268,6 +268,17 @@ struct fwhip_dstate {
     hipGraphExec_t graph = nullptr;
     fwhip_filter graph_filter;
     std::vector<void *> owned;
+    // the window loop (fwhip_decode_window): filtered rows of every step, the
+    // raw prefill rows, per-stream loop state, forced flags, exact-sum scratch,
+    // log-probabilities; allocated on first use for n_max steps
+    float *w_rows = nullptr, *w_nsrow = nullptr, *w_scratch = nullptr, *w_plogs = nullptr, *w_nslp = nullptr;
+    FwWinStream *w_ws = nullptr;
+    uint8_t *w_forced = nullptr;
+    int *w_ndone = nullptr;
+    int w_nmax = 0, w_ldr = 0;
+    std::vector<void *> w_owned;
+    hipGraphExec_t wgraph = nullptr;
+    FwWinCfg wgraph_cfg;
 };
 
 // Quantize a host f16 [out, inp] matrix to per-row int8 on the device; with
@@ -585,6 +596,8 @@ extern "C" void fwhip_dstate_free(fwhip_dstate *st) {
     hipSetDevice(st->dec->ctx->device);
     hipStreamSynchronize(st->dec->ctx->stream);
     if (st->graph) hipGraphExecDestroy(st->graph);
+    if (st->wgraph) hipGraphExecDestroy(st->wgraph);
+    fw_free_all(st->w_owned);
     fw_free_all(st->owned);
     delete st;
 }
@@ -1025,6 +1038,192 @@ extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *pro
             }
         out_len[s] = n;
         for (int k = 0; k < n_max; k++) out_tokens[(size_t)s * n_max + k] = k < n ? hist[(size_t)s * n_max + k] : 0;
+    }
+    st->len += n_prompt + steps - 1;
+    return FWHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The window loop on the device (decode.rs:3429-3566 with the full
+// process_logits): prefill, then per step the forward of the sampled tokens,
+// the logits and k_win_select (filter, forcing rule, argmax, the loop state);
+// the host only polls for every stream being done.
+
+static fwhip_status win_buffers(fwhip_dstate *st, int n_max) {
+    const fwhip_decoder *dd = st->dec;
+    const int ldr = ((dd->V + 63) / 64) * 64;
+    if (st->w_nmax >= n_max && st->w_ldr == ldr) return FWHIP_OK;
+    HIP_TRY(hipStreamSynchronize(dd->ctx->stream));
+    fw_free_all(st->w_owned);
+    const size_t S = st->S;
+    st->w_rows = (float *)fw_dalloc(st->w_owned, sizeof(float) * S * n_max * ldr);
+    st->w_nsrow = (float *)fw_dalloc(st->w_owned, sizeof(float) * S * ldr);
+    st->w_scratch = (float *)fw_dalloc(st->w_owned, sizeof(float) * S * ldr);
+    st->w_plogs = (float *)fw_dalloc(st->w_owned, sizeof(float) * S * n_max);
+    st->w_nslp = (float *)fw_dalloc(st->w_owned, sizeof(float) * S);
+    st->w_ws = (FwWinStream *)fw_dalloc(st->w_owned, sizeof(FwWinStream) * S);
+    st->w_forced = (uint8_t *)fw_dalloc(st->w_owned, S * n_max);
+    st->w_ndone = (int *)fw_dalloc(st->w_owned, sizeof(int));
+    if (!st->w_rows || !st->w_nsrow || !st->w_scratch || !st->w_plogs || !st->w_nslp || !st->w_ws || !st->w_forced ||
+        !st->w_ndone) {
+        fw_free_all(st->w_owned);
+        st->w_nmax = 0;
+        return fw_fail(FWHIP_ERR_GENERIC, "fwhip_decode_window: device allocation failed");
+    }
+    st->w_nmax = n_max;
+    st->w_ldr = ldr;
+    if (st->wgraph) {
+        hipGraphExecDestroy(st->wgraph);
+        st->wgraph = nullptr;
+    }
+    return FWHIP_OK;
+}
+
+static fwhip_status win_step(fwhip_dstate *st, const FwWinCfg &cfg) {
+    fwhip_status r = dec_forward_row(st, st->tok, false, true, nullptr, false);
+    if (r != FWHIP_OK) return r;
+    fw_launch_win_select(st->dec->ctx->stream, st->logits, st->dec->V, cfg, st->w_ws, st->hist, st->hist_cap,
+                         st->w_rows, st->w_forced, st->w_scratch, st->tok, st->pos, st->w_ndone, st->S);
+    return FWHIP_OK;
+}
+
+static bool win_capture(fwhip_dstate *st, const FwWinCfg &cfg) {
+    static int disabled = -1;
+    if (disabled < 0) disabled = getenv("FWHIP_NO_GRAPH") != nullptr || profiler_preloaded();
+    if (disabled) return false;
+    if (st->wgraph && !memcmp(&st->wgraph_cfg, &cfg, sizeof cfg)) return true;
+    if (st->wgraph) {
+        hipGraphExecDestroy(st->wgraph);
+        st->wgraph = nullptr;
+    }
+    hipStream_t s = st->dec->ctx->stream;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return false;
+    win_step(st, cfg);
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture(s, &g) != hipSuccess || !g) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    st->wgraph = ge;
+    st->wgraph_cfg = cfg;
+    return true;
+}
+
+extern "C" fwhip_status fwhip_decode_window(fwhip_dstate *st, const int32_t *prompt, int32_t n_prompt,
+                                            const fwhip_filter *filter, const fwhip_window_cfg *wc,
+                                            fwhip_window_stream *streams, int32_t *out_tokens, float *out_plogs) {
+    if (!st || !prompt || !filter || !wc || !streams || !out_tokens || !out_plogs)
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_decode_window: NULL argument");
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    HIP_TRY(hipSetDevice(c->device));
+    const int S = st->S, n_max = wc->n_max;
+    if (n_prompt <= 0 || n_max <= 0) return fw_fail(FWHIP_ERR_INVALID, "empty prompt or n_max <= 0");
+    if (st->len + n_prompt + n_max - 1 > dd->nctx) return fw_fail(FWHIP_ERR_INVALID, "prompt + n_max exceeds n_text_ctx");
+    if (n_max > st->hist_cap) return fw_fail(FWHIP_ERR_INVALID, "n_max exceeds n_text_ctx");
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= dd->V) return fw_fail(FWHIP_ERR_INVALID, "prompt token out of range");
+    if (filter->timestamp_begin <= 0 || filter->timestamp_begin > dd->V || dd->V - filter->timestamp_begin > WIN_MAXTS ||
+        filter->eot <= 0 || filter->eot > filter->timestamp_begin)
+        return fw_fail(FWHIP_ERR_UNSUPPORTED, "fwhip_decode_window: the vocabulary's timestamp range is not supported");
+    fwhip_status r = win_buffers(st, n_max);
+    if (r != FWHIP_OK) return r;
+    FwWinCfg cfg;
+    memset(&cfg, 0, sizeof cfg);
+    cfg.V = dd->V;
+    cfg.beg = filter->timestamp_begin;
+    cfg.eot = filter->eot;
+    cfg.sot = filter->sot;
+    cfg.sot_prev = filter->sot_prev;
+    cfg.solm = filter->solm;
+    cfg.no_speech = filter->no_speech;
+    cfg.no_ts = filter->no_timestamps;
+    cfg.translate = filter->translate;
+    cfg.transcribe = filter->transcribe;
+    cfg.space = filter->space_token;
+    cfg.n_lang = filter->n_languages;
+    cfg.timestamps = wc->timestamps ? 1 : 0;
+    cfg.max_initial_tid = wc->max_initial_tid;
+    cfg.max_tokens = wc->max_tokens > 0 ? (wc->max_tokens < n_max ? wc->max_tokens : n_max) : 0;
+    cfg.n_max = n_max;
+    cfg.exact = wc->exact ? 1 : 0;
+    cfg.ldr = st->w_ldr;
+    std::vector<FwWinStream> ws(S);
+    for (int s = 0; s < S; s++) {
+        memset(&ws[s], 0, sizeof ws[s]);
+        ws[s].seek_cs = streams[s].seek_cs;
+        ws[s].seek_end_cs = streams[s].seek_end_cs;
+        ws[s].has_prior = streams[s].has_prior_segments ? 1 : 0;
+        ws[s].seek_delta_cs = 3000;
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipMemcpy(st->w_ws, ws.data(), sizeof(FwWinStream) * S, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemsetAsync(st->w_ndone, 0, sizeof(int), c->stream));
+    std::vector<int32_t> rows((size_t)S * n_prompt);
+    for (int s = 0; s < S; s++)
+        for (int t = 0; t < n_prompt; t++) rows[(size_t)s * n_prompt + t] = prompt[t];
+    r = stage_rows(st, rows.data(), n_prompt, nullptr);
+    if (r != FWHIP_OK) return r;
+    HIP_TRY(hipMemcpy2DAsync(st->w_nsrow, sizeof(float) * cfg.ldr, st->logits, sizeof(float) * dd->V,
+                             sizeof(float) * dd->V, S, hipMemcpyDeviceToDevice, c->stream));
+    fw_launch_win_select(c->stream, st->logits, dd->V, cfg, st->w_ws, st->hist, st->hist_cap, st->w_rows,
+                         st->w_forced, st->w_scratch, st->tok, st->pos, st->w_ndone, S);
+    int steps = 1, ndone = 0;
+    const int poll = 8;
+    bool use_graph = n_max > 1 && win_capture(st, cfg);
+    for (int i = 1; i < n_max; i++) {
+        if (i % poll == 1 || poll == 1) {
+            HIP_TRY(hipMemcpyAsync(&ndone, st->w_ndone, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+            HIP_TRY(hipStreamSynchronize(c->stream));
+            if (ndone >= S) break;
+        }
+        r = check_cancel(c);
+        if (r != FWHIP_OK) {
+            hipStreamSynchronize(c->stream);
+            st->len += n_prompt + steps - 1;
+            return r;
+        }
+        fw_event_pair ev;
+        fw_timed_begin(c, FWHIP_K_DEC_STEP, dec_step_bytes(st, st->len + n_prompt + i), &ev);
+        if (use_graph) HIP_TRY(hipGraphLaunch(st->wgraph, c->stream));
+        else {
+            r = win_step(st, cfg);
+            if (r != FWHIP_OK) return r;
+        }
+        fw_timed_end(c, &ev);
+        steps = i + 1;
+    }
+    fw_launch_win_plogs(c->stream, st->w_rows, st->w_nsrow, cfg, st->w_ws, st->hist, st->hist_cap, st->w_forced,
+                        st->w_plogs, st->w_nslp, S);
+    std::vector<int32_t> hist((size_t)S * n_max);
+    std::vector<float> nslp(S);
+    HIP_TRY(hipMemcpyAsync(ws.data(), st->w_ws, sizeof(FwWinStream) * S, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpy2DAsync(hist.data(), sizeof(int32_t) * n_max, st->hist, sizeof(int32_t) * st->hist_cap,
+                             sizeof(int32_t) * n_max, S, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(out_plogs, st->w_plogs, sizeof(float) * S * n_max, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(nslp.data(), st->w_nslp, sizeof(float) * S, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipGetLastError());
+    for (int s = 0; s < S; s++) {
+        const int n = ws[s].n_dec;
+        fwhip_window_stream &o = streams[s];
+        o.n_tokens = n;
+        o.result_len = ws[s].result_len;
+        o.has_ts = ws[s].has_ts;
+        o.seek_delta_cs = ws[s].seek_delta_cs;
+        o.n_exact = ws[s].n_exact;
+        o.no_speech_logprob = nslp[s];
+        for (int k = 0; k < n_max; k++) {
+            out_tokens[(size_t)s * n_max + k] = k < n ? hist[(size_t)s * n_max + k] : 0;
+            if (k >= n) out_plogs[(size_t)s * n_max + k] = 0.0f;
+        }
     }
     st->len += n_prompt + steps - 1;
     return FWHIP_OK;

@@ -59,6 +59,8 @@ SIGNATURES = {
     "fwhip_dstate_read": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_size_t]),
     "fwhip_decode_greedy": (C.c_int32, [_vp, _i32p, C.c_int32, C.c_int32, C.POINTER(abi.Filter), _i32p,
                                         _i32p]),
+    "fwhip_decode_window": (C.c_int32, [_vp, _i32p, C.c_int32, C.POINTER(abi.Filter), C.POINTER(abi.WindowCfg),
+                                        C.POINTER(abi.WindowStream), _i32p, C.POINTER(C.c_float)]),
     "fwhip_argmax_logits": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.POINTER(abi.Filter), C.c_int32, _i32p]),
     "fwhip_mel_frames": (C.c_int64, [C.c_int64]),
     "fwhip_log_mel": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
@@ -409,6 +411,28 @@ class DecoderState:
             n = c.n_text_layer * c.n_text_ctx * c.n_text_state
         out = np.empty(n, np.uint16)
         check(lib().fwhip_dstate_read(self.h, what, stream, out.ctypes.data_as(_vp), out.nbytes))
+        return out
+
+    def window(self, prompt, filt, cfg, streams):
+        """fwhip_decode_window: the window loop of every stream.  `streams`:
+        (seek_cs, seek_end_cs, has_prior_segments) per stream; returns one dict
+        per stream (tokens, plogs, result_len, has_ts, seek_delta_cs,
+        no_speech_lp, n_exact)."""
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        ws = (abi.WindowStream * self.S)()
+        for s, (sk, se, hp) in enumerate(streams):
+            ws[s].seek_cs, ws[s].seek_end_cs, ws[s].has_prior_segments = sk, se, 1 if hp else 0
+        n = cfg.n_max
+        toks = np.zeros((self.S, n), np.int32)
+        plogs = np.zeros((self.S, n), np.float32)
+        check(lib().fwhip_decode_window(self.h, p.ctypes.data_as(_i32p), p.size, C.byref(filt), C.byref(cfg), ws,
+                                        toks.ctypes.data_as(_i32p), plogs.ctypes.data_as(C.POINTER(C.c_float))))
+        out = []
+        for s in range(self.S):
+            k = ws[s].n_tokens
+            out.append({"tokens": toks[s, :k].tolist(), "plogs": plogs[s, :k].copy(), "result_len": ws[s].result_len,
+                        "has_ts": bool(ws[s].has_ts), "seek_delta_cs": ws[s].seek_delta_cs,
+                        "no_speech_lp": np.float32(ws[s].no_speech_logprob), "n_exact": ws[s].n_exact})
         return out
 
     def greedy(self, prompt, n_max: int, filt):

@@ -331,6 +331,45 @@ fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *prompt, int32_
                                  int32_t n_max_tokens, const fwhip_filter *filter,
                                  int32_t *out_tokens, int32_t *out_len);
 
+/* The window decode loop (the greedy loop of transcribe_samples_uncached,
+ * decode.rs:3456-3566, beam 1, temperature 0) with process_logits in full
+ * (decode.rs:702-867: blank/eot at the first step, control, task and language
+ * tokens, timestamps in no-timestamps mode, the user token budget, timestamp
+ * pairing, the initial-timestamp cap, the monotone timestamp floor and the
+ * timestamp-mass forcing rule).  FilterConfig (decode.rs:671-693) beyond the
+ * filter's ids; suppress_blank is on, suppress_nst off, as the driver sets
+ * them. */
+typedef struct fwhip_window_cfg {
+    int32_t timestamps;      /* 0: no-timestamps mode */
+    int32_t max_initial_tid; /* round(1.0 / (30 / n_audio_ctx)); < 0: no cap */
+    int32_t max_tokens;      /* the user token budget; <= 0: none (min with n_max is applied) */
+    int32_t n_max;           /* sampled-token cap: n_text_ctx / 2 - 4 */
+    int32_t exact;           /* 1: decide the forcing rule from the exact log-softmax on
+                                every step (the default recomputes it only when the
+                                decision is within 1e-3 of its threshold) */
+} fwhip_window_cfg;
+
+/* One stream of the window loop: seek_cs / seek_end_cs / has_prior_segments
+ * in; the rest out (the loop's decoded, result_len, has_ts, seek_delta_cs;
+ * no_speech_logprob: the no-speech token's log-probability on the prefill
+ * logits, compute_logprobs decode.rs:1437-1448; n_exact: steps that took the
+ * exact forcing decision). */
+typedef struct fwhip_window_stream {
+    int32_t seek_cs, seek_end_cs, has_prior_segments;
+    int32_t n_tokens, result_len, has_ts, seek_delta_cs, n_exact;
+    float no_speech_logprob;
+} fwhip_window_stream;
+
+/* Run the window loop for every stream of `st` (cross K/V already set by
+ * fwhip_dstate_set_cross): prefill `prompt` (n_prompt tokens, shared by the
+ * streams), then process_logits + argmax -> step on the device until every
+ * stream ends.  out_tokens / out_plogs are host [n_streams, cfg->n_max]: the
+ * decoded tokens (decoded, decode.rs:3476) and each token's log-probability
+ * (plogs: compute_logprobs of the filtered logits at the chosen token). */
+fwhip_status fwhip_decode_window(fwhip_dstate *st, const int32_t *prompt, int32_t n_prompt,
+                                 const fwhip_filter *filter, const fwhip_window_cfg *cfg,
+                                 fwhip_window_stream *streams, int32_t *out_tokens, float *out_plogs);
+
 /* process_logits in no-timestamps mode + argmax (decode.rs:702-867,
  * 1708-1790) for `n_rows` rows of logits on the device (`logits_dev`
  * [n_rows, n_vocab] f32): the suppress set of `filter` (NULL: raw argmax; with

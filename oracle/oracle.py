@@ -18,6 +18,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SO = os.path.join(HERE, "build", "librefcpu.so")
 
 _lib = None
+
+
+class RefFilterCfg(C.Structure):
+    """FilterConfig (decode.rs:671-693); -1 is None for the optional fields."""
+    _fields_ = [("suppress_blank", C.c_int), ("no_timestamps", C.c_int), ("max_initial_tid", C.c_int),
+                ("max_tokens", C.c_int)]
+
+
 i8p = C.POINTER(C.c_int8)
 u8p = C.POINTER(C.c_uint8)
 i32p = C.POINTER(C.c_int32)
@@ -87,6 +95,9 @@ def lib():
         "ref_process_argmax": (C.c_int, [C.POINTER(abi.Filter), f32p, C.c_int, C.c_int]),
         "ref_decode_greedy": (C.c_int, [C.c_void_p, C.c_void_p, i32p, C.c_int, C.c_int,
                                         C.POINTER(abi.Filter), i32p, i32p]),
+        "ref_compute_logprobs": (None, [f32p, C.c_int, f32p]),
+        "ref_process_logits": (C.c_int, [C.POINTER(abi.Filter), C.POINTER(RefFilterCfg), f32p, f32p, C.c_int, i32p,
+                                         C.c_int, C.c_int, C.c_int64, C.c_int]),
         "ref_mel_frames": (C.c_int64, [C.c_int64]),
         "ref_log_mel": (None, [f32p, C.c_int64, f32p, C.c_int, f32p]),
         "ref_mel_fft400": (None, [f32p, f32p]),
@@ -462,3 +473,22 @@ def process_argmax(filt, logits, initial):
     lg = _c(logits, np.float32)
     return int(lib().ref_process_argmax(C.byref(filt), _p(lg, C.c_float), lg.size,
                                         1 if initial else 0))
+
+
+def compute_logprobs(logits):
+    """compute_logprobs (decode.rs:1666-1701)."""
+    lg = _c(logits, np.float32)
+    out = np.empty_like(lg)
+    lib().ref_compute_logprobs(_p(lg, C.c_float), lg.size, _p(out, C.c_float))
+    return out
+
+
+def process_logits(filt, cfg, logits, prev, has_ts, seek_delta_cs, tokens_in_window):
+    """process_logits (decode.rs:702-867): (filtered logits, logprobs, forced)."""
+    lg = _c(logits, np.float32).copy()
+    lp = np.empty_like(lg)
+    pv = _c(prev if len(prev) else [0], np.int32)
+    forced = lib().ref_process_logits(C.byref(filt), C.byref(cfg), _p(lg, C.c_float), _p(lp, C.c_float), lg.size,
+                                      _p(pv, C.c_int32), len(prev), 1 if has_ts else 0, int(seek_delta_cs),
+                                      int(tokens_in_window))
+    return lg, lp, bool(forced)

@@ -1248,6 +1248,94 @@ int ref_process_argmax(const fwhip_filter *f, const float *logits, int n, int in
     return tok;
 }
 
+/* compute_logprobs (decode.rs:1666-1701): non-finite logits sanitized to
+ * -inf, max, sequential f32 sum of expf(l - max) over the finite lanes (libm
+ * expf), logf(sum) + max; masked lanes stay -inf. */
+void ref_compute_logprobs(const float *logits, int n, float *lp) {
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++) {
+        float l = isfinite(logits[i]) ? logits[i] : -INFINITY;
+        mx = fmaxf(mx, l);
+    }
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float l = isfinite(logits[i]) ? logits[i] : -INFINITY;
+        if (l > -INFINITY) s += expf(l - mx);
+    }
+    const float lse = logf(s) + mx;
+    for (int i = 0; i < n; i++) {
+        float l = isfinite(logits[i]) ? logits[i] : -INFINITY;
+        lp[i] = l > -INFINITY ? l - lse : -INFINITY;
+    }
+}
+
+/* process_logits (decode.rs:702-867) with FilterConfig (decode.rs:671-693):
+ * the suppression rules in the reference's order, then compute_logprobs and
+ * the timestamp-mass forcing rule.  logits is filtered in place; logprobs
+ * receives the log-softmax (text lanes -inf when a timestamp is forced).
+ * Returns 1 when a timestamp was forced. */
+int ref_process_logits(const fwhip_filter *f, const ref_filter_cfg *cfg, float *l, float *lp, int n,
+                       const int32_t *prev, int n_prev, int has_ts, int64_t seek_delta_cs, int tokens_in_window) {
+    const int beg = f->timestamp_begin;
+    const int initial = n_prev == 0;
+#define SETNEG(id) do { int _i = (id); if (_i >= 0 && _i < n) l[_i] = -INFINITY; } while (0)
+    if (cfg->suppress_blank && initial) {
+        SETNEG(f->eot);
+        if (f->space_token >= 0) SETNEG(f->space_token);
+    }
+    SETNEG(f->no_timestamps);
+    if (cfg->no_timestamps)
+        for (int i = beg; i < n; i++) SETNEG(i);
+    if (!cfg->no_timestamps && cfg->max_tokens > 0 && tokens_in_window >= cfg->max_tokens)
+        for (int i = 0; i < f->eot; i++) SETNEG(i);
+    SETNEG(f->sot);
+    SETNEG(f->no_speech);
+    SETNEG(f->solm);
+    SETNEG(f->translate);
+    SETNEG(f->transcribe);
+    SETNEG(f->sot_prev);
+    for (int li = 0; li < f->n_languages; li++) SETNEG(f->sot + 1 + li);
+    const int last_ts = n_prev > 0 && prev[n_prev - 1] >= beg;
+    const int penult_ts = n_prev < 2 || prev[n_prev - 2] >= beg;
+    if (last_ts) {
+        if (penult_ts)
+            for (int i = beg; i < n; i++) SETNEG(i);
+        else
+            for (int i = 0; i < f->eot; i++) SETNEG(i);
+    }
+    if (initial && cfg->max_initial_tid >= 0)
+        for (int i = beg + cfg->max_initial_tid + 1; i < n; i++) SETNEG(i);
+    if (has_ts) {
+        const int tid0 = (int)(seek_delta_cs / 2);
+        const int end = beg + tid0 < n ? beg + tid0 : n;
+        for (int i = beg; i < end; i++) SETNEG(i);
+    }
+#undef SETNEG
+    ref_compute_logprobs(l, n, lp);
+    const int b = beg > 0 ? beg : 0;
+    float ts_lp = -INFINITY;
+    if (b < n) {
+        float m = -INFINITY;
+        for (int i = b; i < n; i++) m = fmaxf(m, lp[i]);
+        if (isfinite(m)) {
+            float s = 0.0f;
+            for (int i = b; i < n; i++)
+                if (lp[i] > -INFINITY) s += expf(lp[i] - m);
+            if (s > 0.0f) ts_lp = logf(s) + m;
+        }
+    }
+    float max_text = -INFINITY;
+    for (int i = 0; i < b && i < n; i++) max_text = fmaxf(max_text, lp[i]);
+    if (ts_lp > max_text) {
+        for (int i = 0; i < b && i < n; i++) {
+            l[i] = -INFINITY;
+            lp[i] = -INFINITY;
+        }
+        return 1;
+    }
+    return 0;
+}
+
 /* Greedy window loop, decode.rs:3429-3566 (no timestamps, beam 1). */
 int ref_decode_greedy(const ref_decoder *dd, ref_dstate *s, const int32_t *prompt, int n_prompt,
                       int n_max, const fwhip_filter *f, int32_t *out_tokens, int32_t *out_len) {

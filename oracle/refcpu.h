@@ -108,6 +108,13 @@ const uint16_t *ref_dstate_cross_vt_f16(const ref_dstate *s);
 int ref_decoder_step(const ref_decoder *d, ref_dstate *s, const int32_t *tokens, int tq,
                      float *logits);
 int ref_process_argmax(const fwhip_filter *f, const float *logits, int n_vocab, int initial);
+/* FilterConfig (decode.rs:671-693); -1 is None for max_initial_tid / max_tokens */
+typedef struct ref_filter_cfg {
+    int suppress_blank, no_timestamps, max_initial_tid, max_tokens;
+} ref_filter_cfg;
+void ref_compute_logprobs(const float *logits, int n, float *lp);
+int ref_process_logits(const fwhip_filter *f, const ref_filter_cfg *cfg, float *logits, float *logprobs, int n,
+                       const int32_t *prev, int n_prev, int has_ts, int64_t seek_delta_cs, int tokens_in_window);
 int ref_decode_greedy(const ref_decoder *d, ref_dstate *s, const int32_t *prompt, int n_prompt,
                       int n_max, const fwhip_filter *f, int32_t *out_tokens, int32_t *out_len);
 

@@ -65,6 +65,25 @@ int main(void) {
 """
 
 
+LOG_HARNESS = r"""
+#include <math.h>
+#include <stdio.h>
+#include "fw_math.h"
+int main(void) {
+    long bad = 0, n = 0;
+    #pragma omp parallel for reduction(+:bad,n) schedule(static)
+    for (int64_t u = 0; u <= 0x7f800000LL; u++) {
+        uint32_t v = (uint32_t)u; float x; memcpy(&x, &v, 4);
+        n++;
+        if (fw_f2u(logf(x)) != fw_f2u(fw_logf_host(x))) bad++;
+    }
+    if (!isnan(fw_logf_host(-1.0f)) || !isnan(fw_logf_host(NAN)) || fw_logf_host(-0.0f) != -INFINITY) bad++;
+    printf("%ld %ld\n", n, bad);
+    return bad != 0;
+}
+"""
+
+
 def _compile_run(tmp_path, src, name, extra):
     c = tmp_path / f"{name}.c"
     c.write_text(src)
@@ -87,6 +106,12 @@ def test_device_expf_restatement_matches_glibc_exhaustive(tmp_path):
     r = _compile_run(tmp_path, EXP_HARNESS, "expx", ["-I", os.path.join(ROOT, "franken_whisper_amd", "csrc")])
     n, bad = map(int, r.stdout.split())
     assert bad == 0 and n > 2_000_000_000, r.stdout
+
+
+def test_device_logf_restatement_matches_glibc_exhaustive(tmp_path):
+    r = _compile_run(tmp_path, LOG_HARNESS, "logx", ["-I", os.path.join(ROOT, "franken_whisper_amd", "csrc")])
+    n, bad = map(int, r.stdout.split())
+    assert bad == 0 and n == 0x7f800001, r.stdout
 
 
 def _f(bits):
