@@ -96,6 +96,29 @@ class WindowStream(C.Structure):
                                          "has_ts", "seek_delta_cs", "n_exact")] + [("no_speech_logprob", C.c_float)]
 
 
+class Vocab(C.Structure):
+    _fields_ = [("n_tokens", C.c_int32), ("bytes", C.POINTER(C.c_uint8)), ("offsets", C.POINTER(C.c_uint64))]
+
+
+class TranscribeParams(C.Structure):
+    _fields_ = [("timestamps", C.c_int32), ("max_context", C.c_int32), ("max_context_set", C.c_int32),
+                ("max_tokens", C.c_int32), ("no_context", C.c_int32), ("retry_failed_window", C.c_int32),
+                ("tiny_en_ts_context", C.c_int32), ("carry_initial_prompt", C.c_int32),
+                ("initial_prompt", C.POINTER(C.c_int32)), ("n_initial_prompt", C.c_int32),
+                ("sot_sequence", C.POINTER(C.c_int32)), ("n_sot", C.c_int32),
+                ("no_speech_threshold", C.c_double), ("logprob_threshold", C.c_double), ("exact_forcing", C.c_int32)]
+
+
+class SegmentInfo(C.Structure):
+    _fields_ = [("start_cs", C.c_int64), ("end_cs", C.c_int64), ("text", C.c_char_p), ("confidence", C.c_double)]
+
+
+class WindowInfo(C.Structure):
+    _fields_ = [("seek_cs", C.c_int64), ("avg_logprob", C.c_double), ("no_speech_prob", C.c_double)] + [
+        (n, C.c_int32) for n in ("result_len", "n_tokens", "has_ts", "seek_delta_cs", "no_speech", "dropped",
+                                 "retried")] + [("tokens", C.POINTER(C.c_int32)), ("plogs", C.POINTER(C.c_float))]
+
+
 class ExecRecord(C.Structure):
     _fields_ = [("route", C.c_char * 48), ("precision", C.c_int32), ("n_windows", C.c_int32),
                 ("device_ms", C.c_double)]

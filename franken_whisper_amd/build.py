@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["fwhip.hip", "dec_kernels.hip", "load_kernels.hip", "encoder.hip", "enc_kernels.hip", "enc_gemm.hip", "dec_fast.hip", "dec_gemv16.hip", "enc_tome.hip", "mel.hip", "ggml.hip", "dec_window.hip"]
+HIP_SOURCES = ["fwhip.hip", "dec_kernels.hip", "load_kernels.hip", "encoder.hip", "enc_kernels.hip", "enc_gemm.hip", "dec_fast.hip", "dec_gemv16.hip", "enc_tome.hip", "mel.hip", "ggml.hip", "dec_window.hip", "transcribe.hip"]
 # Packed-FP32 instructions are disabled for every HIP translation unit; exact
 # reference epilogues need -ffp-contract=off (Rust never contracts a*b+c).
 HIP_FLAGS = [

@@ -39,7 +39,11 @@ __device__ __forceinline__ double eln_wave_sum(double v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
-template <int NV>
+// With SEQ the row's sum and sum of squared deviations are taken by lane 0 in
+// index order from an LDS copy of the row (the reference's sequential f64
+// loops, bit for bit); the wave's tree order differs from them in the last f64
+// bits, which the f32 result shows on rows of nearly equal values (silence).
+template <int NV, bool SEQ>
 __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, const float *b, int rows, int d,
                                                 int mode, float *yf, uint16_t *hi, uint16_t *lo, int8_t *q,
                                                 float *qs) {
@@ -64,20 +68,42 @@ __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, 
         wv4[k] = wr[c4];
         bv4[k] = br[c4];
     }
-    double s = 0.0;
+    double mean, var;
+    if constexpr (SEQ) {
+        __shared__ float srow[4][64 * 4 * ELN_V4];
+        float *sr = srow[threadIdx.x >> 6];
 #pragma unroll
-    for (int k = 0; k < ELN_V4; k++)
-        if (ok[k]) s += ((double)xv[k].x + (double)xv[k].y) + ((double)xv[k].z + (double)xv[k].w);
-    const double mean = eln_wave_sum(s) / (double)d;
-    double v = 0.0;
-#pragma unroll
-    for (int k = 0; k < ELN_V4; k++)
-        if (ok[k]) {
-            double t0 = (double)xv[k].x - mean, t1 = (double)xv[k].y - mean;
-            double t2 = (double)xv[k].z - mean, t3 = (double)xv[k].w - mean;
-            v += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
+        for (int k = 0; k < ELN_V4; k++)
+            if (ok[k]) ((float4 *)sr)[lane + 64 * k] = xv[k];
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        double s = 0.0, v = 0.0;
+        if (lane == 0) {
+            for (int j = 0; j < d; j++) s += (double)sr[j];
+            const double m = s / (double)d;
+            for (int j = 0; j < d; j++) {
+                const double t = (double)sr[j] - m;
+                v += t * t;
+            }
         }
-    const double var = eln_wave_sum(v) / (double)d;
+        mean = __shfl(s, 0, 64) / (double)d;
+        var = __shfl(v, 0, 64) / (double)d;
+    } else {
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < ELN_V4; k++)
+            if (ok[k]) s += ((double)xv[k].x + (double)xv[k].y) + ((double)xv[k].z + (double)xv[k].w);
+        mean = eln_wave_sum(s) / (double)d;
+        double v = 0.0;
+#pragma unroll
+        for (int k = 0; k < ELN_V4; k++)
+            if (ok[k]) {
+                double t0 = (double)xv[k].x - mean, t1 = (double)xv[k].y - mean;
+                double t2 = (double)xv[k].z - mean, t3 = (double)xv[k].w - mean;
+                v += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
+            }
+        var = eln_wave_sum(v) / (double)d;
+    }
     const double inv = 1.0 / sqrt(var + (double)1e-5f);
     float yv[ELN_V4][4];
     float amax = 0.0f;
@@ -711,16 +737,23 @@ void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qof
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
                       float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs) {
     const dim3 g((rows + 3) / 4), blk(256);
+    const bool seq = (mode & FW_LN_SEQ) != 0;
+    mode &= ~FW_LN_SEQ;
+#define ELN_CASE(NV)                                                                                              \
+    if (seq) hipLaunchKernelGGL((k_enc_ln<NV, true>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); \
+    else hipLaunchKernelGGL((k_enc_ln<NV, false>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs);    \
+    break;
     switch ((d + 255) / 256) {
-    case 1: hipLaunchKernelGGL(k_enc_ln<1>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
-    case 2: hipLaunchKernelGGL(k_enc_ln<2>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
-    case 3: hipLaunchKernelGGL(k_enc_ln<3>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
-    case 4: hipLaunchKernelGGL(k_enc_ln<4>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
-    case 5: hipLaunchKernelGGL(k_enc_ln<5>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
-    case 6: hipLaunchKernelGGL(k_enc_ln<6>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
-    case 7: hipLaunchKernelGGL(k_enc_ln<7>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
-    default: hipLaunchKernelGGL(k_enc_ln<8>, g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); break;
+    case 1: ELN_CASE(1)
+    case 2: ELN_CASE(2)
+    case 3: ELN_CASE(3)
+    case 4: ELN_CASE(4)
+    case 5: ELN_CASE(5)
+    case 6: ELN_CASE(6)
+    case 7: ELN_CASE(7)
+    default: ELN_CASE(8)
     }
+#undef ELN_CASE
 }
 void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs) {
     const dim3 g4((rows + 3) / 4), b4(256);

@@ -109,6 +109,9 @@ static std::vector<uint16_t> conv_reorder(const uint16_t *w, int cout, int cin, 
     return r;
 }
 
+fwhip_ctx *fw_encoder_ctx(const fwhip_encoder *e) { return e->ctx; }
+fwhip_hparams fw_encoder_hparams(const fwhip_encoder *e) { return e->hp; }
+
 extern "C" fwhip_status fwhip_encoder_load(fwhip_ctx *c, const fwhip_encoder_weights *w, int32_t precision,
                                            fwhip_encoder **out) {
     if (!c || !w || !out) return fw_fail(FWHIP_ERR_INVALID, "fwhip_encoder_load: NULL argument");
@@ -492,11 +495,11 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
     for (int li = 0; li < e->L; li++) {
         const EncLayerDev &l = e->layers[li];
         if (i8) {
-            fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_I7, nullptr, nullptr, nullptr, b.hq, b.hs);
+            fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_I7 | FW_LN_SEQ, nullptr, nullptr, nullptr, b.hq, b.hs);
             FwGemm g = gemm_args(b.hq, nullptr, l.qkv7, Mc, 3 * d, d, b.hs, l.qkv7s, l.qkv_b, FW_EPI_F32, x.qkv, 3 * d);
             fw_launch_gemm(st, FW_KIND_I8, g);
         } else {
-            fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_F32, x.h, nullptr, nullptr, nullptr,
+            fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_F32 | FW_LN_SEQ, x.h, nullptr, nullptr, nullptr,
                              nullptr);
             fw_launch_gemm_strict(st, x.h, l.qkv16, Mc, 3 * d, d, 0, x.qkv, l.qkv_b, 1.0f, nullptr, Tc, 0, 0, 0,
                                   3 * d, nullptr, nullptr);
@@ -506,7 +509,7 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
             fw_launch_quant_exact_rows(st, x.att, Mc, d, b.aq, b.as);
             FwGemm g = gemm_args(b.aq, nullptr, l.o8, Mc, d, d, b.as, l.o8s, l.o_b, FW_EPI_RESID, X, d);
             fw_launch_gemm(st, FW_KIND_I8, g);
-            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_I7, nullptr, nullptr, nullptr, b.hq, b.hs);
+            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_I7 | FW_LN_SEQ, nullptr, nullptr, nullptr, b.hq, b.hs);
             g = gemm_args(b.hq, nullptr, l.fc1_7, Mc, dff, d, b.hs, l.fc1_7s, l.fc1_b, FW_EPI_F32, b.ff, dff);
             fw_launch_gemm(st, FW_KIND_I8, g);
             fw_launch_gelu_quant_i7_rows(st, b.ff, Mc, dff, gt, b.gq, b.gs);
@@ -515,7 +518,7 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
         } else {
             fw_launch_gemm_strict(st, x.att, l.o16, Mc, d, d, 5, X, l.o_b, 1.0f, nullptr, Tc, 0, 0, 0, d, nullptr,
                                   nullptr);
-            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_F32, x.h, nullptr, nullptr, nullptr, nullptr);
+            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_F32 | FW_LN_SEQ, x.h, nullptr, nullptr, nullptr, nullptr);
             fw_launch_gemm_strict(st, x.h, l.fc1_16, Mc, dff, d, 3, x.ff, l.fc1_b, 1.0f, nullptr, Tc, 0, 0, 0, dff, gt,
                                   nullptr);
             fw_launch_gemm_strict(st, x.ff, l.fc2_16, Mc, d, dff, 5, X, l.fc2_b, 1.0f, nullptr, Tc, 0, 0, 0, d,
@@ -533,7 +536,7 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
         }
     }
     if (merged) fw_launch_tome_unmerge(st, X, B, Tc, b.umap, T2, d, b.x);
-    fw_launch_enc_ln(st, b.x, e->lnpw, e->lnpb, M, d, FW_LN_F32, out_dev, nullptr, nullptr, nullptr, nullptr);
+    fw_launch_enc_ln(st, b.x, e->lnpw, e->lnpb, M, d, FW_LN_F32 | FW_LN_SEQ, out_dev, nullptr, nullptr, nullptr, nullptr);
     hipError_t err = hipStreamSynchronize(st);
     if (err == hipSuccess) err = hipGetLastError();
     if (err != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("encoder (exact): ") + hipGetErrorString(err));

@@ -35,6 +35,9 @@ __host__ __device__ __forceinline__ int fw_vt_pos(int t) { return (t & ~12) | ((
 #define FW_LN_F32 0
 #define FW_LN_SPLIT 1
 #define FW_LN_I7 2
+// or-ed into the mode: the f64 statistics summed in index order, as the
+// reference's loops do (exact mode), instead of the wave's tree order
+#define FW_LN_SEQ 0x100
 
 struct FwGemm {
     const void *A;  // [M, lda] i8, or f16 hi

@@ -51,6 +51,12 @@ void fw_timed_end(fwhip_ctx *c, fw_event_pair *ev);
 void *fw_dalloc(std::vector<void *> &owned, size_t bytes);
 void *fw_dupload(std::vector<void *> &owned, const void *host, size_t bytes);
 void fw_free_all(std::vector<void *> &owned);
+// The context and model shape of a loaded encoder / decoder (encoder.hip,
+// fwhip.hip), for the window driver.
+fwhip_ctx *fw_encoder_ctx(const fwhip_encoder *e);
+fwhip_hparams fw_encoder_hparams(const fwhip_encoder *e);
+fwhip_ctx *fw_decoder_ctx(const fwhip_decoder *d);
+fwhip_hparams fw_decoder_hparams(const fwhip_decoder *d);
 // Resolve the allocation-free log-mel's device scratch and tables on `device`
 // (the current device), once per device; called by fwhip_init.
 void fw_mel_noalloc_setup(int device);

@@ -403,6 +403,9 @@ static bool hp_decoder_ok(const fwhip_hparams &hp, std::string &why) {
     return true;
 }
 
+fwhip_ctx *fw_decoder_ctx(const fwhip_decoder *d) { return d->ctx; }
+fwhip_hparams fw_decoder_hparams(const fwhip_decoder *d) { return d->hp; }
+
 extern "C" fwhip_status fwhip_decoder_load(fwhip_ctx *c, const fwhip_decoder_weights *w, int32_t arm,
                                            fwhip_decoder **out) {
     if (!c || !w || !out) return fw_fail(FWHIP_ERR_INVALID, "fwhip_decoder_load: NULL argument");

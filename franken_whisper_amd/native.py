@@ -61,6 +61,13 @@ SIGNATURES = {
                                         _i32p]),
     "fwhip_decode_window": (C.c_int32, [_vp, _i32p, C.c_int32, C.POINTER(abi.Filter), C.POINTER(abi.WindowCfg),
                                         C.POINTER(abi.WindowStream), _i32p, C.POINTER(C.c_float)]),
+    "fwhip_transcribe": (C.c_int32, [_vp, _vp, _vp, _vp, C.c_int64, _vp, C.c_int32, C.POINTER(abi.Filter),
+                                     C.POINTER(abi.Vocab), C.POINTER(abi.TranscribeParams), C.POINTER(_vp)]),
+    "fwhip_transcript_n_segments": (C.c_int32, [_vp]),
+    "fwhip_transcript_segment": (C.c_int32, [_vp, C.c_int32, C.POINTER(abi.SegmentInfo)]),
+    "fwhip_transcript_n_windows": (C.c_int32, [_vp]),
+    "fwhip_transcript_window": (C.c_int32, [_vp, C.c_int32, C.POINTER(abi.WindowInfo)]),
+    "fwhip_transcript_free": (None, [_vp]),
     "fwhip_argmax_logits": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.POINTER(abi.Filter), C.c_int32, _i32p]),
     "fwhip_mel_frames": (C.c_int64, [C.c_int64]),
     "fwhip_log_mel": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
@@ -447,3 +454,50 @@ class DecoderState:
         if self.h:
             lib().fwhip_dstate_free(self.h)
             self.h = None
+
+
+def transcribe(ctx: Context, enc: Encoder, dec: Decoder, samples_dev: DeviceArray, n_samples: int,
+               filters_dev: DeviceArray, n_mel: int, filt, vocab, sot_sequence, timestamps: bool = False,
+               max_context: int | None = None, max_tokens: int | None = None, no_context: bool = False,
+               retry_failed_window: bool = True, tiny_en_ts_context: bool = False, carry_initial_prompt: bool = False,
+               initial_prompt=(), no_speech_threshold: float = 0.6, logprob_threshold: float = -1.0,
+               exact_forcing: bool = False):
+    """fwhip_transcribe (transcribe_samples, decode.rs:2880-3960, greedy path):
+    returns {"segments": [(start_cs, end_cs, text, confidence | None)],
+    "windows": [dict]}.  `vocab` is the list of token byte strings."""
+    blob = b"".join(vocab)
+    offs = np.zeros(len(vocab) + 1, np.uint64)
+    offs[1:] = np.cumsum([len(v) for v in vocab], dtype=np.uint64)
+    buf = np.frombuffer(blob, np.uint8).copy() if blob else np.zeros(1, np.uint8)
+    voc = abi.Vocab(len(vocab), buf.ctypes.data_as(C.POINTER(C.c_uint8)), offs.ctypes.data_as(C.POINTER(C.c_uint64)))
+    sot = np.ascontiguousarray(sot_sequence, dtype=np.int32)
+    ip = np.ascontiguousarray(list(initial_prompt) or [0], dtype=np.int32)
+    p = abi.TranscribeParams(1 if timestamps else 0, max_context if max_context is not None else -1,
+                             0 if max_context is None else 1, max_tokens or 0, 1 if no_context else 0,
+                             1 if retry_failed_window else 0, 1 if tiny_en_ts_context else 0,
+                             1 if carry_initial_prompt else 0, ip.ctypes.data_as(_i32p), len(initial_prompt),
+                             sot.ctypes.data_as(_i32p), sot.size, no_speech_threshold, logprob_threshold,
+                             1 if exact_forcing else 0)
+    h = _vp()
+    check(lib().fwhip_transcribe(ctx.h, enc.h, dec.h, samples_dev.ptr, n_samples, filters_dev.ptr, n_mel,
+                                 C.byref(filt), C.byref(voc), C.byref(p), C.byref(h)))
+    try:
+        segs = []
+        for i in range(lib().fwhip_transcript_n_segments(h)):
+            si = abi.SegmentInfo()
+            check(lib().fwhip_transcript_segment(h, i, C.byref(si)))
+            conf = None if si.confidence != si.confidence else si.confidence
+            segs.append((si.start_cs, si.end_cs, si.text.decode("utf-8"), conf))
+        wins = []
+        for i in range(lib().fwhip_transcript_n_windows(h)):
+            wi = abi.WindowInfo()
+            check(lib().fwhip_transcript_window(h, i, C.byref(wi)))
+            n = wi.n_tokens
+            wins.append({"seek_cs": wi.seek_cs, "avg_logprob": wi.avg_logprob, "no_speech_prob": wi.no_speech_prob,
+                         "result_len": wi.result_len, "has_ts": bool(wi.has_ts), "seek_delta_cs": wi.seek_delta_cs,
+                         "no_speech": bool(wi.no_speech), "dropped": bool(wi.dropped), "retried": bool(wi.retried),
+                         "tokens": [wi.tokens[k] for k in range(n)],
+                         "plogs": np.array([wi.plogs[k] for k in range(n)], np.float32)})
+    finally:
+        lib().fwhip_transcript_free(h)
+    return {"segments": segs, "windows": wins}

@@ -370,6 +370,83 @@ fwhip_status fwhip_decode_window(fwhip_dstate *st, const int32_t *prompt, int32_
                                  const fwhip_filter *filter, const fwhip_window_cfg *cfg,
                                  fwhip_window_stream *streams, int32_t *out_tokens, float *out_plogs);
 
+/* ---- the window driver ---------------------------------------------------- */
+
+/* A byte-level vocabulary (Tokenizer's token bytes, tokenizer.rs:230-300):
+ * token i is bytes[offsets[i] .. offsets[i + 1]); offsets has n_tokens + 1
+ * entries.  Tokens >= eot are special and never rendered. */
+typedef struct fwhip_vocab {
+    int32_t n_tokens;
+    const uint8_t *bytes;
+    const uint64_t *offsets;
+} fwhip_vocab;
+
+/* The DecodeParams fields (decode.rs:239-447) and process switches the greedy
+ * driver reads. */
+typedef struct fwhip_transcribe_params {
+    int32_t timestamps;           /* DecodeParams.timestamps (segment timestamps) */
+    int32_t max_context;          /* DecodeParams.max_context when max_context_set:
+                                     < 0 the default (n_text_ctx / 2), 0 no carried prompt, n a cap */
+    int32_t max_context_set;      /* 0: max_context is None */
+    int32_t max_tokens;           /* DecodeParams.max_text_ctx, the user token budget; <= 0: none */
+    int32_t no_context;           /* FW_NO_CONTEXT: never condition on previous text */
+    int32_t retry_failed_window;  /* FW_RETRY_FAILED_WINDOW (the reference's default: 1) */
+    int32_t tiny_en_ts_context;   /* FW_TINY_EN_TS_CONTEXT: keep tiny.en's carried context with timestamps */
+    int32_t carry_initial_prompt; /* DecodeParams.carry_initial_prompt */
+    const int32_t *initial_prompt;  /* Tokenizer::encode of DecodeParams.initial_prompt (may be NULL) */
+    int32_t n_initial_prompt;
+    const int32_t *sot_sequence;    /* Tokenizer::sot_sequence(language, translate, timestamps) */
+    int32_t n_sot;
+    double no_speech_threshold;   /* the quality gates (decode.rs:1082-1104): 0.6 */
+    double logprob_threshold;     /* -1.0 */
+    int32_t exact_forcing;        /* fwhip_window_cfg.exact */
+} fwhip_transcribe_params;
+
+typedef struct fwhip_transcript fwhip_transcript;
+
+/* TranscriptionSegment: centisecond bounds, trimmed text (UTF-8, owned by the
+ * transcript), text confidence (NaN when the reference gives None). */
+typedef struct fwhip_segment_info {
+    int64_t start_cs, end_cs;
+    const char *text;
+    double confidence;
+} fwhip_segment_info;
+
+/* WindowStats plus the window's decode: every accepted window in order;
+ * `dropped` marks the reference's DroppedWindow records (a later window that
+ * closed no timestamp and is not silence), `retried` a window decoded again
+ * without its carried prompt; tokens / plogs (owned by the transcript) are the
+ * window's decoded tokens and their log-probabilities. */
+typedef struct fwhip_window_info {
+    int64_t seek_cs;
+    double avg_logprob, no_speech_prob;
+    int32_t result_len, n_tokens, has_ts, seek_delta_cs, no_speech, dropped, retried;
+    const int32_t *tokens;
+    const float *plogs;
+} fwhip_window_info;
+
+/* Replaces transcribe_samples (decode.rs:2880-2955 -> 2956-3960) on its
+ * greedy path (beam 1, no temperature fallback, no word timestamps, the
+ * language given by the sot sequence, full 30 s windows): the log-mel of the
+ * whole audio (samples_dev, n_samples 16 kHz f32 on the device; filters_dev
+ * [n_mel, 201]), then window by window the encoder at the seek, the window
+ * loop (fwhip_decode_window) and the rules between windows — prompt carry,
+ * the short-tail prompt clear, the no-speech gate, the failed-window retry,
+ * the single-timestamp-ending skip, segment building, the seek advance.
+ * Without timestamps and without a carried prompt the windows are
+ * independent and run as batched cohorts, with the same results.  enc and dec
+ * must belong to ctx; FWHIP_ERR_INVALID "transcribe_samples: empty audio" for
+ * n_samples == 0.  Release the result with fwhip_transcript_free. */
+fwhip_status fwhip_transcribe(fwhip_ctx *ctx, fwhip_encoder *enc, fwhip_decoder *dec, const float *samples_dev,
+                              int64_t n_samples, const float *filters_dev, int32_t n_mel, const fwhip_filter *filter,
+                              const fwhip_vocab *vocab, const fwhip_transcribe_params *params,
+                              fwhip_transcript **out);
+int32_t fwhip_transcript_n_segments(const fwhip_transcript *t);
+fwhip_status fwhip_transcript_segment(const fwhip_transcript *t, int32_t i, fwhip_segment_info *out);
+int32_t fwhip_transcript_n_windows(const fwhip_transcript *t);
+fwhip_status fwhip_transcript_window(const fwhip_transcript *t, int32_t i, fwhip_window_info *out);
+void fwhip_transcript_free(fwhip_transcript *t);
+
 /* process_logits in no-timestamps mode + argmax (decode.rs:702-867,
  * 1708-1790) for `n_rows` rows of logits on the device (`logits_dev`
  * [n_rows, n_vocab] f32): the suppress set of `filter` (NULL: raw argmax; with

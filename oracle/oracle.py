@@ -297,6 +297,15 @@ def log_mel(samples, filters):
     return out
 
 
+def mel_window(mel, frame_offset, n_frames):
+    """time_major_mel_window_from_full_mel (encoder.rs:684-737): [n_frames,
+    n_mel] from the mel-major full mel, -1.5 past its end."""
+    m = _c(mel, np.float32)
+    out = np.empty((n_frames, m.shape[0]), np.float32)
+    lib().ref_mel_window(_p(m, C.c_float), m.shape[0], m.shape[1], frame_offset, n_frames, _p(out, C.c_float))
+    return out
+
+
 def mel_fft400(frame):
     """fft_twoforone, mel.rs:648-695, of one 400-sample frame: 400 complex bins."""
     x = _c(frame, np.float32)
