@@ -55,7 +55,8 @@ def _args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--workload", default="job", choices=["job", "enc-f32", "enc-int8", "decode", "copy", "load"])
+    p.add_argument("--workload", default="job",
+                   choices=["job", "enc-f32", "enc-int8", "decode", "copy", "load", "transcribe"])
     p.add_argument("--windows", type=int, default=None)
     p.add_argument("--tokens", type=int, default=220)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -308,6 +309,59 @@ def load_workload(a):
     }))
 
 
+def transcribe_workload(a):
+    """The window driver end to end (fwhip_transcribe: log-mel of the whole
+    audio, encoder windows at the seeks, the device window loop, the rules
+    between windows) on the job's audio (300 s of seeded synthetic 16 kHz
+    audio with silent gaps) and the large-v3-turbo architecture (seeded
+    random-init weights, int8 encoder, f16 decoder arm), in two settings:
+    no timestamps without a carried prompt (independent windows, batched as
+    cohorts: the job's own decode semantics), and the reference's timestamp
+    mode with its default prompt carry (windows in sequence, one stream)."""
+    from franken_whisper_amd import abi, native, synth
+    from franken_whisper_amd import ggml as gg
+
+    cfg = synth.TURBO
+    W = a.windows or 10
+    model = synth.Model(cfg, seed=0)
+    ctx = native.Context(0)
+    enc = native.Encoder(ctx, model, abi.ENC_INT8)
+    dec = native.Decoder(ctx, model, abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8)
+    samples = synth.audio(AUDIO_SEED, 30.0 * W, gaps=True)
+    sd = ctx.array(samples)
+    fd = ctx.array(synth.mel_filterbank(cfg.n_mels))
+    tk = model.tokens
+    vocab = gg.synthetic_vocab(tk.eot)
+    res = {}
+    for name, kw in (("independent_no_timestamps", dict(timestamps=False, max_context=0)),
+                     ("timestamps_prompt_carry", dict(timestamps=True))):
+        sot = tk.sot_sequence(language_id=0, timestamps=kw["timestamps"])
+        out = None
+        for _ in range(a.warmup):
+            native.transcribe(ctx, enc, dec, sd, samples.size, fd, cfg.n_mels, tk.filter(), vocab, sot, **kw)
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            out = native.transcribe(ctx, enc, dec, sd, samples.size, fd, cfg.n_mels, tk.filter(), vocab, sot, **kw)
+        ctx.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / a.steps
+        wins = out["windows"]
+        res[name] = {"value": round(30.0 * W / (ms * 1e-3), 2), "ms_per_run": round(ms, 2), "windows": len(wins),
+                     "sampled_tokens": int(sum(len(w["tokens"]) for w in wins)), "segments": len(out["segments"])}
+    enc.close()
+    dec.close()
+    ctx.close()
+    first = res["independent_no_timestamps"]
+    print(json.dumps({
+        "metric": "audio-s/sec large-v3-turbo transcribe_samples (fwhip_transcribe, from audio)",
+        "value": first["value"], "unit": "audio-s/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": first["ms_per_run"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8+f16" if a.dec_arm == "f16" else "int8+f32",
+        "data": "synthetic (seeded random-init weights, seeded synthetic 16 kHz audio with gaps)",
+        "config": {"workload": f"fwhip_transcribe over {30 * W} s of audio, greedy, {a.dec_arm} decoder arm",
+                   "audio_s": 30.0 * W}, "modes": res}))
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -320,6 +374,9 @@ def main():
         return
     if a.workload == "load":
         load_workload(a)
+        return
+    if a.workload == "transcribe":
+        transcribe_workload(a)
         return
     from franken_whisper_amd import abi, native, synth
 
