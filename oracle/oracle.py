@@ -105,6 +105,8 @@ def lib():
         "ref_mel_hann": (None, [f32p]),
         "ref_num_threads": (C.c_int, []),
         "ref_set_num_threads": (None, [C.c_int]),
+        "ref_set_fast": (None, [C.c_int]),
+        "ref_get_fast": (C.c_int, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -9,6 +9,7 @@
  * count (the reference's own rayon splits are disjoint row bands too).
  */
 #include "refcpu.h"
+#include "refcpu_fast.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -36,6 +37,13 @@ void ref_set_num_threads(int n) {
     (void)n;
 #endif
 }
+
+/* FAST restatement switch: the dense loops below hand their work to the
+ * register-blocked kernels of refcpu_fast.c, which form every output by the
+ * same sequence of operations (the same bits); off, the scalar loops run. */
+static int g_fast = 0;
+void ref_set_fast(int on) { g_fast = on != 0; }
+int ref_get_fast(void) { return g_fast; }
 
 /* ------------------------------------------------------------------------ */
 /* IEEE binary16 <-> binary32, round-to-nearest-even: the `half` 2.7.1 crate's */
@@ -234,6 +242,7 @@ void ref_quantize_enc_i8_rows(const uint16_t *w, int64_t out, int inp, int8_t *q
 
 /* dot_i8, nn.rs:2635-2686: exact i32 sum (|sum| < 2^31 for n <= 5120). */
 int32_t ref_dot_i8(const int8_t *w, const int8_t *x, int n) {
+    if (g_fast) return rf_dot_i8(w, x, n);
     int32_t acc = 0;
     for (int i = 0; i < n; i++) acc += (int32_t)w[i] * (int32_t)x[i];
     return acc;
@@ -244,6 +253,7 @@ int32_t ref_dot_i8(const int8_t *w, const int8_t *x, int n) {
  * then each 8-wide tail chunk reduced the same way and added; then scalar
  * mul+add. */
 float ref_dot_f16c(const uint16_t *w, const float *x, int n) {
+    if (g_fast) return rf_dot_f16c(w, x, n);
     float a[4][8];
     memset(a, 0, sizeof a);
     int i = 0;
@@ -265,6 +275,7 @@ float ref_dot_f16c(const uint16_t *w, const float *x, int n) {
 
 /* dot_i8w_f32, nn.rs:3501-3564: dot_f16c's shape with an i8 weight. */
 float ref_dot_i8w_f32(const int8_t *w, const float *x, int n) {
+    if (g_fast) return rf_dot_i8w_f32(w, x, n);
     float a[4][8];
     memset(a, 0, sizeof a);
     int i = 0;
@@ -393,6 +404,10 @@ void ref_gelu_inplace(float *x, int64_t n) {
 /* softmax_rows, nn.rs:4880-4963 (FW_SIMD_EXP off): max fold from -inf (NaN
  * ignored), glibc expf, non-finite terms -> 0, sequential sum, *= 1/sum. */
 static void softmax_row(float *row, int cols) {
+    if (g_fast) {
+        rf_softmax_row(row, cols);
+        return;
+    }
     float mx = -INFINITY;
     for (int j = 0; j < cols; j++) mx = fmaxf(mx, row[j]);
     if (!isfinite(mx)) return;
@@ -416,6 +431,10 @@ void ref_softmax_rows(float *x, int64_t rows, int cols) {
 /* matmul with FT_SGEMM_STRICT_PARITY (nn.rs:587-604; m == 1 SAXPY nn.rs:565-577
  * is the same order): ascending-k sequential f32 mul+add per output. */
 void ref_matmul_strict(const float *a, const float *b, float *c, int64_t m, int k, int n) {
+    if (g_fast) {
+        rf_matmul(a, k, b, n, c, n, m, k, n);
+        return;
+    }
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < m; i++) {
         float *orow = c + i * n;
@@ -491,12 +510,28 @@ static void attention_per_head(const float *q, int tq, const float *k, const flo
      * inner loop runs across independent keys). */
     float *qh = (float *)malloc(sizeof(float) * (size_t)tq * dh);
     float *kht = (float *)malloc(sizeof(float) * (size_t)tk * dh);
+    /* FAST: the whole score block of a head as one strict-order matmul
+     * (score j of row i: d ascending from +0.0f), the mask and softmax per
+     * row, then P @ V_h (value d of row i: j ascending from +0.0f) */
+    float *sc = g_fast ? (float *)malloc(sizeof(float) * (size_t)tq * tk) : NULL;
     for (int h = 0; h < n_head; h++) {
         int base = h * dh;
         for (int i = 0; i < tq; i++)
             for (int d = 0; d < dh; d++) qh[i * dh + d] = q[(int64_t)i * n_state + base + d] * scale;
         for (int j = 0; j < tk; j++)
             for (int d = 0; d < dh; d++) kht[(int64_t)d * tk + j] = k[(int64_t)j * n_state + base + d] * scale;
+        if (sc) {
+            rf_matmul(qh, dh, kht, tk, sc, tk, tq, dh, tk);
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < tq; i++) {
+                float *srow = sc + (int64_t)i * tk;
+                if (causal)
+                    for (int j = cache_len + i + 1; j < tk; j++) srow[j] = -INFINITY;
+                softmax_row(srow, tk);
+            }
+            rf_matmul(sc, tk, v + base, n_state, out + base, n_state, tq, tk, dh);
+            continue;
+        }
 #pragma omp parallel
         {
             float *srow = (float *)malloc(sizeof(float) * (size_t)tk);
@@ -523,6 +558,7 @@ static void attention_per_head(const float *q, int tq, const float *k, const flo
             free(srow);
         }
     }
+    free(sc);
     free(qh);
     free(kht);
 }
@@ -638,6 +674,10 @@ static void i7_gemm(const float *x, int64_t m, int inp, const int8_t *w, const f
 #pragma omp for schedule(static)
         for (int64_t r = 0; r < m; r++) {
             const float *xr = x + r * inp;
+            if (g_fast) {
+                xs[r] = rf_quant_row_i7(xr, inp, gelu_first ? gt : NULL, ref_f32_to_f16, g, xq + r * inp);
+                continue;
+            }
             for (int i = 0; i < inp; i++) {
                 float v = xr[i];
                 if (gelu_first) v = v <= -10.0f ? 0.0f : (v >= 10.0f ? v : gt[ref_f32_to_f16(v)]);
@@ -649,18 +689,23 @@ static void i7_gemm(const float *x, int64_t m, int inp, const int8_t *w, const f
         }
         free(g);
     }
+    if (g_fast) {
+        rf_epi e = {xs, ws, bias, wc, y, acc_out, 0};
+        rf_gemm_u8i8(xq, w, m, inp, out, &e);
+    } else {
 #pragma omp parallel for schedule(static)
-    for (int64_t r = 0; r < m; r++) {
-        const uint8_t *xr = xq + r * inp;
-        for (int o = 0; o < out; o++) {
-            const int8_t *wr = w + (int64_t)o * inp;
-            int32_t raw = 0;
-            for (int i = 0; i < inp; i++) raw += (int32_t)xr[i] * (int32_t)wr[i];
-            int32_t acc = raw - 128 * wc[o];
-            if (acc_out) acc_out[r * out + o] = acc;
-            float v = (float)acc * xs[r] * ws[o];
-            if (bias) v += bias[o];
-            y[r * out + o] = v;
+        for (int64_t r = 0; r < m; r++) {
+            const uint8_t *xr = xq + r * inp;
+            for (int o = 0; o < out; o++) {
+                const int8_t *wr = w + (int64_t)o * inp;
+                int32_t raw = 0;
+                for (int i = 0; i < inp; i++) raw += (int32_t)xr[i] * (int32_t)wr[i];
+                int32_t acc = raw - 128 * wc[o];
+                if (acc_out) acc_out[r * out + o] = acc;
+                float v = (float)acc * xs[r] * ws[o];
+                if (bias) v += bias[o];
+                y[r * out + o] = v;
+            }
         }
     }
     free(xq);
@@ -679,12 +724,17 @@ static void i8_gemm_enc(const float *x, int64_t m, int inp, const int8_t *w, con
         xs[r] = s;
         ref_quant_row_i8_exact(x + r * inp, inp, 1.0f / s, xq + r * inp);
     }
+    if (g_fast) {
+        rf_epi e = {xs, ws, bias, NULL, y, acc_out, 1};
+        rf_gemm_i8i8(xq, w, m, inp, out, &e);
+    } else {
 #pragma omp parallel for schedule(static)
-    for (int64_t r = 0; r < m; r++) {
-        for (int o = 0; o < out; o++) {
-            int32_t acc = ref_dot_i8(w + (int64_t)o * inp, xq + r * inp, inp);
-            if (acc_out) acc_out[r * out + o] = acc;
-            y[r * out + o] = (float)acc * xs[r] * ws[o] + (bias ? bias[o] : 0.0f);
+        for (int64_t r = 0; r < m; r++) {
+            for (int o = 0; o < out; o++) {
+                int32_t acc = ref_dot_i8(w + (int64_t)o * inp, xq + r * inp, inp);
+                if (acc_out) acc_out[r * out + o] = acc;
+                y[r * out + o] = (float)acc * xs[r] * ws[o] + (bias ? bias[o] : 0.0f);
+            }
         }
     }
     free(xq);
@@ -939,6 +989,12 @@ struct ref_dstate {
     uint16_t *ck16, *cvt16;  /* [L*H][T*dh] natural K, [L*H][dh*T] transposed V */
     int8_t *ck8, *cvt8;
     float *ck8s, *cvt8s;     /* [L*H][T], [L*H][dh] */
+    /* FAST restatement only: per layer the scaled self-attention keys
+     * f16_to_f32(k) * d_head^-0.25 of cached rows [0, kt_len[l]), transposed
+     * [H][dh][kt_ld] so a key block is one vector; rows are appended as the
+     * cache grows (the f16 cache stays the source of truth). */
+    float *kt;
+    int *kt_len, kt_ld, kt_nl;
 };
 
 static void q8_alloc(const uint16_t *w, int64_t out, int inp, int8_t **q, float **s) {
@@ -1058,11 +1114,15 @@ ref_dstate *ref_dstate_new(const ref_decoder *dd, const float *enc, int T) {
 
 void ref_dstate_free(ref_dstate *s) {
     if (!s) return;
+    free(s->kt); free(s->kt_len);
     free(s->kv_k); free(s->kv_v); free(s->ck16); free(s->cvt16);
     free(s->ck8); free(s->cvt8); free(s->ck8s); free(s->cvt8s);
     free(s);
 }
-void ref_dstate_reset(ref_dstate *s) { s->len = 0; }
+void ref_dstate_reset(ref_dstate *s) {
+    s->len = 0;
+    if (s->kt_len) memset(s->kt_len, 0, sizeof(int) * (size_t)s->kt_nl);
+}
 int ref_dstate_len(const ref_dstate *s) { return s->len; }
 const uint16_t *ref_dstate_cross_k_f16(const ref_dstate *s) { return s->ck16; }
 const uint16_t *ref_dstate_cross_vt_f16(const ref_dstate *s) { return s->cvt16; }
@@ -1127,6 +1187,51 @@ static void self_attn_f16(const float *q, const uint16_t *kc, const uint16_t *vc
     free(sc);
 }
 
+/* self_attn_f16 in the FAST restatement: the same per-element arithmetic
+ * (score j = sequential sum over i of qh[i] * (f16_to_f32(k[j][i]) * s) from
+ * +0.0f; value i = sequential sum over j of p[j] * f16_to_f32(v[j][i]) from
+ * +0.0f), with the scaled keys kept transposed per state and the heads in
+ * parallel. */
+static void self_attn_fast(const ref_decoder *dd, ref_dstate *s, int li, const float *q, int tk, float *out) {
+    int d = dd->d, H = dd->H, dh = d / H, nctx = dd->nctx;
+    float scale = powf((float)dh, -0.25f);
+    if (!s->kt) {
+        s->kt_ld = (nctx + 7) & ~7;
+        s->kt_nl = dd->L;
+        s->kt = (float *)calloc((size_t)dd->L * d * s->kt_ld, sizeof(float));
+        s->kt_len = (int *)calloc((size_t)dd->L, sizeof(int));
+    }
+    int ld = s->kt_ld;
+    float *kt = s->kt + (size_t)li * d * ld;
+    const uint16_t *kc = s->kv_k + (size_t)li * nctx * d, *vc = s->kv_v + (size_t)li * nctx * d;
+    int from = s->kt_len[li] < tk - 1 ? s->kt_len[li] : tk - 1;
+    for (int p = from; p < tk; p++)
+        for (int c = 0; c < d; c++) kt[(size_t)c * ld + p] = ref_f16_to_f32(kc[(size_t)p * d + c]) * scale;
+    s->kt_len[li] = tk;
+#pragma omp parallel for schedule(static)
+    for (int h = 0; h < H; h++) {
+        int base = h * dh;
+        float qh[256];
+        float *sc = (float *)malloc(sizeof(float) * (size_t)ld);
+        for (int i = 0; i < dh; i++) qh[i] = q[base + i] * scale;
+        rf_scores_t(qh, kt + (size_t)base * ld, ld, dh, tk, sc);
+        rf_softmax_row(sc, tk);
+        rf_pv_f16(sc, vc + base, d, tk, dh, out + base);
+        free(sc);
+    }
+}
+
+/* gemv_i8 (nn.rs:3168-3231) of one thread: the arithmetic of ref_gemv_i8. */
+static void gemv_i8_serial(const int8_t *W, const float *s_w, int64_t out, int inp, const float *x, float *y,
+                           int8_t *xq) {
+    float xs = ref_act_scale(x, inp);
+    ref_quantize_act_i8(x, inp, 1.0f / xs, xq);
+    for (int64_t o = 0; o < out; o++) {
+        float acc = (float)ref_dot_i8(W + o * inp, xq, inp) * s_w[o] * xs;
+        y[o] = acc + 0.0f;
+    }
+}
+
 /* Exported for the KV-cache invariant (nn.rs:8559): one decode-step row
  * attending to an f16 cache of tk rows. */
 void ref_attention_decode_f16(const float *q, const uint16_t *kc, const uint16_t *vc, int tk, int d,
@@ -1141,6 +1246,28 @@ static void cross_attn(const ref_decoder *dd, const ref_dstate *s, int li, const
                        float *out) {
     int d = dd->d, H = dd->H, dh = dd->dh, T = s->enc_frames;
     float scale = powf((float)dh, -0.25f);
+    if (g_fast) { /* the same arithmetic, heads in parallel */
+#pragma omp parallel for schedule(static)
+        for (int h = 0; h < H; h++) {
+            size_t lh = (size_t)li * H + h;
+            float qh[256];
+            float *sc = (float *)malloc(sizeof(float) * (size_t)T);
+            int8_t *xq = (int8_t *)malloc((size_t)(T > dh ? T : dh));
+            for (int i = 0; i < dh; i++) qh[i] = q[h * dh + i] * scale;
+            if (dd->arm == FWHIP_DEC_INT8) {
+                gemv_i8_serial(s->ck8 + lh * T * dh, s->ck8s + lh * T, T, dh, qh, sc, xq);
+                rf_softmax_row(sc, T);
+                gemv_i8_serial(s->cvt8 + lh * T * dh, s->cvt8s + lh * dh, dh, T, sc, out + h * dh, xq);
+            } else {
+                for (int j = 0; j < T; j++) sc[j] = rf_dot_f16c(s->ck16 + (lh * T + j) * dh, qh, dh);
+                rf_softmax_row(sc, T);
+                for (int i = 0; i < dh; i++) out[h * dh + i] = rf_dot_f16c(s->cvt16 + (lh * dh + i) * T, sc, T);
+            }
+            free(sc);
+            free(xq);
+        }
+        return;
+    }
     float *sc = (float *)malloc(sizeof(float) * (size_t)T);
     for (int h = 0; h < H; h++) {
         size_t lh = (size_t)li * H + h;
@@ -1195,7 +1322,8 @@ int ref_decoder_step(const ref_decoder *dd, ref_dstate *s, const int32_t *tokens
                 kc[(size_t)pos * d + i] = ref_f32_to_f16(qkv[d + i]);
                 vc[(size_t)pos * d + i] = ref_f32_to_f16(qkv[2 * d + i]);
             }
-            self_attn_f16(qkv, kc, vc, pos + 1, d, dd->H, att);
+            if (g_fast) self_attn_fast(dd, s, li, qkv, pos + 1, att);
+            else self_attn_f16(qkv, kc, vc, pos + 1, d, dd->H, att);
             dec_linear(dd, l, 1, att, prefill, y);
             for (int i = 0; i < d; i++) x[i] += y[i];
             ref_layer_norm(x, h, 1, d, sw->cross_ln_w, sw->cross_ln_b, LN_EPS);

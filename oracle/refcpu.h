@@ -132,6 +132,10 @@ void ref_mel_hann(float *out400);
 
 int ref_num_threads(void);
 void ref_set_num_threads(int n);
+/* FAST restatement on/off (refcpu_fast.c: register-blocked AVX2 / F16C
+ * kernels giving the same bits as the scalar loops). */
+void ref_set_fast(int on);
+int ref_get_fast(void);
 
 #ifdef __cplusplus
 }

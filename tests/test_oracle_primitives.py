@@ -65,6 +65,40 @@ int main(void) {
 """
 
 
+FAST_EXP_HARNESS = r"""
+#include <math.h>
+#include <stdio.h>
+#include <stdint.h>
+#include <string.h>
+#include "refcpu_fast.h"
+static uint32_t bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+int main(void) {
+    long bad = 0, n = 0;
+    #pragma omp parallel for reduction(+:bad,n) schedule(static)
+    for (int64_t blk = 0; blk < (1LL << 32); blk += 4096) {
+        float x[4096], y[4096];
+        int m = 0;
+        for (int64_t u = blk; u < blk + 4096; u++) {
+            uint32_t v = (uint32_t)u; float f; memcpy(&f, &v, 4);
+            if (f >= -110.0f && f <= 90.0f) x[m++] = f;
+        }
+        rf_expf_n(x, y, m);
+        for (int i = 0; i < m; i++) if (bits(expf(x[i])) != bits(y[i])) bad++;
+        n += m;
+    }
+    float sp[] = {-INFINITY, INFINITY, 0.0f, -0.0f, -104.0f, -103.9f, 88.7f, 89.0f, 1e30f, -1e30f};
+    float y[10];
+    rf_expf_n(sp, y, 10);
+    for (int i = 0; i < 10; i++) if (bits(expf(sp[i])) != bits(y[i])) bad++;
+    float q = NAN;
+    rf_expf_n(&q, y, 1);
+    if (!isnan(y[0])) bad++;
+    printf("%ld %ld\n", n, bad);
+    return bad != 0;
+}
+"""
+
+
 LOG_HARNESS = r"""
 #include <math.h>
 #include <stdio.h>
@@ -98,12 +132,21 @@ def _compile_run(tmp_path, src, name, extra):
 def test_f16_conversions_exhaustive_vs_f16c(tmp_path):
     O.build()
     r = _compile_run(tmp_path, F16_HARNESS, "f16x", ["-I", os.path.join(ROOT, "oracle"), os.path.join(
-        ROOT, "oracle", "refcpu.c")])
+        ROOT, "oracle", "refcpu.c"), os.path.join(ROOT, "oracle", "refcpu_fast.c")])
     assert r.returncode == 0 and r.stdout.strip() == "0", r.stdout + r.stderr
 
 
 def test_device_expf_restatement_matches_glibc_exhaustive(tmp_path):
     r = _compile_run(tmp_path, EXP_HARNESS, "expx", ["-I", os.path.join(ROOT, "franken_whisper_amd", "csrc")])
+    n, bad = map(int, r.stdout.split())
+    assert bad == 0 and n > 2_000_000_000, r.stdout
+
+
+def test_fast_softmax_expf_matches_glibc_exhaustive(tmp_path):
+    """The 8-lane expf of the FAST restatement's softmax (oracle/refcpu_fast.c)
+    against the host's expf over every float of [-110, 90] plus the specials."""
+    r = _compile_run(tmp_path, FAST_EXP_HARNESS, "fexpx", ["-I", os.path.join(ROOT, "oracle"),
+                                                           os.path.join(ROOT, "oracle", "refcpu_fast.c")])
     n, bad = map(int, r.stdout.split())
     assert bad == 0 and n > 2_000_000_000, r.stdout
 
