@@ -24,6 +24,8 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+#include <type_traits>
+
 #include "fw_dec.h"
 
 template <int NV>
@@ -887,9 +889,23 @@ void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *c
 #define XP_MAXG 24 // full 64-key groups of V^T a lane holds in registers
 __device__ __forceinline__ int fw_xp_pos(int e) { return (e & 7) * 8 + (e >> 5) * 4 + ((e >> 3) & 3); }
 
+// FQ: the cross LayerNorm and this head's q rows are formed in the block
+// (gemv_f16 of LN(x_s), nn.rs:2346-2460, on the slot-order matrix of
+// fw_launch_pack_gemv16 at 16 lanes per row, d == 1280): wave 0 normalizes
+// the stream's residual row into LDS (the GEMV's one-wave LayerNorm), then
+// every lane carries 2 of the 64 rows for its 2 dot_f16c slots, the slot tree
+// runs over the 16 lanes of a row, and the bias is added; so q holds the bits
+// the separate GEMV writes.
+#define XQ_D 1280
+#ifndef XQ_EARLY
+#define XQ_EARLY 8 // 64-key rounds requested before the q projection
+#endif
+template <bool FQ>
 __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const uint16_t *ckp, const uint16_t *cvtp,
                                                          float *att, int d, int T, int Tv, int H, int L, int layer,
-                                                         float scale) {
+                                                         float scale, const uint16_t *__restrict__ wq,
+                                                         const float *__restrict__ bq, const float *__restrict__ x,
+                                                         const float *__restrict__ lnw, const float *__restrict__ lnb) {
     extern __shared__ __align__(16) float scf[]; // [Tv]: scores, then p in the value pass order
     __shared__ float red[8];
     __shared__ float inv_s;
@@ -899,24 +915,95 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
     const uint16_t *K = ckp + lh * (size_t)T * 64;
     const uint16_t *V = cvtp + lh * (size_t)Tv * 64;
     const int nc = T >> 5, ng = nc >> 1, ntail = T - nc * 32;
-    // loads retire in order (vmcnt), so the first requests are the ones used
-    // first: q, then every key row this lane multiplies (key j = r * 64 +
-    // wave * 8 + rg)
-    const float *qs = qc + (size_t)s * d + h * 64;
     float q0[4], q1[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        q0[k] = qs[8 * k + l];
-        q1[k] = qs[32 + 8 * k + l];
-    }
     // (no load sits behind a branch: addresses past the end are clamped to
     // the last row and the values unused, so the waits count loads exactly)
     const int nr = (T + 63) >> 6;
     uint4 kv[XP_MAXG];
+    auto load_keys = [&](auto lo_tag, auto hi_tag) {
+        constexpr int LO = decltype(lo_tag)::value, HI = decltype(hi_tag)::value;
 #pragma unroll
-    for (int r = 0; r < XP_MAXG; r++) {
-        const int j = r * 64 + wave * 8 + rg;
-        kv[r] = *(const uint4 *)(K + (size_t)(j < T ? j : T - 1) * 64 + l * 8);
+        for (int r = LO; r < HI; r++) {
+            const int j = r * 64 + wave * 8 + rg;
+            kv[r] = *(const uint4 *)(K + (size_t)(j < T ? j : T - 1) * 64 + l * 8);
+        }
+    };
+    using k0 = std::integral_constant<int, 0>;
+    using kE = std::integral_constant<int, XQ_EARLY>;
+    using kN = std::integral_constant<int, XP_MAXG>;
+    if constexpr (FQ) {
+        constexpr int NV = XQ_D / 256, G = XQ_D / 128; // float4s per lane of a row; 16-byte groups per weight row
+        __shared__ __align__(16) float xl[XQ_D];
+        __shared__ float qf[64];
+        const int p = lane & 15, rq = lane >> 4; // lane of the row group, row group of the wave
+        float4 lv[NV], lw[NV], lb[NV];
+        bool lok[NV];
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            lok[k] = true;
+            lv[k] = ((const float4 *)(x + (size_t)s * XQ_D))[lane + k * 64];
+        }
+        fw_ln_load_wb<NV>(lok, lnw, lnb, lw, lb, lane);
+        // rows h * 64 + wave * 8 + r * 4 + rq, r = 0, 1
+        uint4 wv[2][G];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const uint4 *wr = (const uint4 *)(wq + (size_t)(h * 64 + wave * 8 + r * 4 + rq) * XQ_D) + p;
+#pragma unroll
+            for (int g = 0; g < G; g++) wv[r][g] = wr[g * 16];
+        }
+        const float bv0 = bq ? bq[h * 64 + wave * 8 + rq] : 0.0f, bv1 = bq ? bq[h * 64 + wave * 8 + 4 + rq] : 0.0f;
+        // the first key rows stream in while q is formed (all of them would
+        // not fit the registers beside the q operands)
+        load_keys(k0{}, kE{});
+        if (wave == 0) fw_ln_quant_core<NV>(lv, lok, lw, lb, xl, XQ_D, 0, nullptr, nullptr, lane);
+        __syncthreads();
+        // lane p = kh * 8 + l holds slots 8 (2 kh + kk) + l; a group is 4 chunks
+        float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+        const int kh = p >> 3, pl = p & 7;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const int c = g * 4 + cc;
+                const float x0 = xl[c * 32 + 8 * (2 * kh) + pl], x1 = xl[c * 32 + 8 * (2 * kh + 1) + pl];
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const uint32_t u[4] = {wv[r][g].x, wv[r][g].y, wv[r][g].z, wv[r][g].w};
+                    const float w0 = fw_h2f((uint16_t)(u[cc] & 0xffffu)), w1 = fw_h2f((uint16_t)(u[cc] >> 16));
+                    acc[r][0] = __builtin_fmaf(w0, x0, acc[r][0]);
+                    acc[r][1] = __builtin_fmaf(w1, x1, acc[r][1]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            float v = acc[r][0] + acc[r][1];
+            v = v + __shfl_xor(v, 8, 64);
+            v = v + __shfl_xor(v, 1, 64);
+            v = v + __shfl_xor(v, 2, 64);
+            v = v + __shfl_xor(v, 4, 64);
+            if (bq) v = v + (r ? bv1 : bv0);
+            if (p == 0) qf[wave * 8 + r * 4 + rq] = v;
+        }
+        load_keys(kE{}, kN{});
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            q0[k] = qf[8 * k + l];
+            q1[k] = qf[32 + 8 * k + l];
+        }
+    } else {
+        // loads retire in order (vmcnt), so the first requests are the ones
+        // used first: q, then every key row this lane multiplies (key j =
+        // r * 64 + wave * 8 + rg)
+        const float *qs = qc + (size_t)s * d + h * 64;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            q0[k] = qs[8 * k + l];
+            q1[k] = qs[32 + 8 * k + l];
+        }
+        load_keys(k0{}, kN{});
     }
     // qh = q * s, this lane's slots of both chunks
 #pragma unroll
@@ -1094,8 +1181,20 @@ void fw_launch_pack_cross_f16(hipStream_t st, const uint16_t *ck, const uint16_t
 void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp, float *att,
                                int d, int T, int H, int L, int layer, int ns, float scale) {
     const int Tv = fw_cross_f16p_tv(T);
-    hipLaunchKernelGGL(k_cross_attn_f16p, dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st, qc, ckp, cvtp, att,
-                       d, T, Tv, H, L, layer, scale);
+    hipLaunchKernelGGL(k_cross_attn_f16p<false>, dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st, qc, ckp,
+                       cvtp, att, d, T, Tv, H, L, layer, scale, nullptr, nullptr, nullptr, nullptr, nullptr);
+}
+
+bool fw_cross_f16pq_ok(int d, int T, int H) { return d == XQ_D && H * 64 == d && fw_cross_f16p_ok(T); }
+
+// the same with the cross LayerNorm of x and the q projection (wq: the cross
+// q weights in fw_launch_pack_gemv16's slot order, 16 lanes per row) inside
+void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float *bq, const float *x, const float *lnw,
+                                const float *lnb, const uint16_t *ckp, const uint16_t *cvtp, float *att, int d, int T,
+                                int H, int L, int layer, int ns, float scale) {
+    const int Tv = fw_cross_f16p_tv(T);
+    hipLaunchKernelGGL(k_cross_attn_f16p<true>, dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st, nullptr, ckp,
+                       cvtp, att, d, T, Tv, H, L, layer, scale, wq, bq, x, lnw, lnb);
 }
 
 // ---------------------------------------------------------------------------

@@ -43,6 +43,13 @@ void fw_launch_pack_cross_f16(hipStream_t st, const uint16_t *ck, const uint16_t
                               size_t rows_k, size_t rows_v, int T);
 void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp, float *att,
                                int d, int T, int H, int L, int layer, int ns, float scale);
+// fw_launch_cross_attn_f16p with the cross LayerNorm of x [ns, d] and the q
+// projection inside (wq in fw_launch_pack_gemv16's slot order at 16 lanes per
+// row, bq the bias); needs fw_cross_f16pq_ok(d, T, H)
+bool fw_cross_f16pq_ok(int d, int T, int H);
+void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float *bq, const float *x, const float *lnw,
+                                const float *lnb, const uint16_t *ckp, const uint16_t *cvtp, float *att, int d, int T,
+                                int H, int L, int layer, int ns, float scale);
 void fw_launch_gemm_strict(hipStream_t st, const float *A, const uint16_t *B, int m, int n, int k, int epi,
                            float *C, const float *bias, float scale, uint16_t *out16, int T, int H, int L,
                            int layer, int ldc = 0, const float *gelu_tab = nullptr, const float *pos = nullptr);

@@ -780,9 +780,16 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 fw_gemv16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
             fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
             fw_gemv16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
-            fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0, gt);
-            if (st->ck16p) fw_launch_cross_attn_f16p(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S, scale);
-            else fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
+            if (st->ck16p && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) && fw_gemv16_lpr(d, d) == 16) {
+                // the cross LayerNorm and q projection run inside the cross-attention kernel
+                fw_launch_cross_attn_f16pq(s, l.cq16, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck16p,
+                                           st->cvt16p, st->att, d, T, H, L, li, S, scale);
+            } else {
+                fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0, gt);
+                if (st->ck16p)
+                    fw_launch_cross_attn_f16p(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S, scale);
+                else fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
+            }
             fw_gemv16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
             fw_gemv16_ln(s, l.fc1_16, l.fc1_b, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, st->ff, dff, d, S, dff, 2, gt);
             fw_gemv16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
