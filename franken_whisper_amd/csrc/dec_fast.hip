@@ -1239,6 +1239,69 @@ __device__ __forceinline__ float fw_pv_chain(const float *p, const uint16_t *v, 
 // for the scores; the cache rows of this head are staged in LDS for the
 // value pass.
 #define SA_STG 4
+// The attention of one (head, stream) over cache rows [0, tk) once the
+// token's own row is in the cache and qh (= q * s, LDS) is set; NT threads.
+template <int NT>
+__device__ __forceinline__ void sa_attend(const float *qh, const uint16_t *kc, const uint16_t *vc, size_t cbase,
+                                          int base, int d, int tk, float scale, float *sc, uint16_t *vs, float *red,
+                                          float *inv_s, float *out, float *pmax_slot) {
+    const int t = threadIdx.x;
+    // stage V rows [0, tk) of this head (8 x 16 bytes per row), SA_STG chunks
+    // per thread per round, loads issued before the LDS stores
+    for (int c0 = 0; c0 < tk * 8; c0 += NT * SA_STG) {
+        uint4 v[SA_STG];
+#pragma unroll
+        for (int u = 0; u < SA_STG; u++) {
+            int c = c0 + t + u * NT;
+            int cc = c < tk * 8 ? c : tk * 8 - 1;
+            v[u] = *(const uint4 *)(vc + cbase + (size_t)(cc >> 3) * d + base + (cc & 7) * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < SA_STG; u++) {
+            int c = c0 + t + u * NT;
+            if (c < tk * 8) *(uint4 *)(vs + (c >> 3) * 64 + (c & 7) * 8) = v[u];
+        }
+    }
+    float mx = -INFINITY;
+    for (int j = t; j < tk; j += NT) {
+        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)j * d + base);
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            uint4 u = kr[c];
+            uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                acc += qh[c * 8 + 2 * e] * (fw_h2f(ww[e] & 0xffff) * scale);
+                acc += qh[c * 8 + 2 * e + 1] * (fw_h2f(ww[e] >> 16) * scale);
+            }
+        }
+        sc[j] = acc;
+        mx = fmaxf(mx, acc);
+    }
+    mx = fw_block_max(mx, red);
+    const bool fin = isfinite(mx);
+    if (fin)
+        for (int j = t; j < tk; j += NT) {
+            float e = fw_expf(sc[j] - mx);
+            sc[j] = isfinite(e) ? e : 0.0f;
+        }
+    __syncthreads();
+    if (t == 0) *inv_s = fin ? fw_seq_sum_inv(sc, tk) : 0.0f;
+    __syncthreads();
+    const float inv = *inv_s;
+    if (inv > 0.0f)
+        for (int j = t; j < tk; j += NT) sc[j] = sc[j] * inv;
+    __syncthreads();
+    if (t < 64) {
+        const float acc = fw_pv_chain(sc, vs, tk, t);
+        out[t] = acc;
+        // this head's share of the row amax the int8 consumer needs
+        const float m = fw_dpp_wave_max(fabsf(acc));
+        if (pmax_slot && t == 0) *pmax_slot = m;
+    }
+}
+
 __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *kc, uint16_t *vc, float *att,
                                                     const int *posp, int d, int nctx, int L, int layer,
                                                     float scale, float *pmax) {
@@ -1260,61 +1323,117 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
         qh[t] = q[base + t] * scale;
     }
     __syncthreads(); // this block's own cache row is visible to its threads
-    const int tk = pos + 1;
-    // stage V rows [0, tk) of this head (8 x 16 bytes per row), SA_STG chunks
-    // per thread per round, loads issued before the LDS stores
-    for (int c0 = 0; c0 < tk * 8; c0 += 256 * SA_STG) {
-        uint4 v[SA_STG];
+    sa_attend<256>(qh, kc, vc, cbase, base, d, pos + 1, scale, sc, vs, red, &inv_s, att + (size_t)s * d + base,
+                   pmax ? pmax + (size_t)s * gridDim.x + h : nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// The f16 arm's self-attention sublayer for one (head, stream), d == 1280: the
+// head's 192 rows of the fused q/k/v projection (gemv_f16, nn.rs:2346-2460,
+// bias [q_b | 0 | v_b]) of LN(x_s) (LN: the attention LayerNorm of the
+// residual row, wave 0, the GEMV's one-wave arithmetic; else x is the already
+// normalized row), then k_self_attn2's attention with this token's k/v
+// appended.  The projection runs on the slot-order matrix of
+// fw_launch_pack_gemv16 (16 lanes per row): lane p = kh * 8 + l of a row
+// group holds the normalized row's values of its two dot_f16c slots
+// 8 (2 kh + kk) + l of all 40 chunks in registers, so a 32-row batch (8 waves
+// x 4 row groups) is 10 weight loads and 80 FMAs per lane; the six batches
+// (q, k, v halves) are double-buffered.  The slot tree and the bias are the
+// GEMV's, so q/k/v hold its bits.
+template <bool LN>
+__global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restrict__ wqkv,
+                                                        const float *__restrict__ bqkv, const float *__restrict__ x,
+                                                        const float *__restrict__ lnw, const float *__restrict__ lnb,
+                                                        uint16_t *kc, uint16_t *vc, float *att, const int *posp,
+                                                        int nctx, int L, int layer, float scale) {
+    constexpr int D = XQ_D, NV = D / 256, G = D / 128, NC = D / 32;
+    extern __shared__ __align__(16) unsigned char sm4[];
+    float *sc = (float *)sm4;                                              // [nctx]
+    uint16_t *vs = (uint16_t *)(sm4 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
+    __shared__ __align__(16) float xl[D];
+    __shared__ float qkvl[192];
+    __shared__ float qh[64];
+    __shared__ float red[8];
+    __shared__ float inv_s;
+    const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int p = lane & 15, rq = lane >> 4, kh = p >> 3, pl = p & 7;
+    const int base = h * 64;
+    float4 lv[NV], lw[NV], lb[NV];
+    bool lok[NV];
+    if (wave == 0) {
 #pragma unroll
-        for (int u = 0; u < SA_STG; u++) {
-            int c = c0 + t + u * 256;
-            int cc = c < tk * 8 ? c : tk * 8 - 1;
-            v[u] = *(const uint4 *)(vc + cbase + (size_t)(cc >> 3) * d + base + (cc & 7) * 8);
+        for (int k = 0; k < NV; k++) {
+            lok[k] = true;
+            lv[k] = ((const float4 *)(x + (size_t)s * D))[lane + k * 64];
         }
+        if constexpr (LN) fw_ln_load_wb<NV>(lok, lnw, lnb, lw, lb, lane);
+    }
+    // row of batch b for this lane: local row 32 b + 4 wave + rq of the head's
+    // 192 (q rows 0-63, k 64-127, v 128-191), global row part * d + base + i
+    auto grow = [&](int b) {
+        const int r = 32 * b + 4 * wave + rq;
+        return (r >> 6) * D + base + (r & 63);
+    };
+    uint4 wv[2][G];
+    auto loadw = [&](int set, int b) {
+        const uint4 *wr = (const uint4 *)(wqkv + (size_t)grow(b) * D) + p;
 #pragma unroll
-        for (int u = 0; u < SA_STG; u++) {
-            int c = c0 + t + u * 256;
-            if (c < tk * 8) *(uint4 *)(vs + (c >> 3) * 64 + (c & 7) * 8) = v[u];
+        for (int g = 0; g < G; g++) wv[set][g] = wr[g * 16];
+    };
+    loadw(0, 0);
+    loadw(1, 1);
+    if (wave == 0) {
+        if constexpr (LN) fw_ln_quant_core<NV>(lv, lok, lw, lb, xl, D, 0, nullptr, nullptr, lane);
+        else {
+#pragma unroll
+            for (int k = 0; k < NV; k++) ((float4 *)xl)[lane + k * 64] = lv[k];
         }
     }
-    float mx = -INFINITY;
-    for (int j = t; j < tk; j += 256) {
-        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)j * d + base);
-        float acc = 0.0f;
+    __syncthreads();
+    float xr[NC][2];
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            uint4 u = kr[c];
-            uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+    for (int c = 0; c < NC; c++) {
+        xr[c][0] = xl[c * 32 + 8 * (2 * kh) + pl];
+        xr[c][1] = xl[c * 32 + 8 * (2 * kh + 1) + pl];
+    }
+    auto rowdot = [&](int set, int b) {
+        float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                acc += qh[c * 8 + 2 * e] * (fw_h2f(ww[e] & 0xffff) * scale);
-                acc += qh[c * 8 + 2 * e + 1] * (fw_h2f(ww[e] >> 16) * scale);
+        for (int g = 0; g < G; g++) {
+            const uint32_t u[4] = {wv[set][g].x, wv[set][g].y, wv[set][g].z, wv[set][g].w};
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                a0 = __builtin_fmaf(fw_h2f((uint16_t)(u[cc] & 0xffffu)), xr[g * 4 + cc][0], a0);
+                a1 = __builtin_fmaf(fw_h2f((uint16_t)(u[cc] >> 16)), xr[g * 4 + cc][1], a1);
             }
         }
-        sc[j] = acc;
-        mx = fmaxf(mx, acc);
+        float v = a0 + a1;
+        v = v + __shfl_xor(v, 8, 64);
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        const int gr = grow(b);
+        if (bqkv) v = v + bqkv[gr];
+        if (p == 0) qkvl[32 * b + 4 * wave + rq] = v;
+    };
+#pragma unroll
+    for (int b = 0; b < 6; b++) {
+        rowdot(b & 1, b);
+        if (b + 2 < 6) loadw(b & 1, b + 2);
     }
-    mx = fw_block_max(mx, red);
-    const bool fin = isfinite(mx);
-    if (fin)
-        for (int j = t; j < tk; j += 256) {
-            float e = fw_expf(sc[j] - mx);
-            sc[j] = isfinite(e) ? e : 0.0f;
-        }
     __syncthreads();
-    if (t == 0) inv_s = fin ? fw_seq_sum_inv(sc, tk) : 0.0f;
-    __syncthreads();
-    const float inv = inv_s;
-    if (inv > 0.0f)
-        for (int j = t; j < tk; j += 256) sc[j] = sc[j] * inv;
-    __syncthreads();
+    const int pos = *posp;
+    const size_t cbase = ((size_t)s * L + layer) * nctx * D;
     if (t < 64) {
-        const float acc = fw_pv_chain(sc, vs, tk, t);
-        att[(size_t)s * d + base + t] = acc;
-        // this head's share of the row amax the int8 consumer needs
-        const float m = fw_dpp_wave_max(fabsf(acc));
-        if (pmax && t == 0) pmax[(size_t)s * gridDim.x + h] = m;
+        kc[cbase + (size_t)pos * D + base + t] = fw_f2h(qkvl[64 + t]);
+        vc[cbase + (size_t)pos * D + base + t] = fw_f2h(qkvl[128 + t]);
+        qh[t] = qkvl[t] * scale;
     }
+    __threadfence_block();
+    __syncthreads(); // this block's own cache row is visible to its threads
+    sa_attend<512>(qh, kc, vc, cbase, base, D, pos + 1, scale, sc, vs, red, &inv_s, att + (size_t)s * D + base,
+                   nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1887,6 +2006,23 @@ void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16
     size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
     hipLaunchKernelGGL(k_self_attn2, dim3(H, ns), dim3(256), shm, st, qkv, kc, vc, att, posp, d, nctx, L, layer,
                        scale, pmax);
+}
+
+bool fw_self_attn_f16q_ok(int d, int H) { return d == XQ_D && H * 64 == d; }
+
+// q/k/v projection (wqkv in fw_launch_pack_gemv16's slot order at 16 lanes per
+// row, bias bqkv) of LN(x) (or of x itself when lnw is null: an already
+// normalized row) and the self-attention of k_self_attn2, one launch
+void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
+                              const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
+                              const int *posp, int H, int nctx, int L, int layer, int ns, float scale) {
+    size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
+    if (lnw)
+        hipLaunchKernelGGL(k_self_attn_f16q<true>, dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb, kc, vc,
+                           att, posp, nctx, L, layer, scale);
+    else
+        hipLaunchKernelGGL(k_self_attn_f16q<false>, dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb, kc, vc,
+                           att, posp, nctx, L, layer, scale);
 }
 
 template <int NV>

@@ -46,6 +46,13 @@ void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *
 // fw_launch_cross_attn_f16p with the cross LayerNorm of x [ns, d] and the q
 // projection inside (wq in fw_launch_pack_gemv16's slot order at 16 lanes per
 // row, bq the bias); needs fw_cross_f16pq_ok(d, T, H)
+// the f16 arm's attention LayerNorm (lnw null: x already normalized), q/k/v
+// projection (wqkv in fw_launch_pack_gemv16's slot order at 16 lanes per row)
+// and self-attention in one launch; needs fw_self_attn_f16q_ok(d, H)
+bool fw_self_attn_f16q_ok(int d, int H);
+void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
+                              const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
+                              const int *posp, int H, int nctx, int L, int layer, int ns, float scale);
 bool fw_cross_f16pq_ok(int d, int T, int H);
 void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float *bq, const float *x, const float *lnw,
                                 const float *lnb, const uint16_t *ckp, const uint16_t *cvtp, float *att, int d, int T,

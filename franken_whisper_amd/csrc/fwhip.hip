@@ -773,12 +773,23 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 return fw_fail(FWHIP_ERR_INVALID, "block GEMV: unsupported mlp width");
         } else {
             // (layer 0's attention LayerNorm ran with the embedding, into h)
-            if (li > 0)
-                fw_gemv16_ln(s, l.qkv16, l.qkv_b, st->x, st->h, l.attn_ln_w, l.attn_ln_b, st->qkv, 3 * d, d, S, 3 * d,
-                             0, gt);
-            else
-                fw_gemv16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
-            fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale);
+            if (fw_self_attn_f16q_ok(d, H) && fw_gemv16_ok(3 * d, d) && fw_gemv16_lpr(3 * d, d) == 16) {
+                // the LayerNorm, q/k/v projection and attention in one kernel
+                if (li > 0)
+                    fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, st->x, l.attn_ln_w, l.attn_ln_b, st->kv_k,
+                                             st->kv_v, st->att, st->pos, H, dd->nctx, L, li, S, scale);
+                else
+                    fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, st->h, nullptr, nullptr, st->kv_k, st->kv_v,
+                                             st->att, st->pos, H, dd->nctx, L, li, S, scale);
+            } else {
+                if (li > 0)
+                    fw_gemv16_ln(s, l.qkv16, l.qkv_b, st->x, st->h, l.attn_ln_w, l.attn_ln_b, st->qkv, 3 * d, d, S,
+                                 3 * d, 0, gt);
+                else
+                    fw_gemv16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
+                fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S,
+                                     scale);
+            }
             fw_gemv16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
             if (st->ck16p && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) && fw_gemv16_lpr(d, d) == 16) {
                 // the cross LayerNorm and q projection run inside the cross-attention kernel
