@@ -456,9 +456,23 @@ __global__ void k_fill_u16(uint16_t *p, size_t n, uint16_t v) {
 // 4 x 8 KB) fed global -> LDS directly through an AT_NS-stage ring, one
 // barrier per tile.  Rows are 128 bytes; 16-byte chunk c of row r sits at
 // chunk c ^ (r & 7), which keeps the fragment reads free of bank conflicts.
+// QPW 32-query sub-tiles per wave share each K / V^T fragment read from LDS
+// (the fragment reads, not the MFMAs, set the LDS traffic per query), every
+// query's arithmetic the same whatever QPW is.  Measured on MI355X (16
+// large-v3-turbo windows, per launch): 8 waves x 2 sub-tiles with a 2-stage
+// ring 550 us; 8 x 1 with 3 stages 620 us; 8 x 1 with 2 stages 608 us;
+// 4 x 2 with 2 stages 601 us; 4 x 2 with 3 stages 724 us.
+#ifndef AT_QW
 #define AT_QW 8
-template <int AT_QW_, int AT_NS>
-__global__ void __launch_bounds__(64 * AT_QW_) k_attention2(const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
+#endif
+#ifndef AT_NSTAGE
+#define AT_NSTAGE 2
+#endif
+#ifndef AT_QPW
+#define AT_QPW 2
+#endif
+template <int AT_QW_, int AT_NS, int QPW>
+__global__ void __launch_bounds__(64 * AT_QW_, 2) k_attention2(const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                                                            const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl,
                                                            int T, int Tp, int H, int d, int out_mode, float *of,
                                                            uint16_t *oh, uint16_t *ol) {
@@ -466,12 +480,13 @@ __global__ void __launch_bounds__(64 * AT_QW_) k_attention2(const uint16_t *qh, 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = blockIdx.y, b = blockIdx.z;
     const size_t bh = (size_t)b * H + h;
-    const int q0 = blockIdx.x * 32 * AT_QW_ + wave * 32;
-    const int myq = q0 + (lane & 31);
+    const int q0 = (blockIdx.x * AT_QW_ + wave) * 32 * QPW;
     const int nt = (T + 63) >> 6;
-    // this lane's Q^T fragments: q = myq, dims ks*16 + (l/32)*8 .. +8
-    v8h qfh[4], qfl[4];
-    {
+    // this lane's Q^T fragments: q = q0 + 32 qs + l % 32, dims ks*16 + (l/32)*8 .. +8
+    v8h qfh[QPW][4], qfl[QPW][4];
+#pragma unroll
+    for (int qs = 0; qs < QPW; qs++) {
+        const int myq = q0 + qs * 32 + (lane & 31);
         const int qc = myq < T ? myq : T - 1;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
@@ -479,8 +494,8 @@ __global__ void __launch_bounds__(64 * AT_QW_) k_attention2(const uint16_t *qh, 
             v8h a = *(const v8h *)(qh + (bh * T + qc) * 64 + dd), c = *(const v8h *)(ql + (bh * T + qc) * 64 + dd);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                qfh[ks][e] = myq < T ? a[e] : (_Float16)0.0f;
-                qfl[ks][e] = myq < T ? c[e] : (_Float16)0.0f;
+                qfh[qs][ks][e] = myq < T ? a[e] : (_Float16)0.0f;
+                qfl[qs][ks][e] = myq < T ? c[e] : (_Float16)0.0f;
             }
         }
     }
@@ -517,14 +532,20 @@ __global__ void __launch_bounds__(64 * AT_QW_) k_attention2(const uint16_t *qh, 
         }
     };
     // Each accumulator takes all three f16-pair products in turn (hi*hi,
-    // lo*hi, hi*lo); the two 32-key (or 32-dim) halves are independent
-    // chains, interleaved so consecutive MFMAs never depend on each other.
-    v16f o[2];
+    // lo*hi, hi*lo); the two 32-key (or 32-dim) halves and the sub-tiles are
+    // independent chains, interleaved so consecutive MFMAs never depend on
+    // each other.
+    v16f o[QPW][2];
+    float m[QPW], l[QPW];
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int qs = 0; qs < QPW; qs++) {
+        m[qs] = -INFINITY;
+        l[qs] = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 16; r++) o[j][r] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[qs][j][r] = 0.0f;
+    }
     const float sl2 = 0.125f * 1.4426950408889634f;
 #pragma unroll
     for (int p = 0; p < AT_NS - 1; p++) issue(p);
@@ -536,7 +557,9 @@ __global__ void __launch_bounds__(64 * AT_QW_) k_attention2(const uint16_t *qh, 
         const int k0 = it * 64;
         // the first MFMA of each chain takes a zero accumulator operand
         const v16f zero = {};
-        v16f st[2] = {zero, zero};
+        v16f st[QPW][2];
+#pragma unroll
+        for (int qs = 0; qs < QPW; qs++) st[qs][0] = st[qs][1] = zero;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             v8h ah[2], al[2];
@@ -547,70 +570,72 @@ __global__ void __launch_bounds__(64 * AT_QW_) k_attention2(const uint16_t *qh, 
                 ah[t] = *(const v8h *)(sK + off);
                 al[t] = *(const v8h *)(sK + 64 * 64 + off);
             }
-            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], qfh[ks], st[0], 0, 0, 0);
-            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], qfh[ks], st[1], 0, 0, 0);
-            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0], qfh[ks], st[0], 0, 0, 0);
-            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1], qfh[ks], st[1], 0, 0, 0);
-            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], qfl[ks], st[0], 0, 0, 0);
-            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], qfl[ks], st[1], 0, 0, 0);
+#pragma unroll
+            for (int qs = 0; qs < QPW; qs++) {
+                st[qs][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], qfh[qs][ks], st[qs][0], 0, 0, 0);
+                st[qs][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], qfh[qs][ks], st[qs][1], 0, 0, 0);
+            }
+#pragma unroll
+            for (int qs = 0; qs < QPW; qs++) {
+                st[qs][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0], qfh[qs][ks], st[qs][0], 0, 0, 0);
+                st[qs][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1], qfh[qs][ks], st[qs][1], 0, 0, 0);
+            }
+#pragma unroll
+            for (int qs = 0; qs < QPW; qs++) {
+                st[qs][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], qfl[qs][ks], st[qs][0], 0, 0, 0);
+                st[qs][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], qfl[qs][ks], st[qs][1], 0, 0, 0);
+            }
         }
         // keys past T exist only in the last tile
         if (k0 + 64 > T) {
 #pragma unroll
+            for (int qs = 0; qs < QPW; qs++)
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int key = k0 + t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                        if (key >= T) st[qs][t][r] = -INFINITY;
+                    }
+        }
+#pragma unroll
+        for (int qs = 0; qs < QPW; qs++) {
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, st[qs][t][r]);
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            const float mnew = fmaxf(m[qs], tmax);
+            // exp2((s - mnew) * sl2) as one fma per score
+            const float nms = -mnew * sl2;
+            float psum = 0.0f;
+#pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int key = k0 + t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                    if (key >= T) st[t][r] = -INFINITY;
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qs][t][r], sl2, nms));
+                    st[qs][t][r] = pv;
+                    psum += pv;
                 }
-        }
-        float tmax = -INFINITY;
+            psum += __shfl_xor(psum, 32, 64);
+            // rescale only when some row's running max moved (wave-uniform test)
+            if (__builtin_amdgcn_ballot_w64(mnew != m[qs])) {
+                const float alpha = __builtin_amdgcn_exp2f((m[qs] - mnew) * sl2);
+                l[qs] *= alpha;
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+                for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, st[t][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mnew = fmaxf(m, tmax);
-        // exp2((s - mnew) * sl2) as one fma per score
-        const float nms = -mnew * sl2;
-        float psum = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][r], sl2, nms));
-                st[t][r] = pv;
-                psum += pv;
+                    for (int r = 0; r < 16; r++) o[qs][j][r] *= alpha;
             }
-        psum += __shfl_xor(psum, 32, 64);
-        // rescale only when some row's running max moved (wave-uniform test)
-        if (__builtin_amdgcn_ballot_w64(mnew != m)) {
-            const float alpha = __builtin_amdgcn_exp2f((m - mnew) * sl2);
-            l *= alpha;
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+            l[qs] += psum;
+            m[qs] = mnew;
         }
-        l += psum;
-        m = mnew;
         const uint16_t *sV = &sm[it % AT_NS][2][0];
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                // f16 pair of P, two values per conversion
-                v8h ph, pl;
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const v2f pv = {st[t][8 * u + e], st[t][8 * u + e + 1]};
-                    const v2h hh = __builtin_convertvector(pv, v2h);
-                    const v2h lo = __builtin_convertvector(pv - __builtin_convertvector(hh, v2f), v2h);
-                    ph[e] = hh[0];
-                    ph[e + 1] = hh[1];
-                    pl[e] = lo[0];
-                    pl[e + 1] = lo[1];
-                }
                 // P holds keys {G + 4h + 0..3, G + 8 + 4h + 0..3} (G = 32t + 16u,
                 // h = lane / 32); V^T stores each 16-key group with bits 2 and 3
                 // of the key swapped, so these 8 keys are one 16-byte chunk
@@ -623,27 +648,46 @@ __global__ void __launch_bounds__(64 * AT_QW_) k_attention2(const uint16_t *qh, 
                     vh[j] = *(const v8h *)(sV + a);
                     vl[j] = *(const v8h *)(sV + 64 * 64 + a);
                 }
-                o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[0], ph, o[0], 0, 0, 0);
-                o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[1], ph, o[1], 0, 0, 0);
-                o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[0], ph, o[0], 0, 0, 0);
-                o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[1], ph, o[1], 0, 0, 0);
-                o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[0], pl, o[0], 0, 0, 0);
-                o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[1], pl, o[1], 0, 0, 0);
+#pragma unroll
+                for (int qs = 0; qs < QPW; qs++) {
+                    // f16 pair of P, two values per conversion
+                    v8h ph, pl;
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        const v2f pv = {st[qs][t][8 * u + e], st[qs][t][8 * u + e + 1]};
+                        const v2h hh = __builtin_convertvector(pv, v2h);
+                        const v2h lo = __builtin_convertvector(pv - __builtin_convertvector(hh, v2f), v2h);
+                        ph[e] = hh[0];
+                        ph[e + 1] = hh[1];
+                        pl[e] = lo[0];
+                        pl[e + 1] = lo[1];
+                    }
+                    o[qs][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[0], ph, o[qs][0], 0, 0, 0);
+                    o[qs][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[1], ph, o[qs][1], 0, 0, 0);
+                    o[qs][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[0], ph, o[qs][0], 0, 0, 0);
+                    o[qs][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[1], ph, o[qs][1], 0, 0, 0);
+                    o[qs][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[0], pl, o[qs][0], 0, 0, 0);
+                    o[qs][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh[1], pl, o[qs][1], 0, 0, 0);
+                }
             }
     }
     FW_WAIT_VM(0); // dummy tiles landed before the block exits
-    if (myq >= T) return;
-    const float inv = 1.0f / l;
-    const size_t orow = ((size_t)b * T + myq) * d + (size_t)h * 64;
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int qs = 0; qs < QPW; qs++) {
+        const int myq = q0 + qs * 32 + (lane & 31);
+        if (myq >= T) continue;
+        const float inv = 1.0f / l[qs];
+        const size_t orow = ((size_t)b * T + myq) * d + (size_t)h * 64;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int dim = j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-            const float v = o[j][r] * inv;
-            if (out_mode == 0) of[orow + dim] = v;
-            else fw_split(v, oh[orow + dim], ol[orow + dim]);
-        }
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int dim = j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                const float v = o[qs][j][r] * inv;
+                if (out_mode == 0) of[orow + dim] = v;
+                else fw_split(v, oh[orow + dim], ol[orow + dim]);
+            }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -854,7 +898,8 @@ void fw_launch_fill_u16(hipStream_t st, uint16_t *p, size_t n, uint16_t v) {
 void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                          const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
                          int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol) {
-    dim3 grid((T + 32 * AT_QW - 1) / (32 * AT_QW), H, B);
-    hipLaunchKernelGGL((k_attention2<AT_QW, 3>), grid, dim3(64 * AT_QW), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d,
-                       out_mode, of, oh, ol);
+    constexpr int QB = 32 * AT_QPW * AT_QW; // queries per block
+    dim3 grid((T + QB - 1) / QB, H, B);
+    hipLaunchKernelGGL((k_attention2<AT_QW, AT_NSTAGE, AT_QPW>), grid, dim3(64 * AT_QW), 0, st, qh, ql, kh, kl, vth,
+                       vtl, T, Tp, H, d, out_mode, of, oh, ol);
 }
