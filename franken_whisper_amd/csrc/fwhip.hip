@@ -773,7 +773,14 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 return fw_fail(FWHIP_ERR_INVALID, "block GEMV: unsupported mlp width");
         } else {
             // (layer 0's attention LayerNorm ran with the embedding, into h)
-            if (fw_self_attn_f16q_ok(d, H) && fw_gemv16_ok(3 * d, d) && fw_gemv16_lpr(3 * d, d) == 16) {
+            // The projections fold into the attention kernels when the cohort's
+            // (head, stream) blocks fill one round of the CUs: with fewer streams
+            // a head's rows would be multiplied on that many CUs only (one
+            // stream: 332 against 316 us per step), with more the second round
+            // costs more than the two launches saved (16 streams: 611 against
+            // 606 us); 10 streams: 420 against 443 us.
+            const bool fold = S >= 4 && H * S <= c->n_cu;
+            if (fold && fw_self_attn_f16q_ok(d, H) && fw_gemv16_ok(3 * d, d) && fw_gemv16_lpr(3 * d, d) == 16) {
                 // the LayerNorm, q/k/v projection and attention in one kernel
                 if (li > 0)
                     fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, st->x, l.attn_ln_w, l.attn_ln_b, st->kv_k,
@@ -791,7 +798,7 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                                      scale);
             }
             fw_gemv16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
-            if (st->ck16p && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) && fw_gemv16_lpr(d, d) == 16) {
+            if (fold && st->ck16p && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) && fw_gemv16_lpr(d, d) == 16) {
                 // the cross LayerNorm and q projection run inside the cross-attention kernel
                 fw_launch_cross_attn_f16pq(s, l.cq16, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck16p,
                                            st->cvt16p, st->att, d, T, H, L, li, S, scale);

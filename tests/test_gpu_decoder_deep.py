@@ -1,7 +1,10 @@
 """GPU decoder parity at the large-v3-turbo decoder shape (4 layers, d 1280,
 20 heads, vocab 51866, n_text_ctx 448) deep into the KV cache, on both arms
-(the int8 default and the pure-f16 arm with the f16 tied logits head), with 1
-and 16 concurrent streams.
+(the int8 default and the pure-f16 arm with the f16 tied logits head), with 1,
+10 and 16 concurrent streams (the f16 arm folds the q/k/v and cross q
+projections into its attention kernels at 10 streams and not at 1 or 16, so the
+cohort-vs-alone comparison below also holds the folded kernels to the separate
+ones bit for bit).
 
 Each stream's cache is filled by prompt prefills through fwhip_decoder_step
 (tq > 1) and single steps are checked at cache depths 65, 129, 224 and 447, so
@@ -56,7 +59,7 @@ def _gpu_run(ctx, dec, enc, toks):
     return out
 
 
-@pytest.mark.parametrize("S", [1, 16])
+@pytest.mark.parametrize("S", [1, 10, 16])
 @pytest.mark.parametrize("arm", [abi.DEC_INT8, abi.DEC_F16], ids=["int8", "f16"])
 def test_turbo_deep_cache_bitexact(ctx, arm, S):
     m = model("large-v3-turbo", seed=2, encoder=False)
