@@ -21,7 +21,8 @@
 #include "fw_dec.h"
 #include "fw_kernels.h"
 
-#define WIN_THREADS 1024
+#define WIN_BT 256 // threads per block
+#define WIN_UPT 16 // lanes per thread: WIN_NB * WIN_BT * WIN_UPT covers the vocabulary
 #define WIN_TAU 1.0e-3f
 
 namespace {
@@ -39,16 +40,35 @@ __device__ __forceinline__ float wave_fsum(float v) {
     return v;
 }
 
+// The step's masks (decode.rs:702-867) as ranges: text [0, txt_hi),
+// timestamps [ts_lo, V), the monotone floor [beg, floor_hi), plus the control
+// and language tokens and, at the first step, blank and end-of-text.
+struct WinMask {
+    int txt_hi, ts_lo, floor_hi;
+    bool initial;
+};
+__device__ __forceinline__ bool win_masked(int j, const FwWinCfg &c, const WinMask &k) {
+    return j < k.txt_hi || j >= k.ts_lo || (j >= c.beg && j < k.floor_hi) ||
+           (k.initial && (j == c.eot || j == c.space)) || j == c.no_ts || j == c.sot || j == c.no_speech ||
+           j == c.solm || j == c.translate || j == c.transcribe || j == c.sot_prev || (j > c.sot && j <= c.sot + c.n_lang);
+}
+// the filtered, sanitized value of lane j (non-finite and masked lanes -> -inf)
+__device__ __forceinline__ float win_u(const float *lg, int j, const FwWinCfg &c, const WinMask &k) {
+    return win_masked(j, c, k) ? -INFINITY : win_san(lg[j]);
+}
+
 // the forcing rule for log-sum-exp `lse` (decode.rs:845-864): returns
-// ts_logprob - max_text_logprob (>0: force a timestamp); E holds the
-// timestamp terms, bc a broadcast slot
-__device__ float win_margin(const float *row, const FwWinCfg &c, float lse, float mtxt, float mts, float *E, float *bc) {
+// ts_logprob - max_text_logprob (>0: force a timestamp); the timestamp lanes
+// are formed again from the raw row; E holds the timestamp terms, bc a
+// broadcast slot
+__device__ float win_margin(const float *lg, const FwWinCfg &c, const WinMask &k, float lse, float mtxt, float mts,
+                            float *E, float *bc) {
     const int tid = threadIdx.x, nts = c.V - c.beg;
     const float lpmax = mts - lse;
-    for (int j = tid; j < nts + 4; j += WIN_THREADS) {
+    for (int j = tid; j < nts + 4; j += WIN_BT) {
         float e = 0.0f;
         if (j < nts) {
-            const float u = win_san(row[c.beg + j]);
+            const float u = win_u(lg, c.beg + j, c, k);
             if (u > -INFINITY) e = fw_expf((u - lse) - lpmax);
         }
         E[j] = e;
@@ -66,60 +86,89 @@ __device__ float win_margin(const float *row, const FwWinCfg &c, float lse, floa
     return ts_lp - max_text;
 }
 
+template <int NW>
+__device__ __forceinline__ float block_fmax(float v, float *sh) {
+    v = wave_fmax(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    float r = sh[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) r = fmaxf(r, sh[w]);
+    return r;
+}
+
 } // namespace
 
-__global__ void __launch_bounds__(WIN_THREADS) k_win_select(const float *__restrict__ logits, int ldl, FwWinCfg c,
-                                                            FwWinStream *ws, int32_t *hist, int hist_cap,
-                                                            float *rows, uint8_t *forced, float *scratch,
-                                                            int32_t *tok_out, int *posp, int *ndone) {
-    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// One step of the window loop.  Grid (WIN_NB, streams): block b of stream s
+// filters lanes [b * CH, (b + 1) * CH) of the row (masks, stored row, argmax
+// keys of all lanes and of the timestamp lanes, maxima, and with timestamps
+// the sum of expf(u - m_b) over its lanes against its own maximum m_b), writes
+// them to its slot of `part`, and counts itself in; the block that counts last
+// merges the slots in block order (log-sum-exp sum_b s_b expf(m_b - M) for the
+// decision), runs the forcing rule, the exact fallback and the loop state.
+// The counter is reset by that block, so every launch starts from zero.
+__global__ void __launch_bounds__(WIN_BT) k_win_select(const float *__restrict__ logits, int ldl, FwWinCfg c,
+                                                       FwWinStream *ws, int32_t *hist, int hist_cap, float *rows,
+                                                       uint8_t *forced, float *scratch, int32_t *tok_out, int *posp,
+                                                       int *ndone, FwWinPart *part, int *cnt) {
+    constexpr int NW = WIN_BT / 64;
+    const int b = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __shared__ __align__(16) float E[WIN_MAXTS + 8];
-    __shared__ unsigned long long kred[16][2];
-    __shared__ float fred[16][3];
+    __shared__ unsigned long long kred[NW][2];
+    __shared__ float fred[NW][4];
     __shared__ float bc[2];
-    if (s == 0 && tid == 0) *posp = *posp + 1; // the next forward's position
+    __shared__ int last;
+    if (s == 0 && b == 0 && tid == 0) *posp = *posp + 1; // the next forward's position
     const FwWinStream st = ws[s];
     if (st.done) {
-        if (tid == 0) tok_out[s] = c.eot; // a valid token for the forward nobody reads
+        if (b == 0 && tid == 0) tok_out[s] = c.eot; // a valid token for the forward nobody reads
         return;
     }
     const int i = st.n_dec;
     const int32_t *prev = hist + (size_t)s * hist_cap;
-    const bool initial = i == 0;
+    WinMask mk;
+    mk.initial = i == 0;
     const bool last_ts = i > 0 && prev[i - 1] >= c.beg;
     const bool penult_ts = i < 2 || prev[i - 2] >= c.beg;
-    // the range masks: [0, txt_hi), [ts_lo, V), [beg, floor_hi)
-    int txt_hi = 0, ts_lo = c.V;
-    if (!c.timestamps) ts_lo = c.beg;
-    if (c.timestamps && c.max_tokens > 0 && i >= c.max_tokens) txt_hi = c.eot;
+    mk.txt_hi = 0;
+    mk.ts_lo = c.V;
+    if (!c.timestamps) mk.ts_lo = c.beg;
+    if (c.timestamps && c.max_tokens > 0 && i >= c.max_tokens) mk.txt_hi = c.eot;
     if (last_ts) {
-        if (penult_ts) ts_lo = min(ts_lo, c.beg);
-        else txt_hi = max(txt_hi, c.eot);
+        if (penult_ts) mk.ts_lo = min(mk.ts_lo, c.beg);
+        else mk.txt_hi = max(mk.txt_hi, c.eot);
     }
-    if (initial && c.max_initial_tid >= 0) ts_lo = min(ts_lo, c.beg + c.max_initial_tid + 1);
-    const int floor_hi = st.has_ts ? min(c.beg + st.seek_delta_cs / 2, c.V) : c.beg;
+    if (mk.initial && c.max_initial_tid >= 0) mk.ts_lo = min(mk.ts_lo, c.beg + c.max_initial_tid + 1);
+    mk.floor_hi = st.has_ts ? min(c.beg + st.seek_delta_cs / 2, c.V) : c.beg;
 
     const float *lg = logits + (size_t)s * ldl;
     float *row = rows + ((size_t)s * c.n_max + i) * c.ldr;
+    const int CH = ((c.V + WIN_NB * WIN_BT - 1) / (WIN_NB * WIN_BT)) * WIN_BT; // lanes per block
+    const int j0 = b * CH, j1 = min(c.V, j0 + CH);
     unsigned long long ka = 0ull, kt = 0ull;
     float mall = -INFINITY, mtxt = -INFINITY, mts = -INFINITY;
-    for (int j = tid; j < c.V; j += WIN_THREADS) {
-        float v = lg[j];
-        const bool m = j < txt_hi || j >= ts_lo || (j >= c.beg && j < floor_hi) ||
-                       (initial && (j == c.eot || j == c.space)) || j == c.no_ts || j == c.sot ||
-                       j == c.no_speech || j == c.solm || j == c.translate || j == c.transcribe || j == c.sot_prev ||
-                       (j > c.sot && j <= c.sot + c.n_lang);
-        if (m) v = -INFINITY;
-        row[j] = v;
-        const unsigned long long k = am_key(v, j);
-        ka = k > ka ? k : ka;
-        const float u = win_san(v);
-        mall = fmaxf(mall, u);
-        if (j < c.beg) {
-            mtxt = fmaxf(mtxt, u);
-        } else {
-            kt = k > kt ? k : kt;
-            mts = fmaxf(mts, u);
+    float uv[WIN_UPT];
+#pragma unroll
+    for (int q = 0; q < WIN_UPT; q++) {
+        const int j = j0 + q * WIN_BT + tid;
+        uv[q] = -INFINITY;
+        if (j < j1) {
+            float v = lg[j];
+            if (win_masked(j, c, mk)) v = -INFINITY;
+            row[j] = v;
+            const unsigned long long k = am_key(v, j);
+            ka = k > ka ? k : ka;
+            const float u = win_san(v);
+            uv[q] = u;
+            mall = fmaxf(mall, u);
+            if (j < c.beg) {
+                mtxt = fmaxf(mtxt, u);
+            } else {
+                kt = k > kt ? k : kt;
+                mts = fmaxf(mts, u);
+            }
         }
     }
     ka = wave_max_u64(ka);
@@ -127,7 +176,6 @@ __global__ void __launch_bounds__(WIN_THREADS) k_win_select(const float *__restr
     mall = wave_fmax(mall);
     mtxt = wave_fmax(mtxt);
     mts = wave_fmax(mts);
-    __threadfence_block(); // the stored row is read back across threads below
     if (lane == 0) {
         kred[wave][0] = ka;
         kred[wave][1] = kt;
@@ -139,38 +187,75 @@ __global__ void __launch_bounds__(WIN_THREADS) k_win_select(const float *__restr
     ka = kt = 0ull;
     mall = mtxt = mts = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < WIN_THREADS / 64; w++) {
+    for (int w = 0; w < NW; w++) {
         ka = kred[w][0] > ka ? kred[w][0] : ka;
         kt = kred[w][1] > kt ? kred[w][1] : kt;
         mall = fmaxf(mall, fred[w][0]);
         mtxt = fmaxf(mtxt, fred[w][1]);
         mts = fmaxf(mts, fred[w][2]);
     }
+    // the block's exp sum against its own maximum (the decision's estimate)
+    float sb = 0.0f;
+    if (c.timestamps && mall > -INFINITY) {
+#pragma unroll
+        for (int q = 0; q < WIN_UPT; q++)
+            if (uv[q] > -INFINITY) sb += fw_expf(uv[q] - mall);
+        sb = wave_fsum(sb);
+        __syncthreads();
+        if (lane == 0) fred[wave][3] = sb;
+        __syncthreads();
+        sb = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) sb += fred[w][3];
+    }
+    if (tid == 0) {
+        FwWinPart o;
+        o.ka = ka;
+        o.kt = kt;
+        o.mall = mall;
+        o.mtxt = mtxt;
+        o.mts = mts;
+        o.sb = sb;
+        part[(size_t)s * WIN_NB + b] = o;
+        __threadfence(); // the slot is visible device-wide before the count
+        last = atomicAdd(cnt + s, 1) == WIN_NB - 1;
+    }
     __syncthreads();
+    if (!last) return;
+    __threadfence(); // every other block's slot is visible to this block
+    ka = kt = 0ull;
+    mall = mtxt = mts = -INFINITY;
+    float sa = 0.0f;
+    {
+        const volatile FwWinPart *pp = part + (size_t)s * WIN_NB;
+        float mb[WIN_NB], sbv[WIN_NB];
+#pragma unroll
+        for (int q = 0; q < WIN_NB; q++) {
+            const unsigned long long qa = pp[q].ka, qt = pp[q].kt;
+            ka = qa > ka ? qa : ka;
+            kt = qt > kt ? qt : kt;
+            mb[q] = pp[q].mall;
+            sbv[q] = pp[q].sb;
+            mall = fmaxf(mall, mb[q]);
+            mtxt = fmaxf(mtxt, pp[q].mtxt);
+            mts = fmaxf(mts, pp[q].mts);
+        }
+#pragma unroll
+        for (int q = 0; q < WIN_NB; q++)
+            if (mb[q] > -INFINITY) sa += sbv[q] * fw_expf(mb[q] - mall);
+    }
 
     // the forcing rule; with every timestamp lane masked it cannot fire
     // (ts_logprob stays -inf), so no-timestamps mode skips it
     bool force = false, used_exact = false;
     if (c.timestamps && mts > -INFINITY) {
-        float part = 0.0f;
-        for (int j = tid; j < c.V; j += WIN_THREADS) {
-            const float u = win_san(row[j]);
-            if (u > -INFINITY) part += fw_expf(u - mall);
-        }
-        part = wave_fsum(part);
-        if (lane == 0) fred[wave][0] = part;
-        __syncthreads();
-        float sa = 0.0f;
-#pragma unroll
-        for (int w = 0; w < WIN_THREADS / 64; w++) sa += fred[w][0];
-        __syncthreads();
-        float mg = win_margin(row, c, fw_logf(sa) + mall, mtxt, mts, E, bc);
+        float mg = win_margin(lg, c, mk, fw_logf(sa) + mall, mtxt, mts, E, bc);
         if (c.exact || fabsf(mg) <= WIN_TAU) {
             // the reference's own log-sum-exp: expf(l - max) over the finite
             // lanes summed sequentially in index order (masked lanes add +0)
             float *sc = scratch + (size_t)s * c.ldr;
-            for (int j = tid; j < c.V; j += WIN_THREADS) {
-                const float u = win_san(row[j]);
+            for (int j = tid; j < c.V; j += WIN_BT) {
+                const float u = win_u(lg, j, c, mk);
                 sc[j] = u > -INFINITY ? fw_expf(u - mall) : 0.0f;
             }
             __threadfence_block();
@@ -179,27 +264,28 @@ __global__ void __launch_bounds__(WIN_THREADS) k_win_select(const float *__restr
                 float sum = 0.0f;
                 int j = 0;
                 for (; j + 8 <= c.V; j += 8) {
-                    const float4 a = *(const float4 *)(sc + j), b = *(const float4 *)(sc + j + 4);
+                    const float4 a = *(const float4 *)(sc + j), e = *(const float4 *)(sc + j + 4);
                     sum = sum + a.x;
                     sum = sum + a.y;
                     sum = sum + a.z;
                     sum = sum + a.w;
-                    sum = sum + b.x;
-                    sum = sum + b.y;
-                    sum = sum + b.z;
-                    sum = sum + b.w;
+                    sum = sum + e.x;
+                    sum = sum + e.y;
+                    sum = sum + e.z;
+                    sum = sum + e.w;
                 }
                 for (; j < c.V; j++) sum = sum + sc[j];
                 bc[1] = fw_logf(sum) + mall;
             }
             __syncthreads();
-            mg = win_margin(row, c, bc[1], mtxt, mts, E, bc);
+            mg = win_margin(lg, c, mk, bc[1], mtxt, mts, E, bc);
             used_exact = true;
         }
         force = mg > 0.0f;
     }
 
     if (tid == 0) {
+        cnt[s] = 0; // every block of this stream has counted: ready for the next launch
         const unsigned long long k = force ? kt : ka;
         const int tok = k ? (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull)) : 0;
         hist[(size_t)s * hist_cap + i] = tok;
@@ -302,11 +388,13 @@ __global__ void __launch_bounds__(256) k_win_plogs(const float *__restrict__ row
     }
 }
 
+bool fw_win_select_ok(int V) { return V > 0 && V <= WIN_NB * WIN_BT * WIN_UPT; }
+
 void fw_launch_win_select(hipStream_t st, const float *logits, int ldl, const FwWinCfg &c, FwWinStream *ws,
                           int32_t *hist, int hist_cap, float *rows, uint8_t *forced, float *scratch, int32_t *tok,
-                          int *posp, int *ndone, int ns) {
-    hipLaunchKernelGGL(k_win_select, dim3(ns), dim3(WIN_THREADS), 0, st, logits, ldl, c, ws, hist, hist_cap, rows,
-                       forced, scratch, tok, posp, ndone);
+                          int *posp, int *ndone, FwWinPart *part, int *cnt, int ns) {
+    hipLaunchKernelGGL(k_win_select, dim3(WIN_NB, ns), dim3(WIN_BT), 0, st, logits, ldl, c, ws, hist, hist_cap, rows,
+                       forced, scratch, tok, posp, ndone, part, cnt);
 }
 
 void fw_launch_win_plogs(hipStream_t st, const float *rows, const float *nsrow, const FwWinCfg &c,

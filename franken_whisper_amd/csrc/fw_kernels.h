@@ -80,9 +80,18 @@ struct FwWinStream {
     int seek_cs, seek_end_cs, has_prior;                               // set by the host
     int n_dec, has_ts, seek_delta_cs, result_len, done, n_exact;       // loop state
 };
+// one stream's row is filtered by WIN_NB blocks, each leaving its partial
+// results in a slot; the last block to count (cnt[s], zero between launches)
+// merges them
+#define WIN_NB 16
+struct FwWinPart {
+    unsigned long long ka, kt;  // argmax keys: every lane, the timestamp lanes
+    float mall, mtxt, mts, sb;  // maxima (all, text, timestamp lanes); sum of expf(u - mall) over the block's lanes
+};
+bool fw_win_select_ok(int V);
 void fw_launch_win_select(hipStream_t st, const float *logits, int ldl, const FwWinCfg &c, FwWinStream *ws,
                           int32_t *hist, int hist_cap, float *rows, uint8_t *forced, float *scratch, int32_t *tok,
-                          int *posp, int *ndone, int ns);
+                          int *posp, int *ndone, FwWinPart *part, int *cnt, int ns);
 void fw_launch_win_plogs(hipStream_t st, const float *rows, const float *nsrow, const FwWinCfg &c,
                          const FwWinStream *ws, const int32_t *hist, int hist_cap, const uint8_t *forced,
                          float *plogs, float *nslp, int ns);

@@ -275,6 +275,8 @@ struct fwhip_dstate {
     FwWinStream *w_ws = nullptr;
     uint8_t *w_forced = nullptr;
     int *w_ndone = nullptr;
+    FwWinPart *w_part = nullptr; // [S][WIN_NB] partial results of the select blocks
+    int *w_cnt = nullptr;        // [S] select blocks counted in (zero between launches)
     int w_nmax = 0, w_ldr = 0;
     std::vector<void *> w_owned;
     hipGraphExec_t wgraph = nullptr;
@@ -1092,12 +1094,15 @@ static fwhip_status win_buffers(fwhip_dstate *st, int n_max) {
     st->w_ws = (FwWinStream *)fw_dalloc(st->w_owned, sizeof(FwWinStream) * S);
     st->w_forced = (uint8_t *)fw_dalloc(st->w_owned, S * n_max);
     st->w_ndone = (int *)fw_dalloc(st->w_owned, sizeof(int));
+    st->w_part = (FwWinPart *)fw_dalloc(st->w_owned, sizeof(FwWinPart) * S * WIN_NB);
+    st->w_cnt = (int *)fw_dalloc(st->w_owned, sizeof(int) * S);
     if (!st->w_rows || !st->w_nsrow || !st->w_scratch || !st->w_plogs || !st->w_nslp || !st->w_ws || !st->w_forced ||
-        !st->w_ndone) {
+        !st->w_ndone || !st->w_part || !st->w_cnt) {
         fw_free_all(st->w_owned);
         st->w_nmax = 0;
         return fw_fail(FWHIP_ERR_GENERIC, "fwhip_decode_window: device allocation failed");
     }
+    HIP_TRY(hipMemsetAsync(st->w_cnt, 0, sizeof(int) * S, dd->ctx->stream)); // (outside any capture)
     st->w_nmax = n_max;
     st->w_ldr = ldr;
     if (st->wgraph) {
@@ -1111,7 +1116,8 @@ static fwhip_status win_step(fwhip_dstate *st, const FwWinCfg &cfg) {
     fwhip_status r = dec_forward_row(st, st->tok, false, true, nullptr, false);
     if (r != FWHIP_OK) return r;
     fw_launch_win_select(st->dec->ctx->stream, st->logits, st->dec->V, cfg, st->w_ws, st->hist, st->hist_cap,
-                         st->w_rows, st->w_forced, st->w_scratch, st->tok, st->pos, st->w_ndone, st->S);
+                         st->w_rows, st->w_forced, st->w_scratch, st->tok, st->pos, st->w_ndone, st->w_part, st->w_cnt,
+                         st->S);
     return FWHIP_OK;
 }
 
@@ -1161,6 +1167,8 @@ extern "C" fwhip_status fwhip_decode_window(fwhip_dstate *st, const int32_t *pro
     if (filter->timestamp_begin <= 0 || filter->timestamp_begin > dd->V || dd->V - filter->timestamp_begin > WIN_MAXTS ||
         filter->eot <= 0 || filter->eot > filter->timestamp_begin)
         return fw_fail(FWHIP_ERR_UNSUPPORTED, "fwhip_decode_window: the vocabulary's timestamp range is not supported");
+    if (!fw_win_select_ok(dd->V))
+        return fw_fail(FWHIP_ERR_UNSUPPORTED, "fwhip_decode_window: vocabulary larger than the select kernel covers");
     fwhip_status r = win_buffers(st, n_max);
     if (r != FWHIP_OK) return r;
     FwWinCfg cfg;
@@ -1202,7 +1210,7 @@ extern "C" fwhip_status fwhip_decode_window(fwhip_dstate *st, const int32_t *pro
     HIP_TRY(hipMemcpy2DAsync(st->w_nsrow, sizeof(float) * cfg.ldr, st->logits, sizeof(float) * dd->V,
                              sizeof(float) * dd->V, S, hipMemcpyDeviceToDevice, c->stream));
     fw_launch_win_select(c->stream, st->logits, dd->V, cfg, st->w_ws, st->hist, st->hist_cap, st->w_rows,
-                         st->w_forced, st->w_scratch, st->tok, st->pos, st->w_ndone, S);
+                         st->w_forced, st->w_scratch, st->tok, st->pos, st->w_ndone, st->w_part, st->w_cnt, S);
     int steps = 1, ndone = 0;
     const int poll = 8;
     bool use_graph = n_max > 1 && win_capture(st, cfg);
