@@ -51,14 +51,16 @@ __global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, cons
 // per block (one wave), followed, when w is given, by the first layer's
 // attention LayerNorm of the row (into ln_y and/or the int8 activation rows,
 // as k_ln_quant).
+// Row s sits at position *posp + s / rps (rps: rows per position, the streams
+// of a prefill chunk whose rows are [position][stream]).
 template <int NV>
 __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *posp, const uint16_t *emb,
                                                  const float *pemb, float *x, int d, const float *w, const float *b,
-                                                 float *ln_y, int8_t *xq, float *xs) {
+                                                 float *ln_y, int8_t *xq, float *xs, int rps) {
     const int s = blockIdx.x, lane = threadIdx.x;
     const int n4 = d >> 2;
     const uint2 *er = (const uint2 *)(emb + (size_t)tok[s] * d);
-    const float4 *pr = (const float4 *)(pemb + (size_t)(*posp) * d);
+    const float4 *pr = (const float4 *)(pemb + (size_t)(*posp + s / rps) * d);
     float4 xv[NV];
     bool ok[NV];
 #pragma unroll
@@ -905,13 +907,16 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
                                                          float *att, int d, int T, int Tv, int H, int L, int layer,
                                                          float scale, const uint16_t *__restrict__ wq,
                                                          const float *__restrict__ bq, const float *__restrict__ x,
-                                                         const float *__restrict__ lnw, const float *__restrict__ lnb) {
+                                                         const float *__restrict__ lnw, const float *__restrict__ lnb,
+                                                         int ns) {
     extern __shared__ __align__(16) float scf[]; // [Tv]: scores, then p in the value pass order
     __shared__ float red[8];
     __shared__ float inv_s;
+    // row s = blockIdx.y attends with the cross K/V of stream s % ns (a prefill
+    // chunk's rows are [position][stream])
     const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6, l = lane & 7, rg = lane >> 3;
-    const size_t lh = ((size_t)s * L + layer) * H + h;
+    const size_t lh = ((size_t)(s % ns) * L + layer) * H + h;
     const uint16_t *K = ckp + lh * (size_t)T * 64;
     const uint16_t *V = cvtp + lh * (size_t)Tv * 64;
     const int nc = T >> 5, ng = nc >> 1, ntail = T - nc * 32;
@@ -1179,10 +1184,11 @@ void fw_launch_pack_cross_f16(hipStream_t st, const uint16_t *ck, const uint16_t
 }
 
 void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp, float *att,
-                               int d, int T, int H, int L, int layer, int ns, float scale) {
+                               int d, int T, int H, int L, int layer, int ns, float scale, int rows) {
     const int Tv = fw_cross_f16p_tv(T);
-    hipLaunchKernelGGL(k_cross_attn_f16p<false>, dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st, qc, ckp,
-                       cvtp, att, d, T, Tv, H, L, layer, scale, nullptr, nullptr, nullptr, nullptr, nullptr);
+    hipLaunchKernelGGL(k_cross_attn_f16p<false>, dim3(H, rows > 0 ? rows : ns), dim3(512), sizeof(float) * (size_t)Tv,
+                       st, qc, ckp, cvtp, att, d, T, Tv, H, L, layer, scale, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, ns);
 }
 
 bool fw_cross_f16pq_ok(int d, int T, int H) { return d == XQ_D && H * 64 == d && fw_cross_f16p_ok(T); }
@@ -1194,7 +1200,7 @@ void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float 
                                 int H, int L, int layer, int ns, float scale) {
     const int Tv = fw_cross_f16p_tv(T);
     hipLaunchKernelGGL(k_cross_attn_f16p<true>, dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st, nullptr, ckp,
-                       cvtp, att, d, T, Tv, H, L, layer, scale, wq, bq, x, lnw, lnb);
+                       cvtp, att, d, T, Tv, H, L, layer, scale, wq, bq, x, lnw, lnb, ns);
 }
 
 // ---------------------------------------------------------------------------
@@ -1302,29 +1308,49 @@ __device__ __forceinline__ void sa_attend(const float *qh, const uint16_t *kc, c
     }
 }
 
+// Row r = blockIdx.y is stream r % ns at position *posp + r / ns (a prefill
+// chunk's rows are [position][stream]; a step has one row per stream).  With
+// `append` the row's own k/v go into the cache first; a prefill chunk appends
+// every row beforehand (k_kv_append16), so a row sees the earlier rows of its
+// chunk.
 __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *kc, uint16_t *vc, float *att,
                                                     const int *posp, int d, int nctx, int L, int layer,
-                                                    float scale, float *pmax) {
+                                                    float scale, float *pmax, int ns, int append) {
     extern __shared__ __align__(16) unsigned char sm2[];
     float *sc = (float *)sm2;                               // [nctx]
     uint16_t *vs = (uint16_t *)(sm2 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
     __shared__ float qh[64];
     __shared__ float red[4];
     __shared__ float inv_s;
-    const int pos = *posp;
-    const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const int h = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
+    const int s = r % ns, pos = *posp + r / ns;
     const int base = h * 64;
-    const float *q = qkv + (size_t)s * 3 * d;
+    const float *q = qkv + (size_t)r * 3 * d;
     const size_t cbase = ((size_t)s * L + layer) * nctx * d;
     if (t < 64) {
-        uint16_t kh = fw_f2h(q[d + base + t]), vh = fw_f2h(q[2 * d + base + t]);
-        kc[cbase + (size_t)pos * d + base + t] = kh;
-        vc[cbase + (size_t)pos * d + base + t] = vh;
+        if (append) {
+            uint16_t kh = fw_f2h(q[d + base + t]), vh = fw_f2h(q[2 * d + base + t]);
+            kc[cbase + (size_t)pos * d + base + t] = kh;
+            vc[cbase + (size_t)pos * d + base + t] = vh;
+        }
         qh[t] = q[base + t] * scale;
     }
     __syncthreads(); // this block's own cache row is visible to its threads
-    sa_attend<256>(qh, kc, vc, cbase, base, d, pos + 1, scale, sc, vs, red, &inv_s, att + (size_t)s * d + base,
-                   pmax ? pmax + (size_t)s * gridDim.x + h : nullptr);
+    sa_attend<256>(qh, kc, vc, cbase, base, d, pos + 1, scale, sc, vs, red, &inv_s, att + (size_t)r * d + base,
+                   pmax ? pmax + (size_t)r * gridDim.x + h : nullptr);
+}
+
+// The k/v of every row of a prefill chunk into the f16 cache (KvCache::append,
+// nn.rs:5352-5416: RNE to f16), row r = stream r % ns at position *posp + r / ns.
+__global__ void __launch_bounds__(256) k_kv_append16(const float *qkv, uint16_t *kc, uint16_t *vc, const int *posp,
+                                                     int d, int nctx, int L, int layer, int ns) {
+    const int r = blockIdx.x, s = r % ns, pos = *posp + r / ns;
+    const float *q = qkv + (size_t)r * 3 * d;
+    const size_t o = ((size_t)s * L + layer) * nctx * d + (size_t)pos * d;
+    for (int c = threadIdx.x; c < d; c += 256) {
+        kc[o + c] = fw_f2h(q[d + c]);
+        vc[o + c] = fw_f2h(q[2 * d + c]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1930,8 +1956,10 @@ void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w
 }
 
 void fw_launch_embed_ln(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,
-                        float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs) {
-    FW_ROWS_DISPATCH(k_embed_ln, d, dim3(ns), dim3(64), 0, st, tok, posp, emb, pemb, x, d, w, b, ln_y, xq, xs);
+                        float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs,
+                        int rps) {
+    FW_ROWS_DISPATCH(k_embed_ln, d, dim3(ns), dim3(64), 0, st, tok, posp, emb, pemb, x, d, w, b, ln_y, xq, xs,
+                     rps > 0 ? rps : ns);
 }
 
 int fw_gemv_i8m_blocks(int N) { return N >= 16384 ? (N + 63) / 64 : (N + 15) / 16; }
@@ -2002,10 +2030,16 @@ int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const 
 }
 
 void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
-                          int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax) {
+                          int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax, int rows,
+                          int append) {
     size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
-    hipLaunchKernelGGL(k_self_attn2, dim3(H, ns), dim3(256), shm, st, qkv, kc, vc, att, posp, d, nctx, L, layer,
-                       scale, pmax);
+    hipLaunchKernelGGL(k_self_attn2, dim3(H, rows > 0 ? rows : ns), dim3(256), shm, st, qkv, kc, vc, att, posp, d,
+                       nctx, L, layer, scale, pmax, ns, append);
+}
+
+void fw_launch_kv_append16(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, const int *posp, int d,
+                           int nctx, int L, int layer, int ns, int rows) {
+    hipLaunchKernelGGL(k_kv_append16, dim3(rows), dim3(256), 0, st, qkv, kc, vc, posp, d, nctx, L, layer, ns);
 }
 
 bool fw_self_attn_f16q_ok(int d, int H) { return d == XQ_D && H * 64 == d; }

@@ -41,8 +41,10 @@ bool fw_cross_f16p_ok(int T);
 int fw_cross_f16p_tv(int T);
 void fw_launch_pack_cross_f16(hipStream_t st, const uint16_t *ck, const uint16_t *cvt, uint16_t *ckp, uint16_t *cvtp,
                               size_t rows_k, size_t rows_v, int T);
+// rows > 0: a prefill chunk of `rows` rows ([position][stream], the q rows and
+// outputs indexed by row, the cross K/V by row % ns); else one row per stream
 void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp, float *att,
-                               int d, int T, int H, int L, int layer, int ns, float scale);
+                               int d, int T, int H, int L, int layer, int ns, float scale, int rows = 0);
 // fw_launch_cross_attn_f16p with the cross LayerNorm of x [ns, d] and the q
 // projection inside (wq in fw_launch_pack_gemv16's slot order at 16 lanes per
 // row, bq the bias); needs fw_cross_f16pq_ok(d, T, H)
@@ -99,8 +101,11 @@ void fw_launch_win_plogs(hipStream_t st, const float *rows, const float *nsrow, 
 // int8 decoder arm (dec_fast.hip)
 void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d, int rows,
                         int8_t *xq, float *xs);
+// rps > 0: row s sits at position *posp + s / rps (a prefill chunk of rps
+// streams); else every row at *posp
 void fw_launch_embed_ln(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,
-                        float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs);
+                        float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs,
+                        int rps = 0);
 int fw_gemv_i8m_blocks(int N);
 // W of fw_launch_gemv_i8m is stored as MFMA operand fragments: bytes needed
 // for an [N, K] matrix (K % 64 == 0), and the repacking of a row-major one
@@ -116,8 +121,14 @@ int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const 
                         int N, int K, int ns, int ldy, int mode, int n_cu);
 // pmax (nullable): [ns, H] max |output| of each head block, for a consumer
 // that quantizes the rows itself (fw_launch_gemv_i8m with xf)
+// rows > 0: a prefill chunk of `rows` rows, row r = stream r % ns at position
+// *posp + r / ns, its k/v already appended (append = 0, fw_launch_kv_append16)
 void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
-                          int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax = nullptr);
+                          int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax = nullptr,
+                          int rows = 0, int append = 1);
+// the k/v of every row of a prefill chunk into the f16 caches
+void fw_launch_kv_append16(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, const int *posp, int d,
+                           int nctx, int L, int layer, int ns, int rows);
 // The int8 arm's self-attention sublayer: attention LayerNorm of the residual
 // rows x, the fused q/k/v projection (int8 rows wqkv [3d, d], row scales sqkv,
 // bias bqkv), cache append and attention; per-head output maxima into pmax.

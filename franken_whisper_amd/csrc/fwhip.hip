@@ -275,6 +275,10 @@ struct fwhip_dstate {
     FwWinStream *w_ws = nullptr;
     uint8_t *w_forced = nullptr;
     int *w_ndone = nullptr;
+    // batched prompt prefill (f16 arm): activation rows of a chunk of
+    // PF_CHUNK positions x S streams, allocated on first use
+    std::vector<void *> pf_owned;
+    float *pf_x = nullptr, *pf_h = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_y = nullptr, *pf_ff = nullptr;
     FwWinPart *w_part = nullptr; // [S][WIN_NB] partial results of the select blocks
     int *w_cnt = nullptr;        // [S] select blocks counted in (zero between launches)
     int w_nmax = 0, w_ldr = 0;
@@ -603,6 +607,7 @@ extern "C" void fwhip_dstate_free(fwhip_dstate *st) {
     if (st->graph) hipGraphExecDestroy(st->graph);
     if (st->wgraph) hipGraphExecDestroy(st->wgraph);
     fw_free_all(st->w_owned);
+    fw_free_all(st->pf_owned);
     fw_free_all(st->owned);
     delete st;
 }
@@ -734,6 +739,7 @@ static bool gemv_blk_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const
 // want_logits the final LayerNorm, the logits and the per-block argmax keys
 // over the filtered logits (filt may be NULL: raw argmax) are produced too.
 // `timed` brackets the logits GEMV with events (never inside a graph capture).
+static void dec_logits_f16(fwhip_dstate *st, const float *x, float *h, const fwhip_filter *filt, bool timed);
 static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool prefill, bool want_logits,
                                     const fwhip_filter *filt, bool timed) {
     fwhip_decoder *dd = st->dec;
@@ -824,20 +830,93 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             gemv_i8_all(st, s, dd->emb8, dd->emb8s, nullptr, st->logits, dd->V, d, dd->V, 3, filt);
             if (timed) fw_timed_end(c, &ev);
         } else {
-            if (timed) fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d * 2.0, &ev);
-            if (f16_fused_keys(dd)) {
-                // final LayerNorm, tied f16 logits head and per-tile argmax keys in one kernel
-                fw_launch_gemv16(s, dd->emb16f, nullptr, st->x, st->logits, dd->V, d, S, dd->V, 0, gt, dd->ln_w,
-                                 dd->ln_b, filt, st->initial, st->keys);
-                if (timed) fw_timed_end(c, &ev);
-            } else {
-                fw_gemv16_ln(s, dd->emb16f, nullptr, st->x, st->h, dd->ln_w, dd->ln_b, st->logits, dd->V, d, S, dd->V,
-                             0, gt);
-                if (timed) fw_timed_end(c, &ev);
-                fw_launch_logits_keys(s, st->logits, dd->V, S, filt, st->initial, st->keys);
-            }
+            dec_logits_f16(st, st->x, st->h, filt, timed);
         }
     }
+    return FWHIP_OK;
+}
+
+// The f16 arm's final LayerNorm and tied logits head of the S rows x (h:
+// LayerNorm scratch), with the per-tile argmax keys of the filtered rows.
+static void dec_logits_f16(fwhip_dstate *st, const float *x, float *h, const fwhip_filter *filt, bool timed) {
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    hipStream_t s = c->stream;
+    const int d = dd->d, S = st->S;
+    const float *gt = c->gelu_tab;
+    fw_event_pair ev;
+    ev.active = false;
+    if (timed) fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d * 2.0, &ev);
+    if (f16_fused_keys(dd)) {
+        // final LayerNorm, tied f16 logits head and per-tile argmax keys in one kernel
+        fw_launch_gemv16(s, dd->emb16f, nullptr, x, st->logits, dd->V, d, S, dd->V, 0, gt, dd->ln_w, dd->ln_b, filt,
+                         st->initial, st->keys);
+        if (timed) fw_timed_end(c, &ev);
+    } else {
+        fw_gemv16_ln(s, dd->emb16f, nullptr, x, h, dd->ln_w, dd->ln_b, st->logits, dd->V, d, S, dd->V, 0, gt);
+        if (timed) fw_timed_end(c, &ev);
+        fw_launch_logits_keys(s, st->logits, dd->V, S, filt, st->initial, st->keys);
+    }
+}
+
+// Batched prompt prefill (f16 arm): the rows of PF_CHUNK positions of every
+// stream go through each layer together, [position][stream] order, row r at
+// stream r % S and position *pos + r / S.  Every projection is row-local
+// (gemv_f16 per row), so a batch gives each row the bits of its own forward;
+// the self attention appends every row's k/v first and then lets row r see
+// positions [0, *pos + r / S] of its stream, exactly the keys the row-by-row
+// forward gives it (decoder.rs:1754-1906).
+#define PF_CHUNK 32
+static bool prefill_batch_ok(const fwhip_dstate *st) {
+    const fwhip_decoder *dd = st->dec;
+    return dd->arm == FWHIP_DEC_F16 && st->ck16p && fw_cross_f16p_ok(st->T) && dd->d == dd->H * 64 &&
+           fw_gemv16_ok(3 * dd->d, dd->d) && fw_gemv16_ok(dd->d, dd->d) && fw_gemv16_ok(dd->dff, dd->d) &&
+           fw_gemv16_ok(dd->d, dd->dff);
+}
+static fwhip_status prefill_buffers(fwhip_dstate *st) {
+    if (st->pf_x) return FWHIP_OK;
+    const fwhip_decoder *dd = st->dec;
+    const size_t R = (size_t)st->S * PF_CHUNK, d = dd->d;
+    st->pf_x = (float *)fw_dalloc(st->pf_owned, sizeof(float) * R * d);
+    st->pf_h = (float *)fw_dalloc(st->pf_owned, sizeof(float) * R * dd->dff);
+    st->pf_qkv = (float *)fw_dalloc(st->pf_owned, sizeof(float) * R * 3 * d);
+    st->pf_att = (float *)fw_dalloc(st->pf_owned, sizeof(float) * R * d);
+    st->pf_y = (float *)fw_dalloc(st->pf_owned, sizeof(float) * R * d);
+    st->pf_ff = (float *)fw_dalloc(st->pf_owned, sizeof(float) * R * dd->dff);
+    if (!st->pf_x || !st->pf_h || !st->pf_qkv || !st->pf_att || !st->pf_y || !st->pf_ff) {
+        fw_free_all(st->pf_owned);
+        st->pf_x = nullptr;
+        return fw_fail(FWHIP_ERR_GENERIC, "prefill: device allocation failed");
+    }
+    return FWHIP_OK;
+}
+static fwhip_status dec_forward_chunk(fwhip_dstate *st, const int32_t *tok, int n_pos, bool want_logits,
+                                      const fwhip_filter *filt, bool timed) {
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    hipStream_t s = c->stream;
+    const int d = dd->d, H = dd->H, L = dd->L, T = st->T, S = st->S, dff = dd->dff, R = S * n_pos;
+    const float scale = powf(64.0f, -0.25f);
+    const float *gt = c->gelu_tab;
+    float *x = st->pf_x, *h = st->pf_h, *qkv = st->pf_qkv, *att = st->pf_att, *y = st->pf_y, *ff = st->pf_ff;
+    fw_launch_embed_ln(s, tok, st->pos, dd->emb16, dd->pos_emb, x, d, R, dd->layers[0].attn_ln_w,
+                       dd->layers[0].attn_ln_b, h, nullptr, nullptr, S);
+    for (int li = 0; li < L; li++) {
+        const DecLayerDev &l = dd->layers[li];
+        if (li > 0) fw_gemv16_ln(s, l.qkv16, l.qkv_b, x, h, l.attn_ln_w, l.attn_ln_b, qkv, 3 * d, d, R, 3 * d, 0, gt);
+        else fw_gemv16(s, l.qkv16, l.qkv_b, h, qkv, 3 * d, d, R, 3 * d, 0, gt);
+        fw_launch_kv_append16(s, qkv, st->kv_k, st->kv_v, st->pos, d, dd->nctx, L, li, S, R);
+        fw_launch_self_attn2(s, qkv, st->kv_k, st->kv_v, att, st->pos, d, H, dd->nctx, L, li, S, scale, nullptr, R,
+                             0);
+        fw_gemv16(s, l.o16, l.o_b, att, x, d, d, R, d, 1, gt);
+        fw_gemv16_ln(s, l.cq16, l.cq_b, x, h, l.cross_ln_w, l.cross_ln_b, y, d, d, R, d, 0, gt);
+        fw_launch_cross_attn_f16p(s, y, st->ck16p, st->cvt16p, att, d, T, H, L, li, S, scale, R);
+        fw_gemv16(s, l.co16, l.co_b, att, x, d, d, R, d, 1, gt);
+        fw_gemv16_ln(s, l.fc1_16, l.fc1_b, x, h, l.mlp_ln_w, l.mlp_ln_b, ff, dff, d, R, dff, 2, gt);
+        fw_gemv16(s, l.fc2_16, l.fc2_b, ff, x, d, dff, R, d, 1, gt);
+    }
+    // the last position's rows of every stream
+    if (want_logits) dec_logits_f16(st, x + (size_t)(n_pos - 1) * S * d, h, filt, timed);
     return FWHIP_OK;
 }
 
@@ -865,6 +944,29 @@ static fwhip_status stage_rows(fwhip_dstate *st, const int32_t *tokens, int tq, 
     int p0 = st->len;
     fwhip_status r = set_dev_ints(c, st->pos, &p0, 1);
     if (r != FWHIP_OK) return r;
+    if (tq > 1 && prefill_batch_ok(st)) {
+        r = prefill_buffers(st);
+        if (r != FWHIP_OK) return r;
+        for (int c0 = 0; c0 < tq; c0 += PF_CHUNK) {
+            const int n = tq - c0 < PF_CHUNK ? tq - c0 : PF_CHUNK, p = p0 + c0;
+            r = set_dev_ints(c, st->pos, &p, 1);
+            if (r != FWHIP_OK) return r;
+            r = dec_forward_chunk(st, st->rows + (size_t)c0 * S, n, c0 + n == tq, filt, true);
+            if (r != FWHIP_OK) return r;
+            r = check_cancel(c);
+            if (r != FWHIP_OK) {
+                hipStreamSynchronize(c->stream);
+                return r;
+            }
+        }
+        // the position of the last row, where the row-by-row forward leaves it
+        const int pl = p0 + tq - 1;
+        r = set_dev_ints(c, st->pos, &pl, 1);
+        if (r != FWHIP_OK) return r;
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("launch failed: ") + hipGetErrorString(e));
+        return FWHIP_OK;
+    }
     for (int t = 0; t < tq; t++) {
         r = dec_forward_row(st, st->rows + (size_t)t * S, tq > 1, t == tq - 1, filt, true);
         if (r != FWHIP_OK) return r;
