@@ -898,8 +898,22 @@ void fw_launch_fill_u16(hipStream_t st, uint16_t *p, size_t n, uint16_t v) {
 void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                          const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
                          int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol) {
-    constexpr int QB = 32 * AT_QPW * AT_QW; // queries per block
-    dim3 grid((T + QB - 1) / QB, H, B);
-    hipLaunchKernelGGL((k_attention2<AT_QW, AT_NSTAGE, AT_QPW>), grid, dim3(64 * AT_QW), 0, st, qh, ql, kh, kl, vth,
-                       vtl, T, Tp, H, d, out_mode, of, oh, ol);
+    // the largest query tile whose launch still covers every CU (one window:
+    // 20 heads x 12 blocks of 128 queries; ten: 20 x 10 x 3 of 512); every
+    // tile gives the same bits
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    auto nblk = [&](int qb) { return (long long)B * H * ((T + qb - 1) / qb); };
+#define AT_GO(QW_, QPW_)                                                                                           \
+    hipLaunchKernelGGL((k_attention2<QW_, AT_NSTAGE, QPW_>), dim3((T + 32 * QW_ * QPW_ - 1) / (32 * QW_ * QPW_), H, B), \
+                       dim3(64 * QW_), 0, st, qh, ql, kh, kl, vth, vtl, T, Tp, H, d, out_mode, of, oh, ol)
+    if (nblk(32 * AT_QPW * AT_QW) >= n_cu) AT_GO(AT_QW, AT_QPW);
+    else if (nblk(256) >= n_cu) AT_GO(8, 1);
+    else AT_GO(4, 1);
+#undef AT_GO
 }
