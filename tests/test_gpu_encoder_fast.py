@@ -20,6 +20,9 @@ mode) and of the configs' own workloads.
   checked by teacher forcing in the decoder's fast-mode tests.)
 - Config 0: tiny.en (4 + 4 layers) f32 encoder within max-abs 1e-3 relative,
   and 64 greedy tokens identical on both decoder arms.
+- The attention's query tile follows the launch size (128, 256 or 512 queries
+  per block); a window's encoder states are bit-identical whichever tile its
+  batch gets.
 """
 import numpy as np
 import pytest
@@ -213,3 +216,23 @@ def test_encoder_cancel_then_resume(ctx):
     enc.forward_time_major(x, 1, nf, out)
     assert_bitexact(out.download(), ref, "forward after a cancelled one")
     enc.close()
+
+
+@pytest.mark.parametrize("precision", [abi.ENC_INT8, abi.ENC_F32], ids=["int8", "f32"])
+def test_attention_tiles_bit_identical_across_batch_sizes(ctx, precision):
+    """large-v3-turbo: one window (128-query tiles), four (256) and six (512)
+    give window 0 the same encoder states bit for bit, in both plans."""
+    cfg = synth.TURBO
+    m = synth.Model(cfg, seed=11, decoder=False)
+    nf = 2 * cfg.n_audio_ctx
+    x = synth.mel_input(12, 6, nf, cfg.n_mels) * 0.5
+    enc = native.Encoder(ctx, m, precision)
+    outs = {}
+    for B in (1, 4, 6):
+        print(f"attention tiles: batch {B}", flush=True)
+        out = ctx.empty((B, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+        enc.forward_time_major(ctx.array(np.ascontiguousarray(x[:B])), B, nf, out)
+        outs[B] = out.download()
+    enc.close()
+    for B in (1, 4):
+        assert_bitexact(outs[B][0], outs[6][0], f"window 0 at batch {B} vs 6")
