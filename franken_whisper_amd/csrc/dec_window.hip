@@ -65,13 +65,26 @@ __device__ float win_margin(const float *lg, const FwWinCfg &c, const WinMask &k
                             float *E, float *bc) {
     const int tid = threadIdx.x, nts = c.V - c.beg;
     const float lpmax = mts - lse;
-    for (int j = tid; j < nts + 4; j += WIN_BT) {
-        float e = 0.0f;
-        if (j < nts) {
-            const float u = win_u(lg, c.beg + j, c, k);
-            if (u > -INFINITY) e = fw_expf((u - lse) - lpmax);
+    // the lanes' raw values requested together (clamped indices, no load
+    // behind a branch), then filtered
+    constexpr int PT = (WIN_MAXTS + 4 + WIN_BT - 1) / WIN_BT;
+    float raw[PT];
+#pragma unroll
+    for (int q = 0; q < PT; q++) {
+        const int j = tid + q * WIN_BT;
+        raw[q] = lg[c.beg + (j < nts ? j : nts - 1)];
+    }
+#pragma unroll
+    for (int q = 0; q < PT; q++) {
+        const int j = tid + q * WIN_BT;
+        if (j < nts + 4) {
+            float e = 0.0f;
+            if (j < nts) {
+                const float u = win_masked(c.beg + j, c, k) ? -INFINITY : win_san(raw[q]);
+                if (u > -INFINITY) e = fw_expf((u - lse) - lpmax);
+            }
+            E[j] = e;
         }
-        E[j] = e;
     }
     __syncthreads();
     if (tid < 64) {
@@ -150,12 +163,19 @@ __global__ void __launch_bounds__(WIN_BT) k_win_select(const float *__restrict__
     unsigned long long ka = 0ull, kt = 0ull;
     float mall = -INFINITY, mtxt = -INFINITY, mts = -INFINITY;
     float uv[WIN_UPT];
+    // every lane's value requested at once (clamped indices: no load behind a
+    // branch, so no load waits for the one before it)
 #pragma unroll
     for (int q = 0; q < WIN_UPT; q++) {
         const int j = j0 + q * WIN_BT + tid;
-        uv[q] = -INFINITY;
+        uv[q] = lg[j < j1 ? j : j1 - 1];
+    }
+#pragma unroll
+    for (int q = 0; q < WIN_UPT; q++) {
+        const int j = j0 + q * WIN_BT + tid;
         if (j < j1) {
-            float v = lg[j];
+            float v = uv[q];
+            uv[q] = -INFINITY;
             if (win_masked(j, c, mk)) v = -INFINITY;
             row[j] = v;
             const unsigned long long k = am_key(v, j);
@@ -169,6 +189,8 @@ __global__ void __launch_bounds__(WIN_BT) k_win_select(const float *__restrict__
                 kt = k > kt ? k : kt;
                 mts = fmaxf(mts, u);
             }
+        } else {
+            uv[q] = -INFINITY;
         }
     }
     ka = wave_max_u64(ka);
@@ -223,26 +245,24 @@ __global__ void __launch_bounds__(WIN_BT) k_win_select(const float *__restrict__
     __syncthreads();
     if (!last) return;
     __threadfence(); // every other block's slot is visible to this block
-    ka = kt = 0ull;
-    mall = mtxt = mts = -INFINITY;
+    // lane q of every wave holds slot q; the maxima by lane exchanges, the
+    // sum in slot order
+    FwWinPart pq = part[(size_t)s * WIN_NB + (lane < WIN_NB ? lane : 0)];
+    if (lane >= WIN_NB) {
+        pq.ka = pq.kt = 0ull;
+        pq.mall = pq.mtxt = pq.mts = -INFINITY;
+        pq.sb = 0.0f;
+    }
+    ka = wave_max_u64(pq.ka);
+    kt = wave_max_u64(pq.kt);
+    mall = wave_fmax(pq.mall);
+    mtxt = wave_fmax(pq.mtxt);
+    mts = wave_fmax(pq.mts);
     float sa = 0.0f;
     {
-        const volatile FwWinPart *pp = part + (size_t)s * WIN_NB;
-        float mb[WIN_NB], sbv[WIN_NB];
+        const float t = pq.mall > -INFINITY ? pq.sb * fw_expf(pq.mall - mall) : 0.0f;
 #pragma unroll
-        for (int q = 0; q < WIN_NB; q++) {
-            const unsigned long long qa = pp[q].ka, qt = pp[q].kt;
-            ka = qa > ka ? qa : ka;
-            kt = qt > kt ? qt : kt;
-            mb[q] = pp[q].mall;
-            sbv[q] = pp[q].sb;
-            mall = fmaxf(mall, mb[q]);
-            mtxt = fmaxf(mtxt, pp[q].mtxt);
-            mts = fmaxf(mts, pp[q].mts);
-        }
-#pragma unroll
-        for (int q = 0; q < WIN_NB; q++)
-            if (mb[q] > -INFINITY) sa += sbv[q] * fw_expf(mb[q] - mall);
+        for (int q = 0; q < WIN_NB; q++) sa += __shfl(t, q, 64);
     }
 
     // the forcing rule; with every timestamp lane masked it cannot fire
