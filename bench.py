@@ -382,7 +382,7 @@ def transcribe_workload(a):
 def main():
     a = _args()
     if a.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs shard windows/streams "
+        print(json.dumps({"error": "bench.py measures one GPU; multi-GPU runs shard windows/streams "
                                    "(data parallel, no exchange) and are not part of this benchmark",
                           "n_gpus": a.gpus}))
         sys.exit(2)
