@@ -1148,6 +1148,203 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
     }
 }
 
+// The same cross attention in two launches for cohorts too small to fill the
+// CUs with one block per (head, stream): k_cross_scores_f16p spreads a head's
+// keys over XS_KC blocks (the per-key dot_f16c of k_cross_attn_f16p, and each
+// block's maximum), k_cross_pv_f16p gives each of XS_DC blocks 64 / XS_DC of
+// the head's output dims, every one forming the same softmax (the maximum of
+// the chunk maxima, expf, the sequential sum by one wave, p in the value pass
+// order) before its value pass.  Every value has the one-launch kernel's bits.
+#define XS_KC 8
+#define XS_DC 4
+__global__ void __launch_bounds__(256) k_cross_scores_f16p(const float *qc, const uint16_t *ckp, float *sbuf,
+                                                           float *mbuf, int d, int T, int Tv, int H, int L, int layer,
+                                                           int ns, float scale) {
+    __shared__ float red[4];
+    const int h = blockIdx.x, kc = blockIdx.y, r = blockIdx.z, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6, l = lane & 7, rg = lane >> 3;
+    const size_t lh = ((size_t)(r % ns) * L + layer) * H + h;
+    const uint16_t *K = ckp + lh * (size_t)T * 64;
+    const int CH = ((T + XS_KC * 64 - 1) / (XS_KC * 64)) * 64, j0 = kc * CH, j1 = min(T, j0 + CH);
+    const float *qs = qc + (size_t)r * d + h * 64;
+    float q0[4], q1[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        q0[k] = qs[8 * k + l] * scale;
+        q1[k] = qs[32 + 8 * k + l] * scale;
+    }
+    constexpr int NR = 1536 / XS_KC / 32; // 32-key rounds a block holds at most (T <= 1536)
+    uint4 kv[NR];
+#pragma unroll
+    for (int q = 0; q < NR; q++) {
+        const int j = j0 + q * 32 + wave * 8 + rg;
+        kv[q] = *(const uint4 *)(K + (size_t)(j < j1 ? j : (j1 > j0 ? j1 - 1 : 0)) * 64 + l * 8);
+    }
+    float mx = -INFINITY;
+    float *sc = sbuf + ((size_t)r * H + h) * Tv;
+#pragma unroll
+    for (int q = 0; q < NR; q++) {
+        const int j = j0 + q * 32 + wave * 8 + rg;
+        const uint32_t u[4] = {kv[q].x, kv[q].y, kv[q].z, kv[q].w};
+        float a[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float w0 = fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16)));
+            const float w1 = fw_h2f((uint16_t)(u[2 + (k >> 1)] >> ((k & 1) * 16)));
+            a[k] = __builtin_fmaf(w1, q1[k], __builtin_fmaf(w0, q0[k], 0.0f));
+        }
+        float v = (a[0] + a[1]) + (a[2] + a[3]);
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        if (j < j1) {
+            if (l == 0) sc[j] = v;
+            mx = fmaxf(mx, v);
+        }
+    }
+    mx = fw_block_max(mx, red);
+    if (t == 0) mbuf[((size_t)r * H + h) * XS_KC + kc] = mx;
+}
+
+__global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const float *mbuf, const uint16_t *cvtp,
+                                                       float *att, int d, int T, int Tv, int H, int L, int layer,
+                                                       int ns) {
+    extern __shared__ __align__(16) float scf[]; // [Tv]
+    __shared__ float inv_s;
+    const int h = blockIdx.x, dc = blockIdx.y, r = blockIdx.z, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6, l = lane & 7, rg = lane >> 3;
+    const size_t lh = ((size_t)(r % ns) * L + layer) * H + h;
+    const uint16_t *V = cvtp + lh * (size_t)Tv * 64;
+    const int nc = T >> 5, ng = nc >> 1, ntail = T - nc * 32;
+    constexpr int DPB = 64 / XS_DC; // dims of this block: threads [0, 8 * DPB) hold one each
+    const bool pvt = t < 8 * DPB;
+    const int dd = dc * DPB + (pvt ? t >> 3 : 0);
+    // the value rows first: they stream in while the softmax is formed
+    const uint16_t *vr = V + (size_t)dd * Tv;
+    uint4 vreg[XP_MAXG];
+#pragma unroll
+    for (int g = 0; g < XP_MAXG; g++) vreg[g] = *(const uint4 *)(vr + (g < ng ? g : 0) * 64 + l * 8);
+    const uint2 vodd = *(const uint2 *)(vr + ((nc & 1) ? ng * 64 : 0) + l * 4);
+    uint4 vtail[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) vtail[i] = *(const uint4 *)(vr + (ntail > 0 ? nc * 32 : 0) + i * 8);
+    const float *sc = sbuf + ((size_t)r * H + h) * Tv;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < XS_KC; k++) mx = fmaxf(mx, mbuf[((size_t)r * H + h) * XS_KC + k]);
+    const bool fin = isfinite(mx);
+    for (int j = t; j < T; j += 256) {
+        const float v = sc[j];
+        if (fin) {
+            const float e = fw_expf(v - mx);
+            scf[j] = isfinite(e) ? e : 0.0f;
+        } else {
+            scf[j] = v;
+        }
+    }
+    __syncthreads();
+    if (t < 64) {
+        float sum = 0.0f;
+        if (fin) {
+            if (T <= 64 * SW_MAXC) {
+                sum = fw_seq_sum_wave(scf, T);
+            } else if (t == 0) {
+                for (int j = 0; j < T; j++) sum += scf[j];
+            }
+        }
+        if (t == 0) inv_s = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    // p (normalized when the sum is positive; a non-finite max leaves the raw
+    // scores), moved to the value pass order as in k_cross_attn_f16p
+    const float inv = inv_s;
+    constexpr int PU = 1536 / 256;
+    float pv[PU];
+#pragma unroll
+    for (int u = 0; u < PU; u++) {
+        const int j = t + u * 256;
+        pv[u] = j < T ? (inv > 0.0f ? scf[j] * inv : scf[j]) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < PU; u++) {
+        const int j = t + u * 256;
+        if (j < T) {
+            const int e = j & 31;
+            scf[j < nc * 32 ? (j & ~31) + (e & 7) * 4 + (e >> 3) : j] = pv[u];
+        }
+    }
+    __syncthreads();
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < XP_MAXG; g++) {
+        if (g < ng) {
+            const float4 p0 = *(const float4 *)(scf + g * 64 + l * 4);
+            const float4 p1 = *(const float4 *)(scf + g * 64 + 32 + l * 4);
+            const uint32_t u[4] = {vreg[g].x, vreg[g].y, vreg[g].z, vreg[g].w};
+            const float pa[4] = {p0.x, p0.y, p0.z, p0.w}, pb[4] = {p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16))), pa[k], a[k]);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[2 + (k >> 1)] >> ((k & 1) * 16))), pb[k], a[k]);
+        }
+    }
+    if (nc & 1) {
+        const float4 p0 = *(const float4 *)(scf + (nc - 1) * 32 + l * 4);
+        const float pa[4] = {p0.x, p0.y, p0.z, p0.w};
+        const uint32_t u[2] = {vodd.x, vodd.y};
+#pragma unroll
+        for (int k = 0; k < 4; k++) a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16))), pa[k], a[k]);
+    }
+    float acc = (a[0] + a[1]) + (a[2] + a[3]);
+    acc = acc + __shfl_xor(acc, 1, 64);
+    acc = acc + __shfl_xor(acc, 2, 64);
+    acc = acc + __shfl_xor(acc, 4, 64);
+    if (pvt && l == 0) {
+        // dot_f16c's tails: whole 8-wide chunks (products, then their tree), then scalars
+        const uint32_t tw[16] = {vtail[0].x, vtail[0].y, vtail[0].z, vtail[0].w, vtail[1].x, vtail[1].y,
+                                 vtail[1].z, vtail[1].w, vtail[2].x, vtail[2].y, vtail[2].z, vtail[2].w,
+                                 vtail[3].x, vtail[3].y, vtail[3].z, vtail[3].w};
+        const float *pt = scf + nc * 32;
+        int i = 0;
+#pragma unroll
+        for (int c8 = 0; c8 < 4; c8++) {
+            if (i + 8 <= ntail) {
+                float pp[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int ii = c8 * 8 + e;
+                    pp[e] = fw_h2f((uint16_t)(tw[ii >> 1] >> ((ii & 1) * 16))) * pt[ii];
+                }
+                acc += ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
+                i += 8;
+            }
+        }
+#pragma unroll
+        for (int ii = 0; ii < 32; ii++)
+            if (ii >= i && ii < ntail) acc += fw_h2f((uint16_t)(tw[ii >> 1] >> ((ii & 1) * 16))) * pt[ii];
+        att[(size_t)r * d + h * 64 + dd] = acc;
+    }
+}
+
+size_t fw_cross_split_floats(int T, int H, int ns) {
+    return (size_t)ns * H * (fw_cross_f16p_tv(T) + XS_KC);
+}
+
+// scratch: fw_cross_split_floats(T, H, ns) floats
+void fw_launch_cross_attn_f16p_split(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp,
+                                     float *att, int d, int T, int H, int L, int layer, int ns, float scale,
+                                     float *scratch) {
+    const int Tv = fw_cross_f16p_tv(T);
+    float *sbuf = scratch, *mbuf = scratch + (size_t)ns * H * Tv;
+    hipLaunchKernelGGL(k_cross_scores_f16p, dim3(H, XS_KC, ns), dim3(256), 0, st, qc, ckp, sbuf, mbuf, d, T, Tv, H,
+                       L, layer, ns, scale);
+    hipLaunchKernelGGL(k_cross_pv_f16p, dim3(H, XS_DC, ns), dim3(256), sizeof(float) * (size_t)Tv, st, sbuf, mbuf,
+                       cvtp, att, d, T, Tv, H, L, layer, ns);
+}
+
 // K [rows_k, 64] and V^T [rows_v, T] (natural order) to the slot order of
 // k_cross_attn_f16p; V^T rows take stride Tv (pad left as it is).
 __global__ void __launch_bounds__(256) k_pack_cross_f16(const uint16_t *ck, const uint16_t *cvt, uint16_t *ckp,

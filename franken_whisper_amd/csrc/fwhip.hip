@@ -252,6 +252,7 @@ struct fwhip_dstate {
     int S, T, Tq, Sp, len;
     uint16_t *kv_k, *kv_v, *ck16, *cvt16;
     uint16_t *ck16p = nullptr, *cvt16p = nullptr; // f16 arm: slot-order copies for the cross attention
+    float *xsplit = nullptr; // f16 arm: scores and block maxima of the two-launch cross attention
     int8_t *ck8 = nullptr, *cvt8 = nullptr; // cvt8 rows have stride Tq (T rounded up to 16)
     float *ck8s = nullptr, *cvt8s = nullptr;
     float *x, *h, *qkv, *att, *y, *ff, *logits;
@@ -554,7 +555,8 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
         st->ck16p = (uint16_t *)fw_dalloc(own, crn * 2);
         const size_t vpn = (size_t)S * L * dd->H * 64 * fw_cross_f16p_tv(T);
         st->cvt16p = (uint16_t *)fw_dalloc(own, vpn * 2);
-        ok = ok && st->ck16p && st->cvt16p;
+        st->xsplit = (float *)fw_dalloc(own, sizeof(float) * fw_cross_split_floats(T, dd->H, S));
+        ok = ok && st->ck16p && st->cvt16p && st->xsplit;
         if (ok) ok = hipMemset(st->cvt16p, 0, vpn * 2) == hipSuccess;
     }
     if (dd->arm == FWHIP_DEC_INT8) {
@@ -812,7 +814,13 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                                            st->cvt16p, st->att, d, T, H, L, li, S, scale);
             } else {
                 fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0, gt);
-                if (st->ck16p)
+                // a cohort whose (head, stream) blocks fill under half the CUs
+                // spreads each head over more blocks in two launches (one
+                // stream: 20 blocks for 1,500 keys)
+                if (st->ck16p && S * H * 2 <= c->n_cu)
+                    fw_launch_cross_attn_f16p_split(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S,
+                                                    scale, st->xsplit);
+                else if (st->ck16p)
                     fw_launch_cross_attn_f16p(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S, scale);
                 else fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
             }
