@@ -912,6 +912,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
     extern __shared__ __align__(16) float scf[]; // [Tv]: scores, then p in the value pass order
     __shared__ float red[8];
     __shared__ float inv_s;
+    __shared__ uint64_t etab[32]; // fw_expf's table, in LDS: its lookups then wait on no global load
     // row s = blockIdx.y attends with the cross K/V of stream s % ns (a prefill
     // chunk's rows are [position][stream])
     const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
@@ -920,6 +921,10 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
     const uint16_t *K = ckp + lh * (size_t)T * 64;
     const uint16_t *V = cvtp + lh * (size_t)Tv * 64;
     const int nc = T >> 5, ng = nc >> 1, ntail = T - nc * 32;
+    if (t < 32) {
+        const uint64_t tb[32] = FW_EXP2F_TAB;
+        etab[t] = tb[t];
+    }
     float q0[4], q1[4];
     // (no load sits behind a branch: addresses past the end are clamped to
     // the last row and the values unused, so the waits count loads exactly)
@@ -1056,11 +1061,18 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
     for (int i = 0; i < 4; i++) vtail[i] = *(const uint4 *)(vr + (ntail > 0 ? nc * 32 : 0) + i * 8);
     mx = fw_block_max(mx, red);
     const bool fin = isfinite(mx);
-    if (fin)
-        for (int j = t; j < T; j += 512) {
-            const float e = fw_expf(scf[j] - mx);
-            scf[j] = isfinite(e) ? e : 0.0f;
+    // (the value rows are in flight: reads clamped to the scores, the table
+    // in LDS, so the exps wait on no global load)
+    if (fin) {
+        float sv[3];
+#pragma unroll
+        for (int u = 0; u < 3; u++) sv[u] = scf[min(t + u * 512, T - 1)];
+#pragma unroll
+        for (int u = 0; u < 3; u++) {
+            const float e = fw_expf_tab(sv[u] - mx, etab);
+            if (t + u * 512 < T) scf[t + u * 512] = isfinite(e) ? e : 0.0f;
         }
+    }
     __syncthreads();
     if (t < 64) {
         float sum = 0.0f;
@@ -1209,17 +1221,35 @@ __global__ void __launch_bounds__(256) k_cross_scores_f16p(const float *qc, cons
 __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const float *mbuf, const uint16_t *cvtp,
                                                        float *att, int d, int T, int Tv, int H, int L, int layer,
                                                        int ns) {
-    extern __shared__ __align__(16) float scf[]; // [Tv]
+    // [Tv] the exponentials in key order (the sum's input), then [Tv] the
+    // same in the value pass order: within chunk c element 8k + l sits at
+    // 4l + k, the n % 32 tail in place
+    extern __shared__ __align__(16) float scf[];
+    float *sp = scf + Tv;
     __shared__ float inv_s;
+    __shared__ uint64_t etab[32]; // fw_expf's table, in LDS: its lookups then wait on no global load
     const int h = blockIdx.x, dc = blockIdx.y, r = blockIdx.z, t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6, l = lane & 7, rg = lane >> 3;
+    if (t < 32) {
+        const uint64_t tb[32] = FW_EXP2F_TAB;
+        etab[t] = tb[t];
+    }
+    const int lane = t & 63, l = lane & 7;
     const size_t lh = ((size_t)(r % ns) * L + layer) * H + h;
     const uint16_t *V = cvtp + lh * (size_t)Tv * 64;
     const int nc = T >> 5, ng = nc >> 1, ntail = T - nc * 32;
     constexpr int DPB = 64 / XS_DC; // dims of this block: threads [0, 8 * DPB) hold one each
     const bool pvt = t < 8 * DPB;
     const int dd = dc * DPB + (pvt ? t >> 3 : 0);
-    // the value rows first: they stream in while the softmax is formed
+    // this thread's scores and the block maxima first (loads retire in order),
+    // then the value rows, which stream in while the softmax is formed; no
+    // load sits behind a branch (addresses clamped)
+    constexpr int PU = 1536 / 256;
+    const float *sc = sbuf + ((size_t)r * H + h) * Tv;
+    float sv[PU], mk[XS_KC];
+#pragma unroll
+    for (int u = 0; u < PU; u++) sv[u] = sc[min(t + u * 256, T - 1)];
+#pragma unroll
+    for (int k = 0; k < XS_KC; k++) mk[k] = mbuf[((size_t)r * H + h) * XS_KC + k];
     const uint16_t *vr = V + (size_t)dd * Tv;
     uint4 vreg[XP_MAXG];
 #pragma unroll
@@ -1228,18 +1258,21 @@ __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const 
     uint4 vtail[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) vtail[i] = *(const uint4 *)(vr + (ntail > 0 ? nc * 32 : 0) + i * 8);
-    const float *sc = sbuf + ((size_t)r * H + h) * Tv;
     float mx = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < XS_KC; k++) mx = fmaxf(mx, mbuf[((size_t)r * H + h) * XS_KC + k]);
+    for (int k = 0; k < XS_KC; k++) mx = fmaxf(mx, mk[k]);
     const bool fin = isfinite(mx);
-    for (int j = t; j < T; j += 256) {
-        const float v = sc[j];
-        if (fin) {
-            const float e = fw_expf(v - mx);
-            scf[j] = isfinite(e) ? e : 0.0f;
-        } else {
+    __syncthreads();
+    // expf of every held score (any input keeps fw_expf's table index in
+    // range); a non-finite max keeps the raw scores
+#pragma unroll
+    for (int u = 0; u < PU; u++) {
+        const float e = fw_expf_tab(sv[u] - mx, etab);
+        const float v = fin ? (isfinite(e) ? e : 0.0f) : sv[u];
+        const int j = t + u * 256, ee = j & 31;
+        if (j < T) {
             scf[j] = v;
+            sp[j < nc * 32 ? (j & ~31) + (ee & 7) * 4 + (ee >> 3) : j] = v;
         }
     }
     __syncthreads();
@@ -1255,34 +1288,18 @@ __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const 
         if (t == 0) inv_s = (fin && sum > 0.0f) ? 1.0f / sum : 0.0f;
     }
     __syncthreads();
-    // p (normalized when the sum is positive; a non-finite max leaves the raw
-    // scores), moved to the value pass order as in k_cross_attn_f16p
-    const float inv = inv_s;
-    constexpr int PU = 1536 / 256;
-    float pv[PU];
-#pragma unroll
-    for (int u = 0; u < PU; u++) {
-        const int j = t + u * 256;
-        pv[u] = j < T ? (inv > 0.0f ? scf[j] * inv : scf[j]) : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < PU; u++) {
-        const int j = t + u * 256;
-        if (j < T) {
-            const int e = j & 31;
-            scf[j < nc * 32 ? (j & ~31) + (e & 7) * 4 + (e >> 3) : j] = pv[u];
-        }
-    }
-    __syncthreads();
+    // p = e * inv when the sum is positive, else e (x * 1 is x): the bits of
+    // the one-launch kernel's p
+    const float pm = inv_s > 0.0f ? inv_s : 1.0f;
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int g = 0; g < XP_MAXG; g++) {
         if (g < ng) {
-            const float4 p0 = *(const float4 *)(scf + g * 64 + l * 4);
-            const float4 p1 = *(const float4 *)(scf + g * 64 + 32 + l * 4);
+            const float4 p0 = *(const float4 *)(sp + g * 64 + l * 4);
+            const float4 p1 = *(const float4 *)(sp + g * 64 + 32 + l * 4);
             const uint32_t u[4] = {vreg[g].x, vreg[g].y, vreg[g].z, vreg[g].w};
-            const float pa[4] = {p0.x, p0.y, p0.z, p0.w}, pb[4] = {p1.x, p1.y, p1.z, p1.w};
+            const float pa[4] = {p0.x * pm, p0.y * pm, p0.z * pm, p0.w * pm};
+            const float pb[4] = {p1.x * pm, p1.y * pm, p1.z * pm, p1.w * pm};
 #pragma unroll
             for (int k = 0; k < 4; k++)
                 a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16))), pa[k], a[k]);
@@ -1291,9 +1308,20 @@ __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const 
                 a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[2 + (k >> 1)] >> ((k & 1) * 16))), pb[k], a[k]);
         }
     }
+    // the odd last chunk and the tail's p (rows of sp are Tv >= nc * 32 + 32
+    // long: read whole, used where in range)
+    const float4 po = *(const float4 *)(sp + (nc & 1 ? (nc - 1) * 32 : 0) + l * 4);
+    float pt[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 q = *(const float4 *)(sp + nc * 32 + i * 4);
+        pt[4 * i] = q.x * pm;
+        pt[4 * i + 1] = q.y * pm;
+        pt[4 * i + 2] = q.z * pm;
+        pt[4 * i + 3] = q.w * pm;
+    }
     if (nc & 1) {
-        const float4 p0 = *(const float4 *)(scf + (nc - 1) * 32 + l * 4);
-        const float pa[4] = {p0.x, p0.y, p0.z, p0.w};
+        const float pa[4] = {po.x * pm, po.y * pm, po.z * pm, po.w * pm};
         const uint32_t u[2] = {vodd.x, vodd.y};
 #pragma unroll
         for (int k = 0; k < 4; k++) a[k] = __builtin_fmaf(fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16))), pa[k], a[k]);
@@ -1307,11 +1335,10 @@ __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const 
         const uint32_t tw[16] = {vtail[0].x, vtail[0].y, vtail[0].z, vtail[0].w, vtail[1].x, vtail[1].y,
                                  vtail[1].z, vtail[1].w, vtail[2].x, vtail[2].y, vtail[2].z, vtail[2].w,
                                  vtail[3].x, vtail[3].y, vtail[3].z, vtail[3].w};
-        const float *pt = scf + nc * 32;
-        int i = 0;
+        const int n8 = ntail >> 3;
 #pragma unroll
         for (int c8 = 0; c8 < 4; c8++) {
-            if (i + 8 <= ntail) {
+            if (c8 < n8) {
                 float pp[8];
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
@@ -1319,12 +1346,11 @@ __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const 
                     pp[e] = fw_h2f((uint16_t)(tw[ii >> 1] >> ((ii & 1) * 16))) * pt[ii];
                 }
                 acc += ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
-                i += 8;
             }
         }
 #pragma unroll
         for (int ii = 0; ii < 32; ii++)
-            if (ii >= i && ii < ntail) acc += fw_h2f((uint16_t)(tw[ii >> 1] >> ((ii & 1) * 16))) * pt[ii];
+            if (ii >= n8 * 8 && ii < ntail) acc += fw_h2f((uint16_t)(tw[ii >> 1] >> ((ii & 1) * 16))) * pt[ii];
         att[(size_t)r * d + h * 64 + dd] = acc;
     }
 }
@@ -1341,7 +1367,7 @@ void fw_launch_cross_attn_f16p_split(hipStream_t st, const float *qc, const uint
     float *sbuf = scratch, *mbuf = scratch + (size_t)ns * H * Tv;
     hipLaunchKernelGGL(k_cross_scores_f16p, dim3(H, XS_KC, ns), dim3(256), 0, st, qc, ckp, sbuf, mbuf, d, T, Tv, H,
                        L, layer, ns, scale);
-    hipLaunchKernelGGL(k_cross_pv_f16p, dim3(H, XS_DC, ns), dim3(256), sizeof(float) * (size_t)Tv, st, sbuf, mbuf,
+    hipLaunchKernelGGL(k_cross_pv_f16p, dim3(H, XS_DC, ns), dim3(256), sizeof(float) * 2 * (size_t)Tv, st, sbuf, mbuf,
                        cvtp, att, d, T, Tv, H, L, layer, ns);
 }
 
