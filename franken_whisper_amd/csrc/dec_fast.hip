@@ -1589,12 +1589,19 @@ __global__ void __launch_bounds__(256) k_kv_append16(const float *qkv, uint16_t 
 // x 4 row groups) is 10 weight loads and 80 FMAs per lane; the six batches
 // (q, k, v halves) are double-buffered.  The slot tree and the bias are the
 // GEMV's, so q/k/v hold its bits.
-template <bool LN>
+//
+// EMB (layer 0): the row is first formed as the token embedding
+// f16(emb[tok]) + pemb[pos] (embed_tokens, decoder.rs:1323-1385, k_embed_ln's
+// arithmetic) and the head-0 block stores it to xo, the residual.
+template <bool LN, bool EMB>
 __global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restrict__ wqkv,
                                                         const float *__restrict__ bqkv, const float *__restrict__ x,
                                                         const float *__restrict__ lnw, const float *__restrict__ lnb,
                                                         uint16_t *kc, uint16_t *vc, float *att, const int *posp,
-                                                        int nctx, int L, int layer, float scale) {
+                                                        int nctx, int L, int layer, float scale,
+                                                        const int32_t *__restrict__ tok,
+                                                        const uint16_t *__restrict__ emb,
+                                                        const float *__restrict__ pemb, float *xo) {
     constexpr int D = XQ_D, NV = D / 256, G = D / 128, NC = D / 32;
     extern __shared__ __align__(16) unsigned char sm4[];
     float *sc = (float *)sm4;                                              // [nctx]
@@ -1611,10 +1618,24 @@ __global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restri
     float4 lv[NV], lw[NV], lb[NV];
     bool lok[NV];
     if (wave == 0) {
+        if constexpr (EMB) {
+            const uint2 *er = (const uint2 *)(emb + (size_t)tok[s] * D);
+            const float4 *pr = (const float4 *)(pemb + (size_t)*posp * D);
 #pragma unroll
-        for (int k = 0; k < NV; k++) {
-            lok[k] = true;
-            lv[k] = ((const float4 *)(x + (size_t)s * D))[lane + k * 64];
+            for (int k = 0; k < NV; k++) {
+                lok[k] = true;
+                const uint2 e = er[lane + k * 64];
+                const float4 pp = pr[lane + k * 64];
+                lv[k] = make_float4(fw_h2f(e.x & 0xffff) + pp.x, fw_h2f(e.x >> 16) + pp.y,
+                                    fw_h2f(e.y & 0xffff) + pp.z, fw_h2f(e.y >> 16) + pp.w);
+                if (h == 0) ((float4 *)(xo + (size_t)s * D))[lane + k * 64] = lv[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                lok[k] = true;
+                lv[k] = ((const float4 *)(x + (size_t)s * D))[lane + k * 64];
+            }
         }
         if constexpr (LN) fw_ln_load_wb<NV>(lok, lnw, lnb, lw, lb, lane);
     }
@@ -2272,14 +2293,18 @@ bool fw_self_attn_f16q_ok(int d, int H) { return d == XQ_D && H * 64 == d; }
 // normalized row) and the self-attention of k_self_attn2, one launch
 void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
                               const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
-                              const int *posp, int H, int nctx, int L, int layer, int ns, float scale) {
+                              const int *posp, int H, int nctx, int L, int layer, int ns, float scale,
+                              const int32_t *tok, const uint16_t *emb, const float *pemb, float *xo) {
     size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
-    if (lnw)
-        hipLaunchKernelGGL(k_self_attn_f16q<true>, dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb, kc, vc,
-                           att, posp, nctx, L, layer, scale);
+    if (tok)
+        hipLaunchKernelGGL((k_self_attn_f16q<true, true>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb,
+                           kc, vc, att, posp, nctx, L, layer, scale, tok, emb, pemb, xo);
+    else if (lnw)
+        hipLaunchKernelGGL((k_self_attn_f16q<true, false>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb,
+                           kc, vc, att, posp, nctx, L, layer, scale, nullptr, nullptr, nullptr, nullptr);
     else
-        hipLaunchKernelGGL(k_self_attn_f16q<false>, dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb, kc, vc,
-                           att, posp, nctx, L, layer, scale);
+        hipLaunchKernelGGL((k_self_attn_f16q<false, false>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw,
+                           lnb, kc, vc, att, posp, nctx, L, layer, scale, nullptr, nullptr, nullptr, nullptr);
 }
 
 template <int NV>

@@ -57,11 +57,15 @@ void fw_launch_cross_attn_f16p_split(hipStream_t st, const float *qc, const uint
 // row, bq the bias); needs fw_cross_f16pq_ok(d, T, H)
 // the f16 arm's attention LayerNorm (lnw null: x already normalized), q/k/v
 // projection (wqkv in fw_launch_pack_gemv16's slot order at 16 lanes per row)
-// and self-attention in one launch; needs fw_self_attn_f16q_ok(d, H)
+// and self-attention in one launch; needs fw_self_attn_f16q_ok(d, H).  With
+// tok (layer 0, lnw given) the rows are the token embeddings f16(emb[tok]) +
+// pemb[*posp], stored to xo (x unused).
 bool fw_self_attn_f16q_ok(int d, int H);
 void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
                               const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
-                              const int *posp, int H, int nctx, int L, int layer, int ns, float scale);
+                              const int *posp, int H, int nctx, int L, int layer, int ns, float scale,
+                              const int32_t *tok = nullptr, const uint16_t *emb = nullptr,
+                              const float *pemb = nullptr, float *xo = nullptr);
 bool fw_cross_f16pq_ok(int d, int T, int H);
 void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float *bq, const float *x, const float *lnw,
                                 const float *lnb, const uint16_t *ckp, const uint16_t *cvtp, float *att, int d, int T,

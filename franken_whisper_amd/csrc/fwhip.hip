@@ -751,9 +751,17 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
     bool i8 = dd->arm == FWHIP_DEC_INT8;
     float scale = powf(64.0f, -0.25f);
     const float *gt = c->gelu_tab;
-    // embedding + layer 0's attention LayerNorm (the int8 arm forms both inside
-    // layer 0's self-attention kernel)
-    if (!i8)
+    // The f16 arm's projections fold into the attention kernels when the
+    // cohort's (head, stream) blocks fill one round of the CUs: with fewer
+    // streams a head's rows would be multiplied on that many CUs only (one
+    // stream: 332 against 316 us per step), with more the second round costs
+    // more than the two launches saved (16 streams: 611 against 606 us); 10
+    // streams: 420 against 443 us.
+    const bool fold = !i8 && S >= 4 && H * S <= c->n_cu;
+    const bool sa_fold = fold && fw_self_attn_f16q_ok(d, H) && fw_gemv16_ok(3 * d, d) && fw_gemv16_lpr(3 * d, d) == 16;
+    // embedding + layer 0's attention LayerNorm (the int8 arm, and the f16
+    // arm's folded self-attention, form both inside layer 0's kernel)
+    if (!i8 && !sa_fold)
         fw_launch_embed_ln(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S, dd->layers[0].attn_ln_w,
                            dd->layers[0].attn_ln_b, st->h, nullptr, nullptr);
     for (int li = 0; li < L; li++) {
@@ -782,23 +790,18 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             else if (!gemv_blk_all(st, s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, d))
                 return fw_fail(FWHIP_ERR_INVALID, "block GEMV: unsupported mlp width");
         } else {
-            // (layer 0's attention LayerNorm ran with the embedding, into h)
-            // The projections fold into the attention kernels when the cohort's
-            // (head, stream) blocks fill one round of the CUs: with fewer streams
-            // a head's rows would be multiplied on that many CUs only (one
-            // stream: 332 against 316 us per step), with more the second round
-            // costs more than the two launches saved (16 streams: 611 against
-            // 606 us); 10 streams: 420 against 443 us.
-            const bool fold = S >= 4 && H * S <= c->n_cu;
-            if (fold && fw_self_attn_f16q_ok(d, H) && fw_gemv16_ok(3 * d, d) && fw_gemv16_lpr(3 * d, d) == 16) {
+            if (sa_fold) {
                 // the LayerNorm, q/k/v projection and attention in one kernel
+                // (layer 0: the embedding too)
                 if (li > 0)
                     fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, st->x, l.attn_ln_w, l.attn_ln_b, st->kv_k,
                                              st->kv_v, st->att, st->pos, H, dd->nctx, L, li, S, scale);
                 else
-                    fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, st->h, nullptr, nullptr, st->kv_k, st->kv_v,
-                                             st->att, st->pos, H, dd->nctx, L, li, S, scale);
+                    fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, nullptr, l.attn_ln_w, l.attn_ln_b, st->kv_k,
+                                             st->kv_v, st->att, st->pos, H, dd->nctx, L, li, S, scale, tok,
+                                             dd->emb16, dd->pos_emb, st->x);
             } else {
+                // (layer 0's attention LayerNorm ran with the embedding, into h)
                 if (li > 0)
                     fw_gemv16_ln(s, l.qkv16, l.qkv_b, st->x, st->h, l.attn_ln_w, l.attn_ln_b, st->qkv, 3 * d, d, S,
                                  3 * d, 0, gt);
