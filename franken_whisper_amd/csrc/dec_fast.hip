@@ -2244,10 +2244,53 @@ void fw_launch_gemv_i8m(hipStream_t st, const int8_t *W, const float *sw, const 
 #undef GV_ARGS
 }
 
+// The same argmax and bookkeeping with one block per stream: every key is
+// requested at entry (clamped addresses: a repeated key leaves the maximum
+// unchanged), so the stream's keys cost one round trip instead of a dependent
+// walk.  The block that counts last (cnt, zero between launches) advances the
+// position, clears initial and the step counter; every block has read the
+// step before it counts.
+#define AM_U 16
+__global__ void __launch_bounds__(256) k_argmax_rows(const unsigned long long *keys, int nblk, int ns, int32_t *tok,
+                                                     int32_t *hist, int hist_cap, int *posp, int *initialp,
+                                                     int *stepp, int advance, int *cnt) {
+    __shared__ unsigned long long red[4];
+    const int s = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int step = stepp ? *stepp : 0;
+    const unsigned long long *ks = keys + (size_t)s * nblk;
+    unsigned long long kv[AM_U];
+#pragma unroll
+    for (int u = 0; u < AM_U; u++) kv[u] = ks[min(t + u * 256, nblk - 1)];
+    unsigned long long k = 0ull;
+#pragma unroll
+    for (int u = 0; u < AM_U; u++) k = kv[u] > k ? kv[u] : k;
+    k = wave_max_u64(k);
+    if (lane == 0) red[wave] = k;
+    __syncthreads();
+    if (t == 0) {
+#pragma unroll
+        for (int w = 1; w < 4; w++) k = red[w] > k ? red[w] : k;
+        const int tk = k ? (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull)) : 0;
+        tok[s] = tk;
+        if (hist) hist[(size_t)s * hist_cap + step] = tk;
+        if (atomicAdd(cnt, 1) == ns - 1) {
+            if (advance) *posp = *posp + 1;
+            if (initialp) *initialp = 0;
+            if (stepp) *stepp = step + 1;
+            *cnt = 0;
+        }
+    }
+}
+
 void fw_launch_argmax_finish(hipStream_t st, const unsigned long long *keys, int nblk, int ns, int32_t *tok,
-                             int32_t *hist, int hist_cap, int *posp, int *initialp, int *stepp, int advance) {
-    hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(1024), 0, st, keys, nblk, ns, tok, hist, hist_cap, posp,
-                       initialp, stepp, advance);
+                             int32_t *hist, int hist_cap, int *posp, int *initialp, int *stepp, int advance,
+                             int *cnt) {
+    if (cnt && nblk > 0 && nblk <= 256 * AM_U)
+        hipLaunchKernelGGL(k_argmax_rows, dim3(ns), dim3(256), 0, st, keys, nblk, ns, tok, hist, hist_cap, posp,
+                           initialp, stepp, advance, cnt);
+    else
+        hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(1024), 0, st, keys, nblk, ns, tok, hist, hist_cap, posp,
+                           initialp, stepp, advance);
 }
 
 // Streams go in chunks of SG * floor(512 / nb) (one (block, group) pair per

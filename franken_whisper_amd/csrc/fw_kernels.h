@@ -126,8 +126,11 @@ void fw_launch_gemv_i8m(hipStream_t st, const int8_t *W, const float *sw, const 
                         const float *xs, float *y, int N, int K, int ns, int ldy, int mode, const float *gelu_tab,
                         const fwhip_filter *filt, const int *initialp, unsigned long long *keys,
                         const float *xf = nullptr, const float *pmax = nullptr, int H = 0);
+// cnt (an int that is zero between launches): one block per stream, the last
+// to finish doing the bookkeeping; else one block walks every stream
 void fw_launch_argmax_finish(hipStream_t st, const unsigned long long *keys, int nblk, int ns, int32_t *tok,
-                             int32_t *hist, int hist_cap, int *posp, int *initialp, int *stepp, int advance);
+                             int32_t *hist, int hist_cap, int *posp, int *initialp, int *stepp, int advance,
+                             int *cnt = nullptr);
 int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const float *bias, const float *x, float *y,
                         int N, int K, int ns, int ldy, int mode, int n_cu);
 // pmax (nullable): [ns, H] max |output| of each head block, for a consumer

@@ -253,6 +253,7 @@ struct fwhip_dstate {
     uint16_t *kv_k, *kv_v, *ck16, *cvt16;
     uint16_t *ck16p = nullptr, *cvt16p = nullptr; // f16 arm: slot-order copies for the cross attention
     float *xsplit = nullptr; // f16 arm: scores and block maxima of the two-launch cross attention
+    int *am_cnt = nullptr;   // argmax blocks counted in (zero between launches)
     int8_t *ck8 = nullptr, *cvt8 = nullptr; // cvt8 rows have stride Tq (T rounded up to 16)
     float *ck8s = nullptr, *cvt8s = nullptr;
     float *x, *h, *qkv, *att, *y, *ff, *logits;
@@ -583,16 +584,17 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     st->rows = (int32_t *)fw_dalloc(own, sizeof(int32_t) * (size_t)S * nctx);
     st->hist_cap = nctx;
     st->hist = (int32_t *)fw_dalloc(own, sizeof(int32_t) * (size_t)S * nctx);
-    st->pos = (int *)fw_dalloc(own, sizeof(int) * 4);
+    st->pos = (int *)fw_dalloc(own, sizeof(int) * 5);
     st->initial = st->pos + 1;
     st->stepc = st->pos + 2;
+    st->am_cnt = st->pos + 4;
     st->pmax = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * dd->H);
     st->ench = (uint16_t *)fw_dalloc(own, sizeof(uint16_t) * (size_t)S * T * d);
     st->encl = (uint16_t *)fw_dalloc(own, sizeof(uint16_t) * (size_t)S * T * d);
     ok = ok && st->x && st->h && st->qkv && st->att && st->y && st->ff && st->logits && st->xq && st->xs &&
          st->keys && st->tok && st->rows && st->hist && st->pos && st->pmax && st->ench && st->encl;
     // padding rows of the quantized activations must read as zeros
-    ok = ok && hipMemset(st->xq, 0, (size_t)st->Sp * d) == hipSuccess && hipMemset(st->pos, 0, sizeof(int) * 4) == hipSuccess;
+    ok = ok && hipMemset(st->xq, 0, (size_t)st->Sp * d) == hipSuccess && hipMemset(st->pos, 0, sizeof(int) * 5) == hipSuccess;
     if (!ok) {
         fw_free_all(own);
         delete st;
@@ -1031,7 +1033,7 @@ static fwhip_status greedy_step(fwhip_dstate *st, const fwhip_filter *filt, bool
     fwhip_status r = dec_forward_row(st, st->tok, false, true, filt, timed);
     if (r != FWHIP_OK) return r;
     fw_launch_argmax_finish(st->dec->ctx->stream, st->keys, st->nkeys, st->S, st->tok, st->hist, st->hist_cap, st->pos,
-                            st->initial, st->stepc, 1);
+                            st->initial, st->stepc, 1, st->am_cnt);
     return FWHIP_OK;
 }
 
@@ -1133,7 +1135,7 @@ extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *pro
     if (r != FWHIP_OK) return r;
     // first sampled token: from the prefill's logits
     fw_launch_argmax_finish(c->stream, st->keys, st->nkeys, S, st->tok, st->hist, st->hist_cap, st->pos, st->initial,
-                            st->stepc, 1);
+                            st->stepc, 1, st->am_cnt);
     std::vector<int32_t> hist((size_t)S * n_max, -1);
     int steps = 1;
     const int poll = 8;
