@@ -1475,6 +1475,14 @@ __device__ __forceinline__ void sa_attend(const float *qh, const uint16_t *kc, c
                                           int base, int d, int tk, float scale, float *sc, uint16_t *vs, float *red,
                                           float *inv_s, float *out, float *pmax_slot) {
     const int t = threadIdx.x;
+    // this thread's first key row is requested ahead of the value rows (clamped
+    // address, used when t < tk), so keys and values share one round trip
+    uint4 kpre[8];
+    {
+        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)(t < tk ? t : tk - 1) * d + base);
+#pragma unroll
+        for (int c = 0; c < 8; c++) kpre[c] = kr[c];
+    }
     // stage V rows [0, tk) of this head (8 x 16 bytes per row), SA_STG chunks
     // per thread per round, loads issued before the LDS stores
     for (int c0 = 0; c0 < tk * 8; c0 += NT * SA_STG) {
@@ -1492,19 +1500,30 @@ __device__ __forceinline__ void sa_attend(const float *qh, const uint16_t *kc, c
         }
     }
     float mx = -INFINITY;
-    for (int j = t; j < tk; j += NT) {
-        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)j * d + base);
+    auto score = [&](const uint4 (&kk)[8]) {
         float acc = 0.0f;
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            uint4 u = kr[c];
-            uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+            const uint32_t ww[4] = {kk[c].x, kk[c].y, kk[c].z, kk[c].w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 acc += qh[c * 8 + 2 * e] * (fw_h2f(ww[e] & 0xffff) * scale);
                 acc += qh[c * 8 + 2 * e + 1] * (fw_h2f(ww[e] >> 16) * scale);
             }
         }
+        return acc;
+    };
+    if (t < tk) {
+        const float acc = score(kpre);
+        sc[t] = acc;
+        mx = fmaxf(mx, acc);
+    }
+    for (int j = t + NT; j < tk; j += NT) {
+        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)j * d + base);
+        uint4 kk[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) kk[c] = kr[c];
+        const float acc = score(kk);
         sc[j] = acc;
         mx = fmaxf(mx, acc);
     }
