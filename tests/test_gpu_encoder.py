@@ -3,7 +3,7 @@ encoder.rs + nn.rs in strict-parity mode).
 
 - int8 plan: every GEMM's i32 accumulators are compared BIT-EXACTLY on the same
   quantized inputs, and the epilogue output too (same f32 formula);
-- whole encoder: output within max-abs 1e-3 relative (BASELINE tolerance) on
+- whole encoder: output within max-abs 1e-3 relative (the stated f32 tolerance) on
   both plans; the f32 plan uses f16-pair MFMA products (error <= 2^-22
   relative per product) and a different summation order than the
   reference's sequential f32 GEMM, so it is a tolerance comparison by design."""
@@ -71,7 +71,7 @@ def _encoder_pair(ctx, cfg, precision, n_windows, seed=2, exact=False):
 
 @pytest.mark.parametrize("cfg", [synth.MICRO, TINY2], ids=lambda c: c.name)
 def test_encoder_f32_within_tolerance(ctx, cfg):
-    """f32 plan: max-abs 1e-3 relative (BASELINE tolerance).  The residual
+    """f32 plan: max-abs 1e-3 relative (the stated f32 tolerance).  The residual
     spread (~1e-4) is the reference's own f16-table GELU turning sub-ulp
     summation-order differences into one-f16-ulp steps; the GEMM and attention
     kernels alone are within ~1e-7 of float64."""
