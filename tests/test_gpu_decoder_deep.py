@@ -1,8 +1,9 @@
 """GPU decoder parity at the large-v3-turbo decoder shape (4 layers, d 1280,
 20 heads, vocab 51866, n_text_ctx 448) deep into the KV cache, on both arms
 (the int8 default and the pure-f16 arm with the f16 tied logits head), with 1,
-10 and 16 concurrent streams (the f16 arm folds the q/k/v and cross q
-projections into its attention kernels at 10 streams and not at 1 or 16, so the
+3, 10 and 16 concurrent streams (the f16 arm folds the q/k/v and cross q
+projections into its attention kernels at 10 streams and not at 1, 3 or 16, and
+runs its cross attention in two launches at 1 and 3 streams, so the
 cohort-vs-alone comparison below also holds the folded kernels to the separate
 ones bit for bit).
 
@@ -59,7 +60,7 @@ def _gpu_run(ctx, dec, enc, toks):
     return out
 
 
-@pytest.mark.parametrize("S", [1, 10, 16])
+@pytest.mark.parametrize("S", [1, 3, 10, 16])
 @pytest.mark.parametrize("arm", [abi.DEC_INT8, abi.DEC_F16], ids=["int8", "f16"])
 def test_turbo_deep_cache_bitexact(ctx, arm, S):
     m = model("large-v3-turbo", seed=2, encoder=False)
