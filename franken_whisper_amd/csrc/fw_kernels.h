@@ -46,8 +46,9 @@ void fw_launch_pack_cross_f16(hipStream_t st, const uint16_t *ck, const uint16_t
 void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp, float *att,
                                int d, int T, int H, int L, int layer, int ns, float scale, int rows = 0);
 // fw_launch_cross_attn_f16p (one row per stream) in two launches that spread
-// each head's keys and output dims over more blocks, for cohorts that fill few
-// CUs; the same bits.  scratch: fw_cross_split_floats(T, H, ns) floats.
+// each head's keys and output dims over more blocks, for cohorts whose
+// (head, stream) blocks fill few CUs or more than one round of them; the same
+// bits.  scratch: fw_cross_split_floats(T, H, ns) floats.
 size_t fw_cross_split_floats(int T, int H, int ns);
 void fw_launch_cross_attn_f16p_split(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp,
                                      float *att, int d, int T, int H, int L, int layer, int ns, float scale,

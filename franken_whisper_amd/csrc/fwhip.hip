@@ -820,9 +820,11 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             } else {
                 fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0, gt);
                 // a cohort whose (head, stream) blocks fill under half the CUs
-                // spreads each head over more blocks in two launches (one
-                // stream: 20 blocks for 1,500 keys)
-                if (st->ck16p && S * H * 2 <= c->n_cu)
+                // (one stream: 20 blocks for 1,500 keys) or need more than one
+                // round of them (16 streams: 320 blocks; 591 against 606 us per
+                // step) spreads each head over more blocks in two launches
+                const long long hs = (long long)S * H;
+                if (st->ck16p && (hs * 2 <= c->n_cu || hs > c->n_cu))
                     fw_launch_cross_attn_f16p_split(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S,
                                                     scale, st->xsplit);
                 else if (st->ck16p)

@@ -3,7 +3,7 @@
 (the int8 default and the pure-f16 arm with the f16 tied logits head), with 1,
 3, 10 and 16 concurrent streams (the f16 arm folds the q/k/v and cross q
 projections into its attention kernels at 10 streams and not at 1, 3 or 16, and
-runs its cross attention in two launches at 1 and 3 streams, so the
+runs its cross attention in two launches at 1, 3 and 16 streams, so the
 cohort-vs-alone comparison below also holds the folded kernels to the separate
 ones bit for bit).
 
