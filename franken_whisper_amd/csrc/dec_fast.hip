@@ -902,6 +902,70 @@ __device__ __forceinline__ int fw_xp_pos(int e) { return (e & 7) * 8 + (e >> 5) 
 #ifndef XQ_EARLY
 #define XQ_EARLY 8 // 64-key rounds requested before the q projection
 #endif
+// The cross LayerNorm of x_s (wave 0, the GEMV's one-wave arithmetic) into xl
+// and the head's 64 q rows (gemv_f16 on the slot-order matrix at 16 lanes per
+// row, then the bias) into qf; 512 threads, d == XQ_D.  issue_early runs once
+// the weight rows are requested (key rows that stream in meanwhile),
+// issue_late once the q rows are stored, before the caller's barrier.
+template <typename E, typename F>
+__device__ __forceinline__ void xq_rows(const uint16_t *__restrict__ wq, const float *__restrict__ bq,
+                                        const float *__restrict__ x, const float *__restrict__ lnw,
+                                        const float *__restrict__ lnb, int h, int s, float *xl, float *qf,
+                                        E &&issue_early, F &&issue_late) {
+    constexpr int NV = XQ_D / 256, G = XQ_D / 128; // float4s per lane of a row; 16-byte groups per weight row
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int p = lane & 15, rq = lane >> 4; // lane of the row group, row group of the wave
+    float4 lv[NV], lw[NV], lb[NV];
+    bool lok[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        lok[k] = true;
+        lv[k] = ((const float4 *)(x + (size_t)s * XQ_D))[lane + k * 64];
+    }
+    fw_ln_load_wb<NV>(lok, lnw, lnb, lw, lb, lane);
+    // rows h * 64 + wave * 8 + r * 4 + rq, r = 0, 1
+    uint4 wv[2][G];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const uint4 *wr = (const uint4 *)(wq + (size_t)(h * 64 + wave * 8 + r * 4 + rq) * XQ_D) + p;
+#pragma unroll
+        for (int g = 0; g < G; g++) wv[r][g] = wr[g * 16];
+    }
+    const float bv0 = bq ? bq[h * 64 + wave * 8 + rq] : 0.0f, bv1 = bq ? bq[h * 64 + wave * 8 + 4 + rq] : 0.0f;
+    issue_early();
+    if (wave == 0) fw_ln_quant_core<NV>(lv, lok, lw, lb, xl, XQ_D, 0, nullptr, nullptr, lane);
+    __syncthreads();
+    // lane p = kh * 8 + l holds slots 8 (2 kh + kk) + l; a group is 4 chunks
+    float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+    const int kh = p >> 3, pl = p & 7;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const int c = g * 4 + cc;
+            const float x0 = xl[c * 32 + 8 * (2 * kh) + pl], x1 = xl[c * 32 + 8 * (2 * kh + 1) + pl];
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const uint32_t u[4] = {wv[r][g].x, wv[r][g].y, wv[r][g].z, wv[r][g].w};
+                const float w0 = fw_h2f((uint16_t)(u[cc] & 0xffffu)), w1 = fw_h2f((uint16_t)(u[cc] >> 16));
+                acc[r][0] = __builtin_fmaf(w0, x0, acc[r][0]);
+                acc[r][1] = __builtin_fmaf(w1, x1, acc[r][1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        float v = acc[r][0] + acc[r][1];
+        v = v + __shfl_xor(v, 8, 64);
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        if (bq) v = v + (r ? bv1 : bv0);
+        if (p == 0) qf[wave * 8 + r * 4 + rq] = v;
+    }
+    issue_late();
+}
+
 template <bool FQ>
 __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const uint16_t *ckp, const uint16_t *cvtp,
                                                          float *att, int d, int T, int Tv, int H, int L, int layer,
@@ -942,61 +1006,11 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
     using kE = std::integral_constant<int, XQ_EARLY>;
     using kN = std::integral_constant<int, XP_MAXG>;
     if constexpr (FQ) {
-        constexpr int NV = XQ_D / 256, G = XQ_D / 128; // float4s per lane of a row; 16-byte groups per weight row
         __shared__ __align__(16) float xl[XQ_D];
         __shared__ float qf[64];
-        const int p = lane & 15, rq = lane >> 4; // lane of the row group, row group of the wave
-        float4 lv[NV], lw[NV], lb[NV];
-        bool lok[NV];
-#pragma unroll
-        for (int k = 0; k < NV; k++) {
-            lok[k] = true;
-            lv[k] = ((const float4 *)(x + (size_t)s * XQ_D))[lane + k * 64];
-        }
-        fw_ln_load_wb<NV>(lok, lnw, lnb, lw, lb, lane);
-        // rows h * 64 + wave * 8 + r * 4 + rq, r = 0, 1
-        uint4 wv[2][G];
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const uint4 *wr = (const uint4 *)(wq + (size_t)(h * 64 + wave * 8 + r * 4 + rq) * XQ_D) + p;
-#pragma unroll
-            for (int g = 0; g < G; g++) wv[r][g] = wr[g * 16];
-        }
-        const float bv0 = bq ? bq[h * 64 + wave * 8 + rq] : 0.0f, bv1 = bq ? bq[h * 64 + wave * 8 + 4 + rq] : 0.0f;
         // the first key rows stream in while q is formed (all of them would
         // not fit the registers beside the q operands)
-        load_keys(k0{}, kE{});
-        if (wave == 0) fw_ln_quant_core<NV>(lv, lok, lw, lb, xl, XQ_D, 0, nullptr, nullptr, lane);
-        __syncthreads();
-        // lane p = kh * 8 + l holds slots 8 (2 kh + kk) + l; a group is 4 chunks
-        float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
-        const int kh = p >> 3, pl = p & 7;
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-#pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const int c = g * 4 + cc;
-                const float x0 = xl[c * 32 + 8 * (2 * kh) + pl], x1 = xl[c * 32 + 8 * (2 * kh + 1) + pl];
-#pragma unroll
-                for (int r = 0; r < 2; r++) {
-                    const uint32_t u[4] = {wv[r][g].x, wv[r][g].y, wv[r][g].z, wv[r][g].w};
-                    const float w0 = fw_h2f((uint16_t)(u[cc] & 0xffffu)), w1 = fw_h2f((uint16_t)(u[cc] >> 16));
-                    acc[r][0] = __builtin_fmaf(w0, x0, acc[r][0]);
-                    acc[r][1] = __builtin_fmaf(w1, x1, acc[r][1]);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            float v = acc[r][0] + acc[r][1];
-            v = v + __shfl_xor(v, 8, 64);
-            v = v + __shfl_xor(v, 1, 64);
-            v = v + __shfl_xor(v, 2, 64);
-            v = v + __shfl_xor(v, 4, 64);
-            if (bq) v = v + (r ? bv1 : bv0);
-            if (p == 0) qf[wave * 8 + r * 4 + rq] = v;
-        }
-        load_keys(kE{}, kN{});
+        xq_rows(wq, bq, x, lnw, lnb, h, s, xl, qf, [&] { load_keys(k0{}, kE{}); }, [&] { load_keys(kE{}, kN{}); });
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -1218,6 +1232,70 @@ __global__ void __launch_bounds__(256) k_cross_scores_f16p(const float *qc, cons
     if (t == 0) mbuf[((size_t)r * H + h) * XS_KC + kc] = mx;
 }
 
+// k_cross_scores_f16p with the cross LayerNorm and the head's q rows formed
+// in the block (xq_rows; the separate LN + q GEMV's bits), 512 threads: each
+// of a head's XS_KC blocks forms the same q, its three 64-key rounds
+// requested while q is formed.  For cohorts that fill few CUs: it saves the
+// q GEMV's launch at the price of XS_KC reads of the head's q rows from L2.
+__global__ void __launch_bounds__(512) k_cross_scores_f16pq(const uint16_t *__restrict__ wq,
+                                                            const float *__restrict__ bq, const float *__restrict__ x,
+                                                            const float *__restrict__ lnw,
+                                                            const float *__restrict__ lnb, const uint16_t *ckp,
+                                                            float *sbuf, float *mbuf, int T, int Tv, int H, int L,
+                                                            int layer, int ns, float scale) {
+    __shared__ __align__(16) float xl[XQ_D];
+    __shared__ float qf[64];
+    __shared__ float red[8];
+    const int h = blockIdx.x, kc = blockIdx.y, r = blockIdx.z, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6, l = lane & 7, rg = lane >> 3;
+    const size_t lh = ((size_t)(r % ns) * L + layer) * H + h;
+    const uint16_t *K = ckp + lh * (size_t)T * 64;
+    const int CH = ((T + XS_KC * 64 - 1) / (XS_KC * 64)) * 64, j0 = kc * CH, j1 = min(T, j0 + CH);
+    constexpr int NR = 1536 / XS_KC / 64; // 64-key rounds a block holds at most (T <= 1536)
+    uint4 kv[NR];
+    xq_rows(
+        wq, bq, x, lnw, lnb, h, r, xl, qf,
+        [&] {
+#pragma unroll
+            for (int q = 0; q < NR; q++) {
+                const int j = j0 + q * 64 + wave * 8 + rg;
+                kv[q] = *(const uint4 *)(K + (size_t)(j < j1 ? j : (j1 > j0 ? j1 - 1 : 0)) * 64 + l * 8);
+            }
+        },
+        [] {});
+    __syncthreads();
+    float q0[4], q1[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        q0[k] = qf[8 * k + l] * scale;
+        q1[k] = qf[32 + 8 * k + l] * scale;
+    }
+    float mx = -INFINITY;
+    float *sc = sbuf + ((size_t)r * H + h) * Tv;
+#pragma unroll
+    for (int q = 0; q < NR; q++) {
+        const int j = j0 + q * 64 + wave * 8 + rg;
+        const uint32_t u[4] = {kv[q].x, kv[q].y, kv[q].z, kv[q].w};
+        float a[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float w0 = fw_h2f((uint16_t)(u[k >> 1] >> ((k & 1) * 16)));
+            const float w1 = fw_h2f((uint16_t)(u[2 + (k >> 1)] >> ((k & 1) * 16)));
+            a[k] = __builtin_fmaf(w1, q1[k], __builtin_fmaf(w0, q0[k], 0.0f));
+        }
+        float v = (a[0] + a[1]) + (a[2] + a[3]);
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        if (j < j1) {
+            if (l == 0) sc[j] = v;
+            mx = fmaxf(mx, v);
+        }
+    }
+    mx = fw_block_max(mx, red);
+    if (t == 0) mbuf[((size_t)r * H + h) * XS_KC + kc] = mx;
+}
+
 __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const float *mbuf, const uint16_t *cvtp,
                                                        float *att, int d, int T, int Tv, int H, int L, int layer,
                                                        int ns) {
@@ -1357,6 +1435,21 @@ __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const 
 
 size_t fw_cross_split_floats(int T, int H, int ns) {
     return (size_t)ns * H * (fw_cross_f16p_tv(T) + XS_KC);
+}
+
+// the same with the cross LayerNorm of x and the q projection in the scores
+// launch (wq in fw_launch_pack_gemv16's slot order at 16 lanes per row; needs
+// fw_cross_f16pq_ok(d, T, H))
+void fw_launch_cross_attn_f16pq_split(hipStream_t st, const uint16_t *wq, const float *bq, const float *x,
+                                      const float *lnw, const float *lnb, const uint16_t *ckp, const uint16_t *cvtp,
+                                      float *att, int d, int T, int H, int L, int layer, int ns, float scale,
+                                      float *scratch) {
+    const int Tv = fw_cross_f16p_tv(T);
+    float *sbuf = scratch, *mbuf = scratch + (size_t)ns * H * Tv;
+    hipLaunchKernelGGL(k_cross_scores_f16pq, dim3(H, XS_KC, ns), dim3(512), 0, st, wq, bq, x, lnw, lnb, ckp, sbuf,
+                       mbuf, T, Tv, H, L, layer, ns, scale);
+    hipLaunchKernelGGL(k_cross_pv_f16p, dim3(H, XS_DC, ns), dim3(256), sizeof(float) * 2 * (size_t)Tv, st, sbuf, mbuf,
+                       cvtp, att, d, T, Tv, H, L, layer, ns);
 }
 
 // scratch: fw_cross_split_floats(T, H, ns) floats

@@ -53,6 +53,13 @@ size_t fw_cross_split_floats(int T, int H, int ns);
 void fw_launch_cross_attn_f16p_split(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp,
                                      float *att, int d, int T, int H, int L, int layer, int ns, float scale,
                                      float *scratch);
+// the same with the cross LayerNorm of x [ns, d] and the q projection (wq in
+// fw_launch_pack_gemv16's slot order at 16 lanes per row, bias bq) formed in
+// each scores block; needs fw_cross_f16pq_ok(d, T, H)
+void fw_launch_cross_attn_f16pq_split(hipStream_t st, const uint16_t *wq, const float *bq, const float *x,
+                                      const float *lnw, const float *lnb, const uint16_t *ckp, const uint16_t *cvtp,
+                                      float *att, int d, int T, int H, int L, int layer, int ns, float scale,
+                                      float *scratch);
 // fw_launch_cross_attn_f16p with the cross LayerNorm of x [ns, d] and the q
 // projection inside (wq in fw_launch_pack_gemv16's slot order at 16 lanes per
 // row, bq the bias); needs fw_cross_f16pq_ok(d, T, H)

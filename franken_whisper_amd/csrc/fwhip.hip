@@ -818,18 +818,27 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 fw_launch_cross_attn_f16pq(s, l.cq16, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck16p,
                                            st->cvt16p, st->att, d, T, H, L, li, S, scale);
             } else {
-                fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0, gt);
                 // a cohort whose (head, stream) blocks fill under half the CUs
                 // (one stream: 20 blocks for 1,500 keys) or need more than one
                 // round of them (16 streams: 320 blocks; 591 against 606 us per
-                // step) spreads each head over more blocks in two launches
+                // step) spreads each head over more blocks in two launches; under
+                // half, the scores launch also forms the LayerNorm and q rows
                 const long long hs = (long long)S * H;
-                if (st->ck16p && (hs * 2 <= c->n_cu || hs > c->n_cu))
-                    fw_launch_cross_attn_f16p_split(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S,
-                                                    scale, st->xsplit);
-                else if (st->ck16p)
-                    fw_launch_cross_attn_f16p(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S, scale);
-                else fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
+                const bool xsplit = st->ck16p && (hs * 2 <= c->n_cu || hs > c->n_cu);
+                if (xsplit && hs * 2 <= c->n_cu && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) &&
+                    fw_gemv16_lpr(d, d) == 16) {
+                    fw_launch_cross_attn_f16pq_split(s, l.cq16, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck16p,
+                                                     st->cvt16p, st->att, d, T, H, L, li, S, scale, st->xsplit);
+                } else {
+                    fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0,
+                                 gt);
+                    if (xsplit)
+                        fw_launch_cross_attn_f16p_split(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S,
+                                                        scale, st->xsplit);
+                    else if (st->ck16p)
+                        fw_launch_cross_attn_f16p(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S, scale);
+                    else fw_launch_cross_attn_f16(s, st->y, st->ck16, st->cvt16, st->att, d, T, H, L, li, S, scale);
+                }
             }
             fw_gemv16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
             fw_gemv16_ln(s, l.fc1_16, l.fc1_b, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, st->ff, dff, d, S, dff, 2, gt);
