@@ -431,10 +431,13 @@ void fw_launch_gemv16(hipStream_t st, const uint16_t *Wp, const float *bias, con
     //    weights through the batch pipeline;
     //  - d x d (o, cross q/o): one stream per block, one row per lane (the
     //    most blocks; each re-reads the 3.3 MB matrix from L2 or the MALL);
-    //  - q/k/v, fc1, fc2: 2 streams a block, 2 rows per lane.
-    const bool big = N >= 16384, small = N <= 1280 && K <= 1280;
-    if (r <= 0) r = big || small || ns == 1 ? 1 : 2;
-    if (sb_cap <= 0) sb_cap = big ? (ns >= 16 ? 5 : 10) : small ? 1 : 2;
+    //  - q/k/v, fc1, fc2: 2 streams a block, 2 rows per lane; fc1 (N >= 4K)
+    //    with 8 or more streams: 5 streams a block, one row per lane (10
+    //    streams: step 413 -> 403 us; 16: 590 against 591; 4 streams keep the
+    //    default: 353 against 354).
+    const bool big = N >= 16384, small = N <= 1280 && K <= 1280, wide = !big && !small && N >= 4 * K && ns >= 8;
+    if (r <= 0) r = big || small || ns == 1 || wide ? 1 : 2;
+    if (sb_cap <= 0) sb_cap = big ? (ns >= 16 ? 5 : 10) : small ? 1 : wide ? 5 : 2;
     if (grid_cap <= 0) grid_cap = big ? (ns == 1 ? 4 * n_cu : ns >= 16 ? n_cu : 2 * n_cu) : 1 << 30;
     if (keys) r = 1; // the key layout (fw_gemv16_key_blocks) assumes one row per lane
 #define G16_GO(L_, R_) g16_pipe<L_, R_, 4>(st, grid_cap, sb_cap, a)
