@@ -22,7 +22,9 @@
 #include "fw_kernels.h"
 
 #define WIN_BT 256 // threads per block
+#ifndef WIN_UPT
 #define WIN_UPT 16 // lanes per thread: WIN_NB * WIN_BT * WIN_UPT covers the vocabulary
+#endif
 #define WIN_TAU 1.0e-3f
 
 namespace {

@@ -104,7 +104,9 @@ struct FwWinStream {
 // one stream's row is filtered by WIN_NB blocks, each leaving its partial
 // results in a slot; the last block to count (cnt[s], zero between launches)
 // merges them
+#ifndef WIN_NB
 #define WIN_NB 16
+#endif
 struct FwWinPart {
     unsigned long long ka, kt;  // argmax keys: every lane, the timestamp lanes
     float mall, mtxt, mts, sb;  // maxima (all, text, timestamp lanes); sum of expf(u - mall) over the block's lanes
