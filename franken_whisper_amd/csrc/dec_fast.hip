@@ -28,7 +28,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 #include "fw_dec.h"
 
-template <int NV>
+template <int NV, bool SEQ>
 __global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, const float *w, const float *b, int d,
                                                   int rows, int8_t *xq, float *xs) {
     const int lane = threadIdx.x & 63;
@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, cons
         ok[k] = i < n4;
         xv[k] = xr[ok[k] ? i : 0];
     }
-    fw_ln_quant_vals<NV>(xv, ok, y, w, b, d, r, xq, xs, lane);
+    fw_ln_quant_vals<NV, SEQ>(xv, ok, y, w, b, d, r, xq, xs, lane);
 }
 
 // embed_tokens (decoder.rs:1323-1385: x = f16(E[tok]) + P[pos]) of one stream
@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, cons
 // as k_ln_quant).
 // Row s sits at position *posp + s / rps (rps: rows per position, the streams
 // of a prefill chunk whose rows are [position][stream]).
-template <int NV>
+template <int NV, bool SEQ>
 __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *posp, const uint16_t *emb,
                                                  const float *pemb, float *x, int d, const float *w, const float *b,
                                                  float *ln_y, int8_t *xq, float *xs, int rps) {
@@ -74,7 +74,7 @@ __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *
                             fw_h2f(e.y >> 16) + p.w);
         if (ok[k]) ((float4 *)(x + (size_t)s * d))[i] = xv[k];
     }
-    if (w) fw_ln_quant_vals<NV>(xv, ok, ln_y, w, b, d, s, xq, xs, lane);
+    if (w) fw_ln_quant_vals<NV, SEQ>(xv, ok, ln_y, w, b, d, s, xq, xs, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -86,7 +86,7 @@ __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *
 // of each of its rows, and a lane issues R = 8 groups per round, the next round
 // in flight while the current one is used (a row of 1280 needs one round at 32
 // lanes per row).  Needs K % (8 * LPR) == 0.
-template <int LPR, int SG, bool LN>
+template <int LPR, int SG, bool LN, bool SEQ>
 __global__ void __launch_bounds__(256) k_gemv_f16f(const uint16_t *__restrict__ Wf, const float *__restrict__ bias,
                                                    const float *__restrict__ x, float *y, int N, int K, int ns,
                                                    int ldy, int mode, const float *__restrict__ gelu_tab, int cps,
@@ -135,7 +135,7 @@ __global__ void __launch_bounds__(256) k_gemv_f16f(const uint16_t *__restrict__ 
                 xv[kk] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if (sl < sn) xv[kk] = ((const float4 *)(x + (size_t)(s0 + sl) * K))[okk[kk] ? i : 0];
             }
-            if (sl < sn) fw_ln_quant_vals<5>(xv, okk, nullptr, lnw, lnb, K, 0, nullptr, nullptr, lane);
+            if (sl < sn) fw_ln_quant_vals<5, SEQ>(xv, okk, nullptr, lnw, lnb, K, 0, nullptr, nullptr, lane);
 #pragma unroll
             for (int kk = 0; kk < 5; kk++) {
                 if (okk[kk]) {
@@ -273,7 +273,7 @@ void fw_launch_pack_gemv_f16(hipStream_t st, const uint16_t *W, uint16_t *Wf, in
 // W in fragment order (fw_launch_pack_gemv_f16); K % (8 * lanes per row) == 0
 void fw_launch_gemv_f16f(hipStream_t st, const uint16_t *Wf, const float *bias, const float *x, float *y, int N,
                          int K, int ns, int ldy, int mode, const float *gelu_tab, const float *lnw,
-                         const float *lnb) {
+                         const float *lnb, int lnseq) {
     static int n_cu = 0;
     if (!n_cu) {
         int dev = 0;
@@ -300,12 +300,15 @@ void fw_launch_gemv_f16f(hipStream_t st, const uint16_t *Wf, const float *bias, 
     do {                                                                                                     \
         const int ntile = (N + 256 / LPR_ - 1) / (256 / LPR_);                                               \
         const int grid = one && ntile > 2 * n_cu ? 2 * n_cu : ntile;                                        \
-        if (lnw)                                                                                            \
-            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, true>), dim3(grid, nby), dim3(256), shm, st, Wf, bias, x, y, \
-                               N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);                          \
+        if (lnw && lnseq)                                                                                   \
+            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, true, true>), dim3(grid, nby), dim3(256), shm, st, Wf, bias, \
+                               x, y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);                    \
+        else if (lnw)                                                                                       \
+            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, true, false>), dim3(grid, nby), dim3(256), shm, st, Wf,     \
+                               bias, x, y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);              \
         else                                                                                                \
-            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, false>), dim3(grid, nby), dim3(256), shm, st, Wf, bias, x,   \
-                               y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);                       \
+            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, false, false>), dim3(grid, nby), dim3(256), shm, st, Wf,    \
+                               bias, x, y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);              \
     } while (0)
 #define GF_SG(LPR_)                      \
     do {                                 \
@@ -907,7 +910,7 @@ __device__ __forceinline__ int fw_xp_pos(int e) { return (e & 7) * 8 + (e >> 5) 
 // row, then the bias) into qf; 512 threads, d == XQ_D.  issue_early runs once
 // the weight rows are requested (key rows that stream in meanwhile),
 // issue_late once the q rows are stored, before the caller's barrier.
-template <typename E, typename F>
+template <bool SEQ, typename E, typename F>
 __device__ __forceinline__ void xq_rows(const uint16_t *__restrict__ wq, const float *__restrict__ bq,
                                         const float *__restrict__ x, const float *__restrict__ lnw,
                                         const float *__restrict__ lnb, int h, int s, float *xl, float *qf,
@@ -933,7 +936,7 @@ __device__ __forceinline__ void xq_rows(const uint16_t *__restrict__ wq, const f
     }
     const float bv0 = bq ? bq[h * 64 + wave * 8 + rq] : 0.0f, bv1 = bq ? bq[h * 64 + wave * 8 + 4 + rq] : 0.0f;
     issue_early();
-    if (wave == 0) fw_ln_quant_core<NV>(lv, lok, lw, lb, xl, XQ_D, 0, nullptr, nullptr, lane);
+    if (wave == 0) fw_ln_quant_core<NV, SEQ>(lv, lok, lw, lb, xl, XQ_D, 0, nullptr, nullptr, lane);
     __syncthreads();
     // lane p = kh * 8 + l holds slots 8 (2 kh + kk) + l; a group is 4 chunks
     float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
@@ -966,7 +969,7 @@ __device__ __forceinline__ void xq_rows(const uint16_t *__restrict__ wq, const f
     issue_late();
 }
 
-template <bool FQ>
+template <bool FQ, bool SEQ>
 __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const uint16_t *ckp, const uint16_t *cvtp,
                                                          float *att, int d, int T, int Tv, int H, int L, int layer,
                                                          float scale, const uint16_t *__restrict__ wq,
@@ -1010,7 +1013,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
         __shared__ float qf[64];
         // the first key rows stream in while q is formed (all of them would
         // not fit the registers beside the q operands)
-        xq_rows(wq, bq, x, lnw, lnb, h, s, xl, qf, [&] { load_keys(k0{}, kE{}); }, [&] { load_keys(kE{}, kN{}); });
+        xq_rows<SEQ>(wq, bq, x, lnw, lnb, h, s, xl, qf, [&] { load_keys(k0{}, kE{}); }, [&] { load_keys(kE{}, kN{}); });
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -1237,6 +1240,7 @@ __global__ void __launch_bounds__(256) k_cross_scores_f16p(const float *qc, cons
 // of a head's XS_KC blocks forms the same q, its three 64-key rounds
 // requested while q is formed.  For cohorts that fill few CUs: it saves the
 // q GEMV's launch at the price of XS_KC reads of the head's q rows from L2.
+template <bool SEQ>
 __global__ void __launch_bounds__(512) k_cross_scores_f16pq(const uint16_t *__restrict__ wq,
                                                             const float *__restrict__ bq, const float *__restrict__ x,
                                                             const float *__restrict__ lnw,
@@ -1253,7 +1257,7 @@ __global__ void __launch_bounds__(512) k_cross_scores_f16pq(const uint16_t *__re
     const int CH = ((T + XS_KC * 64 - 1) / (XS_KC * 64)) * 64, j0 = kc * CH, j1 = min(T, j0 + CH);
     constexpr int NR = 1536 / XS_KC / 64; // 64-key rounds a block holds at most (T <= 1536)
     uint4 kv[NR];
-    xq_rows(
+    xq_rows<SEQ>(
         wq, bq, x, lnw, lnb, h, r, xl, qf,
         [&] {
 #pragma unroll
@@ -1443,11 +1447,15 @@ size_t fw_cross_split_floats(int T, int H, int ns) {
 void fw_launch_cross_attn_f16pq_split(hipStream_t st, const uint16_t *wq, const float *bq, const float *x,
                                       const float *lnw, const float *lnb, const uint16_t *ckp, const uint16_t *cvtp,
                                       float *att, int d, int T, int H, int L, int layer, int ns, float scale,
-                                      float *scratch) {
+                                      float *scratch, int lnseq) {
     const int Tv = fw_cross_f16p_tv(T);
     float *sbuf = scratch, *mbuf = scratch + (size_t)ns * H * Tv;
-    hipLaunchKernelGGL(k_cross_scores_f16pq, dim3(H, XS_KC, ns), dim3(512), 0, st, wq, bq, x, lnw, lnb, ckp, sbuf,
-                       mbuf, T, Tv, H, L, layer, ns, scale);
+    if (lnseq)
+        hipLaunchKernelGGL(k_cross_scores_f16pq<true>, dim3(H, XS_KC, ns), dim3(512), 0, st, wq, bq, x, lnw, lnb, ckp,
+                           sbuf, mbuf, T, Tv, H, L, layer, ns, scale);
+    else
+        hipLaunchKernelGGL(k_cross_scores_f16pq<false>, dim3(H, XS_KC, ns), dim3(512), 0, st, wq, bq, x, lnw, lnb, ckp,
+                           sbuf, mbuf, T, Tv, H, L, layer, ns, scale);
     hipLaunchKernelGGL(k_cross_pv_f16p, dim3(H, XS_DC, ns), dim3(256), sizeof(float) * 2 * (size_t)Tv, st, sbuf, mbuf,
                        cvtp, att, d, T, Tv, H, L, layer, ns);
 }
@@ -1502,9 +1510,9 @@ void fw_launch_pack_cross_f16(hipStream_t st, const uint16_t *ck, const uint16_t
 void fw_launch_cross_attn_f16p(hipStream_t st, const float *qc, const uint16_t *ckp, const uint16_t *cvtp, float *att,
                                int d, int T, int H, int L, int layer, int ns, float scale, int rows) {
     const int Tv = fw_cross_f16p_tv(T);
-    hipLaunchKernelGGL(k_cross_attn_f16p<false>, dim3(H, rows > 0 ? rows : ns), dim3(512), sizeof(float) * (size_t)Tv,
-                       st, qc, ckp, cvtp, att, d, T, Tv, H, L, layer, scale, nullptr, nullptr, nullptr, nullptr,
-                       nullptr, ns);
+    hipLaunchKernelGGL((k_cross_attn_f16p<false, false>), dim3(H, rows > 0 ? rows : ns), dim3(512),
+                       sizeof(float) * (size_t)Tv, st, qc, ckp, cvtp, att, d, T, Tv, H, L, layer, scale, nullptr,
+                       nullptr, nullptr, nullptr, nullptr, ns);
 }
 
 bool fw_cross_f16pq_ok(int d, int T, int H) { return d == XQ_D && H * 64 == d && fw_cross_f16p_ok(T); }
@@ -1513,10 +1521,14 @@ bool fw_cross_f16pq_ok(int d, int T, int H) { return d == XQ_D && H * 64 == d &&
 // q weights in fw_launch_pack_gemv16's slot order, 16 lanes per row) inside
 void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float *bq, const float *x, const float *lnw,
                                 const float *lnb, const uint16_t *ckp, const uint16_t *cvtp, float *att, int d, int T,
-                                int H, int L, int layer, int ns, float scale) {
+                                int H, int L, int layer, int ns, float scale, int lnseq) {
     const int Tv = fw_cross_f16p_tv(T);
-    hipLaunchKernelGGL(k_cross_attn_f16p<true>, dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st, nullptr, ckp,
-                       cvtp, att, d, T, Tv, H, L, layer, scale, wq, bq, x, lnw, lnb, ns);
+    if (lnseq)
+        hipLaunchKernelGGL((k_cross_attn_f16p<true, true>), dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st,
+                           nullptr, ckp, cvtp, att, d, T, Tv, H, L, layer, scale, wq, bq, x, lnw, lnb, ns);
+    else
+        hipLaunchKernelGGL((k_cross_attn_f16p<true, false>), dim3(H, ns), dim3(512), sizeof(float) * (size_t)Tv, st,
+                           nullptr, ckp, cvtp, att, d, T, Tv, H, L, layer, scale, wq, bq, x, lnw, lnb, ns);
 }
 
 // ---------------------------------------------------------------------------
@@ -1705,7 +1717,7 @@ __global__ void __launch_bounds__(256) k_kv_append16(const float *qkv, uint16_t 
 // EMB (layer 0): the row is first formed as the token embedding
 // f16(emb[tok]) + pemb[pos] (embed_tokens, decoder.rs:1323-1385, k_embed_ln's
 // arithmetic) and the head-0 block stores it to xo, the residual.
-template <bool LN, bool EMB>
+template <bool LN, bool EMB, bool SEQ>
 __global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restrict__ wqkv,
                                                         const float *__restrict__ bqkv, const float *__restrict__ x,
                                                         const float *__restrict__ lnw, const float *__restrict__ lnb,
@@ -1766,7 +1778,7 @@ __global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restri
     loadw(0, 0);
     loadw(1, 1);
     if (wave == 0) {
-        if constexpr (LN) fw_ln_quant_core<NV>(lv, lok, lw, lb, xl, D, 0, nullptr, nullptr, lane);
+        if constexpr (LN) fw_ln_quant_core<NV, SEQ>(lv, lok, lw, lb, xl, D, 0, nullptr, nullptr, lane);
         else {
 #pragma unroll
             for (int k = 0; k < NV; k++) ((float4 *)xl)[lane + k * 64] = lv[k];
@@ -1834,7 +1846,7 @@ __global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restri
 // EMB (layer 0): the residual row is the token embedding first (embed_tokens,
 // decoder.rs:1323-1385: x = f16(E[tok]) + P[pos], as k_embed_ln), which every
 // block forms for its stream and the head-0 block also stores as x.
-template <int NV, bool EMB>
+template <int NV, bool EMB, bool SEQ>
 __global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restrict__ wqkv, const float *__restrict__ sqkv,
                                                          const float *__restrict__ bqkv, float *x,
                                                          const float *__restrict__ lnw, const float *__restrict__ lnb,
@@ -1919,7 +1931,7 @@ __global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restric
             rbi[b][rr] = bqkv[brow(b) + rr];
         }
     const int pos = *posp;
-    if (wave == 0) fw_ln_quant_core<NV>(lv, lok, lw, lb, nullptr, d, 0, xql, &xsl, lane);
+    if (wave == 0) fw_ln_quant_core<NV, SEQ>(lv, lok, lw, lb, nullptr, d, 0, xql, &xsl, lane);
     __syncthreads();
     {
         // chunks past the row read as zero
@@ -2037,7 +2049,7 @@ __host__ __device__ __forceinline__ int ca_vstride(int Tq) { return Tq + ((16 - 
         FW_WAIT_LGKM0();                                                                           \
         asm volatile("s_barrier" ::: "memory");                                                    \
     } while (0)
-template <int NV>
+template <int NV, bool SEQ>
 __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restrict__ wq, const float *__restrict__ swq,
                                                          const float *__restrict__ bq, const float *__restrict__ x,
                                                          const float *__restrict__ lnw, const float *__restrict__ lnb,
@@ -2113,7 +2125,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
         for (int c = 0; c < 4; c++) kr[u][c] = kp[c];
         ksc[u] = Ks[jc];
     }
-    if (wave == 0) fw_ln_quant_core<NV>(lv, lok, lw, lb, nullptr, d, 0, xql, &xsl, lane);
+    if (wave == 0) fw_ln_quant_core<NV, SEQ>(lv, lok, lw, lb, nullptr, d, 0, xql, &xsl, lane);
     CA_SYNC();
     {
         // chunks past the row read as zero
@@ -2294,27 +2306,36 @@ __global__ void __launch_bounds__(64) k_quant_f16_rows_ld(const uint16_t *src, i
 // launch wrappers
 // Row kernels hold ceil(d/256) float4 groups per lane; d % 4 == 0 and
 // d <= 2048 are checked when the decoder is loaded.
-#define FW_ROWS_DISPATCH(KERNEL, d, ...)                                                           \
+#define FW_ROWS_DISPATCH1(KERNEL, SEQ, d, ...)                                                     \
     switch ((d + 255) / 256) {                                                                      \
-    case 1: hipLaunchKernelGGL(KERNEL<1>, __VA_ARGS__); break;                                      \
-    case 2: hipLaunchKernelGGL(KERNEL<2>, __VA_ARGS__); break;                                      \
-    case 3: hipLaunchKernelGGL(KERNEL<3>, __VA_ARGS__); break;                                      \
-    case 4: hipLaunchKernelGGL(KERNEL<4>, __VA_ARGS__); break;                                      \
-    case 5: hipLaunchKernelGGL(KERNEL<5>, __VA_ARGS__); break;                                      \
-    case 6: hipLaunchKernelGGL(KERNEL<6>, __VA_ARGS__); break;                                      \
-    case 7: hipLaunchKernelGGL(KERNEL<7>, __VA_ARGS__); break;                                      \
-    default: hipLaunchKernelGGL(KERNEL<8>, __VA_ARGS__); break;                                     \
+    case 1: hipLaunchKernelGGL((KERNEL<1, SEQ>), __VA_ARGS__); break;                               \
+    case 2: hipLaunchKernelGGL((KERNEL<2, SEQ>), __VA_ARGS__); break;                               \
+    case 3: hipLaunchKernelGGL((KERNEL<3, SEQ>), __VA_ARGS__); break;                               \
+    case 4: hipLaunchKernelGGL((KERNEL<4, SEQ>), __VA_ARGS__); break;                               \
+    case 5: hipLaunchKernelGGL((KERNEL<5, SEQ>), __VA_ARGS__); break;                               \
+    case 6: hipLaunchKernelGGL((KERNEL<6, SEQ>), __VA_ARGS__); break;                               \
+    case 7: hipLaunchKernelGGL((KERNEL<7, SEQ>), __VA_ARGS__); break;                               \
+    default: hipLaunchKernelGGL((KERNEL<8, SEQ>), __VA_ARGS__); break;                              \
     }
+// KERNEL<rows of d floats, SEQ = seq != 0>
+#define FW_ROWS_DISPATCH(KERNEL, seq, d, ...)                                                      \
+    do {                                                                                            \
+        if (seq) {                                                                                  \
+            FW_ROWS_DISPATCH1(KERNEL, true, d, __VA_ARGS__)                                         \
+        } else {                                                                                    \
+            FW_ROWS_DISPATCH1(KERNEL, false, d, __VA_ARGS__)                                        \
+        }                                                                                           \
+    } while (0)
 
 void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d, int rows,
-                        int8_t *xq, float *xs) {
-    FW_ROWS_DISPATCH(k_ln_quant, d, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, d, rows, xq, xs);
+                        int8_t *xq, float *xs, int seq) {
+    FW_ROWS_DISPATCH(k_ln_quant, seq, d, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, d, rows, xq, xs);
 }
 
 void fw_launch_embed_ln(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,
                         float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs,
-                        int rps) {
-    FW_ROWS_DISPATCH(k_embed_ln, d, dim3(ns), dim3(64), 0, st, tok, posp, emb, pemb, x, d, w, b, ln_y, xq, xs,
+                        int rps, int seq) {
+    FW_ROWS_DISPATCH(k_embed_ln, seq, d, dim3(ns), dim3(64), 0, st, tok, posp, emb, pemb, x, d, w, b, ln_y, xq, xs,
                      rps > 0 ? rps : ns);
 }
 
@@ -2449,17 +2470,17 @@ bool fw_self_attn_f16q_ok(int d, int H) { return d == XQ_D && H * 64 == d; }
 void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
                               const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
                               const int *posp, int H, int nctx, int L, int layer, int ns, float scale,
-                              const int32_t *tok, const uint16_t *emb, const float *pemb, float *xo) {
+                              const int32_t *tok, const uint16_t *emb, const float *pemb, float *xo, int lnseq) {
     size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
-    if (tok)
-        hipLaunchKernelGGL((k_self_attn_f16q<true, true>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb,
-                           kc, vc, att, posp, nctx, L, layer, scale, tok, emb, pemb, xo);
-    else if (lnw)
-        hipLaunchKernelGGL((k_self_attn_f16q<true, false>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb,
-                           kc, vc, att, posp, nctx, L, layer, scale, nullptr, nullptr, nullptr, nullptr);
-    else
-        hipLaunchKernelGGL((k_self_attn_f16q<false, false>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw,
-                           lnb, kc, vc, att, posp, nctx, L, layer, scale, nullptr, nullptr, nullptr, nullptr);
+#define SAQ(LN_, EMB_, SEQ_, ...)                                                                                     \
+    hipLaunchKernelGGL((k_self_attn_f16q<LN_, EMB_, SEQ_>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb, \
+                       kc, vc, att, posp, nctx, L, layer, scale, __VA_ARGS__)
+    if (tok && lnseq) SAQ(true, true, true, tok, emb, pemb, xo);
+    else if (tok) SAQ(true, true, false, tok, emb, pemb, xo);
+    else if (lnw && lnseq) SAQ(true, false, true, nullptr, nullptr, nullptr, nullptr);
+    else if (lnw) SAQ(true, false, false, nullptr, nullptr, nullptr, nullptr);
+    else SAQ(false, false, false, nullptr, nullptr, nullptr, nullptr);
+#undef SAQ
 }
 
 template <int NV>
@@ -2471,8 +2492,11 @@ static void launch_self_attn_fused(hipStream_t st, bool embed, dim3 grid, size_t
                                    const float *sqkv, const float *bqkv, float *x, const float *lnw,
                                    const float *lnb, uint16_t *kc, uint16_t *vc, float *att, const int *posp, int d,
                                    int nctx, int L, int layer, float scale, float *pmax, const int32_t *tok,
-                                   const uint16_t *emb, const float *pemb) {
-    const k_self_attn_fused_e<NV> k = embed ? k_self_attn_fused<NV, true> : k_self_attn_fused<NV, false>;
+                                   const uint16_t *emb, const float *pemb, int lnseq) {
+    const k_self_attn_fused_e<NV> k = embed ? (lnseq ? k_self_attn_fused<NV, true, true>
+                                                     : k_self_attn_fused<NV, true, false>)
+                                            : (lnseq ? k_self_attn_fused<NV, false, true>
+                                                     : k_self_attn_fused<NV, false, false>);
     hipLaunchKernelGGL(k, grid, dim3(512), shm, st, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,
                        layer, scale, pmax, tok, emb, pemb);
 }
@@ -2480,7 +2504,7 @@ static void launch_self_attn_fused(hipStream_t st, bool embed, dim3 grid, size_t
 void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *sqkv, const float *bqkv, float *x,
                                const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
                                const int *posp, int d, int H, int nctx, int L, int layer, int ns, float scale,
-                               float *pmax, const int32_t *tok, const uint16_t *emb, const float *pemb) {
+                               float *pmax, const int32_t *tok, const uint16_t *emb, const float *pemb, int lnseq) {
     size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
     const bool e = emb != nullptr;
     const dim3 grid(H, ns);
@@ -2488,7 +2512,7 @@ void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *
 #define SAF(NV)                                                                                                      \
     case NV:                                                                                                         \
         launch_self_attn_fused<NV>(st, e, grid, shm, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,    \
-                                   layer, scale, pmax, tok, emb, pemb);                                               \
+                                   layer, scale, pmax, tok, emb, pemb, lnseq);                                        \
         break;
         SAF(1)
         SAF(2)
@@ -2498,7 +2522,7 @@ void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *
         SAF(6)
         SAF(7)
     default: launch_self_attn_fused<8>(st, e, grid, shm, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,
-                                       layer, scale, pmax, tok, emb, pemb);
+                                       layer, scale, pmax, tok, emb, pemb, lnseq);
         break;
 #undef SAF
     }
@@ -2507,11 +2531,11 @@ void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *
 void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,
                                const float *lnw, const float *lnb, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
-                               float scale, float *pmax) {
+                               float scale, float *pmax, int lnseq) {
     if (64 * ca_vstride(Tq) > 7 * CA_VKB * 1024) return; // refused where the decoder is loaded (T <= 1536)
     size_t shm = (size_t)64 * ca_vstride(Tq) + sizeof(float) * ((T + 3) & ~3) + Tq;
-    FW_ROWS_DISPATCH(k_cross_attn_i8v2, d, dim3(H, ns), dim3(512), shm, st, wq, swq, bq, x, lnw, lnb, ck, cks, cvt,
-                     cvs, att, d, T, Tq, H, L, layer, scale, pmax);
+    FW_ROWS_DISPATCH(k_cross_attn_i8v2, lnseq, d, dim3(H, ns), dim3(512), shm, st, wq, swq, bq, x, lnw, lnb, ck, cks,
+                     cvt, cvs, att, d, T, Tq, H, L, layer, scale, pmax);
 }
 
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq) {

@@ -28,26 +28,103 @@ __device__ __forceinline__ void fw_ln_load_wb(const bool (&ok)[NV], const float 
     }
 }
 
-// The same with the weight and bias groups already loaded (or in flight).
-template <int NV>
-__device__ __forceinline__ void fw_ln_quant_core(float4 (&xv)[NV], const bool (&ok)[NV], const float4 (&wv)[NV],
-                                                 const float4 (&bv)[NV], float *y, int d, int r, int8_t *xq,
-                                                 float *xs, int lane) {
+// The reference's sequential f64 loops over a row held as above (element
+// 4 (l + 64 k) + j in lane l, component j of xv[k]; d = 4 n4), formed by
+// every lane from the lanes' values read one by one in index order:
+// SQ = false: sum of (f64)x; SQ = true: sum of ((f64)x - mean)^2
+// (nn.rs:4425-4438).  Uniform; every lane of the wave must call it.
+template <int NV, bool SQ>
+__device__ __forceinline__ double fw_row_seq_sum(const float4 (&xv)[NV], int n4, double mean) {
     double s = 0.0;
 #pragma unroll
-    for (int k = 0; k < NV; k++)
-        if (ok[k]) s += ((double)xv[k].x + (double)xv[k].y) + ((double)xv[k].z + (double)xv[k].w);
-    const double mean = fw_dpp_wave_sum_f64(s) / (double)d;
-    double v = 0.0;
+    for (int k = 0; k < NV; k++) {
+        const int nl = n4 - 64 * k < 64 ? n4 - 64 * k : 64; // lanes holding group k
+        for (int l = 0; l < nl; l++) {
+            const float v[4] = {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv[k].x), l)),
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv[k].y), l)),
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv[k].z), l)),
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv[k].w), l))};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (SQ) {
+                    const double t = (double)v[j] - mean;
+                    s = s + t * t;
+                } else {
+                    s = s + (double)v[j];
+                }
+            }
+        }
+    }
+    return s;
+}
+
+// Whether every partial sum of the row's (f64)x, in any order, is exact:
+// each value is a multiple of g = 2^(emin - 150) (emin the smallest biased
+// exponent of a nonzero value, 1 for subnormals) and every partial sum is
+// below d * 2^(emax - 126) in magnitude, so all of them are integers times g
+// below 2^53 g when emax - emin <= 29 - ceil(log2 d).  Then the wave's tree
+// sum equals the sequential one bit for bit.  Non-finite values say no.
+template <int NV>
+__device__ __forceinline__ bool fw_row_sum_exact(const float4 (&xv)[NV], const bool (&ok)[NV], int d) {
+    float emx = 0.0f, nmn = -255.0f; // max exponent, -(min exponent)
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         if (ok[k]) {
-            const double a = (double)xv[k].x - mean, bb = (double)xv[k].y - mean;
-            const double c = (double)xv[k].z - mean, e = (double)xv[k].w - mean;
-            v += (a * a + bb * bb) + (c * c + e * e);
+            const uint32_t u[4] = {__float_as_uint(xv[k].x), __float_as_uint(xv[k].y), __float_as_uint(xv[k].z),
+                                   __float_as_uint(xv[k].w)};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t a = u[j] & 0x7fffffffu;
+                if (a) {
+                    const uint32_t e = (a >> 23) > 1u ? (a >> 23) : 1u;
+                    emx = fmaxf(emx, (float)e);
+                    nmn = fmaxf(nmn, -(float)e);
+                }
+            }
         }
     }
-    const double var = fw_dpp_wave_sum_f64(v) / (double)d;
+    emx = fw_dpp_wave_max(emx);
+    nmn = fw_dpp_wave_max(nmn);
+    if (emx == 0.0f) return true; // every value is zero
+    const int lg = 32 - __builtin_clz((unsigned)(d > 1 ? d - 1 : 1)); // ceil(log2 d)
+    return emx < 255.0f && (int)emx + (int)nmn <= 29 - lg;
+}
+
+// The same with the weight and bias groups already loaded (or in flight).
+// SEQ: the mean and variance sums are the reference's sequential f64 loops
+// (bit for bit, whatever the row); else the mean is the wave's tree sum (the
+// same bits whenever fw_row_sum_exact holds) and the variance the tree sum
+// of per-lane partials, which can differ from the sequential sum in its last
+// bits.
+template <int NV, bool SEQ = false>
+__device__ __forceinline__ void fw_ln_quant_core(float4 (&xv)[NV], const bool (&ok)[NV], const float4 (&wv)[NV],
+                                                 const float4 (&bv)[NV], float *y, int d, int r, int8_t *xq,
+                                                 float *xs, int lane) {
+    double mean;
+    if (SEQ && !fw_row_sum_exact<NV>(xv, ok, d)) {
+        mean = fw_row_seq_sum<NV, false>(xv, d >> 2, 0.0) / (double)d;
+    } else {
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < NV; k++)
+            if (ok[k]) s += ((double)xv[k].x + (double)xv[k].y) + ((double)xv[k].z + (double)xv[k].w);
+        mean = fw_dpp_wave_sum_f64(s) / (double)d;
+    }
+    double var;
+    if constexpr (SEQ) {
+        var = fw_row_seq_sum<NV, true>(xv, d >> 2, mean) / (double)d;
+    } else {
+        double v = 0.0;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            if (ok[k]) {
+                const double a = (double)xv[k].x - mean, bb = (double)xv[k].y - mean;
+                const double c = (double)xv[k].z - mean, e = (double)xv[k].w - mean;
+                v += (a * a + bb * bb) + (c * c + e * e);
+            }
+        }
+        var = fw_dpp_wave_sum_f64(v) / (double)d;
+    }
     const double inv = 1.0 / sqrt(var + (double)1e-5f);
     float m = 0.0f;
 #pragma unroll
@@ -81,12 +158,12 @@ __device__ __forceinline__ void fw_ln_quant_core(float4 (&xv)[NV], const bool (&
     if (lane == 0) xs[r] = sc;
 }
 
-template <int NV>
+template <int NV, bool SEQ = false>
 __device__ __forceinline__ void fw_ln_quant_vals(float4 (&xv)[NV], const bool (&ok)[NV], float *y, const float *w,
                                                  const float *b, int d, int r, int8_t *xq, float *xs, int lane) {
     float4 wv[NV], bv[NV];
     fw_ln_load_wb<NV>(ok, w, b, wv, bv, lane);
-    fw_ln_quant_core<NV>(xv, ok, wv, bv, y, d, r, xq, xs, lane);
+    fw_ln_quant_core<NV, SEQ>(xv, ok, wv, bv, y, d, r, xq, xs, lane);
 }
 
 

@@ -19,7 +19,7 @@ void fw_launch_pack_gemv_f16(hipStream_t st, const uint16_t *W, uint16_t *Wf, in
 // (k_ln_quant's arithmetic), so the GEMV consumes LN(x).
 void fw_launch_gemv_f16f(hipStream_t st, const uint16_t *Wf, const float *bias, const float *x, float *y, int N,
                          int K, int ns, int ldy, int mode, const float *gelu_tab, const float *lnw = nullptr,
-                         const float *lnb = nullptr);
+                         const float *lnb = nullptr, int lnseq = 0);
 // The f16 GEMV for a cohort in slot order (dec_gemv16.hip): weights packed
 // once by fw_launch_pack_gemv16 (needs fw_gemv16_ok(N, K)); bit-identical to
 // fw_launch_gemv_f16.  keys (logits head): per-tile argmax keys
@@ -31,7 +31,8 @@ void fw_launch_pack_gemv16(hipStream_t st, const uint16_t *W, uint16_t *Wp, int 
 void fw_launch_gemv16(hipStream_t st, const uint16_t *Wp, const float *bias, const float *x, float *y, int N, int K,
                       int ns, int ldy, int mode, const float *gelu_tab, const float *lnw = nullptr,
                       const float *lnb = nullptr, const fwhip_filter *filt = nullptr, const int *initialp = nullptr,
-                      unsigned long long *keys = nullptr, int r = 0, int sb_cap = 0, int grid_cap = 0);
+                      unsigned long long *keys = nullptr, int r = 0, int sb_cap = 0, int grid_cap = 0,
+                      int lnseq = 0);
 void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,
                               float *att, int d, int T, int H, int L, int layer, int ns, float scale);
 // The f16 arm's cross attention on slot-order K / V^T copies (dec_fast.hip):
@@ -59,7 +60,7 @@ void fw_launch_cross_attn_f16p_split(hipStream_t st, const float *qc, const uint
 void fw_launch_cross_attn_f16pq_split(hipStream_t st, const uint16_t *wq, const float *bq, const float *x,
                                       const float *lnw, const float *lnb, const uint16_t *ckp, const uint16_t *cvtp,
                                       float *att, int d, int T, int H, int L, int layer, int ns, float scale,
-                                      float *scratch);
+                                      float *scratch, int lnseq = 0);
 // fw_launch_cross_attn_f16p with the cross LayerNorm of x [ns, d] and the q
 // projection inside (wq in fw_launch_pack_gemv16's slot order at 16 lanes per
 // row, bq the bias); needs fw_cross_f16pq_ok(d, T, H)
@@ -73,17 +74,20 @@ void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float 
                               const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
                               const int *posp, int H, int nctx, int L, int layer, int ns, float scale,
                               const int32_t *tok = nullptr, const uint16_t *emb = nullptr,
-                              const float *pemb = nullptr, float *xo = nullptr);
+                              const float *pemb = nullptr, float *xo = nullptr, int lnseq = 0);
 bool fw_cross_f16pq_ok(int d, int T, int H);
 void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float *bq, const float *x, const float *lnw,
                                 const float *lnb, const uint16_t *ckp, const uint16_t *cvtp, float *att, int d, int T,
-                                int H, int L, int layer, int ns, float scale);
+                                int H, int L, int layer, int ns, float scale, int lnseq = 0);
 void fw_launch_gemm_strict(hipStream_t st, const float *A, const uint16_t *B, int m, int n, int k, int epi,
                            float *C, const float *bias, float scale, uint16_t *out16, int T, int H, int L,
                            int layer, int ldc = 0, const float *gelu_tab = nullptr, const float *pos = nullptr);
 void fw_launch_quant_f16_rows(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n);
 void fw_launch_step_bookkeeping(hipStream_t st, int *posp, int *initialp, const int32_t *tok, int32_t *hist,
                                 int hist_stride, int step, int ns);
+
+// lnseq (the kernels with a LayerNorm inside): nonzero sums the LayerNorm's
+// mean and variance in the reference's sequential f64 order (exact mode)
 
 // the window decode loop (dec_window.hip): process_logits in full + argmax +
 // the loop's state per stream, and the post-loop log-probabilities
@@ -107,6 +111,8 @@ struct FwWinStream {
 #ifndef WIN_NB
 #define WIN_NB 16
 #endif
+// the last block merges the slots one per lane of a 64-wide wave
+static_assert(WIN_NB >= 1 && WIN_NB <= 64, "WIN_NB must be in 1..64");
 struct FwWinPart {
     unsigned long long ka, kt;  // argmax keys: every lane, the timestamp lanes
     float mall, mtxt, mts, sb;  // maxima (all, text, timestamp lanes); sum of expf(u - mall) over the block's lanes
@@ -120,13 +126,15 @@ void fw_launch_win_plogs(hipStream_t st, const float *rows, const float *nsrow, 
                          float *plogs, float *nslp, int ns);
 
 // int8 decoder arm (dec_fast.hip)
+// seq: the LayerNorm's mean and variance are the reference's sequential f64
+// sums (bit for bit on every row; exact mode), else the wave's tree sums
 void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d, int rows,
-                        int8_t *xq, float *xs);
+                        int8_t *xq, float *xs, int seq = 0);
 // rps > 0: row s sits at position *posp + s / rps (a prefill chunk of rps
 // streams); else every row at *posp
 void fw_launch_embed_ln(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,
                         float *x, int d, int ns, const float *w, const float *b, float *ln_y, int8_t *xq, float *xs,
-                        int rps = 0);
+                        int rps = 0, int seq = 0);
 int fw_gemv_i8m_blocks(int N);
 // W of fw_launch_gemv_i8m is stored as MFMA operand fragments: bytes needed
 // for an [N, K] matrix (K % 64 == 0), and the repacking of a row-major one
@@ -162,13 +170,13 @@ void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *
                                const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
                                const int *posp, int d, int H, int nctx, int L, int layer, int ns, float scale,
                                float *pmax, const int32_t *tok = nullptr, const uint16_t *emb = nullptr,
-                               const float *pemb = nullptr);
+                               const float *pemb = nullptr, int lnseq = 0);
 // q = Wq LN(x): the cross LayerNorm (lnw, lnb) of the residual rows x and the
 // int8 cross q projection [d, d] (row scales swq, bias bq) run in the kernel
 void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,
                                const float *lnw, const float *lnb, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
-                               float scale, float *pmax = nullptr);
+                               float scale, float *pmax = nullptr, int lnseq = 0);
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq);
 int fw_logits_keys_blocks(int V);
 void fw_launch_logits_keys(hipStream_t st, const float *logits, int V, int ns, const fwhip_filter *filt,

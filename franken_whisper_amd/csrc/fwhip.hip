@@ -242,7 +242,9 @@ struct fwhip_decoder {
     // matching bias [L][0 | cv_b] (one f16-pair GEMM makes every layer's cross K/V)
     const uint16_t *ckv16 = nullptr;
     const float *ckv_b = nullptr;
-    int exact = 0; // 1: strict sequential-k cross K/V precompute
+    // 1: strict sequential-k cross K/V precompute, and every LayerNorm's mean
+    // and variance summed in the reference's sequential order
+    int exact = 0;
     std::vector<DecLayerDev> layers;
     std::vector<void *> owned;
 };
@@ -269,6 +271,7 @@ struct fwhip_dstate {
     // captured sampling step (forward of st->tok + argmax + bookkeeping)
     hipGraphExec_t graph = nullptr;
     fwhip_filter graph_filter;
+    int graph_lnseq = 0, wgraph_lnseq = 0; // the decoder's exact flag when each graph was captured
     std::vector<void *> owned;
     // the window loop (fwhip_decode_window): filtered rows of every step, the
     // raw prefill rows, per-stream loop state, forced flags, exact-sum scratch,
@@ -376,15 +379,17 @@ static void fw_gemv16(hipStream_t st, const uint16_t *W, const float *bias, cons
 }
 // y = W LayerNorm(x) (+ bias): the LayerNorm inside the GEMV where its kernel
 // stages whole rows (K <= 1280), else a LayerNorm pass into h.
+// seq: the LayerNorm's sums in the reference's sequential order (exact mode).
 static void fw_gemv16_ln(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *h,
                          const float *lnw, const float *lnb, float *y, int N, int K, int ns, int ldy, int mode,
-                         const float *gelu_tab) {
+                         const float *gelu_tab, int seq = 0) {
     if (fw_gemv16_ok(N, K) && K <= 1280) {
-        fw_launch_gemv16(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb);
+        fw_launch_gemv16(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb, nullptr, nullptr, nullptr, 0, 0,
+                         0, seq);
     } else if (fw_gemv_f16_frag_ok(N, K) && K <= 1280) {
-        fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb);
+        fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb, seq);
     } else {
-        fw_launch_ln_quant(st, x, h, lnw, lnb, K, ns, nullptr, nullptr);
+        fw_launch_ln_quant(st, x, h, lnw, lnb, K, ns, nullptr, nullptr, seq);
         fw_gemv16(st, W, bias, h, y, N, K, ns, ldy, mode, gelu_tab);
     }
 }
@@ -744,6 +749,8 @@ static bool gemv_blk_all(fwhip_dstate *st, hipStream_t s, const int8_t *W, const
 // over the filtered logits (filt may be NULL: raw argmax) are produced too.
 // `timed` brackets the logits GEMV with events (never inside a graph capture).
 static void dec_logits_f16(fwhip_dstate *st, const float *x, float *h, const fwhip_filter *filt, bool timed);
+// Exact mode (dd->exact): every LayerNorm, wherever it is fused, sums its
+// statistics in the reference's sequential order (the kernels' lnseq).
 static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool prefill, bool want_logits,
                                     const fwhip_filter *filt, bool timed) {
     fwhip_decoder *dd = st->dec;
@@ -753,6 +760,7 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
     bool i8 = dd->arm == FWHIP_DEC_INT8;
     float scale = powf(64.0f, -0.25f);
     const float *gt = c->gelu_tab;
+    const int sq = dd->exact;
     // The f16 arm's projections fold into the attention kernels when the
     // cohort's (head, stream) blocks fill one round of the CUs: with fewer
     // streams a head's rows would be multiplied on that many CUs only (one
@@ -765,7 +773,7 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
     // arm's folded self-attention, form both inside layer 0's kernel)
     if (!i8 && !sa_fold)
         fw_launch_embed_ln(s, tok, st->pos, dd->emb16, dd->pos_emb, st->x, d, S, dd->layers[0].attn_ln_w,
-                           dd->layers[0].attn_ln_b, st->h, nullptr, nullptr);
+                           dd->layers[0].attn_ln_b, st->h, nullptr, nullptr, 0, sq);
     for (int li = 0; li < L; li++) {
         const DecLayerDev &l = dd->layers[li];
         if (i8) {
@@ -777,16 +785,16 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             fw_launch_self_attn_fused(s, l.qkv8, l.qkv8s, l.qkv_b, st->x, l.attn_ln_w, l.attn_ln_b, st->kv_k,
                                       st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale, st->pmax,
                                       li == 0 ? tok : nullptr, li == 0 ? dd->emb16 : nullptr,
-                                      li == 0 ? dd->pos_emb : nullptr);
+                                      li == 0 ? dd->pos_emb : nullptr, sq);
             gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr, st->att);
             // the cross LayerNorm and q projection run inside the cross-attention kernel
             fw_launch_cross_attn_i8v2(s, l.cq8, l.cq8s, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck8, st->ck8s,
-                                      st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li, S, scale, st->pmax);
+                                      st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li, S, scale, st->pmax, sq);
             gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr, st->att);
             // mode 4: GELU written block-interleaved for the block GEMV; prefill
             // rows take the f16 mlp_2 (the block-int8 arm has no batch form),
             // which reads natural order
-            fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs);
+            fw_launch_ln_quant(s, st->x, nullptr, l.mlp_ln_w, l.mlp_ln_b, d, S, st->xq, st->xs, sq);
             gemv_i8_all(st, s, l.fc1_8, l.fc1_8s, l.fc1_b, st->ff, dff, d, dff, prefill ? 2 : 4, nullptr);
             if (prefill) fw_gemv16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
             else if (!gemv_blk_all(st, s, l.fc2_b8, l.fc2_b8s, l.fc2_b, st->ff, st->x, d, dff, d))
@@ -797,16 +805,17 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 // (layer 0: the embedding too)
                 if (li > 0)
                     fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, st->x, l.attn_ln_w, l.attn_ln_b, st->kv_k,
-                                             st->kv_v, st->att, st->pos, H, dd->nctx, L, li, S, scale);
+                                             st->kv_v, st->att, st->pos, H, dd->nctx, L, li, S, scale, nullptr,
+                                             nullptr, nullptr, nullptr, sq);
                 else
                     fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, nullptr, l.attn_ln_w, l.attn_ln_b, st->kv_k,
                                              st->kv_v, st->att, st->pos, H, dd->nctx, L, li, S, scale, tok,
-                                             dd->emb16, dd->pos_emb, st->x);
+                                             dd->emb16, dd->pos_emb, st->x, sq);
             } else {
                 // (layer 0's attention LayerNorm ran with the embedding, into h)
                 if (li > 0)
                     fw_gemv16_ln(s, l.qkv16, l.qkv_b, st->x, st->h, l.attn_ln_w, l.attn_ln_b, st->qkv, 3 * d, d, S,
-                                 3 * d, 0, gt);
+                                 3 * d, 0, gt, sq);
                 else
                     fw_gemv16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
                 fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S,
@@ -816,7 +825,7 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             if (fold && st->ck16p && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) && fw_gemv16_lpr(d, d) == 16) {
                 // the cross LayerNorm and q projection run inside the cross-attention kernel
                 fw_launch_cross_attn_f16pq(s, l.cq16, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck16p,
-                                           st->cvt16p, st->att, d, T, H, L, li, S, scale);
+                                           st->cvt16p, st->att, d, T, H, L, li, S, scale, sq);
             } else {
                 // a cohort whose (head, stream) blocks fill under half the CUs
                 // (one stream: 20 blocks for 1,500 keys) or need more than one
@@ -828,10 +837,10 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 if (xsplit && hs * 2 <= c->n_cu && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) &&
                     fw_gemv16_lpr(d, d) == 16) {
                     fw_launch_cross_attn_f16pq_split(s, l.cq16, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck16p,
-                                                     st->cvt16p, st->att, d, T, H, L, li, S, scale, st->xsplit);
+                                                     st->cvt16p, st->att, d, T, H, L, li, S, scale, st->xsplit, sq);
                 } else {
                     fw_gemv16_ln(s, l.cq16, l.cq_b, st->x, st->h, l.cross_ln_w, l.cross_ln_b, st->y, d, d, S, d, 0,
-                                 gt);
+                                 gt, sq);
                     if (xsplit)
                         fw_launch_cross_attn_f16p_split(s, st->y, st->ck16p, st->cvt16p, st->att, d, T, H, L, li, S,
                                                         scale, st->xsplit);
@@ -841,7 +850,8 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 }
             }
             fw_gemv16(s, l.co16, l.co_b, st->att, st->x, d, d, S, d, 1, gt);
-            fw_gemv16_ln(s, l.fc1_16, l.fc1_b, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, st->ff, dff, d, S, dff, 2, gt);
+            fw_gemv16_ln(s, l.fc1_16, l.fc1_b, st->x, st->h, l.mlp_ln_w, l.mlp_ln_b, st->ff, dff, d, S, dff, 2, gt,
+                         sq);
             fw_gemv16(s, l.fc2_16, l.fc2_b, st->ff, st->x, d, dff, S, d, 1, gt);
         }
     }
@@ -849,7 +859,7 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
         fw_event_pair ev;
         ev.active = false;
         if (i8) {
-            fw_launch_ln_quant(s, st->x, nullptr, dd->ln_w, dd->ln_b, d, S, st->xq, st->xs);
+            fw_launch_ln_quant(s, st->x, nullptr, dd->ln_w, dd->ln_b, d, S, st->xq, st->xs, sq);
             if (timed) fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d, &ev);
             gemv_i8_all(st, s, dd->emb8, dd->emb8s, nullptr, st->logits, dd->V, d, dd->V, 3, filt);
             if (timed) fw_timed_end(c, &ev);
@@ -874,10 +884,11 @@ static void dec_logits_f16(fwhip_dstate *st, const float *x, float *h, const fwh
     if (f16_fused_keys(dd)) {
         // final LayerNorm, tied f16 logits head and per-tile argmax keys in one kernel
         fw_launch_gemv16(s, dd->emb16f, nullptr, x, st->logits, dd->V, d, S, dd->V, 0, gt, dd->ln_w, dd->ln_b, filt,
-                         st->initial, st->keys);
+                         st->initial, st->keys, 0, 0, 0, dd->exact);
         if (timed) fw_timed_end(c, &ev);
     } else {
-        fw_gemv16_ln(s, dd->emb16f, nullptr, x, h, dd->ln_w, dd->ln_b, st->logits, dd->V, d, S, dd->V, 0, gt);
+        fw_gemv16_ln(s, dd->emb16f, nullptr, x, h, dd->ln_w, dd->ln_b, st->logits, dd->V, d, S, dd->V, 0, gt,
+                     dd->exact);
         if (timed) fw_timed_end(c, &ev);
         fw_launch_logits_keys(s, st->logits, dd->V, S, filt, st->initial, st->keys);
     }
@@ -923,20 +934,22 @@ static fwhip_status dec_forward_chunk(fwhip_dstate *st, const int32_t *tok, int 
     const float scale = powf(64.0f, -0.25f);
     const float *gt = c->gelu_tab;
     float *x = st->pf_x, *h = st->pf_h, *qkv = st->pf_qkv, *att = st->pf_att, *y = st->pf_y, *ff = st->pf_ff;
+    const int sq = dd->exact;
     fw_launch_embed_ln(s, tok, st->pos, dd->emb16, dd->pos_emb, x, d, R, dd->layers[0].attn_ln_w,
-                       dd->layers[0].attn_ln_b, h, nullptr, nullptr, S);
+                       dd->layers[0].attn_ln_b, h, nullptr, nullptr, S, sq);
     for (int li = 0; li < L; li++) {
         const DecLayerDev &l = dd->layers[li];
-        if (li > 0) fw_gemv16_ln(s, l.qkv16, l.qkv_b, x, h, l.attn_ln_w, l.attn_ln_b, qkv, 3 * d, d, R, 3 * d, 0, gt);
+        if (li > 0)
+            fw_gemv16_ln(s, l.qkv16, l.qkv_b, x, h, l.attn_ln_w, l.attn_ln_b, qkv, 3 * d, d, R, 3 * d, 0, gt, sq);
         else fw_gemv16(s, l.qkv16, l.qkv_b, h, qkv, 3 * d, d, R, 3 * d, 0, gt);
         fw_launch_kv_append16(s, qkv, st->kv_k, st->kv_v, st->pos, d, dd->nctx, L, li, S, R);
         fw_launch_self_attn2(s, qkv, st->kv_k, st->kv_v, att, st->pos, d, H, dd->nctx, L, li, S, scale, nullptr, R,
                              0);
         fw_gemv16(s, l.o16, l.o_b, att, x, d, d, R, d, 1, gt);
-        fw_gemv16_ln(s, l.cq16, l.cq_b, x, h, l.cross_ln_w, l.cross_ln_b, y, d, d, R, d, 0, gt);
+        fw_gemv16_ln(s, l.cq16, l.cq_b, x, h, l.cross_ln_w, l.cross_ln_b, y, d, d, R, d, 0, gt, sq);
         fw_launch_cross_attn_f16p(s, y, st->ck16p, st->cvt16p, att, d, T, H, L, li, S, scale, R);
         fw_gemv16(s, l.co16, l.co_b, att, x, d, d, R, d, 1, gt);
-        fw_gemv16_ln(s, l.fc1_16, l.fc1_b, x, h, l.mlp_ln_w, l.mlp_ln_b, ff, dff, d, R, dff, 2, gt);
+        fw_gemv16_ln(s, l.fc1_16, l.fc1_b, x, h, l.mlp_ln_w, l.mlp_ln_b, ff, dff, d, R, dff, 2, gt, sq);
         fw_gemv16(s, l.fc2_16, l.fc2_b, ff, x, d, dff, R, d, 1, gt);
     }
     // the last position's rows of every stream
@@ -1071,7 +1084,8 @@ static bool capture_step(fwhip_dstate *st, const fwhip_filter *filt) {
     return ok;
 }
 static bool capture_step_impl(fwhip_dstate *st, const fwhip_filter *filt) {
-    if (st->graph && !memcmp(&st->graph_filter, filt, sizeof *filt)) return true;
+    if (st->graph && !memcmp(&st->graph_filter, filt, sizeof *filt) && st->graph_lnseq == st->dec->exact)
+        return true;
     if (st->graph) {
         hipGraphExecDestroy(st->graph);
         st->graph = nullptr;
@@ -1093,6 +1107,7 @@ static bool capture_step_impl(fwhip_dstate *st, const fwhip_filter *filt) {
     }
     st->graph = ge;
     st->graph_filter = *filt;
+    st->graph_lnseq = st->dec->exact;
     return true;
 }
 
@@ -1110,7 +1125,9 @@ static double dec_step_bytes(const fwhip_dstate *st, int tk) {
             V * d + 4 * V;
         cross = L * (2 * T * d + 4 * H * T + 4 * d);
     } else {
-        w = 2.0 * (L * 12 * d * d + V * d);
+        // per layer: self q/k/v (3 d^2), o, cross q, cross o (3 d^2), fc1 and
+        // fc2 (8 d^2), f16; the tied head V x d
+        w = 2.0 * (L * 14 * d * d + V * d);
         cross = L * 2 * T * d * 2;
     }
     const double kv = L * 2 * ((double)tk + 1) * d * 2;
@@ -1251,7 +1268,7 @@ static bool win_capture(fwhip_dstate *st, const FwWinCfg &cfg) {
     static int disabled = -1;
     if (disabled < 0) disabled = getenv("FWHIP_NO_GRAPH") != nullptr || profiler_preloaded();
     if (disabled) return false;
-    if (st->wgraph && !memcmp(&st->wgraph_cfg, &cfg, sizeof cfg)) return true;
+    if (st->wgraph && !memcmp(&st->wgraph_cfg, &cfg, sizeof cfg) && st->wgraph_lnseq == st->dec->exact) return true;
     if (st->wgraph) {
         hipGraphExecDestroy(st->wgraph);
         st->wgraph = nullptr;
@@ -1273,6 +1290,7 @@ static bool win_capture(fwhip_dstate *st, const FwWinCfg &cfg) {
     }
     st->wgraph = ge;
     st->wgraph_cfg = cfg;
+    st->wgraph_lnseq = st->dec->exact;
     return true;
 }
 
@@ -1422,5 +1440,24 @@ extern "C" fwhip_status fwhip_argmax_logits(fwhip_ctx *c, const float *logits_de
     HIP_TRY(hipMemcpyAsync(argmax_host, tok, sizeof(int32_t) * n_rows, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     HIP_TRY(hipGetLastError());
+    return FWHIP_OK;
+}
+
+// layer_norm (nn.rs:4351-4545) of n_rows rows of d f32 on the device, with the
+// decoder's one-wave-per-row kernel: exact = 1 sums the mean and variance in
+// the reference's sequential order, exact = 0 in the wave's tree order.
+extern "C" fwhip_status fwhip_layer_norm(fwhip_ctx *c, const float *x_dev, const float *w_dev, const float *b_dev,
+                                         int64_t n_rows, int32_t d, float *y_dev, int32_t exact) {
+    if (!c || !x_dev || !w_dev || !b_dev || !y_dev) return fw_fail(FWHIP_ERR_INVALID, "fwhip_layer_norm: NULL argument");
+    if (d <= 0 || d % 4 != 0 || d > 2048 || n_rows <= 0 || n_rows > (int64_t)4 * 65535 * 1024)
+        return fw_fail(FWHIP_ERR_INVALID, "fwhip_layer_norm: need d % 4 == 0, 0 < d <= 2048, 0 < n_rows <= 268M");
+    HIP_TRY(hipSetDevice(c->device));
+    for (int64_t r0 = 0; r0 < n_rows; r0 += (int64_t)4 * 65535) {
+        const int n = (int)(n_rows - r0 < (int64_t)4 * 65535 ? n_rows - r0 : (int64_t)4 * 65535);
+        fw_launch_ln_quant(c->stream, x_dev + r0 * d, y_dev + r0 * d, w_dev, b_dev, d, n, nullptr, nullptr,
+                           exact ? 1 : 0);
+    }
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipStreamSynchronize(c->stream));
     return FWHIP_OK;
 }

@@ -69,6 +69,7 @@ SIGNATURES = {
     "fwhip_transcript_window": (C.c_int32, [_vp, C.c_int32, C.POINTER(abi.WindowInfo)]),
     "fwhip_transcript_free": (None, [_vp]),
     "fwhip_argmax_logits": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.POINTER(abi.Filter), C.c_int32, _i32p]),
+    "fwhip_layer_norm": (C.c_int32, [_vp, _vp, _vp, _vp, C.c_int64, C.c_int32, _vp, C.c_int32]),
     "fwhip_mel_frames": (C.c_int64, [C.c_int64]),
     "fwhip_log_mel": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
     "fwhip_log_mel_noalloc": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
@@ -194,6 +195,14 @@ class Context:
                                         C.byref(filt) if filt is not None else None, 1 if initial else 0,
                                         out.ctypes.data_as(_i32p)))
         return out
+
+    def layer_norm(self, x_dev: DeviceArray, w_dev: DeviceArray, b_dev: DeviceArray, y_dev: DeviceArray,
+                   exact: bool):
+        """layer_norm (nn.rs:4351-4545) of every row of x_dev [rows, d] into y_dev
+        with the decoder's kernel; exact: the reference's sequential sums."""
+        rows, d = x_dev.shape
+        check(lib().fwhip_layer_norm(self.h, x_dev.ptr, w_dev.ptr, b_dev.ptr, rows, d, y_dev.ptr,
+                                     1 if exact else 0))
 
     def tome_merge(self, x_dev: DeviceArray, r: int):
         """tome_merge (encoder.rs:1403-1506) of every window of x_dev [n_windows,

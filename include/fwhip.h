@@ -274,8 +274,13 @@ void fwhip_decoder_free(fwhip_decoder *dec);
  * bit-identical to the reference's strict mode.  Fast mode (exact = 0, the
  * default) makes every layer's cross K and V in one f16-pair MFMA GEMM (each
  * K/V value within ~1e-7 relative before its f16 rounding; the reference's
- * default ft sgemm has no pinned summation order either).  The token step is
- * the same in both modes. */
+ * default ft sgemm has no pinned summation order either).  In exact mode every
+ * LayerNorm of the token step also sums its f64 mean and variance in the
+ * reference's sequential index order (layer_norm, nn.rs:4425-4438), so logits
+ * and tokens are bit-identical whatever the rows; fast mode sums them in a
+ * wave tree, whose variance differs in its last f64 bits in most rows (an
+ * f32 output moved by it in 6 of 1.2 M Gaussian rows of width 1280).  The
+ * kernels are the same in both modes apart from that sum. */
 fwhip_status fwhip_decoder_set_exact(fwhip_decoder *dec, int32_t exact);
 
 /* A cohort of n_streams independent DecoderStates (decoder.rs:980-1027), each
@@ -455,6 +460,17 @@ void fwhip_transcript_free(fwhip_transcript *t);
  * and +0.0 tie, a row with no candidate gives 0).  argmax_host is [n_rows]. */
 fwhip_status fwhip_argmax_logits(fwhip_ctx *ctx, const float *logits_dev, int32_t n_rows, int32_t n_vocab,
                                  const fwhip_filter *filter, int32_t initial, int32_t *argmax_host);
+
+/* layer_norm (src/native_engine/nn.rs:4351-4545: f64 mean and variance,
+ * ((x - mean) * inv) * w + b rounded to f32, eps 1e-5) of n_rows rows of d
+ * floats on the device (x_dev, y_dev [n_rows, d]; w_dev, b_dev [d]), with
+ * the decoder's LayerNorm kernel.  exact = 1: the sums run in the reference's
+ * sequential index order (nn.rs:4425-4438), bit-identical to it on every row;
+ * exact = 0: the fast mode's wave-tree sums (fwhip_decoder_set_exact).  A
+ * parity entry for the LayerNorm inside the decoder's kernels.  Needs
+ * d % 4 == 0 and d <= 2048. */
+fwhip_status fwhip_layer_norm(fwhip_ctx *ctx, const float *x_dev, const float *w_dev, const float *b_dev,
+                              int64_t n_rows, int32_t d, float *y_dev, int32_t exact);
 
 /* ---- log-mel frontend ---------------------------------------------------- */
 

@@ -2,11 +2,9 @@
 the reference's decoder, src/native_engine/decoder.rs + nn.rs).
 
 Both arms are built to reproduce the reference's per-output arithmetic order,
-so logits are compared BIT-EXACTLY (exact mode: the strict cross K/V
-precompute) (the only documented deviation is the f64
-LayerNorm reduction order, which changes an f32 output only when a sum lands
-within 2^-53 relative of a rounding boundary — none is expected at these
-sizes; a failure here would print the differing count)."""
+so logits are compared BIT-EXACTLY in exact mode (the strict cross K/V
+precompute, and every LayerNorm's f64 sums in the reference's sequential
+order)."""
 import numpy as np
 import pytest
 
