@@ -384,3 +384,139 @@ def test_process_logits_masks_no_timestamps():
         assert O.process_argmax(f, lg, False) == tk.eot
         lg[tk.eot] = 0.0
         assert O.process_argmax(f, lg, False) == tk.space
+
+
+
+def _f16_weight_rows(amaxes, width):
+    """Rows [amax, w...] covering every non-negative f16 w <= amax with both
+    signs (zero padded to whole rows)."""
+    allw = np.arange(0, 0x7C00, dtype=np.uint16)
+    allf = allw.view(np.float16).astype(np.float64)
+    rows = []
+    for a in amaxes:
+        af = float(np.uint16(a).view(np.float16))
+        ws = allw[allf <= af]
+        ws = np.concatenate([ws, ws | np.uint16(0x8000)])  # both signs
+        n = width - 1
+        pad = (-ws.size) % n
+        ws = np.concatenate([ws, np.zeros(pad, np.uint16)]).reshape(-1, n)
+        rows.append(np.concatenate([np.full((ws.shape[0], 1), a, np.uint16), ws], axis=1))
+    return np.concatenate(rows)
+
+
+def _half_away_of_f32_product(rows, amax_col):
+    """The quantizer written from its definition: v = f32(w) * inv with
+    scale = f32(amax / 127), inv = f32(1 / scale) (nn.rs:2540-2552), then
+    round-half-away of v taken exactly in float64 (|v| + 1/2 is exact for an
+    f32 v) and clamped to 127."""
+    wf = rows.view(np.float16).astype(np.float32)
+    af = amax_col.view(np.float16).astype(np.float32)
+    scale = (af / np.float32(127.0)).astype(np.float32)
+    inv = (np.float32(1.0) / scale).astype(np.float32)
+    v = (wf * inv[:, None]).astype(np.float32).astype(np.float64)
+    return (np.sign(v) * np.minimum(127.0, np.floor(np.abs(v) + 0.5))).astype(np.int8), wf, af
+
+
+def _tie_amaxes():
+    # amax whose f16 mantissa is a multiple of 127 (for them 127 w / amax can
+    # be k + 1/2 for any k; for every other amax only w = amax / 2 gives a
+    # tie, 63.5), plus a seeded sample of others
+    out = set()
+    for a in range(1, 0x7C00):
+        m = a & 0x3FF
+        mant = (m | 0x400) if (a >> 10) else m
+        if mant % 127 == 0:
+            out.add(a)
+    rng = np.random.default_rng(5)
+    out.update(int(x) for x in rng.integers(1, 0x7C00, size=120))
+    return sorted(out)
+
+
+def test_decoder_weight_quantizer_on_every_f16_row():
+    """quantize_f16_row_to_i8_into (nn.rs:2490-2555): the 8-wide body rounds by
+    add-0.5-then-truncate in f32, the n % 8 tail by round-half-away.  The two
+    differ only where f32(w) * inv is +-0x3EFFFFFF (0.49999997 + 0.5 rounds to
+    1.0), and no f16 row lands there, so both equal round-half-away of the
+    product.  Checked for every f16 w against every tie-capable amax, once
+    entirely in the body (rows of 16) and once entirely in the tail (rows of
+    7).  Against the exact rational round(127 w / amax) the quantizer differs
+    only on the exact ties 63.5 (w = amax / 2) where f32(1 / scale) rounds
+    down: the reference gives 63 there, and so must the oracle."""
+    amaxes = _tie_amaxes()
+    n_ties = n_low = 0
+    for width in (16, 7):
+        rows = _f16_weight_rows(amaxes, width)
+        want, wf, af = _half_away_of_f32_product(rows, rows[:, 0])
+        q, s = O.quantize_f16_to_i8(rows)
+        np.testing.assert_array_equal(q, want)
+        np.testing.assert_array_equal(s.view(np.uint32), (af / np.float32(127.0)).astype(np.float32).view(np.uint32))
+        t = 127.0 * np.abs(wf.astype(np.float64)) / af[:, None].astype(np.float64)
+        exact = (np.sign(wf) * np.minimum(127.0, np.floor(t + 0.5))).astype(np.int8)
+        ties = (t % 1.0 == 0.5) & (t < 127)
+        n_ties += int(ties.sum())
+        diff = q != exact
+        n_low += int(diff.sum())
+        assert np.all(t[diff] == 63.5), "only the w = amax / 2 ties may round below the rational value"
+        # planted mistake: ties to even (rint) disagrees on exact ties of even k
+        even = (np.sign(wf) * np.minimum(127.0, np.rint(t))).astype(np.int8)
+        assert np.any(even[ties] != q[ties])
+    assert n_ties > 10_000 and n_low > 0
+
+
+def test_blocked_weight_quantizer_on_f16_rows():
+    """quantize_f16_row_blocked_to_int_into (nn.rs:3619-3693, max_level 127,
+    block 32): the same per 32-wide block, with the body/tail split at each
+    block's multiple of 8.  Rows of 39 = a block of 32 (all body) and a
+    block of 7 (all tail), each [amax, w...]."""
+    amaxes = [a for a in _tie_amaxes() if a % 3 == 0][:60]
+    r32 = _f16_weight_rows(amaxes, 32)
+    r7 = _f16_weight_rows(amaxes, 7)
+    n = min(r32.shape[0], r7.shape[0])
+    rows = np.concatenate([r32[:n], r7[:n]], axis=1)
+    w32, _, a0 = _half_away_of_f32_product(rows[:, :32], rows[:, 0])
+    w7, _, a1 = _half_away_of_f32_product(rows[:, 32:], rows[:, 32])
+    q, s = O.quantize_f16_to_i8_blocked(rows, 32)
+    np.testing.assert_array_equal(q, np.concatenate([w32, w7], axis=1))
+    np.testing.assert_array_equal(s[:, 0], a0 / np.float32(127.0))
+    np.testing.assert_array_equal(s[:, 1], a1 / np.float32(127.0))
+
+
+def test_weight_quantizer_known_answers():
+    # amax 127 (scale 1, inv 1): exact halves round away from zero in the body
+    # and in the tail; 126.5 -> 127, -126.5 -> -127
+    row = np.array([127.0, 2.5, -2.5, 0.5, -0.5, 1.5, 126.5, -126.5,
+                    2.5, -2.5, 0.5, -0.5, 1.5, 126.5, -126.5], np.float16).view(np.uint16)
+    q, s = O.quantize_f16_to_i8(row[None, :])
+    np.testing.assert_array_equal(q[0], [127, 3, -3, 1, -1, 2, 127, -127, 3, -3, 1, -1, 2, 127, -127])
+    assert s[0] == np.float32(1.0)
+    # amax 1143 = 127 * 9: scale 9, f32(1/9) rounds up, so 22.5 -> 2.5 -> 3
+    row = np.array([1143.0, 22.5, -22.5, 4.5, 31.5, 0.0, 0.0, 0.0, 22.5, 4.5], np.float16).view(np.uint16)
+    q, s = O.quantize_f16_to_i8(row[None, :])
+    np.testing.assert_array_equal(q[0], [127, 3, -3, 1, 4, 0, 0, 0, 3, 1])
+    assert s[0] == np.float32(9.0)
+    # w = amax / 2 with f32(1 / scale) rounding down: 63.499996 -> 63 (the
+    # rational value 63.5 would give 64), in the body and in the tail
+    row = np.array([0x24C, 0x126, 0x8126, 0, 0, 0, 0, 0, 0x126], np.uint16)
+    q, s = O.quantize_f16_to_i8(row[None, :])
+    np.testing.assert_array_equal(q[0], [127, 63, -63, 0, 0, 0, 0, 0, 63])
+    # the 1e-9 floor on an all-zero row
+    q, s = O.quantize_f16_to_i8(np.zeros((1, 12), np.uint16))
+    assert not q.any() and s[0] == np.float32(np.float32(1e-9) / np.float32(127.0))
+
+
+def test_no_f16_row_reaches_the_add_trunc_split():
+    """Exhaustive: for every positive f16 amax and every f16 w with |w| <= amax,
+    f32(|w|) * f32(1 / f32(amax / 127)) is never 0x3EFFFFFF, the one product on
+    which add-0.5-then-truncate (1) and round-half-away (0) disagree; so the
+    weight quantizers' body and tail give the same values on every f16 row."""
+    h = np.arange(1, 0x7C00, dtype=np.uint16)
+    hf = h.view(np.float16).astype(np.float32)
+    hits = 0
+    for amax in hf:
+        inv = np.float32(1.0) / (np.float32(amax) / np.float32(127.0))
+        prod = (hf[hf <= amax] * inv).astype(np.float32)
+        hits += int(np.count_nonzero(prod.view(np.uint32) == np.uint32(0x3EFFFFFF)))
+    assert hits == 0
+    # the split itself (planted): 0.49999997 + 0.5 rounds to 1.0 in f32
+    v = np.uint32(0x3EFFFFFF).view(np.float32)
+    assert np.trunc(np.float32(v + np.float32(0.5))) == 1.0 and np.floor(np.float64(v) + 0.5) == 0.0
