@@ -119,9 +119,17 @@ class WindowInfo(C.Structure):
                                  "retried")] + [("tokens", C.POINTER(C.c_int32)), ("plogs", C.POINTER(C.c_float))]
 
 
+# GemmPrecision (encoder.rs:1885-1927) values and GEMM families (fwhip.h)
+PREC_F32, PREC_I7, PREC_I8, PREC_F16, PREC_F16_WEIGHTS, PREC_Q8_0_WEIGHTS, PREC_F16_KV, PREC_MIXED, PREC_F16_PAIR = \
+    range(9)
+FAMILIES = ("conv_stem", "attn_qkv", "attention", "attn_out", "mlp_fc1", "mlp_fc2")
+
+
 class ExecRecord(C.Structure):
+    """EncoderExecution (encoder.rs:1987-2003): route, the precision of each
+    GEMM family and what chose it."""
     _fields_ = [("route", C.c_char * 48), ("precision", C.c_int32), ("n_windows", C.c_int32),
-                ("device_ms", C.c_double)]
+                ("device_ms", C.c_double), ("family", C.c_int32 * 6), ("precision_source", C.c_char * 32)]
 
 
 def ptr(arr, ctype):

@@ -50,27 +50,36 @@ __device__ __forceinline__ void fw_split2(float v, uint16_t &hi, uint16_t &lo) {
     hi = __builtin_bit_cast(uint16_t, h);
     lo = __builtin_bit_cast(uint16_t, (_Float16)r);
 }
+// The same, or-ing into `of` whether the hi half overflows: |v| >= 65520
+// rounds to an infinite f16 (65504 is the largest finite one), and the pair
+// then carries inf / NaN instead of v.
+__device__ __forceinline__ void fw_split2(float v, uint16_t &hi, uint16_t &lo, uint32_t &of) {
+    of |= fabsf(v) >= 65520.0f ? 1u : 0u;
+    fw_split2(v, hi, lo);
+}
 
-__global__ void __launch_bounds__(256) k_split_f16(const float4 *x, size_t n4, uint2 *hi, uint2 *lo) {
+__global__ void __launch_bounds__(256) k_split_f16(const float4 *x, size_t n4, uint2 *hi, uint2 *lo, int *ovf) {
+    uint32_t of = 0;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
         const float4 v = x[i];
         uint16_t h[4], l[4];
-        fw_split2(v.x, h[0], l[0]);
-        fw_split2(v.y, h[1], l[1]);
-        fw_split2(v.z, h[2], l[2]);
-        fw_split2(v.w, h[3], l[3]);
+        fw_split2(v.x, h[0], l[0], of);
+        fw_split2(v.y, h[1], l[1], of);
+        fw_split2(v.z, h[2], l[2], of);
+        fw_split2(v.w, h[3], l[3], of);
         hi[i] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
         lo[i] = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
     }
+    if (of && ovf) *ovf = 1;
 }
 
 // n must be a multiple of 4 (rows of d, d % 128 == 0)
-void fw_launch_split_f16(hipStream_t st, const float *x, size_t n, uint16_t *hi, uint16_t *lo) {
+void fw_launch_split_f16(hipStream_t st, const float *x, size_t n, uint16_t *hi, uint16_t *lo, int *ovf) {
     const size_t n4 = n / 4;
     size_t g = (n4 + 255) / 256;
     g = g < 8192 ? g : 8192;
     hipLaunchKernelGGL(k_split_f16, dim3((unsigned)g), dim3(256), 0, st, (const float4 *)x, n4, (uint2 *)hi,
-                       (uint2 *)lo);
+                       (uint2 *)lo, ovf);
 }
 
 // Epilogue for the 4 consecutive rows row0..row0+3 of one column.
@@ -98,6 +107,7 @@ __device__ __forceinline__ void gemm_store4(const FwGemm &g, int row0, int col, 
         float sw = KIND == FW_KIND_I8 ? g.sw[col] : 1.0f;
         float v[4];
         uint16_t hi[4], lo[4];
+        uint32_t of = 0;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             int row = row0 + e;
@@ -105,8 +115,9 @@ __device__ __forceinline__ void gemm_store4(const FwGemm &g, int row0, int col, 
             if constexpr (KIND == FW_KIND_I8) x = row < g.M ? x * g.sx[row] * sw : 0.0f;
             if (g.bias) x = x + bias;
             v[e] = x;
-            fw_split2(v[e], hi[e], lo[e]);
+            fw_split2(v[e], hi[e], lo[e], of);
         }
+        if (of && g.ovf) *g.ovf = 1;
         if (which < 2) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -165,7 +176,9 @@ __device__ __forceinline__ void gemm_store4(const FwGemm &g, int row0, int col, 
                     g.C[o] = fw_gelu(v, g.gelu_tab);
                 } else if constexpr (EPI == FW_EPI_GELU_SPLIT) {
                     uint16_t hi, lo;
-                    fw_split2(fw_gelu(v, g.gelu_tab), hi, lo);
+                    uint32_t of = 0;
+                    fw_split2(fw_gelu(v, g.gelu_tab), hi, lo, of);
+                    if (of && g.ovf) *g.ovf = 1;
                     g.o16[0][o] = hi;
                     g.o16[1][o] = lo;
                 } else if constexpr (EPI == FW_EPI_CONV2) {
@@ -272,7 +285,9 @@ __device__ __forceinline__ void gemm_epilogue(const FwGemm &g, accT (&acc)[BM / 
                                 g.C[o] = fw_gelu(v, g.gelu_tab);
                             } else if constexpr (EPI == FW_EPI_GELU_SPLIT) {
                                 uint16_t hi, lo;
-                                fw_split2(fw_gelu(v, g.gelu_tab), hi, lo);
+                                uint32_t of = 0;
+                                fw_split2(fw_gelu(v, g.gelu_tab), hi, lo, of);
+                                if (of && g.ovf) *g.ovf = 1;
                                 g.o16[0][o] = hi;
                                 g.o16[1][o] = lo;
                             }
@@ -569,6 +584,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
     const int nsteps = g.K / 64;
     const int total = my_n * nsteps;
     if (total == 0) return;
+    uint32_t ovf_any = 0; // an f16-pair value past the f16 range (FW_EPI_QKV)
     // tile ti of this block -> first row, valid rows, first column
     auto coords = [&](int ti, int &m0, int &mrows, int &n0) {
         const int t = xs + loc + ti * nloc;
@@ -883,7 +899,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
                             const int pb = t0 + 16 * c + 8 * (ln >> 5); // first of 8 positions
                             uint16_t hi[8], lo[8];
 #pragma unroll
-                            for (int e = 0; e < 8; e++) fw_split2(v[8 * c + e], hi[e], lo[e]);
+                            for (int e = 0; e < 8; e++) fw_split2(v[8 * c + e], hi[e], lo[e], ovf_any);
                             if (16 * c + 16 <= vrows) {
                                 uint4 ph, pl;
                                 ph.x = hi[0] | ((uint32_t)hi[1] << 16);
@@ -927,8 +943,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
 #pragma unroll
                             for (int q = 0; q < 8; q++) {
                                 uint16_t h0, l0, h1, l1;
-                                fw_split2(w4[q >> 1][(q & 1) * 2], h0, l0);
-                                fw_split2(w4[q >> 1][(q & 1) * 2 + 1], h1, l1);
+                                fw_split2(w4[q >> 1][(q & 1) * 2], h0, l0, ovf_any);
+                                fw_split2(w4[q >> 1][(q & 1) * 2 + 1], h1, l1, ovf_any);
                                 ph[q] = h0 | ((uint32_t)h1 << 16);
                                 pl[q] = l0 | ((uint32_t)l1 << 16);
                             }
@@ -953,6 +969,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) k_gemm_pi8(FwGemm g, int ntm, 
         s = 0;
     }
     FW_WAIT_VM(0);
+    if constexpr (EPI == FW_EPI_QKV)
+        if (ovf_any && g.ovf) *g.ovf = 1;
 }
 
 // ---------------------------------------------------------------------------

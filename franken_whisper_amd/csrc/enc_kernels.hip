@@ -24,6 +24,11 @@ __device__ __forceinline__ void fw_split(float v, uint16_t &hi, uint16_t &lo) {
     hi = __builtin_bit_cast(uint16_t, h);
     lo = __builtin_bit_cast(uint16_t, (_Float16)r);
 }
+// The same, or-ing into `of` whether the hi half overflows (|v| >= 65520).
+__device__ __forceinline__ void fw_split(float v, uint16_t &hi, uint16_t &lo, uint32_t &of) {
+    of |= fabsf(v) >= 65520.0f ? 1u : 0u;
+    fw_split(v, hi, lo);
+}
 
 // ---------------------------------------------------------------------------
 // LayerNorm per row (nn.rs:4455-4545, f64 statistics) with the output the next
@@ -46,7 +51,7 @@ __device__ __forceinline__ double eln_wave_sum(double v) {
 template <int NV, bool SEQ>
 __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, const float *b, int rows, int d,
                                                 int mode, float *yf, uint16_t *hi, uint16_t *lo, int8_t *q,
-                                                float *qs) {
+                                                float *qs, int *ovf) {
     constexpr int ELN_V4 = NV;
     const int lane = threadIdx.x & 63;
     const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -124,17 +129,19 @@ __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, 
         for (int k = 0; k < ELN_V4; k++)
             if (ok[k]) ((float4 *)(yf + r * d))[lane + 64 * k] = make_float4(yv[k][0], yv[k][1], yv[k][2], yv[k][3]);
     } else if (mode == FW_LN_SPLIT) {
+        uint32_t of = 0;
 #pragma unroll
         for (int k = 0; k < ELN_V4; k++)
             if (ok[k]) {
                 uint16_t h[4], l[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) fw_split(yv[k][e], h[e], l[e]);
+                for (int e = 0; e < 4; e++) fw_split(yv[k][e], h[e], l[e], of);
                 ((uint2 *)(hi + r * d))[lane + 64 * k] =
                     make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
                 ((uint2 *)(lo + r * d))[lane + 64 * k] =
                     make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
             }
+        if (of && ovf) *ovf = 1;
     } else {
         amax = fw_wave_max(amax);
         const float sc = fmaxf(amax, 1e-9f) / 127.0f;
@@ -412,7 +419,7 @@ __global__ void __launch_bounds__(1024) k_gelu_quant_h16(const uint16_t *hx, con
 // pair the GEMM consumes.  Column order kk*Cin + ci (weights are reordered to
 // match at load); columns >= 3*Cin are zero padding up to Kp.
 __global__ void k_im2col(const float *x, int B, int Tin, int Cin, int stride, int Tout, int Kp, uint16_t *hi,
-                         uint16_t *lo) {
+                         uint16_t *lo, int *ovf) {
     size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t total = (size_t)B * Tout * Kp;
     if (idx >= total) return;
@@ -425,7 +432,9 @@ __global__ void k_im2col(const float *x, int B, int Tin, int Cin, int stride, in
         int ti = t * stride + kk - 1;
         if (ti >= 0 && ti < Tin) v = x[((size_t)b * Tin + ti) * Cin + ci];
     }
-    fw_split(v, hi[idx], lo[idx]);
+    uint32_t of = 0;
+    fw_split(v, hi[idx], lo[idx], of);
+    if (of && ovf) *ovf = 1;
 }
 
 // time_major_mel_window_from_full_mel (encoder.rs:684-714) for a batch of windows.
@@ -779,13 +788,14 @@ void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qof
 
 // ---------------------------------------------------------------------------
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
-                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs) {
+                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs, int *ovf) {
     const dim3 g((rows + 3) / 4), blk(256);
     const bool seq = (mode & FW_LN_SEQ) != 0;
     mode &= ~FW_LN_SEQ;
 #define ELN_CASE(NV)                                                                                              \
-    if (seq) hipLaunchKernelGGL((k_enc_ln<NV, true>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs); \
-    else hipLaunchKernelGGL((k_enc_ln<NV, false>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs);    \
+    if (seq)                                                                                                    \
+        hipLaunchKernelGGL((k_enc_ln<NV, true>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs, ovf);  \
+    else hipLaunchKernelGGL((k_enc_ln<NV, false>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs, ovf); \
     break;
     switch ((d + 255) / 256) {
     case 1: ELN_CASE(1)
@@ -881,10 +891,10 @@ bool fw_launch_gelu_quant_h16(hipStream_t st, const uint16_t *hx, const float *s
 #undef GQH
 }
 void fw_launch_im2col(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, int Kp,
-                      uint16_t *hi, uint16_t *lo) {
+                      uint16_t *hi, uint16_t *lo, int *ovf) {
     size_t total = (size_t)B * Tout * Kp;
     hipLaunchKernelGGL(k_im2col, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x, B, Tin, Cin, stride,
-                       Tout, Kp, hi, lo);
+                       Tout, Kp, hi, lo, ovf);
 }
 void fw_launch_mel_window(hipStream_t st, const float *mel, int n_mel, long long mel_frames, const long long *offs,
                           int n_frames, float *out, int B) {

@@ -302,6 +302,27 @@ static FwGemm gemm_args(const void *A, const void *A2, const void *B, int M, int
     return g;
 }
 
+// EncoderExecution of a forward (encoder.rs:1987-2003): the route, the
+// arithmetic of each GEMM family and what chose it.
+static void fill_record(fwhip_exec_record *rec, const fwhip_encoder *e, int B, double ms, bool exact,
+                        const char *source) {
+    if (!rec) return;
+    const bool i8 = e->precision == FWHIP_ENC_INT8;
+    snprintf(rec->route, sizeof rec->route, "hip:gfx950:%s%s", i8 ? "int8" : "f32", exact ? ":exact" : "");
+    rec->precision = e->precision;
+    rec->n_windows = B;
+    rec->device_ms = ms;
+    // the f32 parts: strict f32 in exact mode, f16-pair MFMA in fast mode
+    const int f = exact ? FWHIP_PREC_F32 : FWHIP_PREC_F16_PAIR;
+    rec->family[FWHIP_FAM_CONV_STEM] = f;
+    rec->family[FWHIP_FAM_ATTENTION] = f;
+    rec->family[FWHIP_FAM_ATTN_QKV] = i8 ? FWHIP_PREC_I7 : f;
+    rec->family[FWHIP_FAM_ATTN_OUT] = i8 ? FWHIP_PREC_I8 : f;
+    rec->family[FWHIP_FAM_MLP_FC1] = i8 ? FWHIP_PREC_I7 : f;
+    rec->family[FWHIP_FAM_MLP_FC2] = i8 ? FWHIP_PREC_I7 : f;
+    snprintf(rec->precision_source, sizeof rec->precision_source, "%s", source);
+}
+
 static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwhip_exec_record *rec) {
     fwhip_ctx *c = e->ctx;
     hipStream_t st = c->stream;
@@ -316,8 +337,11 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
     hipEventCreate(&e1);
     hipEventRecord(e0, st);
     fw_event_pair ev;
+    // every f16-pair split reports a value past the f16 range into c->ovf_dev
+    int *ovf = c->ovf_dev;
+    fw_ovf_clear(c);
     // conv stem (encoder.rs:1550-1572): conv1 + GELU, conv2 (stride 2) + GELU, + pos_emb
-    fw_launch_im2col(st, b.mel_tm, B, T1, e->nmel, 1, T1, e->Kp1, b.a1h, b.a1l);
+    fw_launch_im2col(st, b.mel_tm, B, T1, e->nmel, 1, T1, e->Kp1, b.a1h, b.a1l, ovf);
     {
         FwGemm g = gemm_args(b.a1h, b.a1l, e->conv1w, M1, d, e->Kp1, nullptr, nullptr, e->conv1b, FW_EPI_GELU_F32,
                              b.a1, d);
@@ -326,7 +350,7 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
         fw_launch_gemm(st, FW_KIND_F16S, g);
         fw_timed_end(c, &ev);
     }
-    fw_launch_im2col(st, b.a1, B, T1, d, 2, T2, 3 * d, b.a2h, b.a2l);
+    fw_launch_im2col(st, b.a1, B, T1, d, 2, T2, 3 * d, b.a2h, b.a2l, ovf);
     {
         FwGemm g = gemm_args(b.a2h, b.a2l, e->conv2w, M, d, 3 * d, nullptr, nullptr, e->conv2b, FW_EPI_CONV2, b.x, d);
         g.gelu_tab = gt;
@@ -346,9 +370,10 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
         const EncLayerDev &l = e->layers[li];
         // self-attention residual (encoder_block, encoder.rs:2608-2681)
         fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, i8 ? FW_LN_I7 : FW_LN_SPLIT, nullptr, b.hh, b.hl,
-                         b.hq, b.hs);
+                         b.hq, b.hs, ovf);
         FwGemm g = i8 ? gemm_args(b.hq, nullptr, l.qkv7, Mc, 3 * d, d, b.hs, l.qkv7s, l.qkv_b, FW_EPI_QKV, nullptr, d)
                       : gemm_args(b.hh, b.hl, l.qkv16, Mc, 3 * d, d, nullptr, nullptr, l.qkv_b, FW_EPI_QKV, nullptr, d);
+        g.ovf = ovf;
         g.o16[0] = b.qh;
         g.o16[1] = b.ql;
         g.o16[2] = b.kh;
@@ -376,7 +401,7 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
         fw_timed_end(c, &ev);
         // MLP residual (encoder.rs:2684-2735)
         fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, i8 ? FW_LN_I7 : FW_LN_SPLIT, nullptr, b.hh, b.hl,
-                         b.hq, b.hs);
+                         b.hq, b.hs, ovf);
         if (i8) {
             // fc1 as f16 GELU-table indices (half the bytes of f32 rows; the
             // rare |v| >= 9.98 values exactly in b.ff), then GELU + quantization;
@@ -399,6 +424,7 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
             g.gelu_tab = gt;
             g.o16[0] = b.gh;
             g.o16[1] = b.gl;
+            g.ovf = ovf;
             fw_timed_begin(c, gcls, 2.0 * Mc * (double)dff * d, &ev);
             fw_launch_gemm(st, kind, g);
             fw_timed_end(c, &ev);
@@ -429,6 +455,7 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
     // ln_post (encoder.rs:1636)
     fw_launch_enc_ln(st, b.x, e->lnpw, e->lnpb, M, d, FW_LN_F32, out_dev, nullptr, nullptr, nullptr, nullptr);
     hipEventRecord(e1, st);
+    fw_ovf_fetch(c);
     hipError_t err = hipStreamSynchronize(st);
     float ms = 0.0f;
     hipEventElapsedTime(&ms, e0, e1);
@@ -437,12 +464,7 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
     if (err != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("encoder: ") + hipGetErrorString(err));
     err = hipGetLastError();
     if (err != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("encoder launch: ") + hipGetErrorString(err));
-    if (rec) {
-        snprintf(rec->route, sizeof rec->route, "hip:gfx950:%s", i8 ? "int8" : "f32");
-        rec->precision = e->precision;
-        rec->n_windows = B;
-        rec->device_ms = ms;
-    }
+    fill_record(rec, e, B, ms, false, "fwhip_encoder_load");
     return FWHIP_OK;
 }
 
@@ -474,9 +496,14 @@ static bool ensure_exact_bufs(fwhip_encoder *e, int B, int nf) {
 // sequential-k f32 GEMMs for the conv stem (and, on the f32 plan, every
 // linear), the per-head attention of attention_raw with glibc-exact softmax,
 // and on the int8 plan the same int8 GEMMs as the fast mode.
-static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_dev, fwhip_exec_record *rec) {
+static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_dev, fwhip_exec_record *rec,
+                                  const char *source) {
     fwhip_ctx *c = e->ctx;
     hipStream_t st = c->stream;
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    hipEventRecord(e0, st);
     EncBufs &b = e->buf;
     EncExactBufs &x = e->xbuf;
     int d = e->d, H = e->H, dff = e->dff;
@@ -532,29 +559,35 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
         }
         if (c->cancel.exchange(0)) {
             hipStreamSynchronize(st);
+            hipEventDestroy(e0);
+            hipEventDestroy(e1);
             return fw_fail(FWHIP_ERR_CANCELLED, "cancelled");
         }
     }
     if (merged) fw_launch_tome_unmerge(st, X, B, Tc, b.umap, T2, d, b.x);
     fw_launch_enc_ln(st, b.x, e->lnpw, e->lnpb, M, d, FW_LN_F32 | FW_LN_SEQ, out_dev, nullptr, nullptr, nullptr, nullptr);
+    hipEventRecord(e1, st);
     hipError_t err = hipStreamSynchronize(st);
+    float ms = 0.0f;
+    hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
     if (err == hipSuccess) err = hipGetLastError();
     if (err != hipSuccess) return fw_fail(FWHIP_ERR_GENERIC, std::string("encoder (exact): ") + hipGetErrorString(err));
-    if (rec) {
-        snprintf(rec->route, sizeof rec->route, "hip:gfx950:%s:exact", i8 ? "int8" : "f32");
-        rec->precision = e->precision;
-        rec->n_windows = B;
-        rec->device_ms = 0.0;
-    }
+    fill_record(rec, e, B, ms, true, source);
     return FWHIP_OK;
 }
 
+// A fast forward whose f16-pair operands met a value past the f16 range
+// (the device flag) is run again in exact mode, which has no f16 pairs; the
+// record says so.
 static fwhip_status enc_dispatch(fwhip_encoder *e, int B, int nf, float *out_dev, fwhip_exec_record *rec) {
-    if (e->exact) {
-        if (!ensure_exact_bufs(e, B, nf)) return fw_fail(FWHIP_ERR_GENERIC, "encoder: exact buffers failed");
-        return enc_run_exact(e, B, nf, out_dev, rec);
+    if (!e->exact) {
+        fwhip_status r = enc_run(e, B, nf, out_dev, rec);
+        if (r != FWHIP_OK || !*e->ctx->ovf_host) return r;
     }
-    return enc_run(e, B, nf, out_dev, rec);
+    if (!ensure_exact_bufs(e, B, nf)) return fw_fail(FWHIP_ERR_GENERIC, "encoder: exact buffers failed");
+    return enc_run_exact(e, B, nf, out_dev, rec, e->exact ? "fwhip_encoder_set_exact" : "f16_pair_range");
 }
 
 extern "C" fwhip_status fwhip_encoder_set_exact(fwhip_encoder *e, int32_t exact) {

@@ -55,12 +55,16 @@ struct FwGemm {
     int L;       // FW_EPI_XKV: decoder layers
     float scale; // FW_EPI_XKV: the key scale
     int map;     // tile order (set by fw_launch_gemm)
+    // f16-pair epilogues (QKV, GELU split): set to 1 when a finite or infinite
+    // value reaches |v| >= 65520, where the pair's hi half overflows (nullable)
+    int *ovf;
 };
 
 // false when the operand kind / epilogue pair has no kernel (nothing launched)
 bool fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g);
+// ovf (nullable): as FwGemm::ovf, for the SPLIT output
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
-                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs);
+                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs, int *ovf = nullptr);
 void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs);
 // The f16 copy of the GELU table that follows the f32 one (65536 entries) in
 // the context's allocation; tab is the context's f32 table.
@@ -73,12 +77,12 @@ void fw_launch_gelu_quant_i7_rows(hipStream_t st, const float *x, int rows, int 
 bool fw_launch_gelu_quant_h16(hipStream_t st, const uint16_t *hx, const float *side, int rows, int n,
                               const float *tab, int8_t *q, float *qs);
 void fw_launch_im2col(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, int Kp,
-                      uint16_t *hi, uint16_t *lo);
+                      uint16_t *hi, uint16_t *lo, int *ovf = nullptr);
 void fw_launch_mel_window(hipStream_t st, const float *mel, int n_mel, long long mel_frames, const long long *offs,
                           int n_frames, float *out, int B);
 void fw_launch_fill_u16(hipStream_t st, uint16_t *p, size_t n, uint16_t v);
 // f32 -> f16 pair (hi = f16(x), lo = f16(x - hi)): the A operand of an f16-pair GEMM
-void fw_launch_split_f16(hipStream_t st, const float *x, size_t n, uint16_t *hi, uint16_t *lo);
+void fw_launch_split_f16(hipStream_t st, const float *x, size_t n, uint16_t *hi, uint16_t *lo, int *ovf = nullptr);
 void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql, const uint16_t *kh,
                          const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
                          int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol);

@@ -43,7 +43,13 @@ struct fwhip_ctx {
     // fwhip_argmax_logits: per-block keys, tokens and the first-step flag
     void *am_scratch = nullptr;
     size_t am_scratch_bytes = 0;
+    // f16-pair range flag: set on the device by a split whose value reaches
+    // |v| >= 65520; copied to pinned host memory before a forward's final sync
+    int *ovf_dev = nullptr, *ovf_host = nullptr;
 };
+// clear the f16-pair range flag (a fill kernel) / queue its copy to the host
+void fw_ovf_clear(fwhip_ctx *c);
+void fw_ovf_fetch(fwhip_ctx *c);
 
 fwhip_status fw_fail(fwhip_status code, const std::string &msg);
 void fw_timed_begin(fwhip_ctx *c, int cls, double units, fw_event_pair *ev);

@@ -77,8 +77,25 @@ extern "C" fwhip_status fwhip_init(int32_t device, fwhip_ctx **out) {
         fwhip_destroy(c);
         return fw_fail(FWHIP_ERR_GENERIC, "gelu table upload failed");
     }
+    if (hipMalloc(&c->ovf_dev, 256) != hipSuccess || hipHostMalloc(&c->ovf_host, 256) != hipSuccess ||
+        hipMemset(c->ovf_dev, 0, 256) != hipSuccess) {
+        fwhip_destroy(c);
+        return fw_fail(FWHIP_ERR_GENERIC, "flag allocation failed");
+    }
+    *c->ovf_host = 0;
     *out = c;
     return FWHIP_OK;
+}
+
+void fw_ovf_clear(fwhip_ctx *c) { fw_launch_fill_u16(c->stream, (uint16_t *)c->ovf_dev, 2, 0); }
+void fw_ovf_fetch(fwhip_ctx *c) {
+    (void)hipMemcpyAsync(c->ovf_host, c->ovf_dev, sizeof(int), hipMemcpyDeviceToHost, c->stream);
+}
+
+extern "C" const char *fwhip_gemm_precision_str(int32_t p) {
+    static const char *const names[] = {"f32", "i7", "i8", "f16", "f16_weights", "q8_0_weights", "f16_kv",
+                                        "mixed", "f16_pair"};
+    return p >= 0 && p < (int32_t)(sizeof names / sizeof names[0]) ? names[p] : nullptr;
 }
 
 extern "C" void fwhip_destroy(fwhip_ctx *c) {
@@ -94,6 +111,8 @@ extern "C" void fwhip_destroy(fwhip_ctx *c) {
     if (c->mel_tab) hipFree(c->mel_tab);
     if (c->mel_scratch) hipFree(c->mel_scratch);
     if (c->am_scratch) hipFree(c->am_scratch);
+    if (c->ovf_dev) hipFree(c->ovf_dev);
+    if (c->ovf_host) hipHostFree(c->ovf_host);
     hipStreamDestroy(c->stream);
     delete c;
 }
@@ -660,16 +679,16 @@ extern "C" fwhip_status fwhip_decoder_set_exact(fwhip_decoder *dd, int32_t exact
 // projections written as per-head f16 K (scaled) and transposed f16 V, then
 // per-row int8 copies for the default arm.  Exact mode: the strict
 // sequential-k f32 GEMM, layer by layer; fast mode: every layer's K and V in
-// one f16-pair MFMA GEMM over the states split into f16 (hi, lo) pairs.
-extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *enc_dev) {
-    if (!st || !enc_dev) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_set_cross: NULL argument");
+// one f16-pair MFMA GEMM over the states split into f16 (hi, lo) pairs.  A
+// state past the f16 range (|v| >= 65520, which a pair cannot carry) sets the
+// range flag, and the strict GEMM then replaces the fast one's results.
+static bool cross_kv(fwhip_dstate *st, const float *enc_dev, bool strict) {
     fwhip_decoder *dd = st->dec;
     fwhip_ctx *c = dd->ctx;
-    HIP_TRY(hipSetDevice(c->device));
-    int d = dd->d, H = dd->H, L = dd->L, T = st->T, S = st->S;
-    float kscale = powf(64.0f, -0.25f);
+    const int d = dd->d, H = dd->H, L = dd->L, T = st->T, S = st->S;
+    const float kscale = powf(64.0f, -0.25f);
     fw_event_pair ev;
-    if (dd->exact) {
+    if (strict) {
         for (int li = 0; li < L; li++) {
             const DecLayerDev &l = dd->layers[li];
             fw_timed_begin(c, FWHIP_K_DEC_GEMV, 2.0 * S * T * (double)d * d, &ev);
@@ -680,7 +699,8 @@ extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *en
                                   H, L, li);
         }
     } else {
-        fw_launch_split_f16(c->stream, enc_dev, (size_t)S * T * d, st->ench, st->encl);
+        fw_ovf_clear(c);
+        fw_launch_split_f16(c->stream, enc_dev, (size_t)S * T * d, st->ench, st->encl, c->ovf_dev);
         FwGemm g;
         memset(&g, 0, sizeof g);
         g.A = st->ench;
@@ -703,7 +723,8 @@ extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *en
         fw_timed_begin(c, FWHIP_K_DEC_CROSS, 2.0 * 2.0 * S * T * (double)L * d * d, &ev);
         const bool ok = fw_launch_gemm(c->stream, FW_KIND_F16S, g);
         fw_timed_end(c, &ev);
-        if (!ok) return fw_fail(FWHIP_ERR_GENERIC, "cross K/V GEMM has no kernel");
+        if (!ok) return false;
+        fw_ovf_fetch(c);
     }
     if (st->ck16p)
         fw_launch_pack_cross_f16(c->stream, st->ck16, st->cvt16, st->ck16p, st->cvt16p, (size_t)S * L * H * T,
@@ -712,9 +733,23 @@ extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *en
         fw_launch_quant_f16_rows(c->stream, st->ck16, st->ck8, st->ck8s, S * L * H * T, 64);
         fw_launch_quant_f16_rows_ld(c->stream, st->cvt16, st->cvt8, st->cvt8s, S * L * H * 64, T, st->Tq);
     }
+    return true;
+}
+
+extern "C" fwhip_status fwhip_dstate_set_cross(fwhip_dstate *st, const float *enc_dev) {
+    if (!st || !enc_dev) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_set_cross: NULL argument");
+    fwhip_decoder *dd = st->dec;
+    fwhip_ctx *c = dd->ctx;
+    HIP_TRY(hipSetDevice(c->device));
+    if (!cross_kv(st, enc_dev, dd->exact)) return fw_fail(FWHIP_ERR_GENERIC, "cross K/V GEMM has no kernel");
     HIP_TRY(hipGetLastError());
-    st->len = 0;
     HIP_TRY(hipStreamSynchronize(c->stream));
+    if (!dd->exact && *c->ovf_host) {
+        cross_kv(st, enc_dev, true);
+        HIP_TRY(hipGetLastError());
+        HIP_TRY(hipStreamSynchronize(c->stream));
+    }
+    st->len = 0;
     return FWHIP_OK;
 }
 

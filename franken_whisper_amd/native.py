@@ -70,6 +70,7 @@ SIGNATURES = {
     "fwhip_transcript_free": (None, [_vp]),
     "fwhip_argmax_logits": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.POINTER(abi.Filter), C.c_int32, _i32p]),
     "fwhip_layer_norm": (C.c_int32, [_vp, _vp, _vp, _vp, C.c_int64, C.c_int32, _vp, C.c_int32]),
+    "fwhip_gemm_precision_str": (C.c_char_p, [C.c_int32]),
     "fwhip_mel_frames": (C.c_int64, [C.c_int64]),
     "fwhip_log_mel": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),
     "fwhip_log_mel_noalloc": (C.c_int32, [_vp, _vp, C.c_int64, _vp, C.c_int32, C.c_int32, _vp]),

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FWHIP_ABI_VERSION 1
+#define FWHIP_ABI_VERSION 2
 
 typedef int32_t fwhip_status;
 #define FWHIP_OK 0
@@ -135,12 +135,50 @@ typedef struct fwhip_filter {
     int32_t n_languages;      /* language tokens sot+1 .. sot+n_languages are masked */
 } fwhip_filter;
 
-/* Per-forward execution record (EncoderExecution, encoder.rs:1883-2048). */
+/* The arithmetic one encoder GEMM family ran in one forward (GemmPrecision,
+ * encoder.rs:1885-1927).  fwhip_gemm_precision_str gives the reference's
+ * stable report strings, plus "f16_pair" for this engine's MFMA form of f32. */
+#define FWHIP_PREC_F32 0          /* "f32": f32 operands and accumulation (exact mode: the
+                                     reference's strict-parity order) */
+#define FWHIP_PREC_I7 1           /* "i7": 7-bit weights x u8 activations, i32 accumulation */
+#define FWHIP_PREC_I8 2           /* "i8": i8 weights x i8 activations, i32 accumulation */
+#define FWHIP_PREC_F16 3          /* "f16" (reference values; not run by this engine) */
+#define FWHIP_PREC_F16_WEIGHTS 4  /* "f16_weights" */
+#define FWHIP_PREC_Q8_0_WEIGHTS 5 /* "q8_0_weights" */
+#define FWHIP_PREC_F16_KV 6       /* "f16_kv" */
+#define FWHIP_PREC_MIXED 7        /* "mixed" */
+#define FWHIP_PREC_F16_PAIR 8     /* "f16_pair": each f32 operand carried as an f16 hi/lo
+                                     pair, three f16 MFMA products (hi*hi + hi*lo + lo*hi)
+                                     accumulated in f32, about 2^-21 relative of f32 */
+/* GEMM families, in EncoderPrecision::families order (encoder.rs:1929-1985). */
+#define FWHIP_FAM_CONV_STEM 0
+#define FWHIP_FAM_ATTN_QKV 1
+#define FWHIP_FAM_ATTENTION 2
+#define FWHIP_FAM_ATTN_OUT 3
+#define FWHIP_FAM_MLP_FC1 4
+#define FWHIP_FAM_MLP_FC2 5
+#define FWHIP_N_FAM 6
+
+/* Per-forward execution record (EncoderExecution, encoder.rs:1987-2003):
+ * what computed this forward, returned by the forward itself.
+ *  - route: "hip:gfx950:int8" / "hip:gfx950:f32", with ":exact" when the
+ *    strict-parity arithmetic ran;
+ *  - family[f]: FWHIP_PREC_* of family FWHIP_FAM_f (EncoderPrecision): on the
+ *    int8 plan in fast mode conv_stem and attention are f16_pair, q/k/v and
+ *    the MLP i7, attn_out i8; exact mode runs f32 where fast mode runs
+ *    f16_pair; the f32 plan is f16_pair (fast) or f32 (exact) throughout;
+ *  - precision_source: what chose family[] (EncoderExecution::
+ *    precision_source): "fwhip_encoder_load" (the plan, fast mode),
+ *    "fwhip_encoder_set_exact" (exact mode), or "f16_pair_range" when a fast
+ *    forward met a value past the f16 range (|v| >= 65520, where an f16 pair
+ *    cannot carry it) and ran again in exact mode, whose results it returns. */
 typedef struct fwhip_exec_record {
-    char route[48];           /* e.g. "hip:gfx950:int8" */
-    int32_t precision;        /* FWHIP_ENC_* */
+    char route[48];
+    int32_t precision;        /* FWHIP_ENC_* (the load-time plan) */
     int32_t n_windows;
     double device_ms;         /* stream time of the forward */
+    int32_t family[FWHIP_N_FAM];
+    char precision_source[32];
 } fwhip_exec_record;
 
 /* ---- context, memory ---------------------------------------------------- */
@@ -157,6 +195,10 @@ fwhip_status fwhip_free(fwhip_ctx *ctx, void *dev);
 fwhip_status fwhip_upload(fwhip_ctx *ctx, void *dev, const void *host, size_t bytes);
 fwhip_status fwhip_download(fwhip_ctx *ctx, void *host, const void *dev, size_t bytes);
 fwhip_status fwhip_synchronize(fwhip_ctx *ctx);
+
+/* GemmPrecision::as_str (encoder.rs:1912-1927) of a FWHIP_PREC_* value
+ * ("f16_pair" for FWHIP_PREC_F16_PAIR), NULL for an unknown value. */
+const char *fwhip_gemm_precision_str(int32_t prec);
 
 /* Cancellation between layers and tokens, the checkpoint() contract of
  * nn.rs:29-37 / encoder.rs:1628 / decoder.rs:1877: the next layer boundary

@@ -35,7 +35,7 @@ def test_binding_covers_every_declared_symbol():
 
 
 def test_abi_version():
-    assert native.lib().fwhip_abi_version() == 1
+    assert native.lib().fwhip_abi_version() == 2
 
 
 def test_init_without_gpu_names_the_cpu_route():
