@@ -68,6 +68,32 @@ def build_hip(jobs: int | None = None):
     return out
 
 
+def build_hip_asan(jobs: int | None = None):
+    """The same library with AddressSanitizer and UndefinedBehaviorSanitizer
+    on its host code only (the ggml parser, argument checks, the drivers; the
+    gfx950 code objects are built as usual), into _build/asan/libfwhip.so.
+    The CPU tests run against it with FWHIP_LIB pointing there and clang's
+    ASan runtime preloaded (see the DESIGN notes); it is never shipped."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(ROOT, "_build", "asan")
+    os.makedirs(objdir, exist_ok=True)
+    out = os.path.join(objdir, "libfwhip.so")
+    san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+           "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-g"]
+    cflags = [f for f in HIP_FLAGS if f != "-shared"] + san
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
+
+    def compile_one(i):
+        _run([HIPCC] + cflags + ["-c", os.path.join(CSRC, HIP_SOURCES[i]), "-o", objs[i]])
+
+    n = jobs or min(len(HIP_SOURCES), os.cpu_count() or 1, 16)
+    with ThreadPoolExecutor(max_workers=n) as ex:
+        list(ex.map(compile_one, range(len(HIP_SOURCES))))
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + san + objs + ["-o", out])
+    return out
+
+
 def build_all():
     build_synth()
     build_hip()
@@ -76,4 +102,4 @@ def build_all():
 if __name__ == "__main__":
     what = sys.argv[1:] or ["all"]
     for w in what:
-        {"all": build_all, "synth": build_synth, "hip": build_hip}[w]()
+        {"all": build_all, "synth": build_synth, "hip": build_hip, "asan": build_hip_asan}[w]()

@@ -245,6 +245,7 @@ static void scan(fwhip_ggml &g) {
         cur.read(tok.data(), len);
         g.vocab.push_back(std::move(tok));
     }
+    bool nul_name = false; // a name with a NUL byte: valid UTF-8, but not a C string
     while (!cur.at_end()) {
         int32_t nd = cur.i32(), nl = cur.i32(), ttype = cur.i32();
         uint64_t n_dims = usize_from(nd, "tensor n_dims");
@@ -278,6 +279,7 @@ static void scan(fwhip_ggml &g) {
             if (!good) gg_throw(FWHIP_ERR_INVALID, "tensor name is not valid UTF-8");
             i += k;
         }
+        nul_name = nul_name || name.find('\0') != std::string::npos;
         std::vector<uint64_t> shape(ne.rbegin(), ne.rend());
         uint64_t n = 1;
         for (uint64_t d : shape)
@@ -287,6 +289,12 @@ static void scan(fwhip_ggml &g) {
         cur.skip(len);
         g.tensors[name] = GgmlEntry{shape, ttype, off, len};
     }
+    // the reference accepts such a name; the C ABI passes names as C strings,
+    // so a file the reference would load is refused here rather than read
+    // with truncated names (the caller keeps its CPU route)
+    if (nul_name)
+        gg_throw(FWHIP_ERR_UNSUPPORTED, "cpu:ggml-nul-in-tensor-name: a tensor name holds a NUL byte, which the "
+                                        "C ABI's string names cannot carry");
     for (auto &kv : g.tensors) g.by_index.push_back(&kv.first);
 }
 

@@ -14,7 +14,9 @@ import numpy as np
 from . import abi
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libfwhip.so")
+# FWHIP_LIB selects another build of the same sources (the host-sanitizer
+# build of build.py's "asan" target, for CPU-only tests)
+LIB_PATH = os.environ.get("FWHIP_LIB") or os.path.join(_HERE, "lib", "libfwhip.so")
 
 _vp = C.c_void_p
 _i32p = C.POINTER(C.c_int32)

@@ -570,7 +570,10 @@ typedef struct fwhip_ggml fwhip_ggml;
  * a truncated or malformed structure (negative counts, n_dims outside 1..=4,
  * element counts that are not a multiple of the type's block), and
  * FWHIP_ERR_UNSUPPORTED for an ftype or tensor type the reference does not
- * decode; FWHIP_ERR_GENERIC ("io: ...") when the file cannot be opened. */
+ * decode; FWHIP_ERR_GENERIC ("io: ...") when the file cannot be opened.  A
+ * file the reference would load but whose tensor names hold a NUL byte (valid
+ * UTF-8 there, not a C string here) is refused with FWHIP_ERR_UNSUPPORTED
+ * ("cpu:ggml-nul-in-tensor-name"). */
 fwhip_status fwhip_ggml_open(const char *path, fwhip_ggml **out);
 /* GgmlModel::from_bytes (ggml.rs:953-955): the same parse over a copy of `len`
  * bytes of caller memory. */

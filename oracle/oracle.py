@@ -15,7 +15,9 @@ import numpy as np
 from franken_whisper_amd import abi
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SO = os.path.join(HERE, "build", "librefcpu.so")
+# FWHIP_REFCPU_SO selects another build of the same sources (the sanitizer
+# build of `make -C oracle asan`)
+SO = os.environ.get("FWHIP_REFCPU_SO") or os.path.join(HERE, "build", "librefcpu.so")
 
 _lib = None
 
