@@ -13,7 +13,7 @@ the timed run's tokens are compared with it window by window; the int8 decoder
 arm is timed on the same job and reported beside the headline with its own
 token comparison.  Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload job|enc-f32|enc-int8|decode]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload job|enc-f32|enc-int8|decode|step|tiny|...]
 """
 from __future__ import annotations
 
@@ -56,7 +56,9 @@ def _args():
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--workload", default="job",
-                   choices=["job", "enc-f32", "enc-int8", "decode", "copy", "load", "transcribe"])
+                   choices=["job", "enc-f32", "enc-int8", "decode", "step", "tiny", "copy", "load", "transcribe"])
+    p.add_argument("--depths", default="0,64,224,447",
+                   help="step workload: KV-cache depths at which one token per stream is stepped")
     p.add_argument("--windows", type=int, default=None)
     p.add_argument("--tokens", type=int, default=220)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -326,6 +328,189 @@ def load_workload(a):
     }))
 
 
+def xattn_roofline(ctx, st, S, cfg, filt, depth=114, n=5):
+    """Roofline entry of the fused cross-attention sublayer kernel
+    (k_cross_attn_f16p / k_cross_attn_i8v2: LayerNorm, q projection, attention
+    over the cohort's cross K/V), measured outside the timed region: the
+    cohort's caches are refilled to `depth` rows (the job's mean cache depth:
+    4 prompt rows + half of 220 steps) with seeded tokens, then `n` one-token
+    steps run with direct launches, each kernel bracketed by HIP events on the
+    library's stream.  Bytes per launch: the layer's cross K/V of every stream
+    and the q weights.  The state is reset afterwards."""
+    from franken_whisper_amd import abi, synth
+
+    toks = synth.uniform_i32(6, "xattn_tokens", 0, cfg.n_vocab, S * (depth + n)).reshape(S, depth + n)
+    st.reset()
+    st.step(toks[:, :depth])
+    ctx.synchronize()
+    ctx.timing(True)
+    for i in range(n):
+        st.step(toks[:, depth + i:depth + i + 1], filt=filt)
+    k, ms, units = ctx.kernel_stats(abi.K_DEC_XATTN)
+    ctx.timing(False)
+    st.reset()
+    if not k:
+        return None
+    gbs = units / (ms * 1e-3) / 1e9
+    return {"kernel": "decoder cross-attention sublayer (k_cross_attn_f16p / k_cross_attn_i8v2: LayerNorm, q, "
+                      f"attention over the cross K/V; one-token steps at cache depth {depth}-{depth + n - 1}, "
+                      "direct launches, outside the timed region)",
+            "bound": "hbm", "launches": k, "avg_launch_ms": round(ms / k, 4), "total_ms": round(ms, 3),
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None, "algorithmic_bytes": round(units / k), "in_timed_region": False}
+
+
+def step_workload(a):
+    """The large-v3-turbo decoder step in isolation (forward_step + logits_last
+    + argmax for every stream of a cohort, decoder.rs:1754-1906, 2048-2147) at
+    fixed cache depths: for each depth L the cohort's caches are filled by a
+    prefill of L seeded tokens (uniform in [0, 51866)) over seeded N(0,1)
+    encoder states (one per stream), then one token per stream is stepped at
+    position L (it attends L cached rows and its own).  Each repetition resets
+    the state, refills it (untimed) and times the step with HIP events on the
+    library's stream (kernel class FWHIP_K_DEC_STEP: direct launches, no graph).
+    Reported per depth: device time, tokens/s and algorithmic HBM bytes / time."""
+    from franken_whisper_amd import abi, native, synth
+
+    cfg = synth.TURBO
+    S = a.windows or 1
+    depths = [int(x) for x in a.depths.split(",")]
+    if any(not 0 <= L < cfg.n_text_ctx for L in depths):
+        raise SystemExit(f"--depths must lie in [0, {cfg.n_text_ctx - 1}]")
+    model = synth.Model(cfg, seed=0, encoder=False, decoder=True)
+    ctx = native.Context(0)
+    arm = abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8
+    dec = native.Decoder(ctx, model, arm)
+    if a.exact:
+        dec.set_exact(True)
+    st = dec.state(S, cfg.n_audio_ctx)
+    st.set_cross(ctx.array(synth.encoder_states(77, S, cfg.n_audio_ctx, cfg.n_audio_state)))
+    toks = synth.uniform_i32(5, "step_tokens", 0, cfg.n_vocab, S * cfg.n_text_ctx).reshape(S, cfg.n_text_ctx)
+    filt = model.tokens.filter()
+    rows = []
+    for L in depths:
+        def once():
+            st.reset()
+            if L:
+                st.step(toks[:, :L])
+            return st.step(toks[:, L:L + 1], filt=filt, initial=L == 0)
+        for _ in range(a.warmup):
+            once()
+        ctx.synchronize()
+        ctx.timing(True)
+        t0 = time.perf_counter()
+        host = 0.0
+        for _ in range(a.steps):
+            st.reset()
+            if L:
+                st.step(toks[:, :L])
+            t = time.perf_counter()
+            st.step(toks[:, L:L + 1], filt=filt, initial=L == 0)
+            host += time.perf_counter() - t
+        n, ms, units = ctx.kernel_stats(abi.K_DEC_STEP)
+        xk, xms, xunits = ctx.kernel_stats(abi.K_DEC_XATTN)
+        ctx.timing(False)
+        wall = time.perf_counter() - t0
+        if n != a.steps:
+            raise SystemExit(f"expected {a.steps} timed steps at depth {L}, the library recorded {n}")
+        us = ms * 1e3 / n
+        gbs = units / (ms * 1e-3) / 1e9
+        rows.append({"depth": L, "device_us_per_step": round(us, 1), "tok_s": round(S / (us * 1e-6), 1),
+                     "host_us_per_step": round(host * 1e6 / a.steps, 1),
+                     "algorithmic_bytes": round(units / n), "achieved_GBs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "wall_s": round(wall, 2)})
+        if xk:  # the fused cross-attention sublayer kernel, when the cohort takes it
+            rows[-1]["xattn_us"] = round(xms * 1e3 / xk, 2)
+            rows[-1]["xattn_GBs"] = round(xunits / (xms * 1e-3) / 1e9, 1)
+    mean_us = sum(r["device_us_per_step"] for r in rows) / len(rows)
+    top = max(rows, key=lambda r: r["device_us_per_step"])
+    out = {"metric": "decode tok/s, large-v3-turbo decoder step in isolation", "value": round(S / (mean_us * 1e-6), 1),
+           "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "ms_per_step": round(mean_us * 1e-3, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f16" if a.dec_arm == "f16" else "int8+f32",
+           "data": "synthetic (seeded random-init weights N(0,0.02), seeded N(0,1) encoder states, seeded tokens)",
+           "config": {"workload": f"large-v3-turbo decoder step, {S} stream(s), {a.dec_arm} arm, f16 KV cache "
+                                  f"filled to depth L in {depths}, logits + argmax", "streams": S, "depths": depths,
+                      "mode": "exact" if a.exact else "fast"},
+           "roofline": {"kernel": f"decoder step at depth {top['depth']} (forward, logits, argmax; direct launches)",
+                        "bound": "hbm", "achieved": top["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": top["frac"], "traffic": None},
+           "per_depth": rows}
+    st.close()
+    dec.close()
+    ctx.close()
+    print(json.dumps(out))
+
+
+def tiny_workload(a):
+    """Whisper tiny.en end to end on one window: 30 s of seeded synthetic
+    16 kHz audio -> GPU log-mel (80 bins) -> f32-plan encoder (4 layers,
+    d 384) -> cross K/V -> greedy no-timestamps decode of up to `--tokens`
+    tokens from the SOT prefix (the reference loop's end-of-text stop).
+    Reported: audio-s/s of the whole window and the decoder's tokens/s."""
+    from franken_whisper_amd import abi, native, synth
+
+    cfg = synth.TINY_EN
+    W = a.windows or 1
+    nf = 2 * cfg.n_audio_ctx
+    model = synth.Model(cfg, seed=0)
+    ctx = native.Context(0)
+    samples = synth.audio(AUDIO_SEED, 30.0 * W)
+    sd = ctx.array(samples)
+    fd = ctx.array(synth.mel_filterbank(cfg.n_mels))
+    mel_frames = native.mel_frames(samples.size)
+    mel_dev = ctx.empty((cfg.n_mels, mel_frames), np.float32)
+    offsets = np.arange(W, dtype=np.int64) * nf
+    enc = native.Encoder(ctx, model, abi.ENC_F32)
+    dec = native.Decoder(ctx, model, abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8)
+    if a.exact:
+        enc.set_exact(True)
+        dec.set_exact(True)
+    st = dec.state(W, cfg.n_audio_ctx)
+    enc_out = ctx.empty((W, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+    tk = model.tokens
+    filt = tk.filter()
+    prompt = tk.sot_sequence()
+    n_tok = [0]
+
+    def one():
+        ctx.log_mel(sd, samples.size, fd, cfg.n_mels, mel_dev)
+        enc.forward_mel(mel_dev, mel_frames, offsets, nf, enc_out)
+        st.set_cross(enc_out)
+        out = st.greedy(prompt, a.tokens, filt)
+        n_tok[0] = sum(len(t) for t in out)
+
+    for _ in range(a.warmup):
+        one()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        one()
+    ctx.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / a.steps
+    # the decode alone (cross K/V in place), for the decoder's tokens/s
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        st.reset()
+        st.greedy(prompt, a.tokens, filt)
+    ctx.synchronize()
+    dms = (time.perf_counter() - t0) * 1e3 / a.steps
+    out = {"metric": "audio-s/sec whisper tiny.en encode+greedy decode", "value": round(30.0 * W / (ms * 1e-3), 2),
+           "unit": "audio-s/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 3),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f32 (f16-pair MFMA)+" + ("f16" if a.dec_arm == "f16" else "int8"),
+           "data": "synthetic (seeded random-init weights N(0,0.02), seeded synthetic 16 kHz audio)",
+           "config": {"workload": f"whisper tiny.en: {W} x 30 s window(s), log-mel (80 bins), f32 encoder, "
+                                  f"greedy decode of up to {a.tokens} tokens, {a.dec_arm} decoder arm",
+                      "windows": W, "max_tokens": a.tokens, "mode": "exact" if a.exact else "fast"},
+           "tokens": n_tok[0], "decode_ms": round(dms, 3), "decode_tok_s": round(n_tok[0] / (dms * 1e-3), 1)}
+    st.close()
+    dec.close()
+    enc.close()
+    ctx.close()
+    print(json.dumps(out))
+
+
 def transcribe_workload(a):
     """The window driver end to end (fwhip_transcribe: log-mel of the whole
     audio, encoder windows at the seeks, the device window loop, the rules
@@ -394,6 +579,12 @@ def main():
         return
     if a.workload == "transcribe":
         transcribe_workload(a)
+        return
+    if a.workload == "step":
+        step_workload(a)
+        return
+    if a.workload == "tiny":
+        tiny_workload(a)
         return
     from franken_whisper_amd import abi, native, synth
 
@@ -533,6 +724,10 @@ def main():
         rooflines.append(r)
     rooflines.sort(key=lambda r: -r["total_ms"])
     roof = dict(rooflines[0]) if rooflines else None
+    if st is not None:
+        xr = xattn_roofline(ctx, st, W, cfg, filt)
+        if xr:
+            rooflines.append(xr)
 
     # the int8 decoder arm (the reference's default arm) on the same job:
     # timed the same way, reported beside the headline with its token check

@@ -25,6 +25,7 @@ K_DEC_LOGITS = 5
 K_DEC_CROSS = 6
 K_DEC_STEP = 7
 K_DEQUANT = 8
+K_DEC_XATTN = 9
 
 DS_CROSS_K_F16 = 1
 DS_CROSS_VT_F16 = 2

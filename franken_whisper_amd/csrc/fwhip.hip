@@ -796,6 +796,13 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
     float scale = powf(64.0f, -0.25f);
     const float *gt = c->gelu_tab;
     const int sq = dd->exact;
+    // a one-token step times its fused cross-attention sublayer launches
+    // (algorithmic bytes: the cohort's cross K/V of the layer and the q weights)
+    const bool xt = timed && !prefill;
+    fw_event_pair xev;
+    xev.active = false;
+    const double xbytes = i8 ? (double)S * (2.0 * T * d + 4.0 * H * T + 4.0 * d) + (double)d * d + 4.0 * d
+                             : (double)S * 4.0 * T * d + 2.0 * d * d + 4.0 * d;
     // The f16 arm's projections fold into the attention kernels when the
     // cohort's (head, stream) blocks fill one round of the CUs: with fewer
     // streams a head's rows would be multiplied on that many CUs only (one
@@ -823,8 +830,10 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                                       li == 0 ? dd->pos_emb : nullptr, sq);
             gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr, st->att);
             // the cross LayerNorm and q projection run inside the cross-attention kernel
+            if (xt) fw_timed_begin(c, FWHIP_K_DEC_XATTN, xbytes, &xev);
             fw_launch_cross_attn_i8v2(s, l.cq8, l.cq8s, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck8, st->ck8s,
                                       st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li, S, scale, st->pmax, sq);
+            if (xt) fw_timed_end(c, &xev);
             gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr, st->att);
             // mode 4: GELU written block-interleaved for the block GEMV; prefill
             // rows take the f16 mlp_2 (the block-int8 arm has no batch form),
@@ -859,8 +868,10 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             fw_gemv16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
             if (fold && st->ck16p && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) && fw_gemv16_lpr(d, d) == 16) {
                 // the cross LayerNorm and q projection run inside the cross-attention kernel
+                if (xt) fw_timed_begin(c, FWHIP_K_DEC_XATTN, xbytes, &xev);
                 fw_launch_cross_attn_f16pq(s, l.cq16, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck16p,
                                            st->cvt16p, st->att, d, T, H, L, li, S, scale, sq);
+                if (xt) fw_timed_end(c, &xev);
             } else {
                 // a cohort whose (head, stream) blocks fill under half the CUs
                 // (one stream: 20 blocks for 1,500 keys) or need more than one
@@ -1004,7 +1015,13 @@ static fwhip_status set_dev_ints(fwhip_ctx *c, int *dst, const int *v, int n) {
 // stream: the token matrix is uploaded once (position-major) and each row reads
 // its column; the device position starts at st->len and advances between rows.
 // The last row produces the logits and argmax keys.
-static fwhip_status stage_rows(fwhip_dstate *st, const int32_t *tokens, int tq, const fwhip_filter *filt) {
+static double dec_step_bytes(const fwhip_dstate *st, int tk);
+
+// Forward of tq rows per stream from position st->len.  With `ev` (tq == 1,
+// the step in isolation) the forward is bracketed as a FWHIP_K_DEC_STEP launch
+// from its first kernel; the caller ends the pair.
+static fwhip_status stage_rows(fwhip_dstate *st, const int32_t *tokens, int tq, const fwhip_filter *filt,
+                               fw_event_pair *ev = nullptr) {
     fwhip_decoder *dd = st->dec;
     fwhip_ctx *c = dd->ctx;
     int S = st->S;
@@ -1040,6 +1057,7 @@ static fwhip_status stage_rows(fwhip_dstate *st, const int32_t *tokens, int tq, 
         return FWHIP_OK;
     }
     for (int t = 0; t < tq; t++) {
+        if (ev && tq == 1) fw_timed_begin(c, FWHIP_K_DEC_STEP, dec_step_bytes(st, p0 + 1), ev);
         r = dec_forward_row(st, st->rows + (size_t)t * S, tq > 1, t == tq - 1, filt, true);
         if (r != FWHIP_OK) return r;
         if (t + 1 < tq) fw_launch_step_bookkeeping(c->stream, st->pos, nullptr, st->rows, nullptr, 0, 0, S);
@@ -1071,16 +1089,23 @@ extern "C" fwhip_status fwhip_decoder_step(fwhip_dstate *st, const int32_t *toke
     int init = initial ? 1 : 0;
     fwhip_status r = set_dev_ints(c, st->initial, &init, 1);
     if (r != FWHIP_OK) return r;
-    r = stage_rows(st, tokens, tq, filter);
-    if (r != FWHIP_OK) return r;
+    // a one-token step (forward, logits, argmax) is timed as FWHIP_K_DEC_STEP
+    fw_event_pair ev;
+    ev.active = false;
+    r = stage_rows(st, tokens, tq, filter, &ev);
+    if (r != FWHIP_OK) {
+        fw_timed_end(c, &ev);
+        return r;
+    }
     st->len += tq;
+    if (argmax_host)
+        fw_launch_argmax_finish(c->stream, st->keys, st->nkeys, S, st->tok, nullptr, 0, st->pos, nullptr, nullptr, 0);
+    fw_timed_end(c, &ev);
     if (logits_dev)
         HIP_TRY(hipMemcpyAsync(logits_dev, st->logits, sizeof(float) * (size_t)S * dd->V, hipMemcpyDeviceToDevice,
                                c->stream));
-    if (argmax_host) {
-        fw_launch_argmax_finish(c->stream, st->keys, st->nkeys, S, st->tok, nullptr, 0, st->pos, nullptr, nullptr, 0);
+    if (argmax_host)
         HIP_TRY(hipMemcpyAsync(argmax_host, st->tok, sizeof(int32_t) * S, hipMemcpyDeviceToHost, c->stream));
-    }
     HIP_TRY(hipStreamSynchronize(c->stream));
     HIP_TRY(hipGetLastError());
     return FWHIP_OK;

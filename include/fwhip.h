@@ -214,8 +214,11 @@ fwhip_status fwhip_request_cancel(fwhip_ctx *ctx);
 #define FWHIP_K_DEC_GEMV 4
 #define FWHIP_K_DEC_LOGITS 5
 #define FWHIP_K_DEC_CROSS 6  /* cross K/V precompute (fast mode) */
-#define FWHIP_K_DEC_STEP 7   /* one sampled decoder step of the greedy loop */
+#define FWHIP_K_DEC_STEP 7   /* one sampled decoder step of the greedy loop, or a one-token
+                                fwhip_decoder_step (forward, logits and argmax) */
 #define FWHIP_K_DEQUANT 8    /* ggml payload decode (fwhip_dequant, fwhip_ggml_tensor_f32) */
+#define FWHIP_K_DEC_XATTN 9  /* the fused cross-attention sublayer (LayerNorm, q, attention over the
+                                cross K/V) of a one-token fwhip_decoder_step */
 fwhip_status fwhip_kernel_timing(fwhip_ctx *ctx, int32_t enable);
 fwhip_status fwhip_kernel_stats(fwhip_ctx *ctx, int32_t kclass, int64_t *launches,
                                 double *total_ms, double *work_units);
