@@ -211,6 +211,14 @@ __global__ void __launch_bounds__(256) k_tome_unmerge(const float *xm, int Tm, c
     for (int i = threadIdx.x; i < (d >> 2); i += 256) dst[i] = src[i];
 }
 
+// cum[w][p] = step[w][cum[w][p]] for the T0 original rows of every window:
+// original row -> row after the latest merge (step: [B, Tprev])
+__global__ void __launch_bounds__(256) k_tome_compose(int32_t *cum, const int32_t *step, int B, int T0, int Tprev) {
+    const size_t n = (size_t)B * T0;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        cum[i] = step[(i / T0) * Tprev + cum[i]];
+}
+
 // zero the columns [T, Tp) of V^T rows [rows, Tp] (f16)
 __global__ void __launch_bounds__(256) k_tome_vpad(uint16_t *vt, size_t rows, int T, int Tp) {
     const int np = Tp - T;
@@ -267,4 +275,11 @@ int fw_launch_tome_merge(hipStream_t st, const float *x, int B, int T, int d, in
 void fw_launch_tome_unmerge(hipStream_t st, const float *xm, int B, int Tm, const int32_t *umap, int T, int d,
                             float *out) {
     hipLaunchKernelGGL(k_tome_unmerge, dim3(T, B), dim3(256), 0, st, xm, Tm, umap, T, d, out);
+}
+
+void fw_launch_tome_compose(hipStream_t st, int32_t *cum, const int32_t *step, int B, int T0, int Tprev) {
+    const size_t n = (size_t)B * T0;
+    size_t g = (n + 255) / 256;
+    g = g < 4096 ? g : 4096;
+    hipLaunchKernelGGL(k_tome_compose, dim3((unsigned)g), dim3(256), 0, st, cum, step, B, T0, Tprev);
 }

@@ -34,7 +34,7 @@ struct EncBufs {
     long long *offs;
     // ToMe: merged rows, unmerge map, merge workspace
     float *xm;
-    int32_t *umap;
+    int32_t *umap, *umap2; // original row -> current row; the latest merge's map
     void *tws;
     std::vector<void *> owned;
 };
@@ -53,6 +53,7 @@ struct fwhip_encoder {
     // tome_after; 0 = the un-merged encoder (the strict-parity setting)
     int tome_r = 0, tome_after = 3;
     int tome_min_rows = 0; // the default rule merges full 30 s windows only (1500 rows)
+    int tome_every = 0, tome_floor = 128; // FW_TOME_EVERY (0: single shot) / FW_TOME_FLOOR
     const uint16_t *conv1n = nullptr, *conv2n = nullptr; // natural [d, Cin*3] (exact mode)
     EncExactBufs xbuf;
     fwhip_hparams hp;
@@ -259,6 +260,7 @@ static bool ensure_bufs(fwhip_encoder *e, int B, int nf) {
     b.offs = (long long *)A(sizeof(long long) * B);
     b.xm = (float *)A(4 * M * d);
     b.umap = (int32_t *)A(sizeof(int32_t) * M);
+    b.umap2 = (int32_t *)A(sizeof(int32_t) * M);
     b.tws = A(fw_tome_ws_bytes(B, (int)T2));
     for (void *p : o)
         if (!p) return false;
@@ -274,11 +276,38 @@ static bool enc_h16_ok(int n) {
     return n > 0 && n % 512 == 0 && (k <= 8 || k == 10 || k == 12 || k == 16);
 }
 
-// The single-shot schedule of forward_time_major (encoder.rs:1590-1632): merge
-// after block tome_after when rows > r + 2 and rows - r >= 128 (the floor).
-static bool tome_due(const fwhip_encoder *e, int li, int rows, bool merged) {
-    return !merged && e->tome_r > 0 && li == e->tome_after && rows >= e->tome_min_rows && rows > e->tome_r + 2 &&
-           rows - e->tome_r >= 128 && fw_tome_ok(rows, e->d);
+// The ToMe schedule of forward_time_major (encoder.rs:1590-1632): a merge is
+// due after block li when, single shot (tome_every 0), none ran yet and
+// li == tome_after, or, progressive, li >= tome_after and (li - tome_after) is
+// a multiple of tome_every; it runs when rows > r + 2 and rows - r >= the
+// floor.  The default rule's full-window test (tome_r_for) looks at the
+// window's rows before any merge (T0).
+static bool tome_due(const fwhip_encoder *e, int li, int rows, int T0, int n_merges) {
+    if (e->tome_r <= 0 || T0 < e->tome_min_rows) return false;
+    const bool due = e->tome_every == 0 ? (n_merges == 0 && li == e->tome_after)
+                                        : (li >= e->tome_after && (li - e->tome_after) % e->tome_every == 0);
+    return due && rows > e->tome_r + 2 && rows - e->tome_r >= e->tome_floor && fw_tome_ok(rows, e->d);
+}
+
+// One merge of the current rows X [B, Tc, d] into the other of b.x / b.xm
+// (b.x is free once the first merge has read it); the first merge writes the
+// original-row map b.umap, later ones their own map into b.umap2, composed
+// into b.umap.  Returns the merged rows; Tc becomes their count.
+static float *tome_step(hipStream_t st, EncBufs &b, float *X, int B, int T0, int &Tc, int d, int r, int n_merges) {
+    float *dst = X == b.xm ? b.x : b.xm;
+    const int Tprev = Tc;
+    Tc = fw_launch_tome_merge(st, X, B, Tprev, d, r, b.tws, dst, n_merges ? b.umap2 : b.umap);
+    if (n_merges) fw_launch_tome_compose(st, b.umap, b.umap2, B, T0, Tprev);
+    return dst;
+}
+
+// tome_unmerge before ln_post (encoder.rs:1629-1631): the full rows, in b.x
+// or, when the merged rows are there, in b.att (free after the last block)
+static float *tome_finish(hipStream_t st, EncBufs &b, float *X, int B, int Tc, int T0, int d, int n_merges) {
+    if (!n_merges) return X;
+    float *fin = X == b.x ? b.att : b.x;
+    fw_launch_tome_unmerge(st, X, B, Tc, b.umap, T0, d, fin);
+    return fin;
 }
 
 static FwGemm gemm_args(const void *A, const void *A2, const void *B, int M, int N, int K, const float *sx,
@@ -364,7 +393,7 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
     // the current rows: b.x [B, T2, d], or after a ToMe merge b.xm [B, Tc, d]
     float *X = b.x;
     int Tc = T2, Mc = M, Tpc = Tp;
-    bool merged = false;
+    int n_merges = 0;
     int kind = i8 ? FW_KIND_I8 : FW_KIND_F16S;
     for (int li = 0; li < e->L; li++) {
         const EncLayerDev &l = e->layers[li];
@@ -433,12 +462,10 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
         fw_timed_begin(c, gcls, 2.0 * Mc * (double)d * dff, &ev);
         fw_launch_gemm(st, kind, g);
         fw_timed_end(c, &ev);
-        if (tome_due(e, li, Tc, merged)) {
-            Tc = fw_launch_tome_merge(st, X, B, Tc, d, e->tome_r, b.tws, b.xm, b.umap);
-            X = b.xm;
+        if (tome_due(e, li, Tc, T2, n_merges)) {
+            X = tome_step(st, b, X, B, T2, Tc, d, e->tome_r, n_merges++);
             Mc = B * Tc;
             Tpc = (Tc + 63) / 64 * 64;
-            merged = true;
             // V^T rows now have stride Tpc: their padding keys must be finite
             fw_launch_tome_vpad(st, b.vth, (size_t)B * H * 64, Tc, Tpc);
             fw_launch_tome_vpad(st, b.vtl, (size_t)B * H * 64, Tc, Tpc);
@@ -450,10 +477,9 @@ static fwhip_status enc_run(fwhip_encoder *e, int B, int nf, float *out_dev, fwh
             return fw_fail(FWHIP_ERR_CANCELLED, "cancelled");
         }
     }
-    // tome_unmerge before ln_post (encoder.rs:1629-1631)
-    if (merged) fw_launch_tome_unmerge(st, X, B, Tc, b.umap, T2, d, b.x);
+    X = tome_finish(st, b, X, B, Tc, T2, d, n_merges);
     // ln_post (encoder.rs:1636)
-    fw_launch_enc_ln(st, b.x, e->lnpw, e->lnpb, M, d, FW_LN_F32, out_dev, nullptr, nullptr, nullptr, nullptr);
+    fw_launch_enc_ln(st, X, e->lnpw, e->lnpb, M, d, FW_LN_F32, out_dev, nullptr, nullptr, nullptr, nullptr);
     hipEventRecord(e1, st);
     fw_ovf_fetch(c);
     hipError_t err = hipStreamSynchronize(st);
@@ -518,7 +544,7 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
                           e->pos);
     float *X = b.x;
     int Tc = T2, Mc = M;
-    bool merged = false;
+    int n_merges = 0;
     for (int li = 0; li < e->L; li++) {
         const EncLayerDev &l = e->layers[li];
         if (i8) {
@@ -551,11 +577,9 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
             fw_launch_gemm_strict(st, x.ff, l.fc2_16, Mc, d, dff, 5, X, l.fc2_b, 1.0f, nullptr, Tc, 0, 0, 0, d,
                                   nullptr, nullptr);
         }
-        if (tome_due(e, li, Tc, merged)) {
-            Tc = fw_launch_tome_merge(st, X, B, Tc, d, e->tome_r, b.tws, b.xm, b.umap);
-            X = b.xm;
+        if (tome_due(e, li, Tc, T2, n_merges)) {
+            X = tome_step(st, b, X, B, T2, Tc, d, e->tome_r, n_merges++);
             Mc = B * Tc;
-            merged = true;
         }
         if (c->cancel.exchange(0)) {
             hipStreamSynchronize(st);
@@ -564,8 +588,8 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
             return fw_fail(FWHIP_ERR_CANCELLED, "cancelled");
         }
     }
-    if (merged) fw_launch_tome_unmerge(st, X, B, Tc, b.umap, T2, d, b.x);
-    fw_launch_enc_ln(st, b.x, e->lnpw, e->lnpb, M, d, FW_LN_F32 | FW_LN_SEQ, out_dev, nullptr, nullptr, nullptr, nullptr);
+    X = tome_finish(st, b, X, B, Tc, T2, d, n_merges);
+    fw_launch_enc_ln(st, X, e->lnpw, e->lnpb, M, d, FW_LN_F32 | FW_LN_SEQ, out_dev, nullptr, nullptr, nullptr, nullptr);
     hipEventRecord(e1, st);
     hipError_t err = hipStreamSynchronize(st);
     float ms = 0.0f;
@@ -614,6 +638,17 @@ extern "C" fwhip_status fwhip_encoder_set_tome(fwhip_encoder *e, int32_t r, int3
     e->tome_r = r;
     e->tome_after = after;
     e->tome_min_rows = min_rows;
+    return FWHIP_OK;
+}
+
+// FW_TOME_EVERY / FW_TOME_FLOOR (encoder.rs:1379-1402): every = 0 keeps the
+// single-shot schedule, every > 0 merges again after every `every` blocks from
+// the first; no merge leaves fewer than `floor` rows.
+extern "C" fwhip_status fwhip_encoder_set_tome_schedule(fwhip_encoder *e, int32_t every, int32_t floor) {
+    if (!e) return fw_fail(FWHIP_ERR_INVALID, "NULL encoder");
+    if (every < 0 || floor < 0) return fw_fail(FWHIP_ERR_INVALID, "ToMe schedule: every and floor must be >= 0");
+    e->tome_every = every;
+    e->tome_floor = floor;
     return FWHIP_OK;
 }
 

@@ -98,3 +98,5 @@ int fw_launch_tome_merge(hipStream_t st, const float *x, int B, int T, int d, in
 void fw_launch_tome_unmerge(hipStream_t st, const float *xm, int B, int Tm, const int32_t *umap, int T, int d,
                             float *out);
 void fw_launch_tome_vpad(hipStream_t st, uint16_t *vt, size_t rows, int T, int Tp);
+// cum [B, T0] = step[cum] per window (step [B, Tprev]): the unmerge map through one more merge
+void fw_launch_tome_compose(hipStream_t st, int32_t *cum, const int32_t *step, int B, int T0, int Tprev);

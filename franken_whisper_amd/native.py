@@ -45,6 +45,7 @@ SIGNATURES = {
                                                      C.POINTER(abi.ExecRecord)]),
     "fwhip_encoder_set_exact": (C.c_int32, [_vp, C.c_int32]),
     "fwhip_encoder_set_tome": (C.c_int32, [_vp, C.c_int32, C.c_int32]),
+    "fwhip_encoder_set_tome_schedule": (C.c_int32, [_vp, C.c_int32, C.c_int32]),
     "fwhip_tome_merge": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _vp, _vp, _i32p]),
     "fwhip_encoder_gemm_i8": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, _vp, _vp]),
     "fwhip_encoder_gemm_i8_fused": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, C.c_int32, _vp, _vp]),
@@ -347,6 +348,11 @@ class Encoder:
     def set_tome(self, r: int, after: int = 3):
         """FW_TOME_R / FW_TOME_LAYER; r < 0 takes the reference's default rule."""
         check(lib().fwhip_encoder_set_tome(self.h, r, after))
+
+    def set_tome_schedule(self, every: int = 0, floor: int = 128):
+        """FW_TOME_EVERY / FW_TOME_FLOOR: every > 0 merges again after every
+        `every` blocks; no merge leaves fewer than `floor` rows."""
+        check(lib().fwhip_encoder_set_tome_schedule(self.h, every, floor))
 
     def gemm_i8(self, layer: int, which: int, x_dev: DeviceArray, acc_dev: DeviceArray, y_dev: DeviceArray):
         check(lib().fwhip_encoder_gemm_i8(self.h, layer, which, x_dev.ptr, x_dev.shape[0], acc_dev.ptr,

@@ -252,11 +252,12 @@ fwhip_status fwhip_encoder_forward(fwhip_encoder *enc, const float *mel_dev, int
 fwhip_status fwhip_encoder_set_exact(fwhip_encoder *enc, int32_t exact);
 
 /* ToMe token merging (FW_TOME_R / FW_TOME_LAYER, encoder.rs:1264-1337 and
- * 1590-1632, single-shot schedule): merge r of the rows of every window after
- * block `after` (0-based) by bipartite soft matching (tome_merge,
- * encoder.rs:1403-1506), run the later blocks on the merged rows and unmerge
- * before ln_post (tome_unmerge, encoder.rs:1509-1517).  The merge runs when
- * rows > r + 2 and rows - r >= 128.  r = 0 (the initial setting) is the
+ * 1590-1632; the single-shot schedule unless fwhip_encoder_set_tome_schedule
+ * says otherwise): merge r of the rows of every window after block `after`
+ * (0-based) by bipartite soft matching (tome_merge, encoder.rs:1403-1506), run
+ * the later blocks on the merged rows and unmerge before ln_post
+ * (tome_unmerge, encoder.rs:1509-1517).  The merge runs when rows > r + 2 and
+ * rows - r >= the floor (128 unless set).  r = 0 (the initial setting) is the
  * un-merged encoder, FW_TOME_R=0; r < 0 applies the reference's default for
  * the model (tome_r_for: 500 after block 3 on the 20-head large class for full
  * 1500-row windows, none otherwise).  The merge itself is computed in the
@@ -264,6 +265,15 @@ fwhip_status fwhip_encoder_set_exact(fwhip_encoder *enc, int32_t exact);
  * sequential f32), so in exact mode the whole forward stays bit-identical to
  * the reference's strict mode with the same FW_TOME_R. */
 fwhip_status fwhip_encoder_set_tome(fwhip_encoder *enc, int32_t r, int32_t after);
+
+/* Replaces FW_TOME_EVERY / FW_TOME_FLOOR (tome_every_layers / tome_floor,
+ * encoder.rs:1379-1402; defaults 0 and 128, the initial setting here).
+ * every = 0: the single-shot schedule (one merge after block `after`).
+ * every > 0: the progressive schedule, a merge after block `after` and again
+ * after every `every` blocks, the unmerge map composed through each merge
+ * (one unmerge before ln_post).  A merge is skipped when it would leave fewer
+ * than `floor` rows.  Negative values are FWHIP_ERR_INVALID. */
+fwhip_status fwhip_encoder_set_tome_schedule(fwhip_encoder *enc, int32_t every, int32_t floor);
 
 /* tome_merge of rows x_dev [n_windows, T, d] (f32) per window: merged rows
  * into merged_dev [n_windows, T - r', d] (r' = min(r, ceil(T/2), T - 1)) and

@@ -81,6 +81,8 @@ def lib():
         "ref_encoder_free": (None, [C.c_void_p]),
         "ref_encoder_forward": (C.c_int, [C.c_void_p, f32p, C.c_int, f32p, C.c_int]),
         "ref_encoder_forward_tome": (C.c_int, [C.c_void_p, f32p, C.c_int, f32p, C.c_int, C.c_int, C.c_int]),
+        "ref_encoder_forward_tome2": (C.c_int, [C.c_void_p, f32p, C.c_int, f32p, C.c_int, C.c_int, C.c_int,
+                                                C.c_int, C.c_int]),
         "ref_tome_merge": (C.c_int, [f32p, C.c_int, C.c_int, C.c_int, f32p, i32p]),
         "ref_tome_unmerge": (None, [f32p, i32p, C.c_int, C.c_int, f32p]),
         "ref_mel_window": (None, [f32p, C.c_int, C.c_int64, C.c_int64, C.c_int, f32p]),
@@ -365,14 +367,16 @@ class Encoder:
         self.h = lib().ref_encoder_new(C.byref(self.desc), precision)
         self.cfg = model.cfg
 
-    def forward(self, x_time_major, n_layers=-1, tome_r=0, tome_after=3):
+    def forward(self, x_time_major, n_layers=-1, tome_r=0, tome_after=3, tome_every=0, tome_floor=128):
         """forward_time_major; tome_r > 0 merges tome_r rows after block
-        tome_after (0-based), as FW_TOME_R / FW_TOME_LAYER do."""
+        tome_after (0-based), as FW_TOME_R / FW_TOME_LAYER do, and with
+        tome_every > 0 again after every tome_every blocks (FW_TOME_EVERY) while
+        the merged length stays >= tome_floor (FW_TOME_FLOOR)."""
         x = _c(x_time_major, np.float32)
         n_frames = x.shape[0]
         out = np.empty((n_frames // 2, self.cfg.n_audio_state), np.float32)
-        rc = lib().ref_encoder_forward_tome(self.h, _p(x, C.c_float), n_frames, _p(out, C.c_float),
-                                            n_layers, tome_r, tome_after)
+        rc = lib().ref_encoder_forward_tome2(self.h, _p(x, C.c_float), n_frames, _p(out, C.c_float),
+                                             n_layers, tome_r, tome_after, tome_every, tome_floor)
         if rc != 0:
             raise ValueError(f"ref_encoder_forward rc={rc}")
         return out

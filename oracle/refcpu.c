@@ -916,14 +916,21 @@ void ref_tome_unmerge(const float *merged, const int32_t *umap, int seq, int d, 
     for (int p = 0; p < seq; p++) memcpy(out + (size_t)p * d, merged + (size_t)umap[p] * d, sizeof(float) * d);
 }
 
-/* forward_time_major, encoder.rs:1520-1677 (CPU blocks).  ToMe (encoder.rs:
- * 1590-1632, single-shot schedule): with tome_r > 0, after block tome_after
- * (0-based) the rows merge by ref_tome_merge when seq > r + 2 and
- * seq - r >= 128 (the floor), the later blocks run on the merged rows and
- * ln_post follows the unmerge. */
-int ref_encoder_forward_tome(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run,
-                             int tome_r, int tome_after) {
+/* forward_time_major, encoder.rs:1520-1677 (CPU blocks), with the ToMe
+ * schedule of encoder.rs:1590-1632: with tome_r > 0 a merge is due after block
+ * li when
+ *   tome_every == 0 (single shot, FW_TOME_EVERY unset): no merge yet and
+ *     li == tome_after;
+ *   tome_every > 0 (progressive): li >= tome_after and (li - tome_after) is a
+ *     multiple of tome_every;
+ * and it runs (ref_tome_merge) when rows > r + 2 and rows - r >= tome_floor
+ * (FW_TOME_FLOOR, 128 by default).  The map from every original row to its
+ * current row is composed through each merge (cum[p] = umap[cum[p]]), so one
+ * unmerge before ln_post restores the full sequence. */
+int ref_encoder_forward_tome2(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run,
+                              int tome_r, int tome_after, int tome_every, int tome_floor) {
     if (n_frames <= 0 || n_frames % 2 || n_frames > 2 * e->nctx) return FWHIP_ERR_INVALID;
+    if (tome_every < 0 || tome_floor < 0) return FWHIP_ERR_INVALID;
     int d = e->d, t1, t2;
     float *a = (float *)malloc(sizeof(float) * (size_t)n_frames * d);
     conv1d_wt(x, n_frames, e->nmel, e->conv1_t, d, e->conv1_b, 1, a, &t1);
@@ -934,27 +941,49 @@ int ref_encoder_forward_tome(const ref_encoder *e, const float *x, int n_frames,
     for (int64_t r = 0; r < t2; r++)
         for (int j = 0; j < d; j++) out[r * d + j] += e->pos_emb[r * d + j];
     int n_run = n_layers_run < 0 || n_layers_run > e->L ? e->L : n_layers_run;
-    float *xm = NULL;
-    int32_t *umap = NULL;
-    int rows = t2;
+    /* cur: the current rows (out until the first merge); nxt: the next merge's
+     * output; cum: original row -> current row */
+    float *cur = out, *xa = NULL, *xb = NULL;
+    int32_t *cum = NULL, *step = NULL;
+    int rows = t2, n_merges = 0;
     for (int li = 0; li < n_run; li++) {
-        encoder_block(e, &e->layers[li], xm ? xm : out, rows);
-        if (tome_r > 0 && !xm && li == tome_after && rows > tome_r + 2 && rows - tome_r >= 128) {
-            xm = (float *)malloc(sizeof(float) * (size_t)t2 * d);
-            umap = (int32_t *)malloc(sizeof(int32_t) * t2);
-            rows = ref_tome_merge(out, t2, d, tome_r, xm, umap);
+        encoder_block(e, &e->layers[li], cur, rows);
+        int due = tome_every == 0 ? (n_merges == 0 && li == tome_after)
+                                  : (li >= tome_after && (li - tome_after) % tome_every == 0);
+        if (tome_r > 0 && due && rows > tome_r + 2 && rows - tome_r >= tome_floor) {
+            if (!xa) {
+                xa = (float *)malloc(sizeof(float) * (size_t)t2 * d);
+                xb = (float *)malloc(sizeof(float) * (size_t)t2 * d);
+                cum = (int32_t *)malloc(sizeof(int32_t) * t2);
+                step = (int32_t *)malloc(sizeof(int32_t) * t2);
+            }
+            float *nxt = cur == xa ? xb : xa;
+            int pre = rows;
+            rows = ref_tome_merge(cur, pre, d, tome_r, nxt, step);
+            if (n_merges == 0) memcpy(cum, step, sizeof(int32_t) * t2);
+            else
+                for (int p = 0; p < t2; p++) cum[p] = step[cum[p]];
+            cur = nxt;
+            n_merges++;
         }
     }
-    if (xm) {
-        ref_tome_unmerge(xm, umap, t2, d, out);
-        free(xm);
-        free(umap);
-    }
+    if (n_merges) ref_tome_unmerge(cur, cum, t2, d, out);
+    free(xa);
+    free(xb);
+    free(cum);
+    free(step);
     float *y = (float *)malloc(sizeof(float) * (size_t)t2 * d);
     ref_layer_norm(out, y, t2, d, e->ln_post_w, e->ln_post_b, LN_EPS);
     memcpy(out, y, sizeof(float) * (size_t)t2 * d);
     free(y);
     return FWHIP_OK;
+}
+
+/* the single-shot schedule with the default floor (FW_TOME_EVERY and
+ * FW_TOME_FLOOR unset) */
+int ref_encoder_forward_tome(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run,
+                             int tome_r, int tome_after) {
+    return ref_encoder_forward_tome2(e, x, n_frames, out, n_layers_run, tome_r, tome_after, 0, 128);
 }
 
 int ref_encoder_forward(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run) {

@@ -85,6 +85,8 @@ int ref_encoder_forward(const ref_encoder *e, const float *x, int n_frames, floa
                         int n_layers_run);
 int ref_encoder_forward_tome(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run,
                              int tome_r, int tome_after);
+int ref_encoder_forward_tome2(const ref_encoder *e, const float *x, int n_frames, float *out, int n_layers_run,
+                              int tome_r, int tome_after, int tome_every, int tome_floor);
 int ref_tome_merge(const float *x, int seq, int d, int r, float *merged, int32_t *umap);
 void ref_tome_unmerge(const float *merged, const int32_t *umap, int seq, int d, float *out);
 void ref_mel_window(const float *full_mel, int n_mel, int64_t mel_frames, int64_t frame_offset,

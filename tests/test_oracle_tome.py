@@ -178,3 +178,72 @@ def test_tome_planted_mistakes_are_detected(mutation):
     e = rel_maxabs(want, bad)
     print(f"{mutation}: max-abs {e:.2e}")
     assert e > 1e-2
+
+
+# ---- the progressive schedule (FW_TOME_EVERY / FW_TOME_FLOOR, encoder.rs:1379-1402, 1590-1632)
+# (cfg, r, after, every, floor, merges): TOME_MICRO has 400 rows and 3 blocks
+# (seed-5 input: every merge decision at least 1e-5 from a tie)
+PROG_CASES = [(TOME_MICRO, 50, 0, 1, 128, 3),   # after blocks 0, 1, 2: 400 -> 350 -> 300 -> 250
+              (TOME_MICRO, 60, 0, 1, 250, 2),   # the floor stops the third merge (220 < 250)
+              (TOME_MICRO, 60, 0, 2, 128, 2),   # after blocks 0 and 2
+              (TINY2, 300, 0, 1, 128, 2)]       # 1500 -> 1200 -> 900
+_pcache = {}
+
+
+def _prog(cfg, r, after, every, floor):
+    key = (cfg.name, r, after, every, floor)
+    if key not in _pcache:
+        m = synth.Model(cfg, seed=4, decoder=False)
+        x = synth.mel_input(5, 1, 2 * cfg.n_audio_ctx, cfg.n_mels)[0]
+        want = O.Encoder(m, abi.ENC_F32).forward(x, tome_r=r, tome_after=after, tome_every=every, tome_floor=floor)
+        _pcache[key] = (m, x, want)
+    return _pcache[key]
+
+
+@pytest.mark.parametrize("cfg,r,after,every,floor,merges", PROG_CASES,
+                         ids=lambda v: getattr(v, "name", str(v)))
+def test_encoder_tome_progressive_matches_textbook(cfg, r, after, every, floor, merges):
+    """The oracle's progressive schedule (each merge's map composed into the
+    original-row map, one unmerge) against the float64 textbook encoder, which
+    composes the maps with numpy indexing: the same merges, within 1e-3."""
+    m, x, want = _prog(cfg, r, after, every, floor)
+    info = {}
+    tb = TB.Encoder(m).forward(x, tome_r=r, tome_after=after, tome_every=every, tome_floor=floor, info=info)
+    print(f"{cfg.name} r={r} every={every} floor={floor}: {info['merges']} merges, rank margin "
+          f"{info['rank_margin']:.3e}, edge margin {info['edge_margin']:.3e}")
+    assert info["merges"] == merges
+    assert info["rank_margin"] > 1e-5 and info["edge_margin"] > 1e-5
+    e = rel_maxabs(want, tb)
+    print(f"  max-abs {e:.2e}")
+    assert e <= 1e-3
+    # the unmerged rows repeat each final row once per original row merged into
+    # it: T - merges * r distinct rows
+    assert np.unique(want, axis=0).shape[0] == cfg.n_audio_ctx - merges * r
+
+
+@pytest.mark.parametrize("mutation,case", [("tome_every_off_by_one", 2), ("tome_ignore_floor", 1)])
+def test_tome_progressive_planted_mistakes_are_detected(mutation, case):
+    cfg, r, after, every, floor, _ = PROG_CASES[case]
+    m, x, want = _prog(cfg, r, after, every, floor)
+    bad = TB.Encoder(m, TB.Numerics(mutate=mutation)).forward(x, tome_r=r, tome_after=after, tome_every=every,
+                                                               tome_floor=floor)
+    e = rel_maxabs(want, bad)
+    print(f"{mutation}: max-abs {e:.2e}")
+    assert e > 1e-2
+
+
+def test_tome_schedule_special_cases_are_exact():
+    """Closed cases of the schedule, bit for bit in the oracle: a progressive
+    cadence with no second due block is the single-shot schedule; a floor at
+    the full length never merges (the dense encoder); r = 0 never merges."""
+    cfg = TOME_MICRO
+    m = synth.Model(cfg, seed=4, decoder=False)
+    x = synth.mel_input(5, 1, 2 * cfg.n_audio_ctx, cfg.n_mels)[0]
+    enc = O.Encoder(m, abi.ENC_F32)
+    single = enc.forward(x, tome_r=60, tome_after=1)
+    assert np.array_equal(enc.forward(x, tome_r=60, tome_after=1, tome_every=5), single)
+    assert np.array_equal(enc.forward(x, tome_r=60, tome_after=1, tome_every=0, tome_floor=128), single)
+    dense = enc.forward(x)
+    assert np.array_equal(enc.forward(x, tome_r=60, tome_after=0, tome_every=1, tome_floor=cfg.n_audio_ctx), dense)
+    assert np.array_equal(enc.forward(x, tome_r=0, tome_after=0, tome_every=1), dense)
+    assert not np.array_equal(single, dense)

@@ -50,6 +50,8 @@ MUTATIONS = (
     "tome_no_average",    # ToMe adds merged rows into their partner without dividing by the count
     "tome_merge_lowest",  # ToMe merges the r least similar A rows instead of the most similar
     "tome_dot_not_cos",   # ToMe ranks by the raw dot product instead of the cosine
+    "tome_every_off_by_one",  # the progressive schedule merges one block after each due block
+    "tome_ignore_floor",  # the progressive schedule merges past the floor
 )
 
 
@@ -223,7 +225,12 @@ class Encoder:
         f = nm.gelu(self.linear(h, p + ".mlp.0", bias=not nm.m("no_fc1_bias")))
         return x + self.linear(f, p + ".mlp.2", bias=not nm.m("no_fc2_bias"))
 
-    def forward(self, mel_time_major, n_layers=None, tome_r=0, tome_after=3, info=None):
+    def forward(self, mel_time_major, n_layers=None, tome_r=0, tome_after=3, info=None, tome_every=0,
+                tome_floor=128):
+        """With tome_every > 0 the merge repeats after every tome_every blocks
+        from tome_after on (the ToMe paper's progressive schedule) while the
+        merged length stays >= tome_floor; the unmerge broadcasts each final
+        row to every original row that was merged into it."""
         nm = self.nm
         x = np.asarray(mel_time_major, np.float64)
         x = nm.gelu(self.conv(x, "encoder.conv1.weight", "encoder.conv1.bias", 1))
@@ -232,13 +239,21 @@ class Encoder:
             x = x + self._g("encoder.positional_embedding")[: x.shape[0]]
         L = self.cfg.n_audio_layer if n_layers is None else n_layers
         umap = None
+        n_merges = 0
+        floor = 0 if nm.m("tome_ignore_floor") else tome_floor
+        phase = 1 if nm.m("tome_every_off_by_one") else 0
         for i in range(L):
             x = self.block(x, i)
-            if tome_r > 0 and umap is None and i == tome_after and x.shape[0] > tome_r + 2 \
-                    and x.shape[0] - tome_r >= 128:
-                x, umap, tinfo = tome_merge(x, tome_r, nm)
+            due = (umap is None and i == tome_after) if tome_every == 0 else \
+                (i >= tome_after and (i - tome_after) % tome_every == phase)
+            if tome_r > 0 and due and x.shape[0] > tome_r + 2 and x.shape[0] - tome_r >= floor:
+                x, step, tinfo = tome_merge(x, tome_r, nm)
+                umap = step if umap is None else step[umap]  # original row -> current row
+                n_merges += 1
                 if info is not None:
-                    info.update(tinfo)
+                    info["rank_margin"] = min(info.get("rank_margin", np.inf), tinfo["rank_margin"])
+                    info["edge_margin"] = min(info.get("edge_margin", np.inf), tinfo["edge_margin"])
+                    info["merges"] = n_merges
         if umap is not None:
             x = x[umap]
         if nm.m("no_ln_post"):
