@@ -57,6 +57,8 @@ def _args():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--workload", default="job",
                    choices=["job", "enc-f32", "enc-int8", "decode", "step", "tiny", "copy", "load", "transcribe"])
+    p.add_argument("--kv", default="f16", choices=["f16", "f32"],
+                   help="decoder self-attention cache: f16 (FW_KV_F16) or f32 (the reference's default)")
     p.add_argument("--depths", default="0,64,224,447",
                    help="step workload: KV-cache depths at which one token per stream is stepped")
     p.add_argument("--windows", type=int, default=None)
@@ -383,6 +385,7 @@ def step_workload(a):
     dec = native.Decoder(ctx, model, arm)
     if a.exact:
         dec.set_exact(True)
+    dec.set_kv_f16(a.kv == "f16")
     st = dec.state(S, cfg.n_audio_ctx)
     st.set_cross(ctx.array(synth.encoder_states(77, S, cfg.n_audio_ctx, cfg.n_audio_state)))
     toks = synth.uniform_i32(5, "step_tokens", 0, cfg.n_vocab, S * cfg.n_text_ctx).reshape(S, cfg.n_text_ctx)
@@ -429,7 +432,7 @@ def step_workload(a):
            "ms_per_step": round(mean_us * 1e-3, 4), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "f16" if a.dec_arm == "f16" else "int8+f32",
            "data": "synthetic (seeded random-init weights N(0,0.02), seeded N(0,1) encoder states, seeded tokens)",
-           "config": {"workload": f"large-v3-turbo decoder step, {S} stream(s), {a.dec_arm} arm, f16 KV cache "
+           "config": {"workload": f"large-v3-turbo decoder step, {S} stream(s), {a.dec_arm} arm, {a.kv} KV cache "
                                   f"filled to depth L in {depths}, logits + argmax", "streams": S, "depths": depths,
                       "mode": "exact" if a.exact else "fast"},
            "roofline": {"kernel": f"decoder step at depth {top['depth']} (forward, logits, argmax; direct launches)",
@@ -632,6 +635,7 @@ def main():
         dec = native.Decoder(ctx, model, abi.DEC_INT8 if a.dec_arm == "int8" else abi.DEC_F16)
         if a.exact:
             dec.set_exact(True)
+        dec.set_kv_f16(a.kv == "f16")
         st = dec.state(W, cfg.n_audio_ctx)
         if a.workload == "decode":
             enc_out.upload(synth.encoder_states(77, W, cfg.n_audio_ctx, cfg.n_audio_state))
@@ -826,7 +830,7 @@ def main():
         out["unit"] = "tok/s"
         out["value"] = round(tokens_out[0] / (ms_per_step * 1e-3), 1)
         out["config"] = {"workload": f"large-v3-turbo decoder: {W} streams, prompt + {a.tokens} greedy steps, "
-                                     f"{a.dec_arm} arm, f16 KV cache", "streams": W}
+                                     f"{a.dec_arm} arm, {a.kv} KV cache", "streams": W}
     enc_ms = comp.get("encoder_ms")
     out["enc_tflops"] = round(ENC_GOP_PER_WINDOW * W / enc_ms, 1) if enc_ms else None
     if "decode_ms" in comp:

@@ -1535,7 +1535,25 @@ void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float 
 // sum_j p[j] * v[j*64 + t] (f16 values) in ascending j, one f32 chain per
 // thread (the attention value pass of one output column); the operands of 32
 // keys are read before their adds, so LDS latency is paid once per 32 keys.
-__device__ __forceinline__ float fw_pv_chain(const float *p, const uint16_t *v, int tk, int t) {
+// The self-attention KV cache element: f16 (FW_KV_F16: the row rounded to
+// f16 on append, read back exactly) or f32 (the reference's default cache, the
+// row as computed).  Attention reads either as f32 with the same arithmetic
+// (attention_decode_step / _f16, nn.rs:6340-6523).
+template <typename KV>
+struct KvT;
+template <>
+struct KvT<uint16_t> {
+    static __device__ __forceinline__ float val(uint16_t x) { return fw_h2f(x); }
+    static __device__ __forceinline__ void put(uint16_t *p, size_t i, float v) { p[i] = fw_f2h(v); }
+};
+template <>
+struct KvT<float> {
+    static __device__ __forceinline__ float val(float x) { return x; }
+    static __device__ __forceinline__ void put(float *p, size_t i, float v) { p[i] = v; }
+};
+
+template <typename KV>
+__device__ __forceinline__ float fw_pv_chain(const float *p, const KV *v, int tk, int t) {
     float acc = 0.0f;
     int j = 0;
     for (; j + 32 <= tk; j += 32) {
@@ -1543,7 +1561,7 @@ __device__ __forceinline__ float fw_pv_chain(const float *p, const uint16_t *v, 
 #pragma unroll
         for (int u = 0; u < 32; u++) {
             pv[u] = p[j + u];
-            vv[u] = fw_h2f(v[(j + u) * 64 + t]);
+            vv[u] = KvT<KV>::val(v[(j + u) * 64 + t]);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1554,12 +1572,12 @@ __device__ __forceinline__ float fw_pv_chain(const float *p, const uint16_t *v, 
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             pv[u] = p[j + u];
-            vv[u] = fw_h2f(v[(j + u) * 64 + t]);
+            vv[u] = KvT<KV>::val(v[(j + u) * 64 + t]);
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) acc += pv[u] * vv[u];
     }
-    for (; j < tk; j++) acc += p[j] * fw_h2f(v[j * 64 + t]);
+    for (; j < tk; j++) acc += p[j] * KvT<KV>::val(v[j * 64 + t]);
     return acc;
 }
 
@@ -1573,51 +1591,67 @@ __device__ __forceinline__ float fw_pv_chain(const float *p, const uint16_t *v, 
 // for the scores; the cache rows of this head are staged in LDS for the
 // value pass.
 #define SA_STG 4
-// The attention of one (head, stream) over cache rows [0, tk) once the
-// token's own row is in the cache and qh (= q * s, LDS) is set; NT threads.
-template <int NT>
-__device__ __forceinline__ void sa_attend(const float *qh, const uint16_t *kc, const uint16_t *vc, size_t cbase,
-                                          int base, int d, int tk, float scale, float *sc, uint16_t *vs, float *red,
-                                          float *inv_s, float *out, float *pmax_slot) {
-    const int t = threadIdx.x;
-    // this thread's first key row is requested ahead of the value rows (clamped
-    // address, used when t < tk), so keys and values share one round trip
-    uint4 kpre[8];
-    {
-        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)(t < tk ? t : tk - 1) * d + base);
+// A head's cache row is KW 16-byte chunks (8 for f16, 16 for f32)
+template <typename KV>
+struct SaRow {
+    static constexpr int KW = 64 * (int)sizeof(KV) / 16, EPC = 16 / (int)sizeof(KV);
+};
+// score = sequential sum over the head's 64 dims of qh[i] * (k[i] * s)
+// (attention_decode_step / _f16, nn.rs:6340-6523)
+template <typename KV>
+__device__ __forceinline__ float sa_score(const float *qh, const uint4 (&kk)[SaRow<KV>::KW], float scale) {
+    float acc = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 8; c++) kpre[c] = kr[c];
-    }
-    // stage V rows [0, tk) of this head (8 x 16 bytes per row), SA_STG chunks
-    // per thread per round, loads issued before the LDS stores
-    for (int c0 = 0; c0 < tk * 8; c0 += NT * SA_STG) {
-        uint4 v[SA_STG];
-#pragma unroll
-        for (int u = 0; u < SA_STG; u++) {
-            int c = c0 + t + u * NT;
-            int cc = c < tk * 8 ? c : tk * 8 - 1;
-            v[u] = *(const uint4 *)(vc + cbase + (size_t)(cc >> 3) * d + base + (cc & 7) * 8);
-        }
-#pragma unroll
-        for (int u = 0; u < SA_STG; u++) {
-            int c = c0 + t + u * NT;
-            if (c < tk * 8) *(uint4 *)(vs + (c >> 3) * 64 + (c & 7) * 8) = v[u];
-        }
-    }
-    float mx = -INFINITY;
-    auto score = [&](const uint4 (&kk)[8]) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const uint32_t ww[4] = {kk[c].x, kk[c].y, kk[c].z, kk[c].w};
+    for (int c = 0; c < SaRow<KV>::KW; c++) {
+        const uint32_t ww[4] = {kk[c].x, kk[c].y, kk[c].z, kk[c].w};
+        if constexpr (sizeof(KV) == 2) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 acc += qh[c * 8 + 2 * e] * (fw_h2f(ww[e] & 0xffff) * scale);
                 acc += qh[c * 8 + 2 * e + 1] * (fw_h2f(ww[e] >> 16) * scale);
             }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc += qh[c * 4 + e] * (__uint_as_float(ww[e]) * scale);
         }
-        return acc;
-    };
+    }
+    return acc;
+}
+
+// The attention of one (head, stream) over cache rows [0, tk) once the
+// token's own row is in the cache and qh (= q * s, LDS) is set; NT threads.
+template <int NT, typename KV>
+__device__ __forceinline__ void sa_attend(const float *qh, const KV *kc, const KV *vc, size_t cbase, int base, int d,
+                                          int tk, float scale, float *sc, KV *vs, float *red, float *inv_s,
+                                          float *out, float *pmax_slot) {
+    constexpr int KW = SaRow<KV>::KW, EPC = SaRow<KV>::EPC;
+    const int t = threadIdx.x;
+    // this thread's first key row is requested ahead of the value rows (clamped
+    // address, used when t < tk), so keys and values share one round trip
+    uint4 kpre[KW];
+    {
+        const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)(t < tk ? t : tk - 1) * d + base);
+#pragma unroll
+        for (int c = 0; c < KW; c++) kpre[c] = kr[c];
+    }
+    // stage V rows [0, tk) of this head (KW x 16 bytes per row), SA_STG chunks
+    // per thread per round, loads issued before the LDS stores
+    for (int c0 = 0; c0 < tk * KW; c0 += NT * SA_STG) {
+        uint4 v[SA_STG];
+#pragma unroll
+        for (int u = 0; u < SA_STG; u++) {
+            int c = c0 + t + u * NT;
+            int cc = c < tk * KW ? c : tk * KW - 1;
+            v[u] = *(const uint4 *)(vc + cbase + (size_t)((unsigned)cc / KW) * d + base + ((unsigned)cc % KW) * EPC);
+        }
+#pragma unroll
+        for (int u = 0; u < SA_STG; u++) {
+            int c = c0 + t + u * NT;
+            if (c < tk * KW) ((uint4 *)vs)[c] = v[u];
+        }
+    }
+    float mx = -INFINITY;
+    auto score = [&](const uint4 (&kk)[KW]) { return sa_score<KV>(qh, kk, scale); };
     if (t < tk) {
         const float acc = score(kpre);
         sc[t] = acc;
@@ -1625,9 +1659,9 @@ __device__ __forceinline__ void sa_attend(const float *qh, const uint16_t *kc, c
     }
     for (int j = t + NT; j < tk; j += NT) {
         const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)j * d + base);
-        uint4 kk[8];
+        uint4 kk[KW];
 #pragma unroll
-        for (int c = 0; c < 8; c++) kk[c] = kr[c];
+        for (int c = 0; c < KW; c++) kk[c] = kr[c];
         const float acc = score(kk);
         sc[j] = acc;
         mx = fmaxf(mx, acc);
@@ -1660,12 +1694,13 @@ __device__ __forceinline__ void sa_attend(const float *qh, const uint16_t *kc, c
 // `append` the row's own k/v go into the cache first; a prefill chunk appends
 // every row beforehand (k_kv_append16), so a row sees the earlier rows of its
 // chunk.
-__global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *kc, uint16_t *vc, float *att,
-                                                    const int *posp, int d, int nctx, int L, int layer,
-                                                    float scale, float *pmax, int ns, int append) {
+template <typename KV>
+__global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, KV *kc, KV *vc, float *att, const int *posp,
+                                                    int d, int nctx, int L, int layer, float scale, float *pmax,
+                                                    int ns, int append) {
     extern __shared__ __align__(16) unsigned char sm2[];
-    float *sc = (float *)sm2;                               // [nctx]
-    uint16_t *vs = (uint16_t *)(sm2 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
+    float *sc = (float *)sm2;                                    // [nctx]
+    KV *vs = (KV *)(sm2 + sizeof(float) * ((nctx + 3) & ~3));   // [nctx][64]
     __shared__ float qh[64];
     __shared__ float red[4];
     __shared__ float inv_s;
@@ -1676,27 +1711,28 @@ __global__ void __launch_bounds__(256) k_self_attn2(const float *qkv, uint16_t *
     const size_t cbase = ((size_t)s * L + layer) * nctx * d;
     if (t < 64) {
         if (append) {
-            uint16_t kh = fw_f2h(q[d + base + t]), vh = fw_f2h(q[2 * d + base + t]);
-            kc[cbase + (size_t)pos * d + base + t] = kh;
-            vc[cbase + (size_t)pos * d + base + t] = vh;
+            KvT<KV>::put(kc, cbase + (size_t)pos * d + base + t, q[d + base + t]);
+            KvT<KV>::put(vc, cbase + (size_t)pos * d + base + t, q[2 * d + base + t]);
         }
         qh[t] = q[base + t] * scale;
     }
     __syncthreads(); // this block's own cache row is visible to its threads
-    sa_attend<256>(qh, kc, vc, cbase, base, d, pos + 1, scale, sc, vs, red, &inv_s, att + (size_t)r * d + base,
+    sa_attend<256, KV>(qh, kc, vc, cbase, base, d, pos + 1, scale, sc, vs, red, &inv_s, att + (size_t)r * d + base,
                    pmax ? pmax + (size_t)r * gridDim.x + h : nullptr);
 }
 
-// The k/v of every row of a prefill chunk into the f16 cache (KvCache::append,
-// nn.rs:5352-5416: RNE to f16), row r = stream r % ns at position *posp + r / ns.
-__global__ void __launch_bounds__(256) k_kv_append16(const float *qkv, uint16_t *kc, uint16_t *vc, const int *posp,
-                                                     int d, int nctx, int L, int layer, int ns) {
+// The k/v of every row of a prefill chunk into the cache (KvCache::append,
+// nn.rs:5352-5416: RNE to f16 for an f16 cache), row r = stream r % ns at
+// position *posp + r / ns.
+template <typename KV>
+__global__ void __launch_bounds__(256) k_kv_append(const float *qkv, KV *kc, KV *vc, const int *posp, int d, int nctx,
+                                                   int L, int layer, int ns) {
     const int r = blockIdx.x, s = r % ns, pos = *posp + r / ns;
     const float *q = qkv + (size_t)r * 3 * d;
     const size_t o = ((size_t)s * L + layer) * nctx * d + (size_t)pos * d;
     for (int c = threadIdx.x; c < d; c += 256) {
-        kc[o + c] = fw_f2h(q[d + c]);
-        vc[o + c] = fw_f2h(q[2 * d + c]);
+        KvT<KV>::put(kc, o + c, q[d + c]);
+        KvT<KV>::put(vc, o + c, q[2 * d + c]);
     }
 }
 
@@ -1717,19 +1753,19 @@ __global__ void __launch_bounds__(256) k_kv_append16(const float *qkv, uint16_t 
 // EMB (layer 0): the row is first formed as the token embedding
 // f16(emb[tok]) + pemb[pos] (embed_tokens, decoder.rs:1323-1385, k_embed_ln's
 // arithmetic) and the head-0 block stores it to xo, the residual.
-template <bool LN, bool EMB, bool SEQ>
+template <bool LN, bool EMB, bool SEQ, typename KV>
 __global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restrict__ wqkv,
                                                         const float *__restrict__ bqkv, const float *__restrict__ x,
                                                         const float *__restrict__ lnw, const float *__restrict__ lnb,
-                                                        uint16_t *kc, uint16_t *vc, float *att, const int *posp,
+                                                        KV *kc, KV *vc, float *att, const int *posp,
                                                         int nctx, int L, int layer, float scale,
                                                         const int32_t *__restrict__ tok,
                                                         const uint16_t *__restrict__ emb,
                                                         const float *__restrict__ pemb, float *xo) {
     constexpr int D = XQ_D, NV = D / 256, G = D / 128, NC = D / 32;
     extern __shared__ __align__(16) unsigned char sm4[];
-    float *sc = (float *)sm4;                                              // [nctx]
-    uint16_t *vs = (uint16_t *)(sm4 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
+    float *sc = (float *)sm4;                                  // [nctx]
+    KV *vs = (KV *)(sm4 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
     __shared__ __align__(16) float xl[D];
     __shared__ float qkvl[192];
     __shared__ float qh[64];
@@ -1820,13 +1856,13 @@ __global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restri
     const int pos = *posp;
     const size_t cbase = ((size_t)s * L + layer) * nctx * D;
     if (t < 64) {
-        kc[cbase + (size_t)pos * D + base + t] = fw_f2h(qkvl[64 + t]);
-        vc[cbase + (size_t)pos * D + base + t] = fw_f2h(qkvl[128 + t]);
+        KvT<KV>::put(kc, cbase + (size_t)pos * D + base + t, qkvl[64 + t]);
+        KvT<KV>::put(vc, cbase + (size_t)pos * D + base + t, qkvl[128 + t]);
         qh[t] = qkvl[t] * scale;
     }
     __threadfence_block();
     __syncthreads(); // this block's own cache row is visible to its threads
-    sa_attend<512>(qh, kc, vc, cbase, base, D, pos + 1, scale, sc, vs, red, &inv_s, att + (size_t)s * D + base,
+    sa_attend<512, KV>(qh, kc, vc, cbase, base, D, pos + 1, scale, sc, vs, red, &inv_s, att + (size_t)s * D + base,
                    nullptr);
 }
 
@@ -1846,16 +1882,16 @@ __global__ void __launch_bounds__(512) k_self_attn_f16q(const uint16_t *__restri
 // EMB (layer 0): the residual row is the token embedding first (embed_tokens,
 // decoder.rs:1323-1385: x = f16(E[tok]) + P[pos], as k_embed_ln), which every
 // block forms for its stream and the head-0 block also stores as x.
-template <int NV, bool EMB, bool SEQ>
+template <int NV, bool EMB, bool SEQ, typename KV>
 __global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restrict__ wqkv, const float *__restrict__ sqkv,
                                                          const float *__restrict__ bqkv, float *x,
                                                          const float *__restrict__ lnw, const float *__restrict__ lnb,
-                                                         uint16_t *kc, uint16_t *vc, float *att, const int *posp, int d,
-                                                         int nctx, int L, int layer, float scale, float *pmax,
-                                                         const int32_t *tok, const uint16_t *emb, const float *pemb) {
+                                                         KV *kc, KV *vc, float *att, const int *posp, int d, int nctx,
+                                                         int L, int layer, float scale, float *pmax, const int32_t *tok,
+                                                         const uint16_t *emb, const float *pemb) {
     extern __shared__ __align__(16) unsigned char sm3[];
-    float *sc = (float *)sm3;                                              // [nctx]
-    uint16_t *vs = (uint16_t *)(sm3 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
+    float *sc = (float *)sm3;                                  // [nctx]
+    KV *vs = (KV *)(sm3 + sizeof(float) * ((nctx + 3) & ~3)); // [nctx][64]
     __shared__ float qkvl[192];
     __shared__ float qh[64];
     __shared__ __align__(16) int8_t xql[256 * NV];
@@ -1962,42 +1998,36 @@ __global__ void __launch_bounds__(512) k_self_attn_fused(const int8_t *__restric
     __syncthreads();
     const size_t cbase = ((size_t)s * L + layer) * nctx * d;
     if (t < 64) {
-        kc[cbase + (size_t)pos * d + base + t] = fw_f2h(qkvl[64 + t]);
-        vc[cbase + (size_t)pos * d + base + t] = fw_f2h(qkvl[128 + t]);
+        KvT<KV>::put(kc, cbase + (size_t)pos * d + base + t, qkvl[64 + t]);
+        KvT<KV>::put(vc, cbase + (size_t)pos * d + base + t, qkvl[128 + t]);
         qh[t] = qkvl[t] * scale;
     }
     __syncthreads(); // this block's own cache row is visible to its threads
+    constexpr int KW = SaRow<KV>::KW, EPC = SaRow<KV>::EPC;
     const int tk = pos + 1;
-    // stage V rows [0, tk) of this head (8 x 16 bytes per row), loads issued
+    // stage V rows [0, tk) of this head (KW x 16 bytes per row), loads issued
     // before the LDS stores
-    for (int c0 = 0; c0 < tk * 8; c0 += 512 * 2) {
+    for (int c0 = 0; c0 < tk * KW; c0 += 512 * 2) {
         uint4 v[2];
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             int c = c0 + t + u * 512;
-            int cc = c < tk * 8 ? c : tk * 8 - 1;
-            v[u] = *(const uint4 *)(vc + cbase + (size_t)(cc >> 3) * d + base + (cc & 7) * 8);
+            int cc = c < tk * KW ? c : tk * KW - 1;
+            v[u] = *(const uint4 *)(vc + cbase + (size_t)((unsigned)cc / KW) * d + base + ((unsigned)cc % KW) * EPC);
         }
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             int c = c0 + t + u * 512;
-            if (c < tk * 8) *(uint4 *)(vs + (c >> 3) * 64 + (c & 7) * 8) = v[u];
+            if (c < tk * KW) ((uint4 *)vs)[c] = v[u];
         }
     }
     float mx = -INFINITY;
     for (int j = t; j < tk; j += 512) {
         const uint4 *kr = (const uint4 *)(kc + cbase + (size_t)j * d + base);
-        float acc = 0.0f;
+        uint4 kk[KW];
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            uint4 u = kr[c];
-            uint32_t ww[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                acc += qh[c * 8 + 2 * e] * (fw_h2f(ww[e] & 0xffff) * scale);
-                acc += qh[c * 8 + 2 * e + 1] * (fw_h2f(ww[e] >> 16) * scale);
-            }
-        }
+        for (int c = 0; c < KW; c++) kk[c] = kr[c];
+        const float acc = sa_score<KV>(qh, kk, scale);
         sc[j] = acc;
         mx = fmaxf(mx, acc);
     }
@@ -2449,17 +2479,31 @@ int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const 
     return 0;
 }
 
-void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
-                          int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax, int rows,
-                          int append) {
-    size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
-    hipLaunchKernelGGL(k_self_attn2, dim3(H, rows > 0 ? rows : ns), dim3(256), shm, st, qkv, kc, vc, att, posp, d,
-                       nctx, L, layer, scale, pmax, ns, append);
+// LDS of the self-attention blocks: the scores [nctx] and the head's V rows [nctx][64]
+static size_t sa_shm(int nctx, int kv32) {
+    return sizeof(float) * (size_t)((nctx + 3) & ~3) + (kv32 ? 4 : 2) * 64 * (size_t)nctx;
 }
 
-void fw_launch_kv_append16(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, const int *posp, int d,
-                           int nctx, int L, int layer, int ns, int rows) {
-    hipLaunchKernelGGL(k_kv_append16, dim3(rows), dim3(256), 0, st, qkv, kc, vc, posp, d, nctx, L, layer, ns);
+void fw_launch_self_attn2(hipStream_t st, const float *qkv, void *kc, void *vc, float *att, const int *posp, int d,
+                          int H, int nctx, int L, int layer, int ns, float scale, float *pmax, int rows, int append,
+                          int kv32) {
+    const dim3 g(H, rows > 0 ? rows : ns);
+    if (kv32)
+        hipLaunchKernelGGL(k_self_attn2<float>, g, dim3(256), sa_shm(nctx, 1), st, qkv, (float *)kc, (float *)vc, att,
+                           posp, d, nctx, L, layer, scale, pmax, ns, append);
+    else
+        hipLaunchKernelGGL(k_self_attn2<uint16_t>, g, dim3(256), sa_shm(nctx, 0), st, qkv, (uint16_t *)kc,
+                           (uint16_t *)vc, att, posp, d, nctx, L, layer, scale, pmax, ns, append);
+}
+
+void fw_launch_kv_append(hipStream_t st, const float *qkv, void *kc, void *vc, const int *posp, int d, int nctx,
+                         int L, int layer, int ns, int rows, int kv32) {
+    if (kv32)
+        hipLaunchKernelGGL(k_kv_append<float>, dim3(rows), dim3(256), 0, st, qkv, (float *)kc, (float *)vc, posp, d,
+                           nctx, L, layer, ns);
+    else
+        hipLaunchKernelGGL(k_kv_append<uint16_t>, dim3(rows), dim3(256), 0, st, qkv, (uint16_t *)kc, (uint16_t *)vc,
+                           posp, d, nctx, L, layer, ns);
 }
 
 bool fw_self_attn_f16q_ok(int d, int H) { return d == XQ_D && H * 64 == d; }
@@ -2467,14 +2511,15 @@ bool fw_self_attn_f16q_ok(int d, int H) { return d == XQ_D && H * 64 == d; }
 // q/k/v projection (wqkv in fw_launch_pack_gemv16's slot order at 16 lanes per
 // row, bias bqkv) of LN(x) (or of x itself when lnw is null: an already
 // normalized row) and the self-attention of k_self_attn2, one launch
-void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
-                              const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
-                              const int *posp, int H, int nctx, int L, int layer, int ns, float scale,
-                              const int32_t *tok, const uint16_t *emb, const float *pemb, float *xo, int lnseq) {
-    size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
+template <typename KV>
+static void launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
+                                  const float *lnw, const float *lnb, KV *kc, KV *vc, float *att, const int *posp,
+                                  int H, int nctx, int L, int layer, int ns, float scale, const int32_t *tok,
+                                  const uint16_t *emb, const float *pemb, float *xo, int lnseq) {
+    const size_t shm = sa_shm(nctx, sizeof(KV) == 4);
 #define SAQ(LN_, EMB_, SEQ_, ...)                                                                                     \
-    hipLaunchKernelGGL((k_self_attn_f16q<LN_, EMB_, SEQ_>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw, lnb, \
-                       kc, vc, att, posp, nctx, L, layer, scale, __VA_ARGS__)
+    hipLaunchKernelGGL((k_self_attn_f16q<LN_, EMB_, SEQ_, KV>), dim3(H, ns), dim3(512), shm, st, wqkv, bqkv, x, lnw,   \
+                       lnb, kc, vc, att, posp, nctx, L, layer, scale, __VA_ARGS__)
     if (tok && lnseq) SAQ(true, true, true, tok, emb, pemb, xo);
     else if (tok) SAQ(true, true, false, tok, emb, pemb, xo);
     else if (lnw && lnseq) SAQ(true, false, true, nullptr, nullptr, nullptr, nullptr);
@@ -2483,35 +2528,62 @@ void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float 
 #undef SAQ
 }
 
-template <int NV>
+void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
+                              const float *lnw, const float *lnb, void *kc, void *vc, float *att,
+                              const int *posp, int H, int nctx, int L, int layer, int ns, float scale,
+                              const int32_t *tok, const uint16_t *emb, const float *pemb, float *xo, int lnseq,
+                              int kv32) {
+    if (kv32)
+        launch_self_attn_f16q(st, wqkv, bqkv, x, lnw, lnb, (float *)kc, (float *)vc, att, posp, H, nctx, L, layer, ns,
+                              scale, tok, emb, pemb, xo, lnseq);
+    else
+        launch_self_attn_f16q(st, wqkv, bqkv, x, lnw, lnb, (uint16_t *)kc, (uint16_t *)vc, att, posp, H, nctx, L,
+                              layer, ns, scale, tok, emb, pemb, xo, lnseq);
+}
+
+template <int NV, typename KV>
 using k_self_attn_fused_e = void (*)(const int8_t *, const float *, const float *, float *, const float *,
-                                     const float *, uint16_t *, uint16_t *, float *, const int *, int, int, int, int,
-                                     float, float *, const int32_t *, const uint16_t *, const float *);
+                                     const float *, KV *, KV *, float *, const int *, int, int, int, int, float,
+                                     float *, const int32_t *, const uint16_t *, const float *);
+template <int NV, typename KV>
+static void launch_self_attn_fused_t(hipStream_t st, bool embed, dim3 grid, const int8_t *wqkv, const float *sqkv,
+                                     const float *bqkv, float *x, const float *lnw, const float *lnb, KV *kc, KV *vc,
+                                     float *att, const int *posp, int d, int nctx, int L, int layer, float scale,
+                                     float *pmax, const int32_t *tok, const uint16_t *emb, const float *pemb,
+                                     int lnseq) {
+    const k_self_attn_fused_e<NV, KV> k = embed ? (lnseq ? k_self_attn_fused<NV, true, true, KV>
+                                                         : k_self_attn_fused<NV, true, false, KV>)
+                                                : (lnseq ? k_self_attn_fused<NV, false, true, KV>
+                                                         : k_self_attn_fused<NV, false, false, KV>);
+    hipLaunchKernelGGL(k, grid, dim3(512), sa_shm(nctx, sizeof(KV) == 4), st, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc,
+                       att, posp, d, nctx, L, layer, scale, pmax, tok, emb, pemb);
+}
 template <int NV>
-static void launch_self_attn_fused(hipStream_t st, bool embed, dim3 grid, size_t shm, const int8_t *wqkv,
+static void launch_self_attn_fused(hipStream_t st, bool embed, dim3 grid, int kv32, const int8_t *wqkv,
                                    const float *sqkv, const float *bqkv, float *x, const float *lnw,
-                                   const float *lnb, uint16_t *kc, uint16_t *vc, float *att, const int *posp, int d,
+                                   const float *lnb, void *kc, void *vc, float *att, const int *posp, int d,
                                    int nctx, int L, int layer, float scale, float *pmax, const int32_t *tok,
                                    const uint16_t *emb, const float *pemb, int lnseq) {
-    const k_self_attn_fused_e<NV> k = embed ? (lnseq ? k_self_attn_fused<NV, true, true>
-                                                     : k_self_attn_fused<NV, true, false>)
-                                            : (lnseq ? k_self_attn_fused<NV, false, true>
-                                                     : k_self_attn_fused<NV, false, false>);
-    hipLaunchKernelGGL(k, grid, dim3(512), shm, st, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,
-                       layer, scale, pmax, tok, emb, pemb);
+    if (kv32)
+        launch_self_attn_fused_t<NV, float>(st, embed, grid, wqkv, sqkv, bqkv, x, lnw, lnb, (float *)kc, (float *)vc,
+                                            att, posp, d, nctx, L, layer, scale, pmax, tok, emb, pemb, lnseq);
+    else
+        launch_self_attn_fused_t<NV, uint16_t>(st, embed, grid, wqkv, sqkv, bqkv, x, lnw, lnb, (uint16_t *)kc,
+                                               (uint16_t *)vc, att, posp, d, nctx, L, layer, scale, pmax, tok, emb,
+                                               pemb, lnseq);
 }
 
 void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *sqkv, const float *bqkv, float *x,
-                               const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
+                               const float *lnw, const float *lnb, void *kc, void *vc, float *att,
                                const int *posp, int d, int H, int nctx, int L, int layer, int ns, float scale,
-                               float *pmax, const int32_t *tok, const uint16_t *emb, const float *pemb, int lnseq) {
-    size_t shm = sizeof(float) * (size_t)((nctx + 3) & ~3) + sizeof(uint16_t) * 64 * (size_t)nctx;
+                               float *pmax, const int32_t *tok, const uint16_t *emb, const float *pemb, int lnseq,
+                               int kv32) {
     const bool e = emb != nullptr;
     const dim3 grid(H, ns);
     switch ((d + 255) / 256) {
 #define SAF(NV)                                                                                                      \
     case NV:                                                                                                         \
-        launch_self_attn_fused<NV>(st, e, grid, shm, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,    \
+        launch_self_attn_fused<NV>(st, e, grid, kv32, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,   \
                                    layer, scale, pmax, tok, emb, pemb, lnseq);                                        \
         break;
         SAF(1)
@@ -2521,8 +2593,8 @@ void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *
         SAF(5)
         SAF(6)
         SAF(7)
-    default: launch_self_attn_fused<8>(st, e, grid, shm, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx, L,
-                                       layer, scale, pmax, tok, emb, pemb, lnseq);
+    default: launch_self_attn_fused<8>(st, e, grid, kv32, wqkv, sqkv, bqkv, x, lnw, lnb, kc, vc, att, posp, d, nctx,
+                                       L, layer, scale, pmax, tok, emb, pemb, lnseq);
         break;
 #undef SAF
     }

@@ -70,11 +70,13 @@ void fw_launch_cross_attn_f16pq_split(hipStream_t st, const uint16_t *wq, const 
 // tok (layer 0, lnw given) the rows are the token embeddings f16(emb[tok]) +
 // pemb[*posp], stored to xo (x unused).
 bool fw_self_attn_f16q_ok(int d, int H);
+// (kc / vc: the self-attention caches, f16 or, with kv32, f32, in every
+// launcher that takes them)
 void fw_launch_self_attn_f16q(hipStream_t st, const uint16_t *wqkv, const float *bqkv, const float *x,
-                              const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
+                              const float *lnw, const float *lnb, void *kc, void *vc, float *att,
                               const int *posp, int H, int nctx, int L, int layer, int ns, float scale,
                               const int32_t *tok = nullptr, const uint16_t *emb = nullptr,
-                              const float *pemb = nullptr, float *xo = nullptr, int lnseq = 0);
+                              const float *pemb = nullptr, float *xo = nullptr, int lnseq = 0, int kv32 = 0);
 bool fw_cross_f16pq_ok(int d, int T, int H);
 void fw_launch_cross_attn_f16pq(hipStream_t st, const uint16_t *wq, const float *bq, const float *x, const float *lnw,
                                 const float *lnb, const uint16_t *ckp, const uint16_t *cvtp, float *att, int d, int T,
@@ -154,23 +156,23 @@ int fw_launch_gemv_blk2(hipStream_t st, const int8_t *W, const float *sc, const 
 // pmax (nullable): [ns, H] max |output| of each head block, for a consumer
 // that quantizes the rows itself (fw_launch_gemv_i8m with xf)
 // rows > 0: a prefill chunk of `rows` rows, row r = stream r % ns at position
-// *posp + r / ns, its k/v already appended (append = 0, fw_launch_kv_append16)
-void fw_launch_self_attn2(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, float *att, const int *posp,
-                          int d, int H, int nctx, int L, int layer, int ns, float scale, float *pmax = nullptr,
-                          int rows = 0, int append = 1);
-// the k/v of every row of a prefill chunk into the f16 caches
-void fw_launch_kv_append16(hipStream_t st, const float *qkv, uint16_t *kc, uint16_t *vc, const int *posp, int d,
-                           int nctx, int L, int layer, int ns, int rows);
+// *posp + r / ns, its k/v already appended (append = 0, fw_launch_kv_append)
+void fw_launch_self_attn2(hipStream_t st, const float *qkv, void *kc, void *vc, float *att, const int *posp, int d,
+                          int H, int nctx, int L, int layer, int ns, float scale, float *pmax = nullptr, int rows = 0,
+                          int append = 1, int kv32 = 0);
+// the k/v of every row of a prefill chunk into the caches
+void fw_launch_kv_append(hipStream_t st, const float *qkv, void *kc, void *vc, const int *posp, int d, int nctx,
+                         int L, int layer, int ns, int rows, int kv32);
 // The int8 arm's self-attention sublayer: attention LayerNorm of the residual
 // rows x, the fused q/k/v projection (int8 rows wqkv [3d, d], row scales sqkv,
 // bias bqkv), cache append and attention; per-head output maxima into pmax.
 // With emb (layer 0) the rows are first formed as the token embeddings
 // f16(emb[tok]) + pemb[pos] and stored to x.
 void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *sqkv, const float *bqkv, float *x,
-                               const float *lnw, const float *lnb, uint16_t *kc, uint16_t *vc, float *att,
+                               const float *lnw, const float *lnb, void *kc, void *vc, float *att,
                                const int *posp, int d, int H, int nctx, int L, int layer, int ns, float scale,
                                float *pmax, const int32_t *tok = nullptr, const uint16_t *emb = nullptr,
-                               const float *pemb = nullptr, int lnseq = 0);
+                               const float *pemb = nullptr, int lnseq = 0, int kv32 = 0);
 // q = Wq LN(x): the cross LayerNorm (lnw, lnb) of the residual rows x and the
 // int8 cross q projection [d, d] (row scales swq, bias bq) run in the kernel
 void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,

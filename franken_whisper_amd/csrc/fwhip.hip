@@ -264,6 +264,9 @@ struct fwhip_decoder {
     // 1: strict sequential-k cross K/V precompute, and every LayerNorm's mean
     // and variance summed in the reference's sequential order
     int exact = 0;
+    // self-attention cache of the states made next: f16 (FW_KV_F16) or f32
+    // (the reference's default), read when a state is made, as KvCache::new does
+    int kv_f16 = 1;
     std::vector<DecLayerDev> layers;
     std::vector<void *> owned;
 };
@@ -271,7 +274,9 @@ struct fwhip_decoder {
 struct fwhip_dstate {
     fwhip_decoder *dec;
     int S, T, Tq, Sp, len;
-    uint16_t *kv_k, *kv_v, *ck16, *cvt16;
+    void *kv_k, *kv_v; // [S][L][nctx][d] f16, or f32 when kv32
+    int kv32 = 0;
+    uint16_t *ck16, *cvt16;
     uint16_t *ck16p = nullptr, *cvt16p = nullptr; // f16 arm: slot-order copies for the cross attention
     float *xsplit = nullptr; // f16 arm: scores and block maxima of the two-launch cross attention
     int *am_cnt = nullptr;   // argmax blocks counted in (zero between launches)
@@ -571,8 +576,9 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
     auto &own = st->owned;
     size_t kvn = (size_t)S * L * nctx * d;
     size_t crn = (size_t)S * L * T * d;
-    st->kv_k = (uint16_t *)fw_dalloc(own, kvn * 2);
-    st->kv_v = (uint16_t *)fw_dalloc(own, kvn * 2);
+    st->kv32 = dd->kv_f16 ? 0 : 1;
+    st->kv_k = fw_dalloc(own, kvn * (st->kv32 ? 4 : 2));
+    st->kv_v = fw_dalloc(own, kvn * (st->kv32 ? 4 : 2));
     st->ck16 = (uint16_t *)fw_dalloc(own, crn * 2);
     st->cvt16 = (uint16_t *)fw_dalloc(own, crn * 2);
     bool ok = st->kv_k && st->kv_v && st->ck16 && st->cvt16;
@@ -653,7 +659,7 @@ extern "C" fwhip_status fwhip_dstate_read(const fwhip_dstate *st, int32_t what, 
     if (stream < 0 || stream >= st->S) return fw_fail(FWHIP_ERR_INVALID, "fwhip_dstate_read: stream out of range");
     const fwhip_decoder *dd = st->dec;
     HIP_TRY(hipSetDevice(dd->ctx->device));
-    size_t cr = (size_t)dd->L * st->T * dd->d * 2, kv = (size_t)dd->L * dd->nctx * dd->d * 2;
+    size_t cr = (size_t)dd->L * st->T * dd->d * 2, kv = (size_t)dd->L * dd->nctx * dd->d * (st->kv32 ? 4 : 2);
     const void *src = nullptr;
     size_t n = 0;
     switch (what) {
@@ -672,6 +678,15 @@ extern "C" fwhip_status fwhip_dstate_read(const fwhip_dstate *st, int32_t what, 
 extern "C" fwhip_status fwhip_decoder_set_exact(fwhip_decoder *dd, int32_t exact) {
     if (!dd) return fw_fail(FWHIP_ERR_INVALID, "NULL decoder");
     dd->exact = exact != 0;
+    return FWHIP_OK;
+}
+
+// FW_KV_F16 (kv_f16_enabled, nn.rs:5097-5109): the cache type of the states
+// made after this call (1: f16, this library's initial setting; 0: f32, the
+// reference's default)
+extern "C" fwhip_status fwhip_decoder_set_kv_f16(fwhip_decoder *dd, int32_t on) {
+    if (!dd) return fw_fail(FWHIP_ERR_INVALID, "NULL decoder");
+    dd->kv_f16 = on != 0;
     return FWHIP_OK;
 }
 
@@ -827,7 +842,7 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             fw_launch_self_attn_fused(s, l.qkv8, l.qkv8s, l.qkv_b, st->x, l.attn_ln_w, l.attn_ln_b, st->kv_k,
                                       st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S, scale, st->pmax,
                                       li == 0 ? tok : nullptr, li == 0 ? dd->emb16 : nullptr,
-                                      li == 0 ? dd->pos_emb : nullptr, sq);
+                                      li == 0 ? dd->pos_emb : nullptr, sq, st->kv32);
             gemv_i8_all(st, s, l.o8, l.o8s, l.o_b, st->x, d, d, d, 1, nullptr, st->att);
             // the cross LayerNorm and q projection run inside the cross-attention kernel
             if (xt) fw_timed_begin(c, FWHIP_K_DEC_XATTN, xbytes, &xev);
@@ -850,11 +865,11 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 if (li > 0)
                     fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, st->x, l.attn_ln_w, l.attn_ln_b, st->kv_k,
                                              st->kv_v, st->att, st->pos, H, dd->nctx, L, li, S, scale, nullptr,
-                                             nullptr, nullptr, nullptr, sq);
+                                             nullptr, nullptr, nullptr, sq, st->kv32);
                 else
                     fw_launch_self_attn_f16q(s, l.qkv16, l.qkv_b, nullptr, l.attn_ln_w, l.attn_ln_b, st->kv_k,
                                              st->kv_v, st->att, st->pos, H, dd->nctx, L, li, S, scale, tok,
-                                             dd->emb16, dd->pos_emb, st->x, sq);
+                                             dd->emb16, dd->pos_emb, st->x, sq, st->kv32);
             } else {
                 // (layer 0's attention LayerNorm ran with the embedding, into h)
                 if (li > 0)
@@ -863,7 +878,7 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
                 else
                     fw_gemv16(s, l.qkv16, l.qkv_b, st->h, st->qkv, 3 * d, d, S, 3 * d, 0, gt);
                 fw_launch_self_attn2(s, st->qkv, st->kv_k, st->kv_v, st->att, st->pos, d, H, dd->nctx, L, li, S,
-                                     scale);
+                                     scale, nullptr, 0, 1, st->kv32);
             }
             fw_gemv16(s, l.o16, l.o_b, st->att, st->x, d, d, S, d, 1, gt);
             if (fold && st->ck16p && fw_cross_f16pq_ok(d, T, H) && fw_gemv16_ok(d, d) && fw_gemv16_lpr(d, d) == 16) {
@@ -988,9 +1003,9 @@ static fwhip_status dec_forward_chunk(fwhip_dstate *st, const int32_t *tok, int 
         if (li > 0)
             fw_gemv16_ln(s, l.qkv16, l.qkv_b, x, h, l.attn_ln_w, l.attn_ln_b, qkv, 3 * d, d, R, 3 * d, 0, gt, sq);
         else fw_gemv16(s, l.qkv16, l.qkv_b, h, qkv, 3 * d, d, R, 3 * d, 0, gt);
-        fw_launch_kv_append16(s, qkv, st->kv_k, st->kv_v, st->pos, d, dd->nctx, L, li, S, R);
+        fw_launch_kv_append(s, qkv, st->kv_k, st->kv_v, st->pos, d, dd->nctx, L, li, S, R, st->kv32);
         fw_launch_self_attn2(s, qkv, st->kv_k, st->kv_v, att, st->pos, d, H, dd->nctx, L, li, S, scale, nullptr, R,
-                             0);
+                             0, st->kv32);
         fw_gemv16(s, l.o16, l.o_b, att, x, d, d, R, d, 1, gt);
         fw_gemv16_ln(s, l.cq16, l.cq_b, x, h, l.cross_ln_w, l.cross_ln_b, y, d, d, R, d, 0, gt, sq);
         fw_launch_cross_attn_f16p(s, y, st->ck16p, st->cvt16p, att, d, T, H, L, li, S, scale, R);
@@ -1175,7 +1190,7 @@ static bool capture_step_impl(fwhip_dstate *st, const fwhip_filter *filt) {
 // length tk: the weights once (int8 rows + f32 row scales, mlp_2 as 32-blocks
 // with an f32 scale each, or f16), and per stream its cross K/V (int8 + scales,
 // or f16) and self-attention cache (K and V rows [0, tk) read, one row each
-// written, f16).
+// written, f16 or f32).
 static double dec_step_bytes(const fwhip_dstate *st, int tk) {
     const fwhip_decoder *dd = st->dec;
     const double d = dd->d, L = dd->L, V = dd->V, T = st->T, S = st->S, H = dd->H;
@@ -1190,7 +1205,7 @@ static double dec_step_bytes(const fwhip_dstate *st, int tk) {
         w = 2.0 * (L * 14 * d * d + V * d);
         cross = L * 2 * T * d * 2;
     }
-    const double kv = L * 2 * ((double)tk + 1) * d * 2;
+    const double kv = L * 2 * ((double)tk + 1) * d * (st->kv32 ? 4 : 2);
     return w + S * (cross + kv);
 }
 

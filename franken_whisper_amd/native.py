@@ -46,6 +46,7 @@ SIGNATURES = {
     "fwhip_encoder_set_exact": (C.c_int32, [_vp, C.c_int32]),
     "fwhip_encoder_set_tome": (C.c_int32, [_vp, C.c_int32, C.c_int32]),
     "fwhip_encoder_set_tome_schedule": (C.c_int32, [_vp, C.c_int32, C.c_int32]),
+    "fwhip_decoder_set_kv_f16": (C.c_int32, [_vp, C.c_int32]),
     "fwhip_tome_merge": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _vp, _vp, _i32p]),
     "fwhip_encoder_gemm_i8": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, _vp, _vp]),
     "fwhip_encoder_gemm_i8_fused": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, C.c_int32, _vp, _vp]),
@@ -390,6 +391,12 @@ class Decoder:
         f16-pair MFMA one (the default)."""
         check(lib().fwhip_decoder_set_exact(self.h, 1 if exact else 0))
 
+    def set_kv_f16(self, on: bool):
+        """FW_KV_F16: the self-attention cache of states made afterwards, f16
+        (True, the initial setting) or f32 (False, the reference's default)."""
+        check(lib().fwhip_decoder_set_kv_f16(self.h, 1 if on else 0))
+        self.kv_f16 = bool(on)
+
     def state(self, n_streams: int, enc_frames: int) -> "DecoderState":
         return DecoderState(self, n_streams, enc_frames)
 
@@ -404,6 +411,7 @@ class DecoderState:
 
     def __init__(self, dec: Decoder, n_streams: int, enc_frames: int):
         self.dec, self.S, self.T = dec, n_streams, enc_frames
+        self.kv_f16 = getattr(dec, "kv_f16", True)
         h = _vp()
         check(lib().fwhip_dstate_new(dec.h, n_streams, enc_frames, C.byref(h)))
         self.h = h
@@ -434,7 +442,7 @@ class DecoderState:
             n = c.n_text_layer * self.T * c.n_text_state
         else:
             n = c.n_text_layer * c.n_text_ctx * c.n_text_state
-        out = np.empty(n, np.uint16)
+        out = np.empty(n, np.uint16 if what in (abi.DS_CROSS_K_F16, abi.DS_CROSS_VT_F16) or self.kv_f16 else np.float32)
         check(lib().fwhip_dstate_read(self.h, what, stream, out.ctypes.data_as(_vp), out.nbytes))
         return out
 

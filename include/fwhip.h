@@ -338,6 +338,17 @@ void fwhip_decoder_free(fwhip_decoder *dec);
  * kernels are the same in both modes apart from that sum. */
 fwhip_status fwhip_decoder_set_exact(fwhip_decoder *dec, int32_t exact);
 
+/* Replaces FW_KV_F16 (kv_f16_enabled, nn.rs:5097-5109), read when a state is
+ * made (KvCache::new): the self-attention cache of the states that
+ * fwhip_dstate_new makes after this call.  on = 1 (this library's initial
+ * setting): K/V rows rounded to f16 on append (KvCache::append,
+ * nn.rs:5352-5416); on = 0: f32 rows as computed, the reference's default
+ * (FW_KV_F16 unset; attention_decode_step, nn.rs:6340-6400).  Attention reads
+ * either as f32 with the same arithmetic, so the two differ only by the f16
+ * rounding of the cached rows; the f32 cache takes twice the memory
+ * (4 x n_layer x n_text_ctx x d x 2 bytes per stream). */
+fwhip_status fwhip_decoder_set_kv_f16(fwhip_decoder *dec, int32_t on);
+
 /* A cohort of n_streams independent DecoderStates (decoder.rs:980-1027), each
  * with its own f16 self-attention KV cache (KvCache, nn.rs:5138) of
  * n_text_ctx tokens and its own cross K/V over enc_frames encoder rows
@@ -372,7 +383,8 @@ fwhip_status fwhip_decoder_step(fwhip_dstate *st, const int32_t *tokens, int32_t
  * parity checks; decoder.rs:1129-1245 layouts):
  *   FWHIP_DS_CROSS_K_F16   [n_layer, n_head, enc_frames, 64] f16 (scaled keys)
  *   FWHIP_DS_CROSS_VT_F16  [n_layer, n_head, 64, enc_frames] f16
- *   FWHIP_DS_KV_K, _KV_V   [n_layer, n_text_ctx, d] f16
+ *   FWHIP_DS_KV_K, _KV_V   [n_layer, n_text_ctx, d] f16, or f32 for a state made
+ *                          with fwhip_decoder_set_kv_f16(dec, 0)
  * `bytes` must equal the buffer size. */
 #define FWHIP_DS_CROSS_K_F16 1
 #define FWHIP_DS_CROSS_VT_F16 2

@@ -77,6 +77,8 @@ def lib():
         "ref_attention": (None, [f32p, C.c_int, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                  f32p]),
         "ref_attention_decode_f16": (None, [f32p, u16p, u16p, C.c_int, C.c_int, C.c_int, f32p]),
+        "ref_attention_decode_f32": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, f32p]),
+        "ref_decoder_set_kv_f16": (None, [C.c_void_p, C.c_int]),
         "ref_encoder_new": (C.c_void_p, [C.POINTER(abi.EncoderWeights), C.c_int]),
         "ref_encoder_free": (None, [C.c_void_p]),
         "ref_encoder_forward": (C.c_int, [C.c_void_p, f32p, C.c_int, f32p, C.c_int]),
@@ -354,6 +356,17 @@ def attention_decode_f16(q, kc16, vc16, n_head):
     return out
 
 
+def attention_decode_f32(q, kc, vc, n_head):
+    """attention_decode_step (nn.rs:6340-6400): one row over an f32 cache."""
+    q = _c(q, np.float32).ravel()
+    kc, vc = _c(kc, np.float32), _c(vc, np.float32)
+    tk, d = kc.shape
+    out = np.empty(d, np.float32)
+    lib().ref_attention_decode_f32(_p(q, C.c_float), _p(kc, C.c_float), _p(vc, C.c_float), tk, d, n_head,
+                                   _p(out, C.c_float))
+    return out
+
+
 def argmax_first(x):
     x = _c(x, np.float32)
     return int(lib().ref_argmax_first(_p(x, C.c_float), x.size))
@@ -425,6 +438,10 @@ class Decoder:
         self.desc = model.decoder_weights()
         self.h = lib().ref_decoder_new(C.byref(self.desc), arm)
         self.cfg = model.cfg
+
+    def set_kv_f16(self, on):
+        """FW_KV_F16 for the states made next (True: f16 cache; False: f32)."""
+        lib().ref_decoder_set_kv_f16(self.h, 1 if on else 0)
 
     def state(self, enc):
         return DState(self, enc)

@@ -1005,6 +1005,7 @@ typedef struct {
 struct ref_decoder {
     fwhip_hparams hp;
     int arm, d, H, dh, L, V, nctx, dff;
+    int kv_f16; /* FW_KV_F16 for the states made next (1: f16 cache, 0: f32) */
     const uint16_t *tok_emb;
     const float *pos_emb, *ln_w, *ln_b;
     int8_t *emb8;
@@ -1015,6 +1016,7 @@ struct ref_decoder {
 struct ref_dstate {
     int enc_frames, len;
     uint16_t *kv_k, *kv_v;   /* [L, nctx, d] f16 (FW_KV_F16) */
+    float *kvf_k, *kvf_v;    /* [L, nctx, d] f32 (FW_KV_F16 unset: the reference's default) */
     uint16_t *ck16, *cvt16;  /* [L*H][T*dh] natural K, [L*H][dh*T] transposed V */
     int8_t *ck8, *cvt8;
     float *ck8s, *cvt8s;     /* [L*H][T], [L*H][dh] */
@@ -1044,6 +1046,7 @@ ref_decoder *ref_decoder_new(const fwhip_decoder_weights *w, int arm) {
     dd->V = w->hp.n_vocab;
     dd->nctx = w->hp.n_text_ctx;
     dd->dff = 4 * dd->d;
+    dd->kv_f16 = 1;
     dd->tok_emb = w->tok_emb;
     dd->pos_emb = w->pos_emb;
     dd->ln_w = w->ln_w;
@@ -1100,8 +1103,13 @@ ref_dstate *ref_dstate_new(const ref_decoder *dd, const float *enc, int T) {
     int d = dd->d, H = dd->H, dh = dd->dh, L = dd->L;
     ref_dstate *s = (ref_dstate *)calloc(1, sizeof *s);
     s->enc_frames = T;
-    s->kv_k = (uint16_t *)calloc((size_t)L * dd->nctx * d, sizeof(uint16_t));
-    s->kv_v = (uint16_t *)calloc((size_t)L * dd->nctx * d, sizeof(uint16_t));
+    if (dd->kv_f16) { /* KvCache::new reads FW_KV_F16, nn.rs:5097-5109 */
+        s->kv_k = (uint16_t *)calloc((size_t)L * dd->nctx * d, sizeof(uint16_t));
+        s->kv_v = (uint16_t *)calloc((size_t)L * dd->nctx * d, sizeof(uint16_t));
+    } else {
+        s->kvf_k = (float *)calloc((size_t)L * dd->nctx * d, sizeof(float));
+        s->kvf_v = (float *)calloc((size_t)L * dd->nctx * d, sizeof(float));
+    }
     s->ck16 = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)L * H * T * dh);
     s->cvt16 = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)L * H * T * dh);
     float kscale = powf((float)dh, -0.25f);
@@ -1144,7 +1152,7 @@ ref_dstate *ref_dstate_new(const ref_decoder *dd, const float *enc, int T) {
 void ref_dstate_free(ref_dstate *s) {
     if (!s) return;
     free(s->kt); free(s->kt_len);
-    free(s->kv_k); free(s->kv_v); free(s->ck16); free(s->cvt16);
+    free(s->kv_k); free(s->kv_v); free(s->kvf_k); free(s->kvf_v); free(s->ck16); free(s->cvt16);
     free(s->ck8); free(s->cvt8); free(s->ck8s); free(s->cvt8s);
     free(s);
 }
@@ -1216,6 +1224,32 @@ static void self_attn_f16(const float *q, const uint16_t *kc, const uint16_t *vc
     free(sc);
 }
 
+/* attention_decode_step (nn.rs:6340-6400) over an f32 cache: the same
+ * arithmetic as self_attn_f16 on rows stored as computed. */
+static void self_attn_f32(const float *q, const float *kc, const float *vc, int tk, int d, int H, float *out) {
+    int dh = d / H;
+    float scale = powf((float)dh, -0.25f);
+    float *sc = (float *)malloc(sizeof(float) * (size_t)tk);
+    for (int h = 0; h < H; h++) {
+        int base = h * dh;
+        float qh[256];
+        for (int i = 0; i < dh; i++) qh[i] = q[base + i] * scale;
+        for (int j = 0; j < tk; j++) {
+            const float *kr = kc + (size_t)j * d + base;
+            float acc = 0.0f;
+            for (int i = 0; i < dh; i++) acc += qh[i] * (kr[i] * scale);
+            sc[j] = acc;
+        }
+        softmax_row(sc, tk);
+        for (int i = 0; i < dh; i++) out[base + i] = 0.0f;
+        for (int j = 0; j < tk; j++) {
+            const float *vr = vc + (size_t)j * d + base;
+            for (int i = 0; i < dh; i++) out[base + i] += sc[j] * vr[i];
+        }
+    }
+    free(sc);
+}
+
 /* self_attn_f16 in the FAST restatement: the same per-element arithmetic
  * (score j = sequential sum over i of qh[i] * (f16_to_f32(k[j][i]) * s) from
  * +0.0f; value i = sequential sum over j of p[j] * f16_to_f32(v[j][i]) from
@@ -1232,10 +1266,12 @@ static void self_attn_fast(const ref_decoder *dd, ref_dstate *s, int li, const f
     }
     int ld = s->kt_ld;
     float *kt = s->kt + (size_t)li * d * ld;
-    const uint16_t *kc = s->kv_k + (size_t)li * nctx * d, *vc = s->kv_v + (size_t)li * nctx * d;
+    const size_t lo = (size_t)li * nctx * d;
     int from = s->kt_len[li] < tk - 1 ? s->kt_len[li] : tk - 1;
     for (int p = from; p < tk; p++)
-        for (int c = 0; c < d; c++) kt[(size_t)c * ld + p] = ref_f16_to_f32(kc[(size_t)p * d + c]) * scale;
+        for (int c = 0; c < d; c++)
+            kt[(size_t)c * ld + p] = (s->kvf_k ? s->kvf_k[lo + (size_t)p * d + c]
+                                               : ref_f16_to_f32(s->kv_k[lo + (size_t)p * d + c])) * scale;
     s->kt_len[li] = tk;
 #pragma omp parallel for schedule(static)
     for (int h = 0; h < H; h++) {
@@ -1245,7 +1281,8 @@ static void self_attn_fast(const ref_decoder *dd, ref_dstate *s, int li, const f
         for (int i = 0; i < dh; i++) qh[i] = q[base + i] * scale;
         rf_scores_t(qh, kt + (size_t)base * ld, ld, dh, tk, sc);
         rf_softmax_row(sc, tk);
-        rf_pv_f16(sc, vc + base, d, tk, dh, out + base);
+        if (s->kvf_v) rf_pv_f32(sc, s->kvf_v + lo + base, d, tk, dh, out + base);
+        else rf_pv_f16(sc, s->kv_v + lo + base, d, tk, dh, out + base);
         free(sc);
     }
 }
@@ -1267,6 +1304,13 @@ void ref_attention_decode_f16(const float *q, const uint16_t *kc, const uint16_t
                               int H, float *out) {
     self_attn_f16(q, kc, vc, tk, d, H, out);
 }
+/* The same over an f32 cache (attention_decode_step, nn.rs:6340-6400). */
+void ref_attention_decode_f32(const float *q, const float *kc, const float *vc, int tk, int d, int H, float *out) {
+    self_attn_f32(q, kc, vc, tk, d, H, out);
+}
+/* FW_KV_F16 for the states ref_dstate_new makes next (1: f16, the initial
+ * setting; 0: f32, the reference's default). */
+void ref_decoder_set_kv_f16(ref_decoder *dd, int on) { dd->kv_f16 = on != 0; }
 
 /* cross_attention, decoder.rs:1524-1716 (FW_CROSS_F16 on; int8 K/V when the
  * int8 copies exist): qh = q*s; scores = gemv(K_h, qh); softmax; out =
@@ -1346,13 +1390,21 @@ int ref_decoder_step(const ref_decoder *dd, ref_dstate *s, const int32_t *tokens
             const fwhip_dec_layer *sw = l->src;
             ref_layer_norm(x, h, 1, d, sw->attn_ln_w, sw->attn_ln_b, LN_EPS);
             dec_linear(dd, l, 0, h, prefill, qkv);
-            uint16_t *kc = s->kv_k + (size_t)li * nctx * d, *vc = s->kv_v + (size_t)li * nctx * d;
-            for (int i = 0; i < d; i++) { /* KvCache::append f16, nn.rs:5352-5416 */
-                kc[(size_t)pos * d + i] = ref_f32_to_f16(qkv[d + i]);
-                vc[(size_t)pos * d + i] = ref_f32_to_f16(qkv[2 * d + i]);
+            const size_t lo = (size_t)li * nctx * d;
+            if (s->kvf_k) { /* KvCache::append, nn.rs:5352-5416: f32 rows as computed */
+                for (int i = 0; i < d; i++) {
+                    s->kvf_k[lo + (size_t)pos * d + i] = qkv[d + i];
+                    s->kvf_v[lo + (size_t)pos * d + i] = qkv[2 * d + i];
+                }
+            } else { /* FW_KV_F16: rows rounded to f16 */
+                for (int i = 0; i < d; i++) {
+                    s->kv_k[lo + (size_t)pos * d + i] = ref_f32_to_f16(qkv[d + i]);
+                    s->kv_v[lo + (size_t)pos * d + i] = ref_f32_to_f16(qkv[2 * d + i]);
+                }
             }
             if (g_fast) self_attn_fast(dd, s, li, qkv, pos + 1, att);
-            else self_attn_f16(qkv, kc, vc, pos + 1, d, dd->H, att);
+            else if (s->kvf_k) self_attn_f32(qkv, s->kvf_k + lo, s->kvf_v + lo, pos + 1, d, dd->H, att);
+            else self_attn_f16(qkv, s->kv_k + lo, s->kv_v + lo, pos + 1, d, dd->H, att);
             dec_linear(dd, l, 1, att, prefill, y);
             for (int i = 0; i < d; i++) x[i] += y[i];
             ref_layer_norm(x, h, 1, d, sw->cross_ln_w, sw->cross_ln_b, LN_EPS);

@@ -74,6 +74,7 @@ void ref_attention(const float *q, int tq, const float *k, const float *v, int t
                    int n_head, int causal, int cache_len, float *out);
 void ref_attention_decode_f16(const float *q, const uint16_t *kc, const uint16_t *vc, int tk, int d,
                               int H, float *out);
+void ref_attention_decode_f32(const float *q, const float *kc, const float *vc, int tk, int d, int H, float *out);
 
 /* ---- encoder ---- */
 typedef struct ref_encoder ref_encoder;
@@ -97,6 +98,7 @@ void ref_enc_i7_gemm(const ref_encoder *e, int layer, int which, const float *x,
 
 /* ---- decoder ---- */
 typedef struct ref_decoder ref_decoder;
+void ref_decoder_set_kv_f16(ref_decoder *dd, int on); /* FW_KV_F16 for the states made next */
 typedef struct ref_dstate ref_dstate;
 ref_decoder *ref_decoder_new(const fwhip_decoder_weights *w, int arm);
 void ref_decoder_free(ref_decoder *d);

@@ -417,6 +417,24 @@ void rf_pv_f16(const float *p, const uint16_t *v, int64_t ldv, int tk, int dh, f
     }
 }
 
+/* out[i] = sequential sum over j of p[j] * v[j*ldv + i] from +0.0f (f32 rows:
+ * the reference's default cache, attention_decode_step's j-ascending axpy,
+ * nn.rs:6388-6398). */
+void rf_pv_f32(const float *p, const float *v, int64_t ldv, int tk, int dh, float *out) {
+    int i = 0;
+    for (; i + 8 <= dh; i += 8) {
+        __m256 a0 = _mm256_setzero_ps();
+        for (int j = 0; j < tk; j++)
+            a0 = _mm256_add_ps(a0, _mm256_mul_ps(_mm256_broadcast_ss(p + j), _mm256_loadu_ps(v + (int64_t)j * ldv + i)));
+        _mm256_storeu_ps(out + i, a0);
+    }
+    for (; i < dh; i++) {
+        float acc = 0.0f;
+        for (int j = 0; j < tk; j++) acc += p[j] * v[(int64_t)j * ldv + i];
+        out[i] = acc;
+    }
+}
+
 /* quantize_row_i7_u8 (nn.rs:3075-3111): the 8-wide body clamp(trunc(v +
  * copysign(0.5, v)), -127, 127) + 128 with v = x * inv, the n % 8 tail with
  * round-half-away; optionally each x first through the GELU table

@@ -40,5 +40,6 @@ void rf_softmax_row(float *row, int cols);
  * [dh][ld], and the f16 value pass, both in the strict sequential orders */
 void rf_scores_t(const float *qh, const float *kt, int ld, int dh, int tk, float *sc);
 void rf_pv_f16(const float *p, const uint16_t *v, int64_t ldv, int tk, int dh, float *out);
+void rf_pv_f32(const float *p, const float *v, int64_t ldv, int tk, int dh, float *out);
 
 #endif
