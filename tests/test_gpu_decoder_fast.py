@@ -14,10 +14,12 @@ the fragment-order f16 GEMVs with the LayerNorms fused into their staging.
   half away), so a sub-ulp f32 difference upstream moves a rounding boundary
   and greedy tokens can part from the exact ones after a near-tie.  Its fast
   mode is checked by teacher forcing: both modes step along the exact mode's
-  token path, and at every position the fast logits are within 2e-2 rms of
-  the exact logits and the fast argmax agrees with the exact token at >= 90%
-  of the positions.  Exact mode itself is bit-identical to the oracle on this
-  arm (the deep-cache and greedy tests run it).
+  token path, and at every position the fast logits are within 3e-2 rms of
+  the exact logits and the fast argmax agrees with the exact token at >= 95%
+  of the positions (measured 97.7% at turbo with 16 streams, 98.4% on
+  tiny.en; the micro model's fast logits are bit-identical to exact mode's,
+  which the test requires).  Exact mode itself is bit-identical to the oracle
+  on this arm (the deep-cache and greedy tests run it).
 """
 import numpy as np
 import pytest
@@ -133,5 +135,11 @@ def test_fast_mode_int8_arm_teacher_forced(ctx, name, S, n_max):
         total += k
     print(f"{name} int8 arm fast vs exact: rel rms of logits <= {worst:.2e}; "
           f"argmax agreement {agree}/{total}", flush=True)
-    assert worst <= 2e-2
-    assert agree >= 0.9 * total
+    # measured: micro-ml bit-identical (d 128: the fast cross K/V and LayerNorm
+    # sums land on the same f32 values), tiny.en 126/128 at 1.3e-2, turbo
+    # 750/768 at 2.0e-2 (every linear re-quantizes its input, so sub-ulp
+    # differences move int8 rounding steps; exact mode is bit-identical)
+    if name == "micro-ml":
+        assert np.array_equal(lf.view(np.uint32), le.view(np.uint32))
+    assert worst <= 3e-2
+    assert agree >= 0.95 * total
