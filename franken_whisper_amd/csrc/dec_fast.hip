@@ -2079,13 +2079,20 @@ __host__ __device__ __forceinline__ int ca_vstride(int Tq) { return Tq + ((16 - 
         FW_WAIT_LGKM0();                                                                           \
         asm volatile("s_barrier" ::: "memory");                                                    \
     } while (0)
-template <int NV, bool SEQ>
+//
+// VB (FW_CROSS_V_BLOCK, decoder.rs:1605-1608): cvt holds the block-int8 V^T
+// (32-frame blocks, scales vbs [.., 64, nb]) and the value pass is
+// gemv_i8w_f32a_blocked (nn.rs:3756-3824) on the f32 softmax weights: no p
+// quantization; per output dim the blocks' dot_i8w_f32 (nn.rs:3479-3564)
+// times their scale, summed in block order.
+template <int NV, bool SEQ, bool VB = false>
 __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restrict__ wq, const float *__restrict__ swq,
                                                          const float *__restrict__ bq, const float *__restrict__ x,
                                                          const float *__restrict__ lnw, const float *__restrict__ lnb,
                                                          const int8_t *ck, const float *cks, const int8_t *cvt,
                                                          const float *cvs, float *att, int d, int T, int Tq, int H,
-                                                         int L, int layer, float scale, float *pmax) {
+                                                         int L, int layer, float scale, float *pmax,
+                                                         const float *vbs, int nb) {
     extern __shared__ __align__(16) unsigned char smc2[];
     const int vst = ca_vstride(Tq);                                               // LDS row stride of Vt
     int8_t *vl = (int8_t *)smc2;                                                  // [64, vst]
@@ -2271,6 +2278,56 @@ __global__ void __launch_bounds__(512) k_cross_attn_i8v2(const int8_t *__restric
     }
     CA_SYNC();
     const float inv = bc[1];
+    if constexpr (VB) {
+        // p_j = e_j * inv as softmax_rows leaves it (the raw scores when the
+        // maximum is not finite); block dots (dim dd, block b) over the 512
+        // threads into LDS, then one lane per dim sums its blocks in order
+        float *bd = (float *)(smc2 + (((size_t)64 * vst + sizeof(float) * ((T + 3) & ~3) + Tq + 15) & ~(size_t)15));
+        const float *Vbs = vbs + lh * 64 * nb;
+        auto pj = [&](int j) { return inv > 0.0f ? sc[j] * inv : sc[j]; };
+        for (int i = t; i < 64 * nb; i += 512) {
+            const int dd = i / nb, b = i - dd * nb, j0 = b * 32, n = T - j0 < 32 ? T - j0 : 32;
+            const int8_t *vr = vl + (size_t)dd * vst + j0;
+            float sd;
+            if (n == 32) {
+                // one 32-wide step: four 8-lane accumulators from +0, then
+                // (a0 + a1) + (a2 + a3) per lane and the lanes' tree
+                float tt[8];
+#pragma unroll
+                for (int l = 0; l < 8; l++) {
+                    const float a0 = __builtin_fmaf((float)vr[l], pj(j0 + l), 0.0f);
+                    const float a1 = __builtin_fmaf((float)vr[8 + l], pj(j0 + 8 + l), 0.0f);
+                    const float a2 = __builtin_fmaf((float)vr[16 + l], pj(j0 + 16 + l), 0.0f);
+                    const float a3 = __builtin_fmaf((float)vr[24 + l], pj(j0 + 24 + l), 0.0f);
+                    tt[l] = (a0 + a1) + (a2 + a3);
+                }
+                sd = ((tt[0] + tt[1]) + (tt[2] + tt[3])) + ((tt[4] + tt[5]) + (tt[6] + tt[7]));
+            } else {
+                // the last, short block: 8-wide product trees, then scalars
+                sd = 0.0f;
+                int i8 = 0;
+                for (; i8 + 8 <= n; i8 += 8) {
+                    float pp[8];
+#pragma unroll
+                    for (int l = 0; l < 8; l++) pp[l] = (float)vr[i8 + l] * pj(j0 + i8 + l);
+                    sd += ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
+                }
+                for (; i8 < n; i8++) sd += (float)vr[i8] * pj(j0 + i8);
+            }
+            bd[i] = sd * Vbs[i];
+        }
+        CA_SYNC();
+        float om = 0.0f;
+        if (wave == 0) {
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) acc += bd[lane * nb + b];
+            const float o = acc + 0.0f;
+            att[(size_t)s * d + h * 64 + lane] = o;
+            om = fw_dpp_wave_max(fabsf(o));
+        }
+        if (pmax && t == 0) pmax[(size_t)s * H + h] = om;
+        return;
+    }
     am = fmaxf(fmaxf(fmaxf(red[8], red[9]), fmaxf(red[10], red[11])),
                fmaxf(fmaxf(red[12], red[13]), fmaxf(red[14], red[15])));
     // max_j |p_j| of p_j = e_j * inv: rounding is monotonic and sign-symmetric,
@@ -2603,11 +2660,38 @@ void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *
 void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,
                                const float *lnw, const float *lnb, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
-                               float scale, float *pmax, int lnseq) {
+                               float scale, float *pmax, int lnseq, const float *vbs) {
     if (64 * ca_vstride(Tq) > 7 * CA_VKB * 1024) return; // refused where the decoder is loaded (T <= 1536)
     size_t shm = (size_t)64 * ca_vstride(Tq) + sizeof(float) * ((T + 3) & ~3) + Tq;
+    const int nb = (T + 31) / 32;
+    if (vbs) {
+        // + the block dots [64, nb], 16-byte aligned
+        shm = ((shm + 15) & ~(size_t)15) + sizeof(float) * 64 * (size_t)nb;
+#define CA_VBL(NV_)                                                                                                 \
+    case NV_:                                                                                                       \
+        if (lnseq)                                                                                                  \
+            hipLaunchKernelGGL((k_cross_attn_i8v2<NV_, true, true>), dim3(H, ns), dim3(512), shm, st, wq, swq, bq, x, \
+                               lnw, lnb, ck, cks, cvt, cvs, att, d, T, Tq, H, L, layer, scale, pmax, vbs, nb);        \
+        else                                                                                                        \
+            hipLaunchKernelGGL((k_cross_attn_i8v2<NV_, false, true>), dim3(H, ns), dim3(512), shm, st, wq, swq, bq,   \
+                               x, lnw, lnb, ck, cks, cvt, cvs, att, d, T, Tq, H, L, layer, scale, pmax, vbs, nb);     \
+        break;
+        switch ((d + 255) / 256) {
+            CA_VBL(1)
+            CA_VBL(2)
+            CA_VBL(3)
+            CA_VBL(4)
+            CA_VBL(5)
+            CA_VBL(6)
+            CA_VBL(7)
+            CA_VBL(8)
+        default: break;
+        }
+#undef CA_VBL
+        return;
+    }
     FW_ROWS_DISPATCH(k_cross_attn_i8v2, lnseq, d, dim3(H, ns), dim3(512), shm, st, wq, swq, bq, x, lnw, lnb, ck, cks,
-                     cvt, cvs, att, d, T, Tq, H, L, layer, scale, pmax);
+                     cvt, cvs, att, d, T, Tq, H, L, layer, scale, pmax, nullptr, 0);
 }
 
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq) {

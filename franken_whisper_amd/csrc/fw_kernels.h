@@ -174,19 +174,21 @@ void fw_launch_self_attn_fused(hipStream_t st, const int8_t *wqkv, const float *
                                float *pmax, const int32_t *tok = nullptr, const uint16_t *emb = nullptr,
                                const float *pemb = nullptr, int lnseq = 0, int kv32 = 0);
 // q = Wq LN(x): the cross LayerNorm (lnw, lnb) of the residual rows x and the
-// int8 cross q projection [d, d] (row scales swq, bias bq) run in the kernel
+// int8 cross q projection [d, d] (row scales swq, bias bq) run in the kernel.
+// With vbs (FW_CROSS_V_BLOCK) cvt is the block-int8 V^T (rows of stride Tq,
+// 32-frame blocks, scales vbs [.., 64, ceil(T / 32)]) and p stays f32.
 void fw_launch_cross_attn_i8v2(hipStream_t st, const int8_t *wq, const float *swq, const float *bq, const float *x,
                                const float *lnw, const float *lnb, const int8_t *ck, const float *cks, const int8_t *cvt,
                                const float *cvs, float *att, int d, int T, int Tq, int H, int L, int layer, int ns,
-                               float scale, float *pmax = nullptr, int lnseq = 0);
+                               float scale, float *pmax = nullptr, int lnseq = 0, const float *vbs = nullptr);
 void fw_launch_quant_f16_rows_ld(hipStream_t st, const uint16_t *src, int8_t *q, float *s, int rows, int n, int ldq);
 int fw_logits_keys_blocks(int V);
 void fw_launch_logits_keys(hipStream_t st, const float *logits, int V, int ns, const fwhip_filter *filt,
                            const int *initialp, unsigned long long *keys);
 
-// load-time quantizers (load_kernels.hip)
+// load-time quantizers (load_kernels.hip); ldq: output row stride (0: inp)
 void fw_launch_quant_blocked(hipStream_t st, const uint16_t *w, int8_t *q, float *s, int64_t out, int inp,
-                             int block);
+                             int block, int ldq = 0);
 void fw_launch_quant_i7(hipStream_t st, const uint16_t *w, int8_t *q, float *s, int32_t *cs, int64_t out,
                         int inp, int ef);
 void fw_launch_quant_enc_i8(hipStream_t st, const uint16_t *w, int8_t *q, float *s, int64_t out, int inp);

@@ -267,6 +267,8 @@ struct fwhip_decoder {
     // self-attention cache of the states made next: f16 (FW_KV_F16) or f32
     // (the reference's default), read when a state is made, as KvCache::new does
     int kv_f16 = 1;
+    // FW_CROSS_V_BLOCK (the int8 arm; default off): read when a state is made
+    int cross_v_block = 0;
     std::vector<DecLayerDev> layers;
     std::vector<void *> owned;
 };
@@ -282,6 +284,8 @@ struct fwhip_dstate {
     int *am_cnt = nullptr;   // argmax blocks counted in (zero between launches)
     int8_t *ck8 = nullptr, *cvt8 = nullptr; // cvt8 rows have stride Tq (T rounded up to 16)
     float *ck8s = nullptr, *cvt8s = nullptr;
+    int8_t *cvb8 = nullptr; // FW_CROSS_V_BLOCK: block-int8 V^T, rows of stride Tq
+    float *cvbs = nullptr;  // its scales [S, L, H, 64, ceil(T / 32)]
     float *x, *h, *qkv, *att, *y, *ff, *logits;
     int8_t *xq;             // [Sp, d] quantized activation rows (rows >= S stay zero)
     float *xs;              // [Sp]
@@ -596,6 +600,11 @@ extern "C" fwhip_status fwhip_dstate_new(fwhip_decoder *dd, int32_t S, int32_t T
         st->ck8s = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * L * dd->H * T);
         st->cvt8s = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * L * d);
         ok = ok && st->ck8 && st->cvt8 && st->ck8s && st->cvt8s;
+        if (dd->cross_v_block) {
+            st->cvb8 = (int8_t *)fw_dalloc(own, (size_t)S * L * dd->H * 64 * st->Tq);
+            st->cvbs = (float *)fw_dalloc(own, sizeof(float) * (size_t)S * L * dd->H * 64 * ((T + 31) / 32));
+            ok = ok && st->cvb8 && st->cvbs;
+        }
     }
     st->x = (float *)fw_dalloc(own, sizeof(float) * S * d);
     st->h = (float *)fw_dalloc(own, sizeof(float) * S * d);
@@ -681,6 +690,16 @@ extern "C" fwhip_status fwhip_decoder_set_exact(fwhip_decoder *dd, int32_t exact
     return FWHIP_OK;
 }
 
+// FW_CROSS_V_BLOCK (cross_v_block_enabled, decoder.rs:1496-1520): states made
+// after this call on the int8 arm keep a block-int8 copy of the cross V
+// (quantize_f16_to_i8_blocked along the frames, 32 per scale,
+// decoder.rs:1249-1263) for a value pass on f32 softmax weights
+extern "C" fwhip_status fwhip_decoder_set_cross_v_block(fwhip_decoder *dd, int32_t on) {
+    if (!dd) return fw_fail(FWHIP_ERR_INVALID, "NULL decoder");
+    dd->cross_v_block = on != 0;
+    return FWHIP_OK;
+}
+
 // FW_KV_F16 (kv_f16_enabled, nn.rs:5097-5109): the cache type of the states
 // made after this call (1: f16, this library's initial setting; 0: f32, the
 // reference's default)
@@ -747,6 +766,8 @@ static bool cross_kv(fwhip_dstate *st, const float *enc_dev, bool strict) {
     if (dd->arm == FWHIP_DEC_INT8) {
         fw_launch_quant_f16_rows(c->stream, st->ck16, st->ck8, st->ck8s, S * L * H * T, 64);
         fw_launch_quant_f16_rows_ld(c->stream, st->cvt16, st->cvt8, st->cvt8s, S * L * H * 64, T, st->Tq);
+        if (st->cvb8) fw_launch_quant_blocked(c->stream, st->cvt16, st->cvb8, st->cvbs, (int64_t)S * L * H * 64, T, 32,
+                                              st->Tq);
     }
     return true;
 }
@@ -847,7 +868,8 @@ static fwhip_status dec_forward_row(fwhip_dstate *st, const int32_t *tok, bool p
             // the cross LayerNorm and q projection run inside the cross-attention kernel
             if (xt) fw_timed_begin(c, FWHIP_K_DEC_XATTN, xbytes, &xev);
             fw_launch_cross_attn_i8v2(s, l.cq8, l.cq8s, l.cq_b, st->x, l.cross_ln_w, l.cross_ln_b, st->ck8, st->ck8s,
-                                      st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li, S, scale, st->pmax, sq);
+                                      st->cvb8 ? st->cvb8 : st->cvt8, st->cvt8s, st->att, d, T, st->Tq, H, L, li, S,
+                                      scale, st->pmax, sq, st->cvbs);
             if (xt) fw_timed_end(c, &xev);
             gemv_i8_all(st, s, l.co8, l.co8s, l.co_b, st->x, d, d, d, 1, nullptr, st->att);
             // mode 4: GELU written block-interleaved for the block GEMV; prefill

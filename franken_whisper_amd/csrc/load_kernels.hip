@@ -8,8 +8,9 @@
 // add-trunc rounding in the 8-wide body and exact rounding in the tail.
 // (k_quant_f16_rows in dec_kernels.hip is the same operation.)
 
-// quantize_f16_to_i8_blocked (nn.rs:3583, 3619-3720): per-32-block amax/127.
-__global__ void k_quant_blocked(const uint16_t *w, int8_t *q, float *s, int64_t out, int inp, int block) {
+// quantize_f16_to_i8_blocked (nn.rs:3583, 3619-3720): per-32-block amax/127;
+// output rows of stride ldq.
+__global__ void k_quant_blocked(const uint16_t *w, int8_t *q, float *s, int64_t out, int inp, int block, int ldq) {
     int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     int nb = (inp + block - 1) / block;
     if (idx >= out * nb) return;
@@ -25,7 +26,7 @@ __global__ void k_quant_blocked(const uint16_t *w, int8_t *q, float *s, int64_t 
     for (int i = st; i < e; i++) {
         float v = fw_h2f(wr[i]) * inv;
         float r = i < e8 ? fw_round_add_trunc(v) : fw_round_away(v);
-        q[o * inp + i] = (int8_t)(int)fw_clamp(r, -127.0f, 127.0f);
+        q[o * ldq + i] = (int8_t)(int)fw_clamp(r, -127.0f, 127.0f);
     }
     s[o * nb + b] = sc;
 }
@@ -75,10 +76,10 @@ __global__ void k_quant_enc_i8(const uint16_t *w, int8_t *q, float *s, int64_t o
 }
 
 void fw_launch_quant_blocked(hipStream_t st, const uint16_t *w, int8_t *q, float *s, int64_t out, int inp,
-                             int block) {
+                             int block, int ldq) {
     int64_t n = out * ((inp + block - 1) / block);
     hipLaunchKernelGGL(k_quant_blocked, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, q, s, out, inp,
-                       block);
+                       block, ldq > 0 ? ldq : inp);
 }
 void fw_launch_quant_i7(hipStream_t st, const uint16_t *w, int8_t *q, float *s, int32_t *cs, int64_t out,
                         int inp, int ef) {

@@ -47,6 +47,7 @@ SIGNATURES = {
     "fwhip_encoder_set_tome": (C.c_int32, [_vp, C.c_int32, C.c_int32]),
     "fwhip_encoder_set_tome_schedule": (C.c_int32, [_vp, C.c_int32, C.c_int32]),
     "fwhip_decoder_set_kv_f16": (C.c_int32, [_vp, C.c_int32]),
+    "fwhip_decoder_set_cross_v_block": (C.c_int32, [_vp, C.c_int32]),
     "fwhip_tome_merge": (C.c_int32, [_vp, _vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _vp, _vp, _i32p]),
     "fwhip_encoder_gemm_i8": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, _vp, _vp]),
     "fwhip_encoder_gemm_i8_fused": (C.c_int32, [_vp, C.c_int32, C.c_int32, _vp, C.c_int32, C.c_int32, _vp, _vp]),
@@ -396,6 +397,11 @@ class Decoder:
         (True, the initial setting) or f32 (False, the reference's default)."""
         check(lib().fwhip_decoder_set_kv_f16(self.h, 1 if on else 0))
         self.kv_f16 = bool(on)
+
+    def set_cross_v_block(self, on: bool):
+        """FW_CROSS_V_BLOCK: block-int8 cross V with f32 softmax weights in the
+        value pass, for int8-arm states made afterwards."""
+        check(lib().fwhip_decoder_set_cross_v_block(self.h, 1 if on else 0))
 
     def state(self, n_streams: int, enc_frames: int) -> "DecoderState":
         return DecoderState(self, n_streams, enc_frames)

@@ -349,6 +349,16 @@ fwhip_status fwhip_decoder_set_exact(fwhip_decoder *dec, int32_t exact);
  * (4 x n_layer x n_text_ctx x d x 2 bytes per stream). */
 fwhip_status fwhip_decoder_set_kv_f16(fwhip_decoder *dec, int32_t on);
 
+/* Replaces FW_CROSS_V_BLOCK (cross_v_block_enabled, decoder.rs:1496-1520; off
+ * by default), read when a state is made: on the int8 arm, the states that
+ * fwhip_dstate_new makes after fwhip_decoder_set_cross_v_block(dec, 1) keep
+ * each head's cross V^T block-quantized along the encoder frames
+ * (quantize_f16_to_i8_blocked, 32 frames per scale, decoder.rs:1249-1263) and
+ * run the cross attention's value pass as gemv_i8w_f32a_blocked on the f32
+ * softmax weights (decoder.rs:1605-1608) instead of gemv_i8.  No effect on the
+ * f16 arm. */
+fwhip_status fwhip_decoder_set_cross_v_block(fwhip_decoder *dec, int32_t on);
+
 /* A cohort of n_streams independent DecoderStates (decoder.rs:980-1027), each
  * with its own f16 self-attention KV cache (KvCache, nn.rs:5138) of
  * n_text_ctx tokens and its own cross K/V over enc_frames encoder rows

@@ -79,6 +79,7 @@ def lib():
         "ref_attention_decode_f16": (None, [f32p, u16p, u16p, C.c_int, C.c_int, C.c_int, f32p]),
         "ref_attention_decode_f32": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, f32p]),
         "ref_decoder_set_kv_f16": (None, [C.c_void_p, C.c_int]),
+        "ref_decoder_set_cross_v_block": (None, [C.c_void_p, C.c_int]),
         "ref_encoder_new": (C.c_void_p, [C.POINTER(abi.EncoderWeights), C.c_int]),
         "ref_encoder_free": (None, [C.c_void_p]),
         "ref_encoder_forward": (C.c_int, [C.c_void_p, f32p, C.c_int, f32p, C.c_int]),
@@ -442,6 +443,10 @@ class Decoder:
     def set_kv_f16(self, on):
         """FW_KV_F16 for the states made next (True: f16 cache; False: f32)."""
         lib().ref_decoder_set_kv_f16(self.h, 1 if on else 0)
+
+    def set_cross_v_block(self, on):
+        """FW_CROSS_V_BLOCK for the states made next (the int8 arm)."""
+        lib().ref_decoder_set_cross_v_block(self.h, 1 if on else 0)
 
     def state(self, enc):
         return DState(self, enc)

@@ -1006,6 +1006,7 @@ struct ref_decoder {
     fwhip_hparams hp;
     int arm, d, H, dh, L, V, nctx, dff;
     int kv_f16; /* FW_KV_F16 for the states made next (1: f16 cache, 0: f32) */
+    int cross_v_block; /* FW_CROSS_V_BLOCK for the states made next (int8 arm) */
     const uint16_t *tok_emb;
     const float *pos_emb, *ln_w, *ln_b;
     int8_t *emb8;
@@ -1019,6 +1020,8 @@ struct ref_dstate {
     float *kvf_k, *kvf_v;    /* [L, nctx, d] f32 (FW_KV_F16 unset: the reference's default) */
     uint16_t *ck16, *cvt16;  /* [L*H][T*dh] natural K, [L*H][dh*T] transposed V */
     int8_t *ck8, *cvt8;
+    int8_t *cvb8;            /* FW_CROSS_V_BLOCK: [L*H][dh*T] block-int8 V^T (32-frame blocks) */
+    float *cvbs;             /* [L*H][dh][ceil(T/32)] block scales */
     float *ck8s, *cvt8s;     /* [L*H][T], [L*H][dh] */
     /* FAST restatement only: per layer the scaled self-attention keys
      * f16_to_f32(k) * d_head^-0.25 of cached rows [0, kt_len[l]), transposed
@@ -1144,6 +1147,16 @@ ref_dstate *ref_dstate_new(const ref_decoder *dd, const float *enc, int T) {
             ref_quantize_f16_to_i8(s->cvt16 + (size_t)lh * T * dh, dh, T, s->cvt8 + (size_t)lh * T * dh,
                                    s->cvt8s + (size_t)lh * dh);
         }
+        if (dd->cross_v_block) {
+            /* FW_CROSS_V_BLOCK (decoder.rs:1249-1263): each head's f16 V^T
+             * [dh, T] block-quantized along the frames, 32 per scale */
+            int nb = (T + 31) / 32;
+            s->cvb8 = (int8_t *)malloc((size_t)L * H * T * dh);
+            s->cvbs = (float *)malloc(sizeof(float) * (size_t)L * H * dh * nb);
+            for (int lh = 0; lh < L * H; lh++)
+                ref_quantize_f16_to_i8_blocked(s->cvt16 + (size_t)lh * T * dh, dh, T, 32,
+                                               s->cvb8 + (size_t)lh * T * dh, s->cvbs + (size_t)lh * dh * nb);
+        }
     }
     s->len = 0;
     return s;
@@ -1153,7 +1166,7 @@ void ref_dstate_free(ref_dstate *s) {
     if (!s) return;
     free(s->kt); free(s->kt_len);
     free(s->kv_k); free(s->kv_v); free(s->kvf_k); free(s->kvf_v); free(s->ck16); free(s->cvt16);
-    free(s->ck8); free(s->cvt8); free(s->ck8s); free(s->cvt8s);
+    free(s->ck8); free(s->cvt8); free(s->ck8s); free(s->cvt8s); free(s->cvb8); free(s->cvbs);
     free(s);
 }
 void ref_dstate_reset(ref_dstate *s) {
@@ -1311,6 +1324,8 @@ void ref_attention_decode_f32(const float *q, const float *kc, const float *vc, 
 /* FW_KV_F16 for the states ref_dstate_new makes next (1: f16, the initial
  * setting; 0: f32, the reference's default). */
 void ref_decoder_set_kv_f16(ref_decoder *dd, int on) { dd->kv_f16 = on != 0; }
+/* FW_CROSS_V_BLOCK for the states made next (the int8 arm; default off). */
+void ref_decoder_set_cross_v_block(ref_decoder *dd, int on) { dd->cross_v_block = on != 0; }
 
 /* cross_attention, decoder.rs:1524-1716 (FW_CROSS_F16 on; int8 K/V when the
  * int8 copies exist): qh = q*s; scores = gemv(K_h, qh); softmax; out =
@@ -1330,7 +1345,11 @@ static void cross_attn(const ref_decoder *dd, const ref_dstate *s, int li, const
             if (dd->arm == FWHIP_DEC_INT8) {
                 gemv_i8_serial(s->ck8 + lh * T * dh, s->ck8s + lh * T, T, dh, qh, sc, xq);
                 rf_softmax_row(sc, T);
-                gemv_i8_serial(s->cvt8 + lh * T * dh, s->cvt8s + lh * dh, dh, T, sc, out + h * dh, xq);
+                if (s->cvb8) /* block-int8 V x f32 softmax weights (decoder.rs:1605-1608) */
+                    ref_gemv_i8w_f32a_blocked(s->cvb8 + lh * T * dh, s->cvbs + lh * dh * ((T + 31) / 32), dh, T,
+                                              32, sc, NULL, out + h * dh);
+                else
+                    gemv_i8_serial(s->cvt8 + lh * T * dh, s->cvt8s + lh * dh, dh, T, sc, out + h * dh, xq);
             } else {
                 for (int j = 0; j < T; j++) sc[j] = rf_dot_f16c(s->ck16 + (lh * T + j) * dh, qh, dh);
                 rf_softmax_row(sc, T);
@@ -1349,7 +1368,11 @@ static void cross_attn(const ref_decoder *dd, const ref_dstate *s, int li, const
         if (dd->arm == FWHIP_DEC_INT8) {
             ref_gemv_i8(s->ck8 + lh * T * dh, s->ck8s + lh * T, T, dh, qh, NULL, sc);
             softmax_row(sc, T);
-            ref_gemv_i8(s->cvt8 + lh * T * dh, s->cvt8s + lh * dh, dh, T, sc, NULL, out + h * dh);
+            if (s->cvb8)
+                ref_gemv_i8w_f32a_blocked(s->cvb8 + lh * T * dh, s->cvbs + lh * dh * ((T + 31) / 32), dh, T, 32,
+                                          sc, NULL, out + h * dh);
+            else
+                ref_gemv_i8(s->cvt8 + lh * T * dh, s->cvt8s + lh * dh, dh, T, sc, NULL, out + h * dh);
         } else {
             ref_gemv_f16(s->ck16 + lh * T * dh, T, dh, qh, NULL, sc);
             softmax_row(sc, T);

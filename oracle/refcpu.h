@@ -99,6 +99,7 @@ void ref_enc_i7_gemm(const ref_encoder *e, int layer, int which, const float *x,
 /* ---- decoder ---- */
 typedef struct ref_decoder ref_decoder;
 void ref_decoder_set_kv_f16(ref_decoder *dd, int on); /* FW_KV_F16 for the states made next */
+void ref_decoder_set_cross_v_block(ref_decoder *dd, int on); /* FW_CROSS_V_BLOCK, likewise */
 typedef struct ref_dstate ref_dstate;
 ref_decoder *ref_decoder_new(const fwhip_decoder_weights *w, int arm);
 void ref_decoder_free(ref_decoder *d);
