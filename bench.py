@@ -197,11 +197,12 @@ def measured_traffic(which):
         return None, path
 
 
-def verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, n_tokens, filt, got, tome=0):
+def verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, n_tokens, filt, got, tome=0, kv_f16=True):
     """The job once more in exact mode (encoder and cross K/V in the reference's
-    strict-parity arithmetic, bit-identical to it; tome: the same ToMe setting
-    as the timed job), decoded on each arm; returns per arm the exact tokens, and
-    how many of the timed job's windows (got: arm -> tokens) match them."""
+    strict-parity arithmetic, bit-identical to it; tome and kv_f16: the same ToMe
+    setting and self-attention cache as the timed job), decoded on each arm;
+    returns per arm the exact tokens, and how many of the timed job's windows
+    (got: arm -> tokens) match them."""
     from franken_whisper_amd import abi, native
 
     cfg = model.cfg
@@ -215,6 +216,7 @@ def verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, n_tok
     for arm, toks in got.items():
         dec = native.Decoder(ctx, model, arm)
         dec.set_exact(True)
+        dec.set_kv_f16(kv_f16)
         st = dec.state(W, cfg.n_audio_ctx)
         st.set_cross(states)
         ref = st.greedy(prompt, n_tokens, filt)
@@ -772,6 +774,44 @@ def main():
         ctx.synchronize()
         tome_run["encoder_ms"] = round((time.perf_counter() - t) * 1e3, 2)
         enc.set_tome(0, 3)
+    # the reference's defaults together: the ToMe encoder above, the int8
+    # decoder arm and the f32 self-attention cache (FW_KV_F16 unset), timed the
+    # same way, with its own exact-mode token check
+    ref_default = None
+    if a.workload == "job" and a.tome == 0 and not a.no_tome_run and not a.no_verify:
+        enc.set_tome(-1, 3)
+        decd = native.Decoder(ctx, model, abi.DEC_INT8)
+        decd.set_kv_f16(False)
+        std = decd.state(W, cfg.n_audio_ctx)
+        toksd = None
+        for i in range(a.warmup + a.steps):
+            if i == a.warmup:
+                ctx.synchronize()
+                td = time.perf_counter()
+            encode()
+            std.set_cross(enc_out)
+            toksd = std.greedy(prompt, a.tokens, filt)
+        ctx.synchronize()
+        msd = (time.perf_counter() - td) * 1e3 / a.steps
+        ref_default = {"value": round(30.0 * W / (msd * 1e-3), 2), "ms_per_step": round(msd, 3), "tokens": toksd}
+        # the same job in exact mode (bit-identical to the reference's strict
+        # mode): one untimed pass for its buffers, one timed
+        enc.set_exact(True)
+        decd.set_exact(True)
+        for i in range(2):
+            if i == 1:
+                ctx.synchronize()
+                td = time.perf_counter()
+            encode()
+            std.set_cross(enc_out)
+            std.greedy(prompt, a.tokens, filt)
+        ctx.synchronize()
+        mse = (time.perf_counter() - td) * 1e3
+        ref_default["exact_mode"] = {"value": round(30.0 * W / (mse * 1e-3), 2), "ms_per_step": round(mse, 3)}
+        enc.set_exact(a.exact)
+        std.close()
+        decd.close()
+        enc.set_tome(0, 3)
     verify = None
     if a.workload == "job" and not a.no_verify:
         got = {abi.DEC_F16 if a.dec_arm == "f16" else abi.DEC_INT8: last_tokens_main}
@@ -788,6 +828,16 @@ def main():
                                 "window after block 3 (tome_r_for, encoder.rs:1264-1337; not byte-exact against "
                                 "the un-merged encoder, WER-certified there); tokens checked against exact mode "
                                 "with the same ToMe")
+        if ref_default:
+            vd = verify_tokens(ctx, model, mel_dev, mel_frames, offsets, nf, W, prompt, a.tokens, filt,
+                               {abi.DEC_INT8: ref_default.pop("tokens")}, tome=-1, kv_f16=False)
+            ref_default["tokens_identical_to_exact"] = f"{vd[abi.DEC_INT8][1]}/{W} windows"
+            ref_default["note"] = ("the reference's default configuration in one job: ToMe (500 of 1500 rows after "
+                                   "block 3), the int8 decoder arm and the f32 self-attention cache (FW_KV_F16 "
+                                   "unset); fast-mode tokens checked against exact mode with the same settings "
+                                   "(the int8 arm re-quantizes every linear's input, so fast mode's sub-ulp "
+                                   "differences move tokens); exact_mode: the same job in exact mode, bit-identical "
+                                   "to the reference's strict mode")
 
     audio_s = 30.0 * W
     out = {
@@ -847,6 +897,8 @@ def main():
         out["int8_decoder_arm"] = int8_arm
     if tome_run:
         out["tome_default_job"] = tome_run
+    if ref_default:
+        out["reference_default_job"] = ref_default
     out["setup_s"] = round(t_setup, 1)
     if a.workload == "job" and not a.no_cpu_baseline:
         cb, cpu_toks = cpu_baseline(model, W, a.tokens, a.cpu_threads, a.cpu_runs, arm_main)

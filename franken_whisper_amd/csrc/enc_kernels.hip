@@ -716,57 +716,191 @@ __global__ void k_im2col_f32(const float *x, int B, int Tin, int Cin, int stride
     out[idx] = (ti >= 0 && ti < Tin) ? x[((size_t)b * Tin + ti) * Cin + ci] : 0.0f;
 }
 
-// Per-head attention of attention_raw (FW_ATTN_NO_SDPA=1, nn.rs:6035-6131):
-// scores[i][j] = sum_d (q[i,d]*s) * (k[j,d]*s) in ascending d (strict matmul),
-// s = 64^-0.25.  q, k, v rows of width ld starting at column offsets.
-__global__ void k_attn_scores_exact(const float *qkv, int ld, int qoff, int koff, int T, int H, float scale,
-                                    float *S) {
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    size_t TT = (size_t)T * T;
-    int bh = blockIdx.y;
-    if (idx >= TT) return;
-    int b = bh / H, h = bh % H;
-    int i = (int)(idx / T), j = (int)(idx % T);
-    const float *q = qkv + ((size_t)b * T + i) * ld + qoff + h * 64;
-    const float *k = qkv + ((size_t)b * T + j) * ld + koff + h * 64;
-    float acc = 0.0f;
-    for (int dd = 0; dd < 64; dd++) acc += (q[dd] * scale) * (k[dd] * scale);
-    S[(size_t)bh * TT + idx] = acc;
+// Per-head attention of attention_raw (FW_ATTN_NO_SDPA=1, nn.rs:6035-6131),
+// in three tiled launches whose every output keeps the reference's own
+// operation sequence (only the scheduling is tiled):
+//   scores[i][j] = sum_d (q[i,d]*s) * (k[j,d]*s) in ascending d (strict matmul),
+//     s = 64^-0.25, each scaled operand rounded once as in the reference;
+//   softmax_rows (nn.rs:4880-4963): max, glibc-exact expf, the sequential sum,
+//     *= 1/sum (a row whose max is not finite is left as it is);
+//   out[i, h*64+dd] = sum_j p[i][j] * v[j, dd] in ascending j (strict matmul).
+// q, k, v rows of width ld at column offsets; S [B*H, T, T].
+
+// 64 x 64 score tile of one (window, head): 256 threads, 4 x 4 outputs each.
+// Also leaves each row's maximum over the tile's columns in pm[row][tile]
+// (the max fold of softmax_rows ignores NaN and is order-free).
+__global__ void __launch_bounds__(256) k_attn_scores_exact(const float *qkv, int ld, int qoff, int koff, int T, int H,
+                                                           float scale, float *S, float *pm) {
+    __shared__ float qs[64][65], ks[64][65];
+    const int bh = blockIdx.z, b = bh / H, h = bh % H;
+    const int i0 = blockIdx.y * 64, j0 = blockIdx.x * 64, t = threadIdx.x;
+    // stage the scaled rows (rows past T read row T - 1; their results are dropped)
+    for (int e = t; e < 64 * 64; e += 256) {
+        const int r = e >> 6, c = e & 63;
+        const int qi = min(i0 + r, T - 1), kj = min(j0 + r, T - 1);
+        qs[r][c] = qkv[((size_t)b * T + qi) * ld + qoff + h * 64 + c] * scale;
+        ks[r][c] = qkv[((size_t)b * T + kj) * ld + koff + h * 64 + c] * scale;
+    }
+    __syncthreads();
+    const int ti = t >> 4, tj = t & 15; // rows ti + 16 a, columns tj + 16 c
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[a][c] = 0.0f;
+    for (int dd = 0; dd < 64; dd++) {
+        float qv[4], kv[4];
+#pragma unroll
+        for (int a = 0; a < 4; a++) qv[a] = qs[ti + 16 * a][dd];
+#pragma unroll
+        for (int c = 0; c < 4; c++) kv[c] = ks[tj + 16 * c][dd];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[a][c] += qv[a] * kv[c];
+    }
+    const size_t TT = (size_t)T * T;
+    const int nt = gridDim.x;
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int i = i0 + ti + 16 * a;
+        float m = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int j = j0 + tj + 16 * c;
+            if (j < T) m = fmaxf(m, acc[a][c]);
+        }
+        // the 16 lanes holding row i's columns
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+        if (i >= T) continue;
+        if (tj == 0) pm[((size_t)bh * T + i) * nt + blockIdx.x] = m;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int j = j0 + tj + 16 * c;
+            if (j < T) S[(size_t)bh * TT + (size_t)i * T + j] = acc[a][c];
+        }
+    }
 }
 
-// softmax_rows (nn.rs:4880-4963): max, glibc-exact expf, sequential sum, *= 1/sum.
-__global__ void k_softmax_rows_exact(float *S, size_t rows, int n) {
-    size_t r = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= rows) return;
-    float *row = S + r * n;
-    float mx = -INFINITY;
-    for (int j = 0; j < n; j++) mx = fmaxf(mx, row[j]);
-    if (!isfinite(mx)) return;
+// softmax_rows over 64 rows per block (4 waves).  Each row's max folds the
+// score tiles' partial maxima pm; then 64-column chunks of the 64 rows go
+// through LDS (double-buffered: the next chunk's loads are in flight while the
+// current one is summed), each exp written back to S in place, and lane r of
+// wave 0 adds row r's exps in index order.  The scaling p = e * (1 / sum) is
+// left to the value pass, which multiplies each staged value by the row's
+// factor sf: 1 / sum, or exactly 1.0 for a row softmax_rows leaves unscaled
+// (a max that is not finite keeps the raw scores; a zero sum keeps the exps).
+#define SMX_CH 64
+__global__ void __launch_bounds__(256) k_softmax_rows_exact(float *S, const float *pm, int nt, size_t rows, int n,
+                                                            float *sf) {
+    __shared__ float ech[2][64][SMX_CH + 1];
+    __shared__ float rmx[64];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const size_t r0 = (size_t)blockIdx.x * 64;
+    const int nr = rows - r0 < 64 ? (int)(rows - r0) : 64;
+    if (t < nr) {
+        const float *p = pm + (r0 + t) * nt;
+        float m = -INFINITY;
+        for (int k = 0; k < nt; k++) m = fmaxf(m, p[k]);
+        rmx[t] = m;
+    }
+    __syncthreads();
+    // thread t stages column c0 + lane of rows w + 4 i
+    float v[16];
+    auto load = [&](int c0) {
+        const int c = c0 + lane;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = w + 4 * i;
+            v[i] = (r < nr && c < n) ? S[(r0 + r) * n + c] : 0.0f;
+        }
+    };
+    auto stash = [&](int c0, int buf) {
+        const int c = c0 + lane;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = w + 4 * i;
+            if (r >= nr || c >= n) continue;
+            const float m = rmx[r];
+            if (!isfinite(m)) continue; // the row is left as it is
+            float e = fw_expf(v[i] - m);
+            e = isfinite(e) ? e : 0.0f;
+            S[(r0 + r) * n + c] = e;
+            ech[buf][r][lane] = e;
+        }
+    };
+    const bool fin = w == 0 && lane < nr && isfinite(rmx[lane]);
+    const int nch = (n + SMX_CH - 1) / SMX_CH;
     float sum = 0.0f;
-    for (int j = 0; j < n; j++) {
-        float e = fw_expf(row[j] - mx);
-        e = isfinite(e) ? e : 0.0f;
-        row[j] = e;
-        sum += e;
+    load(0);
+    for (int ch = 0; ch < nch; ch++) {
+        const int c0 = ch * SMX_CH, buf = ch & 1;
+        stash(c0, buf);
+        __syncthreads();
+        if (ch + 1 < nch) load(c0 + SMX_CH);
+        if (fin) {
+            const int cn = n - c0 < SMX_CH ? n - c0 : SMX_CH;
+            if (cn == SMX_CH) {
+                float e[SMX_CH];
+#pragma unroll
+                for (int j = 0; j < SMX_CH; j++) e[j] = ech[buf][lane][j];
+#pragma unroll
+                for (int j = 0; j < SMX_CH; j++) sum += e[j];
+            } else {
+                for (int j = 0; j < cn; j++) sum += ech[buf][lane][j];
+            }
+        }
     }
-    if (sum > 0.0f) {
-        float inv = 1.0f / sum;
-        for (int j = 0; j < n; j++) row[j] = row[j] * inv;
-    }
+    if (w == 0 && lane < nr) sf[r0 + lane] = (fin && sum > 0.0f) ? 1.0f / sum : 1.0f;
 }
 
-// out[i, h*64+dd] = sum_j P[i][j] * v[j, dd] in ascending j (strict matmul).
-__global__ void k_attn_pv_exact(const float *S, const float *qkv, int ld, int voff, int T, int H, int d, float *out) {
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int bh = blockIdx.y;
-    if (idx >= (size_t)T * 64) return;
-    int b = bh / H, h = bh % H;
-    int i = (int)(idx / 64), dd = (int)(idx % 64);
-    const float *p = S + ((size_t)bh * T + i) * T;
-    const float *v = qkv + (size_t)b * T * ld + voff + h * 64 + dd;
-    float acc = 0.0f;
-    for (int j = 0; j < T; j++) acc += p[j] * v[(size_t)j * ld];
-    out[((size_t)b * T + i) * d + h * 64 + dd] = acc;
+// 64 queries x 64 dims of one (window, head): 256 threads, 4 x 4 outputs
+// each, keys in chunks of 32 through LDS in ascending order
+__global__ void __launch_bounds__(256) k_attn_pv_exact(const float *S, const float *sf, const float *qkv, int ld,
+                                                       int voff, int T, int H, int d, float *out) {
+    __shared__ float ps[64][33], vs[32][65];
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int i0 = blockIdx.x * 64, t = threadIdx.x;
+    const int ti = t >> 4, tj = t & 15; // queries ti + 16 a, dims tj + 16 c
+    const float *P = S + (size_t)bh * T * T;
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[a][c] = 0.0f;
+    for (int k0 = 0; k0 < T; k0 += 32) {
+        const int kn = T - k0 < 32 ? T - k0 : 32;
+        for (int e = t; e < 64 * 32; e += 256) {
+            const int r = e >> 5, c = e & 31;
+            const int qi = min(i0 + r, T - 1);
+            ps[r][c] = c < kn ? P[(size_t)qi * T + k0 + c] * sf[(size_t)bh * T + qi] : 0.0f;
+        }
+        for (int e = t; e < 32 * 64; e += 256) {
+            const int r = e >> 6, c = e & 63;
+            vs[r][c] = r < kn ? qkv[((size_t)b * T + k0 + r) * ld + voff + h * 64 + c] : 0.0f;
+        }
+        __syncthreads();
+        for (int j = 0; j < kn; j++) {
+            float pv[4], vv[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) pv[a] = ps[ti + 16 * a][j];
+#pragma unroll
+            for (int c = 0; c < 4; c++) vv[c] = vs[j][tj + 16 * c];
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[a][c] += pv[a] * vv[c];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int i = i0 + ti + 16 * a;
+        if (i >= T) continue;
+#pragma unroll
+        for (int c = 0; c < 4; c++) out[((size_t)b * T + i) * d + h * 64 + tj + 16 * c] = acc[a][c];
+    }
 }
 
 void fw_launch_im2col_f32(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, float *out) {
@@ -775,15 +909,16 @@ void fw_launch_im2col_f32(hipStream_t st, const float *x, int B, int Tin, int Ci
                        Tout, out);
 }
 void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qoff, int koff, int voff, int B, int T,
-                               int H, int d, float *S, float *out) {
+                               int H, int d, float *S, float *sf, float *out) {
     float scale = powf(64.0f, -0.25f);
-    size_t TT = (size_t)T * T;
-    hipLaunchKernelGGL(k_attn_scores_exact, dim3((unsigned)((TT + 255) / 256), B * H), dim3(256), 0, st, qkv, ld,
-                       qoff, koff, T, H, scale, S);
-    size_t rows = (size_t)B * H * T;
-    hipLaunchKernelGGL(k_softmax_rows_exact, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, st, S, rows, T);
-    hipLaunchKernelGGL(k_attn_pv_exact, dim3((unsigned)(((size_t)T * 64 + 255) / 256), B * H), dim3(256), 0, st, S, qkv,
-                       ld, voff, T, H, d, out);
+    const unsigned nt = (unsigned)((T + 63) / 64);
+    const size_t rows = (size_t)B * H * T;
+    float *pm = sf + rows; // [rows][nt] partial maxima
+    hipLaunchKernelGGL(k_attn_scores_exact, dim3(nt, nt, B * H), dim3(256), 0, st, qkv, ld, qoff, koff, T, H, scale,
+                       S, pm);
+    hipLaunchKernelGGL(k_softmax_rows_exact, dim3((unsigned)((rows + 63) / 64)), dim3(256), 0, st, S, pm, (int)nt,
+                       rows, T, sf);
+    hipLaunchKernelGGL(k_attn_pv_exact, dim3(nt, B * H), dim3(256), 0, st, S, sf, qkv, ld, voff, T, H, d, out);
 }
 
 // ---------------------------------------------------------------------------

@@ -41,7 +41,7 @@ struct EncBufs {
 
 struct EncExactBufs {
     int B = 0, nf = 0;
-    float *c1, *a1, *c2, *h, *qkv, *S, *att, *ff;
+    float *c1, *a1, *c2, *h, *qkv, *S, *sf, *att, *ff; // sf: the softmax rows' scale factors
     std::vector<void *> owned;
 };
 
@@ -511,6 +511,7 @@ static bool ensure_exact_bufs(fwhip_encoder *e, int B, int nf) {
     x.h = A(M * d);
     x.qkv = A(M * 3 * d);
     x.S = A((size_t)B * e->H * T2 * T2);
+    x.sf = A((size_t)B * e->H * T2 * (1 + (T2 + 63) / 64));
     x.att = A(M * d);
     x.ff = A(M * e->dff);
     for (void *p : x.owned)
@@ -557,7 +558,7 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
             fw_launch_gemm_strict(st, x.h, l.qkv16, Mc, 3 * d, d, 0, x.qkv, l.qkv_b, 1.0f, nullptr, Tc, 0, 0, 0,
                                   3 * d, nullptr, nullptr);
         }
-        fw_launch_attention_exact(st, x.qkv, 3 * d, 0, d, 2 * d, B, Tc, H, d, x.S, x.att);
+        fw_launch_attention_exact(st, x.qkv, 3 * d, 0, d, 2 * d, B, Tc, H, d, x.S, x.sf, x.att);
         if (i8) {
             fw_launch_quant_exact_rows(st, x.att, Mc, d, b.aq, b.as);
             FwGemm g = gemm_args(b.aq, nullptr, l.o8, Mc, d, d, b.as, l.o8s, l.o_b, FW_EPI_RESID, X, d);

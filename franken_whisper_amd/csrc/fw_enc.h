@@ -87,8 +87,10 @@ void fw_launch_attention(hipStream_t st, const uint16_t *qh, const uint16_t *ql,
                          const uint16_t *kl, const uint16_t *vth, const uint16_t *vtl, int B, int T, int Tp, int H,
                          int d, int out_mode, float *of, uint16_t *oh, uint16_t *ol);
 void fw_launch_im2col_f32(hipStream_t st, const float *x, int B, int Tin, int Cin, int stride, int Tout, float *out);
+// S [B*H, T, T] and sf [B*H*T * (1 + ceil(T / 64))] are scratch (the scores,
+// then the exps; each row's scale factor, then the score tiles' row maxima)
 void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qoff, int koff, int voff, int B, int T,
-                               int H, int d, float *S, float *out);
+                               int H, int d, float *S, float *sf, float *out);
 // ToMe (enc_tome.hip): merge x [B, T, d] into xm [B, T - r', d] with the
 // unmerge map umap [B, T] (workspace fw_tome_ws_bytes(B, T)); returns T - r'
 bool fw_tome_ok(int T, int d);
