@@ -32,7 +32,7 @@ template <int NV, bool SEQ>
 __global__ void __launch_bounds__(256) k_ln_quant(const float *x, float *y, const float *w, const float *b, int d,
                                                   int rows, int8_t *xq, float *xs) {
     const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (r >= rows) return;
     const int n4 = d >> 2;
     const float4 *xr = (const float4 *)(x + (size_t)r * d);
@@ -86,7 +86,7 @@ __global__ void __launch_bounds__(64) k_embed_ln(const int32_t *tok, const int *
 // of each of its rows, and a lane issues R = 8 groups per round, the next round
 // in flight while the current one is used (a row of 1280 needs one round at 32
 // lanes per row).  Needs K % (8 * LPR) == 0.
-template <int LPR, int SG, bool LN, bool SEQ>
+template <int LPR, int SG, bool LN>
 __global__ void __launch_bounds__(256) k_gemv_f16f(const uint16_t *__restrict__ Wf, const float *__restrict__ bias,
                                                    const float *__restrict__ x, float *y, int N, int K, int ns,
                                                    int ldy, int mode, const float *__restrict__ gelu_tab, int cps,
@@ -135,7 +135,7 @@ __global__ void __launch_bounds__(256) k_gemv_f16f(const uint16_t *__restrict__ 
                 xv[kk] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if (sl < sn) xv[kk] = ((const float4 *)(x + (size_t)(s0 + sl) * K))[okk[kk] ? i : 0];
             }
-            if (sl < sn) fw_ln_quant_vals<5, SEQ>(xv, okk, nullptr, lnw, lnb, K, 0, nullptr, nullptr, lane);
+            if (sl < sn) fw_ln_quant_vals<5>(xv, okk, nullptr, lnw, lnb, K, 0, nullptr, nullptr, lane);
 #pragma unroll
             for (int kk = 0; kk < 5; kk++) {
                 if (okk[kk]) {
@@ -273,7 +273,7 @@ void fw_launch_pack_gemv_f16(hipStream_t st, const uint16_t *W, uint16_t *Wf, in
 // W in fragment order (fw_launch_pack_gemv_f16); K % (8 * lanes per row) == 0
 void fw_launch_gemv_f16f(hipStream_t st, const uint16_t *Wf, const float *bias, const float *x, float *y, int N,
                          int K, int ns, int ldy, int mode, const float *gelu_tab, const float *lnw,
-                         const float *lnb, int lnseq) {
+                         const float *lnb) {
     static int n_cu = 0;
     if (!n_cu) {
         int dev = 0;
@@ -300,15 +300,12 @@ void fw_launch_gemv_f16f(hipStream_t st, const uint16_t *Wf, const float *bias, 
     do {                                                                                                     \
         const int ntile = (N + 256 / LPR_ - 1) / (256 / LPR_);                                               \
         const int grid = one && ntile > 2 * n_cu ? 2 * n_cu : ntile;                                        \
-        if (lnw && lnseq)                                                                                   \
-            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, true, true>), dim3(grid, nby), dim3(256), shm, st, Wf, bias, \
-                               x, y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);                    \
-        else if (lnw)                                                                                       \
-            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, true, false>), dim3(grid, nby), dim3(256), shm, st, Wf,     \
-                               bias, x, y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);              \
+        if (lnw)                                                                                            \
+            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, true>), dim3(grid, nby), dim3(256), shm, st, Wf, bias, x,   \
+                               y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);                       \
         else                                                                                                \
-            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, false, false>), dim3(grid, nby), dim3(256), shm, st, Wf,    \
-                               bias, x, y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);              \
+            hipLaunchKernelGGL((k_gemv_f16f<LPR_, SG, false>), dim3(grid, nby), dim3(256), shm, st, Wf, bias, x,  \
+                               y, N, K, ns, ldy, mode, gelu_tab, cps, spb, lnw, lnb);                       \
     } while (0)
 #define GF_SG(LPR_)                      \
     do {                                 \
@@ -2414,9 +2411,12 @@ __global__ void __launch_bounds__(64) k_quant_f16_rows_ld(const uint16_t *src, i
         }                                                                                           \
     } while (0)
 
+// (seq: one row per block, so that the rows' sequential sums, bound by their
+// LDS reads, each have a CU's LDS to themselves)
 void fw_launch_ln_quant(hipStream_t st, const float *x, float *y, const float *w, const float *b, int d, int rows,
                         int8_t *xq, float *xs, int seq) {
-    FW_ROWS_DISPATCH(k_ln_quant, seq, d, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, d, rows, xq, xs);
+    if (seq) FW_ROWS_DISPATCH1(k_ln_quant, true, d, dim3(rows), dim3(64), 0, st, x, y, w, b, d, rows, xq, xs)
+    else FW_ROWS_DISPATCH1(k_ln_quant, false, d, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, d, rows, xq, xs)
 }
 
 void fw_launch_embed_ln(hipStream_t st, const int32_t *tok, const int *posp, const uint16_t *emb, const float *pemb,

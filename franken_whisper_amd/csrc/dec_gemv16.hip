@@ -61,7 +61,7 @@ __device__ __forceinline__ int g16_pos(int e) {
     return ((k / CPL) * 8 + l) * CPL + (k % CPL);
 }
 
-template <int LPR, int R, int SB, int WPB, bool LN, bool KEYS, bool SEQ>
+template <int LPR, int R, int SB, int WPB, bool LN, bool KEYS>
 __global__ void __launch_bounds__(64 * WPB) k_gemv16(const uint16_t *__restrict__ Wp, const float *__restrict__ bias,
                                                     const float *__restrict__ x, float *y, int N, int K, int ns,
                                                     int ldy, int mode, const float *__restrict__ gelu_tab,
@@ -116,7 +116,7 @@ __global__ void __launch_bounds__(64 * WPB) k_gemv16(const uint16_t *__restrict_
                 xv[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if (sl < sn) xv[q] = ((const float4 *)(x + (size_t)(s0 + sl) * K))[ok[q] ? i : 0];
             }
-            if (sl < sn) fw_ln_quant_vals<5, SEQ>(xv, ok, nullptr, lnw, lnb, K, 0, nullptr, nullptr, lane);
+            if (sl < sn) fw_ln_quant_vals<5>(xv, ok, nullptr, lnw, lnb, K, 0, nullptr, nullptr, lane);
 #pragma unroll
             for (int q = 0; q < 5; q++) {
                 if (ok[q]) {
@@ -355,28 +355,24 @@ struct G16Args {
     int use_filter;
     const int *initialp;
     unsigned long long *keys;
-    int lnseq;
 };
 
 template <int LPR, int R, int SB, int WPB>
 void g16_go(hipStream_t st, int grid, int nsg, const G16Args &a) {
     const size_t shm = (size_t)SB * a.K * 4;
     dim3 g(grid, nsg), b(64 * WPB);
-#define G16_L(LN_, KEYS_, SEQ_)                                                                                    \
-    hipLaunchKernelGGL((k_gemv16<LPR, R, SB, WPB, LN_, KEYS_, SEQ_>), g, b, shm, st, a.Wp, a.bias, a.x, a.y, a.N,  \
+#define G16_L(LN_, KEYS_)                                                                                          \
+    hipLaunchKernelGGL((k_gemv16<LPR, R, SB, WPB, LN_, KEYS_>), g, b, shm, st, a.Wp, a.bias, a.x, a.y, a.N,        \
                        a.K, a.ns, a.ldy, a.mode, a.gelu_tab, a.lnw, a.lnb, a.filt, a.use_filter, a.initialp, a.keys)
     if (a.keys) {
         if constexpr (R == 1) { // the tiling fw_gemv16_key_blocks assumes
-            if (a.lnw && a.lnseq) G16_L(true, true, true);
-            else if (a.lnw) G16_L(true, true, false);
-            else G16_L(false, true, false);
+            if (a.lnw) G16_L(true, true);
+            else G16_L(false, true);
         }
-    } else if (a.lnw && a.lnseq) {
-        G16_L(true, false, true);
     } else if (a.lnw) {
-        G16_L(true, false, false);
+        G16_L(true, false);
     } else {
-        G16_L(false, false, false);
+        G16_L(false, false);
     }
 #undef G16_L
 }
@@ -423,10 +419,10 @@ void g16_pipe(hipStream_t st, int grid_cap, int sb_cap, const G16Args &a) {
 void fw_launch_gemv16(hipStream_t st, const uint16_t *Wp, const float *bias, const float *x, float *y, int N, int K,
                       int ns, int ldy, int mode, const float *gelu_tab, const float *lnw, const float *lnb,
                       const fwhip_filter *filt, const int *initialp, unsigned long long *keys, int r, int sb_cap,
-                      int grid_cap, int lnseq) {
+                      int grid_cap) {
     const int n_cu = g_n_cu();
     const int lpr = fw_gemv16_lpr(N, K);
-    G16Args a{Wp, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb, {}, filt != nullptr, initialp, keys, lnseq};
+    G16Args a{Wp, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb, {}, filt != nullptr, initialp, keys};
     if (filt) a.filt = *filt;
     else memset(&a.filt, 0, sizeof a.filt);
     // shapes measured on MI355X for cohorts of 1, 10 and 16 streams:

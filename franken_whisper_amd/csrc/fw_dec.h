@@ -29,32 +29,79 @@ __device__ __forceinline__ void fw_ln_load_wb(const bool (&ok)[NV], const float 
 }
 
 // The reference's sequential f64 loops over a row held as above (element
-// 4 (l + 64 k) + j in lane l, component j of xv[k]; d = 4 n4), formed by
-// every lane from the lanes' values read one by one in index order:
+// 4 (l + 64 k) + j in lane l, component j of xv[k]; d = 4 n4):
 // SQ = false: sum of (f64)x; SQ = true: sum of ((f64)x - mean)^2
-// (nn.rs:4425-4438).  Uniform; every lane of the wave must call it.
+// (nn.rs:4425-4438).  Every lane forms its terms into the wave's LDS slot
+// (one slot for each of the block's first 4 waves: only waves 0-3 may call
+// it), then lane 0 adds them in index order, each batch of the slot's reads
+// issued while the previous batch is added (the chain of dependent f64 adds
+// is the floor; an LDS read costs the wave the same for one lane as for 64,
+// so the reads go 16 bytes at a time, a batch ahead), and the sum is
+// broadcast.  Uniform; every lane of the wave must call it.
+#define FW_SEQ_NB 8
+__device__ __forceinline__ void fw_seq_ld(const double2 *t2, int i, double2 (&a)[FW_SEQ_NB]) {
+#pragma unroll
+    for (int u = 0; u < FW_SEQ_NB; u++) a[u] = t2[i + u];
+}
+__device__ __forceinline__ double fw_seq_add(double s, const double2 (&a)[FW_SEQ_NB]) {
+#pragma unroll
+    for (int u = 0; u < FW_SEQ_NB; u++) {
+        s = s + a[u].x;
+        s = s + a[u].y;
+    }
+    return s;
+}
+// the wave's slot (one array per row width, shared by both sums)
+template <int NV>
+__device__ __forceinline__ double2 *fw_seq_slot() {
+    __shared__ double2 fw_seq_tm[4][128 * NV];
+    return fw_seq_tm[(threadIdx.x >> 6) & 3];
+}
 template <int NV, bool SQ>
 __device__ __forceinline__ double fw_row_seq_sum(const float4 (&xv)[NV], int n4, double mean) {
-    double s = 0.0;
+    const int lane = threadIdx.x & 63;
+    double2 *tm = fw_seq_slot<NV>();
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int nl = n4 - 64 * k < 64 ? n4 - 64 * k : 64; // lanes holding group k
-        for (int l = 0; l < nl; l++) {
-            const float v[4] = {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv[k].x), l)),
-                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv[k].y), l)),
-                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv[k].z), l)),
-                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv[k].w), l))};
+        if (lane + 64 * k < n4) {
+            const double v[4] = {(double)xv[k].x, (double)xv[k].y, (double)xv[k].z, (double)xv[k].w};
+            double t[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 if (SQ) {
-                    const double t = (double)v[j] - mean;
-                    s = s + t * t;
+                    const double u = v[j] - mean;
+                    t[j] = u * u;
                 } else {
-                    s = s + (double)v[j];
+                    t[j] = v[j];
                 }
             }
+            tm[2 * (lane + 64 * k)] = make_double2(t[0], t[1]);
+            tm[2 * (lane + 64 * k) + 1] = make_double2(t[2], t[3]);
         }
     }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    double s = 0.0;
+    if (lane == 0) {
+        const int n2 = 2 * n4, nb = n2 / FW_SEQ_NB; // double2 terms, whole batches
+        double2 a[FW_SEQ_NB], b[FW_SEQ_NB];
+        int i = 0;
+        if (nb > 0) fw_seq_ld(tm, 0, a);
+        for (; i + 2 <= nb; i += 2) {
+            fw_seq_ld(tm, (i + 1) * FW_SEQ_NB, b);
+            s = fw_seq_add(s, a);
+            if (i + 2 < nb) fw_seq_ld(tm, (i + 2) * FW_SEQ_NB, a);
+            s = fw_seq_add(s, b);
+        }
+        if (i < nb) s = fw_seq_add(s, a);
+        for (int j = nb * FW_SEQ_NB; j < n2; j++) {
+            s = s + tm[j].x;
+            s = s + tm[j].y;
+        }
+    }
+    s = __shfl(s, 0, 64);
+    // (the slot is rewritten by the wave's next call; its reads above come first)
+    __builtin_amdgcn_wave_barrier();
     return s;
 }
 

@@ -19,7 +19,7 @@ void fw_launch_pack_gemv_f16(hipStream_t st, const uint16_t *W, uint16_t *Wf, in
 // (k_ln_quant's arithmetic), so the GEMV consumes LN(x).
 void fw_launch_gemv_f16f(hipStream_t st, const uint16_t *Wf, const float *bias, const float *x, float *y, int N,
                          int K, int ns, int ldy, int mode, const float *gelu_tab, const float *lnw = nullptr,
-                         const float *lnb = nullptr, int lnseq = 0);
+                         const float *lnb = nullptr);
 // The f16 GEMV for a cohort in slot order (dec_gemv16.hip): weights packed
 // once by fw_launch_pack_gemv16 (needs fw_gemv16_ok(N, K)); bit-identical to
 // fw_launch_gemv_f16.  keys (logits head): per-tile argmax keys
@@ -31,8 +31,7 @@ void fw_launch_pack_gemv16(hipStream_t st, const uint16_t *W, uint16_t *Wp, int 
 void fw_launch_gemv16(hipStream_t st, const uint16_t *Wp, const float *bias, const float *x, float *y, int N, int K,
                       int ns, int ldy, int mode, const float *gelu_tab, const float *lnw = nullptr,
                       const float *lnb = nullptr, const fwhip_filter *filt = nullptr, const int *initialp = nullptr,
-                      unsigned long long *keys = nullptr, int r = 0, int sb_cap = 0, int grid_cap = 0,
-                      int lnseq = 0);
+                      unsigned long long *keys = nullptr, int r = 0, int sb_cap = 0, int grid_cap = 0);
 void fw_launch_cross_attn_f16(hipStream_t st, const float *qc, const uint16_t *ck, const uint16_t *cvt,
                               float *att, int d, int T, int H, int L, int layer, int ns, float scale);
 // The f16 arm's cross attention on slot-order K / V^T copies (dec_fast.hip):

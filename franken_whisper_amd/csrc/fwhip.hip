@@ -407,15 +407,20 @@ static void fw_gemv16(hipStream_t st, const uint16_t *W, const float *bias, cons
 }
 // y = W LayerNorm(x) (+ bias): the LayerNorm inside the GEMV where its kernel
 // stages whole rows (K <= 1280), else a LayerNorm pass into h.
-// seq: the LayerNorm's sums in the reference's sequential order (exact mode).
+// seq: the LayerNorm's sums in the reference's sequential order (exact mode),
+// always as a pass of its own (one row per block) ahead of the plain GEMV: the
+// GEMV's blocks would each run every sequential sum of their rows, several to
+// a CU (10 streams: 72 against 20 us for fc1), for the same normalized values.
 static void fw_gemv16_ln(hipStream_t st, const uint16_t *W, const float *bias, const float *x, float *h,
                          const float *lnw, const float *lnb, float *y, int N, int K, int ns, int ldy, int mode,
                          const float *gelu_tab, int seq = 0) {
-    if (fw_gemv16_ok(N, K) && K <= 1280) {
-        fw_launch_gemv16(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb, nullptr, nullptr, nullptr, 0, 0,
-                         0, seq);
+    if (seq) {
+        fw_launch_ln_quant(st, x, h, lnw, lnb, K, ns, nullptr, nullptr, 1);
+        fw_gemv16(st, W, bias, h, y, N, K, ns, ldy, mode, gelu_tab);
+    } else if (fw_gemv16_ok(N, K) && K <= 1280) {
+        fw_launch_gemv16(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb);
     } else if (fw_gemv_f16_frag_ok(N, K) && K <= 1280) {
-        fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb, seq);
+        fw_launch_gemv_f16f(st, W, bias, x, y, N, K, ns, ldy, mode, gelu_tab, lnw, lnb);
     } else {
         fw_launch_ln_quant(st, x, h, lnw, lnb, K, ns, nullptr, nullptr, seq);
         fw_gemv16(st, W, bias, h, y, N, K, ns, ldy, mode, gelu_tab);
@@ -965,9 +970,16 @@ static void dec_logits_f16(fwhip_dstate *st, const float *x, float *h, const fwh
     ev.active = false;
     if (timed) fw_timed_begin(c, FWHIP_K_DEC_LOGITS, (double)dd->V * d * 2.0, &ev);
     if (f16_fused_keys(dd)) {
-        // final LayerNorm, tied f16 logits head and per-tile argmax keys in one kernel
-        fw_launch_gemv16(s, dd->emb16f, nullptr, x, st->logits, dd->V, d, S, dd->V, 0, gt, dd->ln_w, dd->ln_b, filt,
-                         st->initial, st->keys, 0, 0, 0, dd->exact);
+        // final LayerNorm, tied f16 logits head and per-tile argmax keys in one
+        // kernel (exact mode: the LayerNorm as a pass of its own, as fw_gemv16_ln)
+        if (dd->exact) {
+            fw_launch_ln_quant(s, x, h, dd->ln_w, dd->ln_b, d, S, nullptr, nullptr, 1);
+            fw_launch_gemv16(s, dd->emb16f, nullptr, h, st->logits, dd->V, d, S, dd->V, 0, gt, nullptr, nullptr, filt,
+                             st->initial, st->keys);
+        } else {
+            fw_launch_gemv16(s, dd->emb16f, nullptr, x, st->logits, dd->V, d, S, dd->V, 0, gt, dd->ln_w, dd->ln_b,
+                             filt, st->initial, st->keys);
+        }
         if (timed) fw_timed_end(c, &ev);
     } else {
         fw_gemv16_ln(s, dd->emb16f, nullptr, x, h, dd->ln_w, dd->ln_b, st->logits, dd->V, d, S, dd->V, 0, gt,
