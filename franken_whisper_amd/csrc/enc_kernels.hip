@@ -44,14 +44,14 @@ __device__ __forceinline__ double eln_wave_sum(double v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
-// With SEQ the row's sum and sum of squared deviations are taken by lane 0 in
-// index order from an LDS copy of the row (the reference's sequential f64
-// loops, bit for bit); the wave's tree order differs from them in the last f64
-// bits, which the f32 result shows on rows of nearly equal values (silence).
+// With SEQ the row's mean and variance come from st [rows][2], the
+// reference's sequential f64 loops (k_enc_ln_stats_seq); the wave's tree order
+// differs from them in the last f64 bits, which the f32 result shows on rows
+// of nearly equal values (silence).
 template <int NV, bool SEQ>
 __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, const float *b, int rows, int d,
                                                 int mode, float *yf, uint16_t *hi, uint16_t *lo, int8_t *q,
-                                                float *qs, int *ovf) {
+                                                float *qs, int *ovf, const double *st) {
     constexpr int ELN_V4 = NV;
     const int lane = threadIdx.x & 63;
     const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -75,24 +75,8 @@ __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, 
     }
     double mean, var;
     if constexpr (SEQ) {
-        __shared__ float srow[4][64 * 4 * ELN_V4];
-        float *sr = srow[threadIdx.x >> 6];
-#pragma unroll
-        for (int k = 0; k < ELN_V4; k++)
-            if (ok[k]) ((float4 *)sr)[lane + 64 * k] = xv[k];
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        double s = 0.0, v = 0.0;
-        if (lane == 0) {
-            for (int j = 0; j < d; j++) s += (double)sr[j];
-            const double m = s / (double)d;
-            for (int j = 0; j < d; j++) {
-                const double t = (double)sr[j] - m;
-                v += t * t;
-            }
-        }
-        mean = __shfl(s, 0, 64) / (double)d;
-        var = __shfl(v, 0, 64) / (double)d;
+        mean = st[2 * r];
+        var = st[2 * r + 1];
     } else {
         double s = 0.0;
 #pragma unroll
@@ -155,6 +139,90 @@ __global__ void __launch_bounds__(256) k_enc_ln(const float *x, const float *w, 
                 ((uint32_t *)(q + r * d))[lane + 64 * k] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
             }
         if (lane == 0) qs[r] = sc;
+    }
+}
+
+// The reference's sequential f64 LayerNorm statistics (nn.rs:4425-4438: the
+// sum of (f64)x in index order, mean = sum / d, then the sum of
+// ((f64)x - mean)^2 in index order, var = that / d) of 64 rows per block:
+// 256-column chunks of the rows go through LDS (each of the 4 waves loads 16
+// rows, one coalesced 256-byte run per row and load), and lane r of wave 0
+// adds row r's chunk in index order, so one LDS read serves all 64 chains; the
+// next chunk's loads are in flight while a chunk is added (double buffer).
+// Two passes over the rows (the mean first).  st [rows][2] = mean, var.
+#define LNS_CH 256
+__global__ void __launch_bounds__(256) k_enc_ln_stats_seq(const float *x, int rows, int d, double *st) {
+    __shared__ float xs[2][64][LNS_CH + 1];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const size_t r0 = (size_t)blockIdx.x * 64;
+    const int nr = rows - r0 < 64 ? (int)(rows - r0) : 64;
+    const int nch = (d + LNS_CH - 1) / LNS_CH;
+    // thread t loads columns c0 + lane + 64 i (i < 4) of rows w + 4 k (k < 16)
+    float v[16][4];
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int r = w + 4 * k;
+            const float *row = x + (r0 + (r < nr ? r : 0)) * d;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int c = c0 + lane + 64 * i;
+                v[k][i] = c < d ? row[c] : 0.0f;
+            }
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) xs[buf][w + 4 * k][lane + 64 * i] = v[k][i];
+    };
+    double mean = 0.0;
+    for (int pass = 0; pass < 2; pass++) {
+        double s = 0.0;
+        load(0);
+        for (int ch = 0; ch < nch; ch++) {
+            const int buf = ch & 1, c0 = ch * LNS_CH;
+            stash(buf);
+            __syncthreads();
+            if (ch + 1 < nch) load(c0 + LNS_CH);
+            if (w == 0) {
+                const float *xr = xs[buf][lane];
+                const int cn = d - c0 < LNS_CH ? d - c0 : LNS_CH;
+                int j = 0;
+                // 16 values requested ahead of their 16 adds
+                for (; j + 16 <= cn; j += 16) {
+                    float e[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) e[u] = xr[j + u];
+                    if (pass == 0) {
+#pragma unroll
+                        for (int u = 0; u < 16; u++) s += (double)e[u];
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 16; u++) {
+                            const double dv = (double)e[u] - mean;
+                            s += dv * dv;
+                        }
+                    }
+                }
+                for (; j < cn; j++) {
+                    if (pass == 0) {
+                        s += (double)xr[j];
+                    } else {
+                        const double dv = (double)xr[j] - mean;
+                        s += dv * dv;
+                    }
+                }
+            }
+        }
+        // wave 0 has added the last chunk before the next pass restages buffer 0
+        __syncthreads();
+        if (pass == 0) mean = s / (double)d;
+        else if (w == 0 && lane < nr) {
+            st[2 * (r0 + lane)] = mean;
+            st[2 * (r0 + lane) + 1] = s / (double)d;
+        }
     }
 }
 
@@ -923,14 +991,20 @@ void fw_launch_attention_exact(hipStream_t st, const float *qkv, int ld, int qof
 
 // ---------------------------------------------------------------------------
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
-                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs, int *ovf) {
+                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs, int *ovf, double *stats) {
     const dim3 g((rows + 3) / 4), blk(256);
     const bool seq = (mode & FW_LN_SEQ) != 0;
     mode &= ~FW_LN_SEQ;
+    if (seq) {
+        if (!stats) return; // (callers pass the statistics scratch with FW_LN_SEQ)
+        hipLaunchKernelGGL(k_enc_ln_stats_seq, dim3((rows + 63) / 64), dim3(256), 0, st, x, rows, d, stats);
+    }
 #define ELN_CASE(NV)                                                                                              \
     if (seq)                                                                                                    \
-        hipLaunchKernelGGL((k_enc_ln<NV, true>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs, ovf);  \
-    else hipLaunchKernelGGL((k_enc_ln<NV, false>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs, ovf); \
+        hipLaunchKernelGGL((k_enc_ln<NV, true>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs, ovf,   \
+                           (const double *)stats);                                                              \
+    else hipLaunchKernelGGL((k_enc_ln<NV, false>), g, blk, 0, st, x, w, b, rows, d, mode, yf, hi, lo, q, qs, ovf,  \
+                            (const double *)nullptr);                                                           \
     break;
     switch ((d + 255) / 256) {
     case 1: ELN_CASE(1)

@@ -42,6 +42,7 @@ struct EncBufs {
 struct EncExactBufs {
     int B = 0, nf = 0;
     float *c1, *a1, *c2, *h, *qkv, *S, *sf, *att, *ff; // sf: the softmax rows' scale factors
+    double *lnst;                                       // [rows][2] sequential LayerNorm statistics
     std::vector<void *> owned;
 };
 
@@ -514,6 +515,7 @@ static bool ensure_exact_bufs(fwhip_encoder *e, int B, int nf) {
     x.sf = A((size_t)B * e->H * T2 * (1 + (T2 + 63) / 64));
     x.att = A(M * d);
     x.ff = A(M * e->dff);
+    x.lnst = (double *)fw_dalloc(x.owned, sizeof(double) * 2 * M);
     for (void *p : x.owned)
         if (!p) return false;
     return true;
@@ -549,12 +551,13 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
     for (int li = 0; li < e->L; li++) {
         const EncLayerDev &l = e->layers[li];
         if (i8) {
-            fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_I7 | FW_LN_SEQ, nullptr, nullptr, nullptr, b.hq, b.hs);
+            fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_I7 | FW_LN_SEQ, nullptr, nullptr, nullptr, b.hq, b.hs,
+                             nullptr, x.lnst);
             FwGemm g = gemm_args(b.hq, nullptr, l.qkv7, Mc, 3 * d, d, b.hs, l.qkv7s, l.qkv_b, FW_EPI_F32, x.qkv, 3 * d);
             fw_launch_gemm(st, FW_KIND_I8, g);
         } else {
             fw_launch_enc_ln(st, X, l.attn_ln_w, l.attn_ln_b, Mc, d, FW_LN_F32 | FW_LN_SEQ, x.h, nullptr, nullptr, nullptr,
-                             nullptr);
+                             nullptr, nullptr, x.lnst);
             fw_launch_gemm_strict(st, x.h, l.qkv16, Mc, 3 * d, d, 0, x.qkv, l.qkv_b, 1.0f, nullptr, Tc, 0, 0, 0,
                                   3 * d, nullptr, nullptr);
         }
@@ -563,7 +566,8 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
             fw_launch_quant_exact_rows(st, x.att, Mc, d, b.aq, b.as);
             FwGemm g = gemm_args(b.aq, nullptr, l.o8, Mc, d, d, b.as, l.o8s, l.o_b, FW_EPI_RESID, X, d);
             fw_launch_gemm(st, FW_KIND_I8, g);
-            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_I7 | FW_LN_SEQ, nullptr, nullptr, nullptr, b.hq, b.hs);
+            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_I7 | FW_LN_SEQ, nullptr, nullptr, nullptr, b.hq, b.hs,
+                             nullptr, x.lnst);
             g = gemm_args(b.hq, nullptr, l.fc1_7, Mc, dff, d, b.hs, l.fc1_7s, l.fc1_b, FW_EPI_F32, b.ff, dff);
             fw_launch_gemm(st, FW_KIND_I8, g);
             fw_launch_gelu_quant_i7_rows(st, b.ff, Mc, dff, gt, b.gq, b.gs);
@@ -572,7 +576,8 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
         } else {
             fw_launch_gemm_strict(st, x.att, l.o16, Mc, d, d, 5, X, l.o_b, 1.0f, nullptr, Tc, 0, 0, 0, d, nullptr,
                                   nullptr);
-            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_F32 | FW_LN_SEQ, x.h, nullptr, nullptr, nullptr, nullptr);
+            fw_launch_enc_ln(st, X, l.mlp_ln_w, l.mlp_ln_b, Mc, d, FW_LN_F32 | FW_LN_SEQ, x.h, nullptr, nullptr, nullptr, nullptr,
+                             nullptr, x.lnst);
             fw_launch_gemm_strict(st, x.h, l.fc1_16, Mc, dff, d, 3, x.ff, l.fc1_b, 1.0f, nullptr, Tc, 0, 0, 0, dff, gt,
                                   nullptr);
             fw_launch_gemm_strict(st, x.ff, l.fc2_16, Mc, d, dff, 5, X, l.fc2_b, 1.0f, nullptr, Tc, 0, 0, 0, d,
@@ -590,7 +595,8 @@ static fwhip_status enc_run_exact(fwhip_encoder *e, int B, int nf, float *out_de
         }
     }
     X = tome_finish(st, b, X, B, Tc, T2, d, n_merges);
-    fw_launch_enc_ln(st, X, e->lnpw, e->lnpb, M, d, FW_LN_F32 | FW_LN_SEQ, out_dev, nullptr, nullptr, nullptr, nullptr);
+    fw_launch_enc_ln(st, X, e->lnpw, e->lnpb, M, d, FW_LN_F32 | FW_LN_SEQ, out_dev, nullptr, nullptr, nullptr, nullptr,
+                     nullptr, x.lnst);
     hipEventRecord(e1, st);
     hipError_t err = hipStreamSynchronize(st);
     float ms = 0.0f;

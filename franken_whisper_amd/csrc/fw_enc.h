@@ -62,9 +62,11 @@ struct FwGemm {
 
 // false when the operand kind / epilogue pair has no kernel (nothing launched)
 bool fw_launch_gemm(hipStream_t st, int kind, const FwGemm &g);
-// ovf (nullable): as FwGemm::ovf, for the SPLIT output
+// ovf (nullable): as FwGemm::ovf, for the SPLIT output.  With FW_LN_SEQ,
+// stats [rows][2] (f64) is scratch for the sequential statistics (required).
 void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const float *b, int rows, int d, int mode,
-                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs, int *ovf = nullptr);
+                      float *yf, uint16_t *hi, uint16_t *lo, int8_t *q, float *qs, int *ovf = nullptr,
+                      double *stats = nullptr);
 void fw_launch_quant_exact_rows(hipStream_t st, const float *x, int rows, int n, int8_t *q, float *qs);
 // The f16 copy of the GELU table that follows the f32 one (65536 entries) in
 // the context's allocation; tab is the context's f32 table.
