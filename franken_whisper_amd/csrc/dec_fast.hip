@@ -999,7 +999,7 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
 #pragma unroll
         for (int r = LO; r < HI; r++) {
             const int j = r * 64 + wave * 8 + rg;
-            kv[r] = *(const uint4 *)(K + (size_t)(j < T ? j : T - 1) * 64 + l * 8);
+            kv[r] = fw_ld_stream(K + (size_t)(j < T ? j : T - 1) * 64 + l * 8);
         }
     };
     using k0 = std::integral_constant<int, 0>;
@@ -1066,13 +1066,13 @@ __global__ void __launch_bounds__(512) k_cross_attn_f16p(const float *qc, const 
     const uint16_t *vr = V + (size_t)dd * Tv;
     uint4 vreg[XP_MAXG];
 #pragma unroll
-    for (int g = 0; g < XP_MAXG; g++) vreg[g] = *(const uint4 *)(vr + (g < ng ? g : 0) * 64 + l * 8);
+    for (int g = 0; g < XP_MAXG; g++) vreg[g] = fw_ld_stream(vr + (g < ng ? g : 0) * 64 + l * 8);
     // the odd last chunk (when nc is odd, ng * 64 + 32 <= nc * 32 <= Tv)
     const uint2 vodd = *(const uint2 *)(vr + ((nc & 1) ? ng * 64 : 0) + l * 4);
     // the n % 32 tail (rows are Tv >= nc * 32 + 32 long; used by lane 0 only)
     uint4 vtail[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) vtail[i] = *(const uint4 *)(vr + (ntail > 0 ? nc * 32 : 0) + i * 8);
+    for (int i = 0; i < 4; i++) vtail[i] = fw_ld_stream(vr + (ntail > 0 ? nc * 32 : 0) + i * 8);
     mx = fw_block_max(mx, red);
     const bool fin = isfinite(mx);
     // (the value rows are in flight: reads clamped to the scores, the table
@@ -1204,7 +1204,7 @@ __global__ void __launch_bounds__(256) k_cross_scores_f16p(const float *qc, cons
 #pragma unroll
     for (int q = 0; q < NR; q++) {
         const int j = j0 + q * 32 + wave * 8 + rg;
-        kv[q] = *(const uint4 *)(K + (size_t)(j < j1 ? j : (j1 > j0 ? j1 - 1 : 0)) * 64 + l * 8);
+        kv[q] = fw_ld_stream(K + (size_t)(j < j1 ? j : (j1 > j0 ? j1 - 1 : 0)) * 64 + l * 8);
     }
     float mx = -INFINITY;
     float *sc = sbuf + ((size_t)r * H + h) * Tv;
@@ -1260,7 +1260,7 @@ __global__ void __launch_bounds__(512) k_cross_scores_f16pq(const uint16_t *__re
 #pragma unroll
             for (int q = 0; q < NR; q++) {
                 const int j = j0 + q * 64 + wave * 8 + rg;
-                kv[q] = *(const uint4 *)(K + (size_t)(j < j1 ? j : (j1 > j0 ? j1 - 1 : 0)) * 64 + l * 8);
+                kv[q] = fw_ld_stream(K + (size_t)(j < j1 ? j : (j1 > j0 ? j1 - 1 : 0)) * 64 + l * 8);
             }
         },
         [] {});
@@ -1332,11 +1332,11 @@ __global__ void __launch_bounds__(256) k_cross_pv_f16p(const float *sbuf, const 
     const uint16_t *vr = V + (size_t)dd * Tv;
     uint4 vreg[XP_MAXG];
 #pragma unroll
-    for (int g = 0; g < XP_MAXG; g++) vreg[g] = *(const uint4 *)(vr + (g < ng ? g : 0) * 64 + l * 8);
+    for (int g = 0; g < XP_MAXG; g++) vreg[g] = fw_ld_stream(vr + (g < ng ? g : 0) * 64 + l * 8);
     const uint2 vodd = *(const uint2 *)(vr + ((nc & 1) ? ng * 64 : 0) + l * 4);
     uint4 vtail[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) vtail[i] = *(const uint4 *)(vr + (ntail > 0 ? nc * 32 : 0) + i * 8);
+    for (int i = 0; i < 4; i++) vtail[i] = fw_ld_stream(vr + (ntail > 0 ? nc * 32 : 0) + i * 8);
     float mx = -INFINITY;
 #pragma unroll
     for (int k = 0; k < XS_KC; k++) mx = fmaxf(mx, mk[k]);

@@ -96,7 +96,9 @@ __global__ void __launch_bounds__(64 * WPB) k_gemv16(const uint16_t *__restrict_
                 const int g = b * BG + i;
                 // (unconditional: a partial last batch re-reads group G - 1, unused,
                 // so no load sits behind a branch and the waits count exactly)
-                nxt[i][r] = w[(size_t)(g < G ? g : G - 1) * LPR];
+                // (the logits head's weights are read once per step: streamed)
+                if constexpr (KEYS) nxt[i][r] = fw_ld_stream(w + (size_t)(g < G ? g : G - 1) * LPR);
+                else nxt[i][r] = w[(size_t)(g < G ? g : G - 1) * LPR];
             }
         }
     };
