@@ -4,10 +4,12 @@
 #pragma once
 #include "fw_kernels.h"
 
-// A 16-byte global load marked non-temporal, for data a decode step reads
-// once (the cross K/V rows, the logits head's weights): it then leaves the
-// caches to what the step's other kernels read again (the layer weights);
-// measured on the f16 arm's 10-stream step, 403 -> 384 us.
+// A 16-byte global load marked non-temporal.  Every decode step reads all of
+// its weights and cross K/V again; on the f16 arm that is 647 MB a step
+// (10 streams), past the 256 MB last-level cache, so a cyclic sweep would keep
+// none of it.  Loading the cross K/V rows and the logits head's weights
+// (440 MB) this way leaves the cache to the layer weights, which then stay
+// from one step to the next: 10-stream step 403 -> 384 us.
 __device__ __forceinline__ uint4 fw_ld_stream(const void *p) {
     typedef unsigned int u4v __attribute__((ext_vector_type(4)));
     const u4v q = __builtin_nontemporal_load((const u4v *)p);
