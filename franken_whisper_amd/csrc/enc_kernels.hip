@@ -7,6 +7,7 @@
 // MFMA operand layouts (gfx950): A lane l -> row l%32, k block (l/32)*8
 // halves; B lane l -> col l%32, same k block; accumulator r of lane l -> row
 // (r/4)*8 + (l/32)*4 + r%4, col l%32.
+#include <cstdio>
 #include <cstdlib>
 
 #include "fw_enc.h"
@@ -996,7 +997,10 @@ void fw_launch_enc_ln(hipStream_t st, const float *x, const float *w, const floa
     const bool seq = (mode & FW_LN_SEQ) != 0;
     mode &= ~FW_LN_SEQ;
     if (seq) {
-        if (!stats) return; // (callers pass the statistics scratch with FW_LN_SEQ)
+        if (!stats) { // a caller's mistake in this library, never an input's
+            fprintf(stderr, "fw_launch_enc_ln: FW_LN_SEQ without the statistics scratch\n");
+            abort();
+        }
         hipLaunchKernelGGL(k_enc_ln_stats_seq, dim3((rows + 63) / 64), dim3(256), 0, st, x, rows, d, stats);
     }
 #define ELN_CASE(NV)                                                                                              \
