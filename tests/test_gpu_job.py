@@ -95,3 +95,59 @@ def test_turbo_whole_job(ctx):
             assert np.array_equal(np.asarray(toks), exact_toks[w]), f"window {w}: tokens differ from the oracle"
     finally:
         lib.ref_set_fast(0)
+
+
+def test_turbo_job_reference_defaults_exact(ctx):
+    """The same job with the reference's defaults together (ToMe by the
+    reference's rule, 500 of 1500 rows merged after block 3, tome_r_for in
+    encoder.rs:1264-1337; the int8 decoder arm; the f32 self-attention cache,
+    FW_KV_F16 unset) in exact mode: windows 0 and 9 equal the oracle's
+    encoder states bit for bit and its 220 tokens."""
+    cfg = synth.TURBO
+    model = synth.Model(cfg, seed=0)
+    nf = 2 * cfg.n_audio_ctx
+    tk = model.tokens
+    filt = tk.filter()
+    prompt = tk.sot_sequence(language_id=0)
+
+    samples = synth.audio(AUDIO_SEED, 30.0 * W, gaps=True)
+    filters = synth.mel_filterbank(cfg.n_mels)
+    mel_frames = native.mel_frames(samples.size)
+    mel_dev = ctx.empty((cfg.n_mels, mel_frames), np.float32)
+    ctx.log_mel(ctx.array(samples), samples.size, ctx.array(filters), cfg.n_mels, mel_dev)
+    offsets = np.arange(W, dtype=np.int64) * nf
+
+    enc = native.Encoder(ctx, model, abi.ENC_INT8)
+    enc.set_exact(True)
+    enc.set_tome(-1, 3)
+    states = ctx.empty((W, cfg.n_audio_ctx, cfg.n_audio_state), np.float32)
+    enc.forward_mel(mel_dev, mel_frames, offsets, nf, states)
+    enc.close()
+    dec = native.Decoder(ctx, model, abi.DEC_INT8)
+    dec.set_exact(True)
+    dec.set_kv_f16(False)
+    st = dec.state(W, cfg.n_audio_ctx)
+    st.set_cross(states)
+    toks = st.greedy(prompt, N_TOKENS, filt)
+    st.close()
+    dec.close()
+    host = states.download()
+    states.free()
+    print(f"\nwindow token counts: {[len(t) for t in toks]}")
+
+    lib = O.lib()
+    lib.ref_set_num_threads(min(os.cpu_count() or 1, 16))
+    try:
+        lib.ref_set_fast(1)
+        mel = O.log_mel(samples, filters)
+        oenc = O.Encoder(model, abi.ENC_INT8)
+        odec = O.Decoder(model, abi.DEC_INT8)
+        odec.set_kv_f16(False)
+        for w in (0, W - 1):
+            win = np.ascontiguousarray(mel[:, w * nf:(w + 1) * nf].T)
+            y = oenc.forward(win, tome_r=500, tome_after=3)
+            assert_bitexact(host[w], y, f"exact-mode ToMe encoder states, window {w}")
+            otoks = odec.state(y).greedy(prompt, N_TOKENS, filt)
+            assert np.array_equal(np.asarray(otoks), toks[w]), f"window {w}: tokens differ from the oracle"
+    finally:
+        lib.ref_set_fast(0)
