@@ -137,3 +137,52 @@ def test_exact_encoder_on_silent_gaps_bitexact(ctx, setup, prec):
     for w, seek in enumerate((0, 3000, 6000)):
         np.testing.assert_array_equal(got[w].view(np.uint32),
                                       oe.forward(O.mel_window(mel, seek, 3000)).view(np.uint32), err_msg=f"seek {seek}")
+
+
+def test_transcribe_turbo_timestamps_matches_oracle(ctx):
+    """The window driver at large-v3-turbo scale (32 encoder blocks on the
+    int8 plan, 4 decoder layers on the f16 arm, both in exact mode): 65 s of
+    seeded audio with silent gaps, segment timestamps with the carried prompt
+    (the reference's defaults), every window and segment identical to the
+    oracle's transcribe_samples_uncached."""
+    import os
+
+    cfg = synth.TURBO
+    m = synth.Model(cfg, seed=4)
+    tk = m.tokens
+    filt = tk.filter()
+    sot = tk.sot_sequence(language_id=0, timestamps=True)
+    audio = synth.audio(17, 65.0, gaps=True)
+    fb = synth.mel_filterbank(cfg.n_mels)
+    vocab = W.synthetic_vocab(tk.eot)
+    enc = native.Encoder(ctx, m, abi.ENC_INT8)
+    enc.set_exact(True)
+    dec = native.Decoder(ctx, m, abi.DEC_F16)
+    dec.set_exact(True)
+    print("turbo transcribe", flush=True)
+    try:
+        got = native.transcribe(ctx, enc, dec, ctx.array(audio), audio.size, ctx.array(fb), cfg.n_mels, filt, vocab,
+                                sot, timestamps=True)
+    finally:
+        enc.close()
+        dec.close()
+    lib = O.lib()
+    lib.ref_set_num_threads(min(os.cpu_count() or 1, 16))
+    try:
+        lib.ref_set_fast(1)
+        mel = O.log_mel(audio, fb)
+        oenc = O.Encoder(m, abi.ENC_INT8)
+        cache = {}
+
+        def encode(seek):
+            if seek not in cache:
+                cache[seek] = oenc.forward(O.mel_window(mel, seek, 2 * cfg.n_audio_ctx))
+            return cache[seek]
+        want = R.transcribe(encode, O.Decoder(m, abi.DEC_F16), cfg, audio.size, filt, sot, vocab,
+                            R.Params(timestamps=True))
+    finally:
+        lib.ref_set_fast(0)
+    print([(w["seek_cs"], len(w["tokens"]), w["result_len"], w["no_speech"], w["retried"]) for w in got["windows"]],
+          len(got["segments"]), flush=True)
+    _compare(got, want, "turbo ts-carry")
+    assert got["windows"]
