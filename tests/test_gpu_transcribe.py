@@ -139,12 +139,15 @@ def test_exact_encoder_on_silent_gaps_bitexact(ctx, setup, prec):
                                       oe.forward(O.mel_window(mel, seek, 3000)).view(np.uint32), err_msg=f"seek {seek}")
 
 
-def test_transcribe_turbo_timestamps_matches_oracle(ctx):
+@pytest.mark.parametrize("defaults", [False, True], ids=["f16-arm", "reference-defaults"])
+def test_transcribe_turbo_timestamps_matches_oracle(ctx, defaults):
     """The window driver at large-v3-turbo scale (32 encoder blocks on the
-    int8 plan, 4 decoder layers on the f16 arm, both in exact mode): 65 s of
-    seeded audio with silent gaps, segment timestamps with the carried prompt
-    (the reference's defaults), every window and segment identical to the
-    oracle's transcribe_samples_uncached."""
+    int8 plan, 4 decoder layers, both in exact mode): 65 s of seeded audio with
+    silent gaps, segment timestamps with the carried prompt (the reference's
+    defaults), every window and segment identical to the oracle's
+    transcribe_samples_uncached.  On the f16 arm, and with the reference's
+    default configuration: ToMe by its rule (500 of 1500 rows after block 3),
+    the int8 decoder arm and the f32 self-attention cache."""
     import os
 
     cfg = synth.TURBO
@@ -155,11 +158,16 @@ def test_transcribe_turbo_timestamps_matches_oracle(ctx):
     audio = synth.audio(17, 65.0, gaps=True)
     fb = synth.mel_filterbank(cfg.n_mels)
     vocab = W.synthetic_vocab(tk.eot)
+    arm = abi.DEC_INT8 if defaults else abi.DEC_F16
     enc = native.Encoder(ctx, m, abi.ENC_INT8)
     enc.set_exact(True)
-    dec = native.Decoder(ctx, m, abi.DEC_F16)
+    if defaults:
+        enc.set_tome(-1, 3)
+    dec = native.Decoder(ctx, m, arm)
     dec.set_exact(True)
-    print("turbo transcribe", flush=True)
+    if defaults:
+        dec.set_kv_f16(False)
+    print("turbo transcribe", "reference defaults" if defaults else "f16 arm", flush=True)
     try:
         got = native.transcribe(ctx, enc, dec, ctx.array(audio), audio.size, ctx.array(fb), cfg.n_mels, filt, vocab,
                                 sot, timestamps=True)
@@ -172,17 +180,20 @@ def test_transcribe_turbo_timestamps_matches_oracle(ctx):
         lib.ref_set_fast(1)
         mel = O.log_mel(audio, fb)
         oenc = O.Encoder(m, abi.ENC_INT8)
+        odec = O.Decoder(m, arm)
+        if defaults:
+            odec.set_kv_f16(False)
         cache = {}
 
         def encode(seek):
             if seek not in cache:
-                cache[seek] = oenc.forward(O.mel_window(mel, seek, 2 * cfg.n_audio_ctx))
+                win = O.mel_window(mel, seek, 2 * cfg.n_audio_ctx)
+                cache[seek] = oenc.forward(win, tome_r=500, tome_after=3) if defaults else oenc.forward(win)
             return cache[seek]
-        want = R.transcribe(encode, O.Decoder(m, abi.DEC_F16), cfg, audio.size, filt, sot, vocab,
-                            R.Params(timestamps=True))
+        want = R.transcribe(encode, odec, cfg, audio.size, filt, sot, vocab, R.Params(timestamps=True))
     finally:
         lib.ref_set_fast(0)
     print([(w["seek_cs"], len(w["tokens"]), w["result_len"], w["no_speech"], w["retried"]) for w in got["windows"]],
           len(got["segments"]), flush=True)
-    _compare(got, want, "turbo ts-carry")
+    _compare(got, want, "turbo ts-carry" + (" reference defaults" if defaults else ""))
     assert got["windows"]
