@@ -308,6 +308,10 @@ struct fwhip_dstate {
     FwWinStream *w_ws = nullptr;
     uint8_t *w_forced = nullptr;
     int *w_ndone = nullptr;
+    // pinned host buffer the loops' end-of-text polls copy into: the newest
+    // columns of the token history, or the done count (allocated on first use)
+    int32_t *poll_host = nullptr;
+    int poll_cap = 0;
     // batched prompt prefill (f16 arm): activation rows of a chunk of
     // PF_CHUNK positions x S streams, allocated on first use
     std::vector<void *> pf_owned;
@@ -657,6 +661,7 @@ extern "C" void fwhip_dstate_free(fwhip_dstate *st) {
     fw_free_all(st->w_owned);
     fw_free_all(st->pf_owned);
     fw_free_all(st->owned);
+    if (st->poll_host) hipHostFree(st->poll_host);
     delete st;
 }
 
@@ -1247,6 +1252,25 @@ static double dec_step_bytes(const fwhip_dstate *st, int tk) {
 // argmax -> step.  Sampled tokens, the position and the step count live on the
 // device; each step after the first replays one captured graph; the host polls
 // for end-of-text every few steps, so steps stream without a per-token sync.
+// The pinned poll buffer of a state, at least n int32 (a poll copies a few
+// hundred bytes; pageable copies cost ~100 us of idle GPU each).
+static int32_t *poll_buffer(fwhip_dstate *st, int n) {
+    if (st->poll_cap < n) {
+        if (st->poll_host) {
+            hipStreamSynchronize(st->dec->ctx->stream);
+            hipHostFree(st->poll_host);
+            st->poll_host = nullptr;
+            st->poll_cap = 0;
+        }
+        if (hipHostMalloc((void **)&st->poll_host, sizeof(int32_t) * (size_t)n, hipHostMallocDefault) != hipSuccess) {
+            st->poll_host = nullptr;
+            return nullptr;
+        }
+        st->poll_cap = n;
+    }
+    return st->poll_host;
+}
+
 extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *prompt, int32_t n_prompt,
                                             int32_t n_max, const fwhip_filter *filter, int32_t *out_tokens,
                                             int32_t *out_len) {
@@ -1276,6 +1300,12 @@ extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *pro
     std::vector<int32_t> hist((size_t)S * n_max, -1);
     int steps = 1;
     const int poll = 8;
+    // each poll copies the history's newest `poll` columns into pinned memory
+    // and keeps which streams have produced end-of-text so far
+    int32_t *ph = poll_buffer(st, S * poll);
+    if (!ph) return fw_fail(FWHIP_ERR_GENERIC, "pinned poll buffer");
+    std::vector<uint8_t> done(S, 0);
+    int polled = 0; // history columns already examined
     bool use_graph = n_max > 1 && capture_step(st, filter);
     for (int i = 1; i < n_max; i++) {
         r = check_cancel(c);
@@ -1294,16 +1324,17 @@ extern "C" fwhip_status fwhip_decode_greedy(fwhip_dstate *st, const int32_t *pro
         fw_timed_end(c, &ev);
         steps = i + 1;
         if (steps % poll == 0 && steps < n_max) {
-            HIP_TRY(hipMemcpy2DAsync(hist.data(), sizeof(int32_t) * n_max, st->hist, sizeof(int32_t) * st->hist_cap,
-                                     sizeof(int32_t) * steps, S, hipMemcpyDeviceToHost, c->stream));
+            const int nc = steps - polled; // <= poll
+            HIP_TRY(hipMemcpy2DAsync(ph, sizeof(int32_t) * poll, st->hist + polled, sizeof(int32_t) * st->hist_cap,
+                                     sizeof(int32_t) * nc, S, hipMemcpyDeviceToHost, c->stream));
             HIP_TRY(hipStreamSynchronize(c->stream));
             bool all = true;
-            for (int s = 0; s < S && all; s++) {
-                bool found = false;
-                for (int k = 0; k < steps; k++)
-                    if (hist[(size_t)s * n_max + k] == filter->eot) found = true;
-                all = found;
+            for (int s = 0; s < S; s++) {
+                for (int k = 0; k < nc && !done[s]; k++)
+                    if (ph[(size_t)s * poll + k] == filter->eot) done[s] = 1;
+                all = all && done[s];
             }
+            polled = steps;
             if (all) break;
         }
     }
@@ -1464,14 +1495,16 @@ extern "C" fwhip_status fwhip_decode_window(fwhip_dstate *st, const int32_t *pro
                              sizeof(float) * dd->V, S, hipMemcpyDeviceToDevice, c->stream));
     fw_launch_win_select(c->stream, st->logits, dd->V, cfg, st->w_ws, st->hist, st->hist_cap, st->w_rows,
                          st->w_forced, st->w_scratch, st->tok, st->pos, st->w_ndone, st->w_part, st->w_cnt, S);
-    int steps = 1, ndone = 0;
+    int steps = 1;
     const int poll = 8;
+    int32_t *pnd = poll_buffer(st, 1); // the done count, copied to pinned memory
+    if (!pnd) return fw_fail(FWHIP_ERR_GENERIC, "pinned poll buffer");
     bool use_graph = n_max > 1 && win_capture(st, cfg);
     for (int i = 1; i < n_max; i++) {
         if (i % poll == 1 || poll == 1) {
-            HIP_TRY(hipMemcpyAsync(&ndone, st->w_ndone, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+            HIP_TRY(hipMemcpyAsync(pnd, st->w_ndone, sizeof(int), hipMemcpyDeviceToHost, c->stream));
             HIP_TRY(hipStreamSynchronize(c->stream));
-            if (ndone >= S) break;
+            if (*pnd >= S) break;
         }
         r = check_cancel(c);
         if (r != FWHIP_OK) {
