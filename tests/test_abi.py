@@ -56,3 +56,22 @@ def test_init_without_gpu_names_the_cpu_route():
     with __import__("pytest").raises(native.FwhipError) as e:
         native.Context(0)
     assert e.value.code == abi.ERR_UNSUPPORTED
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """Without the built HIP library the binding raises at its first use and
+    names the build step; nothing falls back to another route."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ)
+    env["FWHIP_LIB"] = str(tmp_path / "libfwhip.so")  # does not exist
+    code = ("from franken_whisper_amd import native\n"
+            "try:\n"
+            "    native.Context(0)\n"
+            "except RuntimeError as e:\n"
+            "    print('RAISED', e)\n")
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "RAISED" in r.stdout and "missing" in r.stdout and "build" in r.stdout, r.stdout
